@@ -1,0 +1,272 @@
+"""Headline benchmark: the 4-layer fused forward at C4 on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 300] [--warmup 20] [--workload C4]
+
+Prints ONE JSON line.  A "step" is one forward of the drop-in hook
+(``UserOptimizedTransformer``) over the workload's synthetic batch, inputs
+already resident in HBM; each step is bracketed by HIP events on torch's
+current stream (the harness's method, torch_transformer_benchmark.py:
+491-504) and ``value`` is the median step latency in ms.  TFLOP/s and % of
+the dense bf16 MFMA peak use the algorithmic FLOPs of the full padded S.
+
+Also reported:
+* ``roofline``: the dominant kernel (largest share of one eager forward,
+  measured per launch with HIP events on the stream it runs on), its
+  algorithmic FLOPs per launch over its average launch time, against the
+  MI355X dense peak; ``traffic`` from the committed rocprofv3 FETCH_SIZE /
+  WRITE_SIZE summary when present;
+* ``breakdown``: per-kernel-class time of one eager forward;
+* ``cpu_baseline``: the CPU oracle (fp32 restatement of the reference
+  forward) timed on the host's cores on a bounded sample (one of the
+  sequences, scaled to a whole forward); its output also checks the GPU
+  result for that sequence (``accuracy``).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path[:0] = [str(ROOT), str(ROOT / "tiktok-techjam-2026_amd")]
+
+PEAK_TFLOPS = {"bf16": 2516.6, "f16": 2516.6, "f32": 157.3}
+HBM_GBPS = 8000.0
+
+
+def _percentile(vals, q):
+    s = sorted(vals)
+    pos = (len(s) - 1) * q
+    lo, hi = int(pos), min(int(pos) + 1, len(s) - 1)
+    return s[lo] * (1 - (pos - lo)) + s[hi] * (pos - lo)
+
+
+def _time_steps(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return [s.elapsed_time(e) for s, e in zip(starts, ends)], wall
+
+
+def _breakdown(engine, x, mask, plan):
+    """Per-kernel-class time of one eager forward: each tjk launch bracketed
+    by HIP events on the current stream (the launch stream)."""
+    import torch
+    from tjkernels import ops
+    classes = {}
+    orig = {name: getattr(ops, name) for name in ("gemm", "flash_attention", "add_layernorm")}
+    events = []
+
+    def wrap(name, fn):
+        def inner(*a, **k):
+            label = name
+            if name == "gemm":
+                a0, w = a[0], a[1]
+                epi = a[4] if len(a) > 4 else k.get("epilogue", 0)
+                d = engine.d_model
+                if epi == 1:
+                    label = "gemm_ffn1_gelu"
+                elif w.shape[0] == 3 * d:
+                    label = "gemm_qkv"
+                else:
+                    label = ("gemm_out" if w.shape[1] == d else "gemm_ffn2") + ("_residual" if epi == 2 else "")
+                flops = 2.0 * a0.shape[0] * w.shape[0] * w.shape[1]
+            elif name == "flash_attention":
+                b, s, _, h, hd = a[0].shape
+                flops = 2.0 * b * h * hd * s * (s + 1) if k.get("causal", True) else 4.0 * b * h * hd * s * s
+            else:
+                flops = 0.0
+            s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s0.record()
+            r = fn(*a, **k)
+            s1.record()
+            events.append((label, flops, s0, s1))
+            return r
+        return inner
+
+    for name, fn in orig.items():
+        setattr(ops, name, wrap(name, fn))
+    try:
+        for _ in range(3):  # warm, then keep the last pass
+            events.clear()
+            engine._forward_impl(x, mask, engine._mask_mode(mask))
+        torch.cuda.synchronize()
+    finally:
+        for name, fn in orig.items():
+            setattr(ops, name, fn)
+    for label, flops, s0, s1 in events:
+        c = classes.setdefault(label, {"ms": 0.0, "launches": 0, "flops": 0.0})
+        c["ms"] += s0.elapsed_time(s1)
+        c["launches"] += 1
+        c["flops"] += flops
+    return classes
+
+
+def _kernel_avg_ms(label, engine, x, plan, reps=50):
+    """Average duration of one launch of the dominant kernel, HIP events on
+    its launch stream, over `reps` back-to-back launches."""
+    import torch
+    from tjkernels import ops
+    ws = engine._workspace(x.shape[0], x.shape[1], plan)
+    lw = engine.layers[0]
+    b, s = x.shape[:2]
+    h, hd = engine.num_heads, engine.head_dim
+    if label == "gemm_ffn1_gelu":
+        fn = lambda: ops.gemm(ws.h, lw.w1, lw.b1, ws.mid, ops.EPI_BIAS_GELU, plan.gemm_ffn1)  # noqa: E731
+    elif label == "gemm_ffn2_residual":
+        fn = lambda: ops.gemm(ws.mid, lw.w2, lw.b2, ws.res, ops.EPI_BIAS_RESIDUAL, plan.gemm_ffn2)  # noqa: E731
+    elif label == "gemm_qkv":
+        fn = lambda: ops.gemm(ws.h, lw.wqkv, lw.bqkv, ws.qkv, ops.EPI_BIAS, plan.gemm_qkv)  # noqa: E731
+    elif label == "gemm_out_residual":
+        fn = lambda: ops.gemm(ws.ctx, lw.wo, lw.bo, ws.res, ops.EPI_BIAS_RESIDUAL, plan.gemm_out)  # noqa: E731
+    elif label == "flash_attention":
+        q5 = ws.qkv.view(b, s, 3, h, hd)
+        fn = lambda: ops.flash_attention(q5, ws.ctx, causal=engine.causal, plan=plan.attn_plan)  # noqa: E731
+    else:
+        return None
+    for _ in range(5):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def _traffic(label):
+    """HBM bytes per launch of `label` from the committed rocprofv3 PMC summary."""
+    path = ROOT / "profiles" / "traffic_c4.txt"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        parts = line.split()
+        if len(parts) >= 2 and parts[0] == f"traffic_bytes_per_launch[{label}]":
+            try:
+                return float(parts[1])
+            except ValueError:
+                return None
+    return None
+
+
+def _cpu_baseline(w, sd, x, mask, got):
+    """Time the CPU oracle on one sequence (a bounded sample), scale to the
+    whole forward, and check the GPU output for that sequence."""
+    import torch
+    from oracle import model as oracle
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    n_seq = 1
+    reps = 2 if w.tokens >= 8192 else 5
+    samples = []
+    ref = None
+    for _ in range(reps):
+        t0 = time.perf_counter_ns()
+        ref = oracle.forward(sd, x[:n_seq], mask[:n_seq], w.heads, w.causal, torch.float32)
+        samples.append((time.perf_counter_ns() - t0) / 1e6)
+    per_forward = statistics.median(samples) * w.batch / n_seq
+    tol = 1e-4 if w.dtype == torch.float32 else 2e-2
+    acc = oracle.compare_outputs(ref, got[:n_seq], rtol=tol, atol=tol)
+    acc["padded_rows_zero"] = bool((got[~mask] == 0).all())
+    return ({"value": round(per_forward, 3), "unit": "ms", "cores": cores, "kind": "port",
+             "sample": f"fp32 CPU oracle (oracle/model.py) on {n_seq} of {w.batch} sequences, "
+                       f"median of {reps} runs, scaled x{w.batch // n_seq} to one forward"},
+            {"vs": "CPU oracle fp32, sequence 0", "tolerance": tol, **acc})
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="C4")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-breakdown", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "sequences are independent, so N GPUs would each run this benchmark on B/N "
+              "sequences with no communication.", file=sys.stderr)
+        return 2
+
+    import torch
+    from tjkernels import UserOptimizedTransformer
+    from tjkernels.workloads import WORKLOADS, flops_per_forward, make_inputs, make_state_dict
+
+    w = WORKLOADS[args.workload]
+    dev = torch.device("cuda", 0)
+    sd = make_state_dict(w, seed=0)
+    model = UserOptimizedTransformer(w.config)
+    model.load_state_dict(sd, strict=True)
+    model = model.to(device=dev, dtype=w.dtype).eval()
+    x, mask, lengths = make_inputs(w, seed=100001)
+    xd, md = x.to(device=dev, dtype=w.dtype), mask.to(dev)
+
+    with torch.inference_mode():
+        samples, wall = _time_steps(lambda: model(xd, md), args.steps, args.warmup)
+        got = model(xd, md).cpu()
+        engine = model._tj_engine
+        plan = engine.plan
+        breakdown = {} if args.no_breakdown else _breakdown(engine, xd, md, plan)
+
+    flops = flops_per_forward(w)
+    med = statistics.median(samples)
+    dtype_name = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}[plan.compute_dtype]
+    peak = PEAK_TFLOPS[dtype_name]
+    tflops = flops / (med * 1e-3) / 1e12
+
+    roofline = None
+    if breakdown:
+        dom = max((k for k in breakdown if breakdown[k]["flops"] > 0), key=lambda k: breakdown[k]["ms"])
+        with torch.inference_mode():
+            avg_ms = _kernel_avg_ms(dom, engine, xd, plan)
+        per_launch = breakdown[dom]["flops"] / breakdown[dom]["launches"]
+        achieved = per_launch / (avg_ms * 1e-3) / 1e12
+        roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 1), "peak": peak,
+                    "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
+                    "flops_per_launch": per_launch, "avg_launch_ms": round(avg_ms, 5),
+                    "traffic": _traffic(dom)}
+        for k, v in breakdown.items():
+            v["ms"] = round(v["ms"], 4)
+            if v["flops"]:
+                v["tflops"] = round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 1)
+
+    cpu, acc = (None, None)
+    if not args.no_cpu_baseline:
+        cpu, acc = _cpu_baseline(w, sd, x, mask, got)
+
+    line = {
+        "metric": "4-layer fused fwd latency (ms) + % bf16 MFMA peak, d=1024 S=2048, 1 GPU",
+        "value": round(med, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(med, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": dtype_name, "data": "synthetic",
+        "config": {"workload": w.describe(), "tokens": w.tokens, "plan": plan.label,
+                   "hipgraph": plan.cuda_graph, "residual_epilogue": plan.residual_epilogue},
+        "p90_ms": round(_percentile(samples, 0.9), 4), "min_ms": round(min(samples), 4),
+        "wall_s": round(wall, 3), "tflops": round(tflops, 1),
+        "pct_peak": round(100 * tflops / peak, 2), "gflop_per_forward": round(flops / 1e9, 2),
+        "roofline": roofline, "cpu_baseline": cpu, "accuracy": acc, "breakdown": breakdown,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,137 @@
+/*
+ * tjk.h -- C-ABI of the MI355X (gfx950) fused Transformer-forward kernels.
+ *
+ * Every entry point takes caller-allocated device pointers, explicit leading
+ * dimensions, a dtype enum and a hipStream_t passed as `void*`, enqueues its
+ * kernels on that stream and returns an int status:
+ *     0              success
+ *     negative       invalid argument / unsupported shape or dtype
+ *                    (nothing was launched; see tjk_last_error_string())
+ *     positive       a hipError_t from the launch
+ * No entry point allocates memory, synchronizes the host, or keeps mutable
+ * global state, so all of them are safe inside hipGraph stream capture and
+ * reentrant across streams.  Row-major layouts throughout.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository):
+ *   tjk_add_layernorm  <- fused_add_layernorm, tjkernels/kernels/__init__.py:48-70
+ *                         (Triton kernel tjkernels/kernels/layernorm.py:30-75,
+ *                         launcher :96-127) and the final masked_fill,
+ *                         tjkernels/engine.py:267-268
+ *   tjk_gemm_bias      <- torch.addmm(bias, h, W), tjkernels/engine.py:245 (QKV)
+ *                         and :247 (out-proj); FFN fallback addmm + gelu,
+ *                         tjkernels/kernels/__init__.py:88-89
+ *   tjk_flash_fwd      <- flash_attention, tjkernels/kernels/attention.py:189-226
+ *                         (kernel :34-125), and the SDPA masked fallback,
+ *                         tjkernels/engine.py:184-203
+ *   tjk_ffn            <- fused_ffn, tjkernels/kernels/__init__.py:80-89
+ *                         (Triton kernel tjkernels/kernels/ffn.py:21-69)
+ */
+#ifndef TJK_H
+#define TJK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TJK_ABI_VERSION 1
+
+/* dtypes */
+#define TJK_F32 0
+#define TJK_F16 1
+#define TJK_BF16 2
+
+/* statuses */
+#define TJK_OK 0
+#define TJK_EINVAL (-1)
+#define TJK_EUNSUPPORTED (-2)
+
+/* GEMM epilogues */
+#define TJK_EPI_BIAS 0          /* C = A W^T + b                                   */
+#define TJK_EPI_BIAS_GELU 1     /* C = gelu_erf(A W^T + b)                          */
+#define TJK_EPI_BIAS_RESIDUAL 2 /* R += A W^T + b, R fp32 (C is the fp32 residual) */
+
+/* Version of this ABI (TJK_ABI_VERSION). */
+int tjk_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* tjk_last_error_string(void);
+
+/*
+ * Fused residual-add + LayerNorm over rows of length n.
+ *   x   = res (+ delta)                       computed in fp32
+ *   res_out = x            (if res_out != NULL; may alias res when res is fp32)
+ *   out = (x - mean) * rsqrt(var + eps) * gamma + beta, biased variance,
+ *         written in out_dtype; rows whose row_mask byte is 0 are written as 0
+ *         (row_mask may be NULL, indexed by row).
+ * res_dtype, delta_dtype, out_dtype in {TJK_F32, TJK_F16, TJK_BF16};
+ * delta may be NULL.  Requires n % 4 == 0, n <= 8192, 8-byte aligned rows.
+ */
+int tjk_add_layernorm(const void* res, int res_dtype, int64_t ld_res,
+                      const void* delta, int delta_dtype, int64_t ld_delta,
+                      float* res_out, int64_t ld_res_out,
+                      void* out, int out_dtype, int64_t ld_out,
+                      const float* gamma, const float* beta,
+                      int64_t rows, int64_t n, float eps,
+                      const uint8_t* row_mask, void* stream);
+
+/*
+ * C[m, n] = epilogue(sum_k A[m, k] * W[n, k] + bias[n]) -- W in nn.Linear
+ * [out, in] layout, so both operands are K-contiguous.
+ * A, W, bias and (for TJK_EPI_BIAS / _GELU) C are `dtype`; for
+ * TJK_EPI_BIAS_RESIDUAL, C is the fp32 residual updated in place.
+ * Accumulation is fp32 (IEEE fp32 MFMA for TJK_F32).  bias may be NULL.
+ * Requires k % 8 == 0 (k % 4 for fp32), n % 4 == 0 and 16-byte aligned rows.
+ * plan_id selects the tile shape (tjk_gemm_plan_count() of them; -1 = auto).
+ */
+int tjk_gemm_bias(const void* a, int64_t lda, const void* w, int64_t ldw,
+                  const void* bias, void* c, int64_t ldc,
+                  int64_t m, int64_t n, int64_t k,
+                  int dtype, int epilogue, int plan_id, void* stream);
+
+/* Number of GEMM tile plans for `dtype`, and the tile of plan `id`. */
+int tjk_gemm_plan_count(int dtype);
+int tjk_gemm_plan_info(int dtype, int id, int* block_m, int* block_n, int* waves);
+
+/*
+ * Flash-attention forward over a packed QKV buffer laid out [B, S, 3, H, hd]
+ * with element strides (stride_b, stride_s, stride_c, stride_h) and a unit
+ * stride on hd.  out[b*S + s, h*hd + i] (leading dimension ld_out).
+ *   softmax(Q K^T * scale) V per (b, h), fp32 accumulation and softmax.
+ *   causal     keys j > query i are excluded
+ *   lengths    if non-NULL, keys j >= lengths[b] are excluded
+ *   key_mask   if non-NULL ([B, S] bytes), keys with a 0 byte are excluded
+ * A query row with no admissible key is written as 0.
+ * head_dim in [1, 128], head_dim % 8 == 0 (16-byte aligned rows).
+ */
+int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s,
+                  int64_t stride_c, int64_t stride_h,
+                  void* out, int64_t ld_out,
+                  int batch, int seq, int heads, int head_dim, float scale,
+                  int causal, const int32_t* lengths, const uint8_t* key_mask,
+                  int dtype, int plan_id, void* stream);
+
+/* Number of attention plans for `dtype`. */
+int tjk_flash_plan_count(int dtype);
+
+/*
+ * Feed-forward block: out = gelu_erf(h W1^T + b1) W2^T + b2 with W1 [f, d],
+ * W2 [d, f] (nn.Linear layout).  The [tokens, f] intermediate is rounded to
+ * `dtype` (as the reference does) and lives in `workspace`
+ * (tjk_ffn_workspace_bytes() bytes).  With epilogue TJK_EPI_BIAS_RESIDUAL
+ * `out` is the fp32 residual and the result is added into it.
+ * plan_ids = (plan of the first GEMM) | (plan of the second GEMM) << 8.
+ */
+int tjk_ffn(const void* h, int64_t ldh, const void* w1, const void* b1,
+            const void* w2, const void* b2, void* out, int64_t ld_out,
+            void* workspace, int64_t tokens, int64_t d, int64_t f,
+            int dtype, int epilogue, int plan_ids, void* stream);
+size_t tjk_ffn_workspace_bytes(int64_t tokens, int64_t f, int dtype);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TJK_H */

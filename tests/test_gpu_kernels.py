@@ -1,0 +1,232 @@
+"""Per-kernel parity of the HIP C-ABI against the CPU oracle (fp64).
+
+Each kernel is called through ``tjkernels.ops`` (ctypes -> libtjk.so) on
+seeded inputs and compared with the oracle's fp64 result.  Tolerances are
+stated per test: fp32 accumulation of exactly-representable products, then
+one rounding to the output dtype.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import model as oracle
+from tjkernels import ops
+
+pytestmark = pytest.mark.gpu
+
+DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+# one rounding of an O(1) value in the output dtype, plus fp32 accumulation noise
+OUT_RTOL = {torch.float32: 2e-6, torch.float16: 1e-3, torch.bfloat16: 8e-3}
+
+
+def _gen(seed):
+    g = torch.Generator()
+    g.manual_seed(seed)
+    return g
+
+
+def _close(got, ref, rtol, atol):
+    got = got.double().cpu()
+    err = (got - ref).abs()
+    bound = atol + rtol * ref.abs()
+    bad = ~(err <= bound)
+    assert not bad.any(), (f"{int(bad.sum())}/{bad.numel()} elements off; "
+                           f"max err {float(err.max()):.3e}")
+
+
+# ------------------------------------------------------------------ LayerNorm
+
+@pytest.mark.parametrize("n", [96, 128, 512, 768, 1024, 2048, 8192])
+@pytest.mark.parametrize("res_dt,delta_dt,out_dt", [
+    ("f32", None, "bf16"), ("bf16", None, "bf16"), ("f32", "bf16", "bf16"),
+    ("f32", "f16", "f16"), ("f16", None, "f16"), ("f32", "f32", "f32"), ("f32", None, "f32"),
+])
+def test_add_layernorm(device, n, res_dt, delta_dt, out_dt):
+    rows = 37
+    g = _gen(n)
+    res = (torch.randn(rows, n, generator=g) * 3 + 0.5).to(DT[res_dt])
+    delta = None if delta_dt is None else torch.randn(rows, n, generator=g).to(DT[delta_dt])
+    gamma = torch.randn(n, generator=g)
+    beta = torch.randn(n, generator=g)
+    mask = torch.rand(rows, generator=g) > 0.3
+    x = res.double() + (0 if delta is None else delta.double())
+    ref = oracle.layer_norm(x, gamma.double(), beta.double(), 1e-5)
+    ref = ref.masked_fill(~mask[:, None], 0.0)
+
+    res_d = res.to(device)
+    out = torch.empty(rows, n, dtype=DT[out_dt], device=device)
+    res_out = torch.empty(rows, n, dtype=torch.float32, device=device)
+    ops.add_layernorm(res_d, None if delta is None else delta.to(device), gamma.to(device),
+                      beta.to(device), 1e-5, out, res_out=res_out, row_mask=mask.to(device))
+    torch.cuda.synchronize()
+    # residual: one fp32 add, bit-exact
+    want = res.float() + (0 if delta is None else delta.float())
+    assert torch.equal(res_out.cpu(), want)
+    _close(out, ref, OUT_RTOL[DT[out_dt]], 1e-5 if out_dt == "f32" else 4e-3)
+    # padded rows are exact zeros
+    assert (out.cpu()[~mask] == 0).all()
+
+
+def test_add_layernorm_in_place_and_closed_forms(device):
+    n, rows = 1024, 8
+    gamma = torch.ones(n, device=device)
+    beta = torch.full((n,), 0.25, device=device)
+    # constant rows normalise to beta
+    res = torch.full((rows, n), 3.0, device=device)
+    out = torch.empty(rows, n, device=device)
+    ops.add_layernorm(res, None, gamma, beta, 1e-5, out)
+    assert torch.allclose(out, torch.full_like(out, 0.25), atol=1e-6)
+    # in place: res_out aliases res
+    g = _gen(5)
+    r0 = torch.randn(rows, n, generator=g)
+    d0 = torch.randn(rows, n, generator=g).to(torch.bfloat16)
+    res = r0.to(device)
+    ops.add_layernorm(res, d0.to(device), gamma, torch.zeros(n, device=device), 1e-5, out, res_out=res)
+    torch.cuda.synchronize()
+    assert torch.equal(res.cpu(), r0 + d0.float())
+    o = out.double().cpu()
+    assert torch.allclose(o.mean(-1), torch.zeros(rows, dtype=torch.double), atol=1e-5)
+    assert torch.allclose((o * o).mean(-1), torch.ones(rows, dtype=torch.double), atol=1e-4)
+
+
+# ----------------------------------------------------------------------- GEMM
+
+def _gemm_case(device, m, n, k, dt, epi, plan, seed=0):
+    g = _gen(seed + m + 7 * n + 13 * k)
+    a = torch.randn(m, k, generator=g).to(dt)
+    w = (torch.randn(n, k, generator=g) / math.sqrt(k)).to(dt)
+    bias = torch.randn(n, generator=g).to(dt)
+    ref = a.double() @ w.double().t() + bias.double()
+    if epi == ops.EPI_BIAS_GELU:
+        ref = 0.5 * ref * (1 + torch.erf(ref / math.sqrt(2)))
+    if epi == ops.EPI_BIAS_RESIDUAL:
+        r0 = torch.randn(m, n, generator=g)
+        out = r0.to(device)
+        ref = ref + r0.double()
+    else:
+        out = torch.full((m, n), float("nan"), dtype=dt, device=device)
+    ops.gemm(a.to(device), w.to(device), bias.to(device), out, epi, plan)
+    torch.cuda.synchronize()
+    rtol = 2e-5 if (dt == torch.float32 or epi == ops.EPI_BIAS_RESIDUAL) else OUT_RTOL[dt]
+    _close(out, ref, rtol, 1e-4 if dt != torch.float32 else 1e-5)
+
+
+@pytest.mark.parametrize("plan", range(6))
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_gemm_plans(device, plan, dt):
+    # ragged M and N (not tile multiples), K not a multiple of BK
+    _gemm_case(device, 300, 200, 96, dt, ops.EPI_BIAS, plan)
+    _gemm_case(device, 513, 1028, 1088, dt, ops.EPI_BIAS, plan)
+
+
+@pytest.mark.parametrize("plan", [0, 1])
+def test_gemm_fp32_plans(device, plan):
+    _gemm_case(device, 300, 200, 96, torch.float32, ops.EPI_BIAS, plan)
+    _gemm_case(device, 257, 516, 260, torch.float32, ops.EPI_BIAS, plan)
+
+
+@pytest.mark.parametrize("epi", [ops.EPI_BIAS_GELU, ops.EPI_BIAS_RESIDUAL])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_gemm_epilogues(device, epi, dt):
+    _gemm_case(device, 256, 384, 512, dt, epi, -1)
+
+
+def test_gemm_headline_shapes(device):
+    # the four C4 projections at full size, against fp64 on the CPU
+    for (m, n, k) in [(8192, 3072, 1024), (8192, 1024, 1024), (8192, 4096, 1024), (8192, 1024, 4096)]:
+        _gemm_case(device, m, n, k, torch.bfloat16, ops.EPI_BIAS, -1)
+
+
+def test_gemm_zero_weight_gives_bias(device):
+    a = torch.randn(64, 128, device=device, dtype=torch.bfloat16)
+    w = torch.zeros(256, 128, device=device, dtype=torch.bfloat16)
+    b = torch.randn(256, device=device, dtype=torch.bfloat16)
+    out = torch.empty(64, 256, device=device, dtype=torch.bfloat16)
+    ops.gemm(a, w, b, out)
+    assert torch.equal(out, b.expand(64, 256))
+
+
+# ------------------------------------------------------------------ attention
+
+def _attn_ref(qkv, causal, key_mask=None):
+    """fp64 brute force on [B,S,3,H,hd] (bench/test_flash.py:36-48 pattern)."""
+    b, s, _, h, hd = qkv.shape
+    q, k, v = (qkv[:, :, i].transpose(1, 2).double() for i in range(3))
+    scores = (q @ k.transpose(-2, -1)) * hd ** -0.5
+    if causal:
+        scores = scores.masked_fill(torch.ones(s, s, dtype=torch.bool).triu(1), float("-inf"))
+    if key_mask is not None:
+        scores = scores.masked_fill(~key_mask[:, None, None, :], float("-inf"))
+    probs = torch.softmax(scores, -1).nan_to_num(0.0)
+    return (probs @ v).transpose(1, 2).reshape(b * s, h * hd)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("hd", [8, 32, 64, 128])
+@pytest.mark.parametrize("seq", [1, 37, 200])
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_shapes(device, dt, hd, seq, causal):
+    b, h = 2, 3
+    g = _gen(hd * 1000 + seq)
+    qkv = torch.randn(b, seq, 3, h, hd, generator=g).to(dt)
+    ref = _attn_ref(qkv, causal)
+    for plan in (0, 1):
+        out = torch.full((b * seq, h * hd), float("nan"), dtype=dt, device=device)
+        ops.flash_attention(qkv.to(device), out, causal=causal, plan=plan)
+        torch.cuda.synchronize()
+        _close(out, ref, 1e-5 if dt == torch.float32 else 1e-2,
+               1e-5 if dt == torch.float32 else 1e-2)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_flash_key_mask_and_lengths(device, dt):
+    b, s, h, hd = 3, 150, 2, 64
+    g = _gen(77)
+    qkv = torch.randn(b, s, 3, h, hd, generator=g).to(dt)
+    key_mask = torch.rand(b, s, generator=g) > 0.4
+    key_mask[:, 0] = True
+    for causal in (True, False):
+        ref = _attn_ref(qkv, causal, key_mask)
+        out = torch.empty(b * s, h * hd, dtype=dt, device=device)
+        ops.flash_attention(qkv.to(device), out, causal=causal, key_mask=key_mask.to(device))
+        torch.cuda.synchronize()
+        _close(out, ref, 1e-5 if dt == torch.float32 else 1e-2, 1e-5 if dt == torch.float32 else 1e-2)
+    lengths = torch.tensor([150, 1, 77], dtype=torch.int32)
+    pm = torch.arange(s)[None, :] < lengths[:, None].long()
+    ref = _attn_ref(qkv, False, pm)
+    out = torch.empty(b * s, h * hd, dtype=dt, device=device)
+    ops.flash_attention(qkv.to(device), out, causal=False, lengths=lengths.to(device))
+    torch.cuda.synchronize()
+    _close(out, ref, 1e-5 if dt == torch.float32 else 1e-2, 1e-5 if dt == torch.float32 else 1e-2)
+
+
+def test_flash_closed_forms(device):
+    b, s, h, hd = 2, 96, 4, 64
+    qkv = torch.randn(b, s, 3, h, hd, device=device, dtype=torch.bfloat16)
+    out = torch.empty(b * s, h * hd, device=device, dtype=torch.bfloat16)
+    ops.flash_attention(qkv, out, causal=True)
+    # causal row 0 sees only key 0: output = V_0 exactly
+    v0 = qkv[:, 0, 2].reshape(b, h * hd)
+    assert torch.equal(out.view(b, s, h * hd)[:, 0], v0)
+    # perturbing the last key changes no earlier row
+    qkv2 = qkv.clone()
+    qkv2[:, -1, 1:] += 1.0
+    out2 = torch.empty_like(out)
+    ops.flash_attention(qkv2, out2, causal=True)
+    assert torch.equal(out.view(b, s, -1)[:, :-1], out2.view(b, s, -1)[:, :-1])
+
+
+def test_flash_packed_layout_headline(device):
+    # C4 attention shape read in place from the packed QKV GEMM output
+    b, s, h, hd = 4, 2048, 16, 64
+    qkv = torch.randn(b * s, 3 * h * hd, device=device, dtype=torch.bfloat16)
+    q5 = qkv.view(b, s, 3, h, hd)
+    out = torch.empty(b * s, h * hd, device=device, dtype=torch.bfloat16)
+    ops.flash_attention(q5, out, causal=True)
+    torch.cuda.synchronize()
+    sel = [0, 1, 777, 2047]
+    ref = _attn_ref(q5[:1].cpu(), True).view(s, h * hd)
+    got = out.view(b, s, h * hd)[0].cpu()
+    _close(got[sel], ref[sel], 1e-2, 1e-2)

@@ -1,0 +1,183 @@
+"""Host-side logic that runs without a GPU: the C-ABI library's exports, the
+plan dispatcher, the module skeleton, the engine's guards, mask
+classification, and graph-capture failure handling."""
+
+import json
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import tjkernels
+from tjkernels import Plan, TransformerConfig, UserOptimizedTransformer, _lib
+from tjkernels import plans as plans_mod
+from tjkernels.engine import MASK_GENERAL, MASK_NONE, MASK_PREFIX, Engine
+from tjkernels.graphs import GraphCache
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def test_library_exports_every_declared_symbol():
+    header = (ROOT / "include" / "tjk.h").read_text()
+    declared = set(re.findall(r"^\s*(?:int|const char\*|size_t)\s+(tjk_\w+)\(", header, re.M))
+    assert declared, "no declarations parsed"
+    lib = _lib.load()
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in tjk.h but not exported"
+    assert declared == set(_lib.EXPORTED_SYMBOLS)
+    assert lib.tjk_abi_version() == _lib.ABI_VERSION
+
+
+def test_abi_rejects_bad_arguments_without_launching():
+    lib = _lib.load()
+    # null pointers / bad shapes return a negative status and set the message
+    assert lib.tjk_gemm_bias(None, 8, None, 8, None, None, 8, 4, 4, 8, _lib.BF16, 0, -1, None) < 0
+    assert b"null" in lib.tjk_last_error_string()
+    assert lib.tjk_flash_fwd(None, 0, 0, 0, 0, None, 0, 1, 4, 1, 12, 0.5, 1, None, None,
+                             _lib.BF16, -1, None) < 0
+    assert lib.tjk_add_layernorm(None, 0, 8, None, 0, 0, None, 0, None, 0, 8, None, None,
+                                 2, 6, 1e-5, None, None) < 0
+    assert b"null pointer" in lib.tjk_last_error_string()
+    # empty work is a successful no-op
+    assert lib.tjk_gemm_bias(None, 8, None, 8, None, None, 8, 0, 4, 8, _lib.BF16, 0, -1, None) == 0
+    assert lib.tjk_gemm_plan_count(_lib.BF16) >= 4
+    assert lib.tjk_flash_plan_count(_lib.F32) == 2
+
+
+def test_state_dict_keys_match_reference_layout():
+    cfg = TransformerConfig(2, 8, 32, 4, 64, 2, True)
+    keys = set(UserOptimizedTransformer(cfg).state_dict())
+    want = set()
+    for i in range(2):
+        p = f"layers.{i}."
+        for n in ("norm1", "norm2"):
+            want |= {p + n + ".weight", p + n + ".bias"}
+        for n in ("q_proj", "k_proj", "v_proj", "out_proj"):
+            want |= {p + f"attention.{n}.weight", p + f"attention.{n}.bias"}
+        for n in ("ffn_in", "ffn_out"):
+            want |= {p + n + ".weight", p + n + ".bias"}
+    want |= {"final_norm.weight", "final_norm.bias"}
+    assert keys == want
+    sd = UserOptimizedTransformer(cfg).state_dict()
+    assert sd["layers.0.ffn_in.weight"].shape == (64, 32)
+    assert sd["layers.0.ffn_out.weight"].shape == (32, 64)
+
+
+def test_config_validation():
+    with pytest.raises(ValueError):
+        TransformerConfig(1, 8, 30, 4, 64, 1, True).validate()
+    with pytest.raises(ValueError):
+        TransformerConfig(0, 8, 32, 4, 64, 1, True).validate()
+
+
+def test_no_cpu_path():
+    cfg = TransformerConfig(1, 4, 32, 4, 64, 1, True)
+    m = UserOptimizedTransformer(cfg).eval()
+    with pytest.raises(RuntimeError, match="ROCm"):
+        m(torch.randn(1, 4, 32))
+    with pytest.raises(RuntimeError, match="ROCm"):
+        plans_mod.default_plan(1, 4, 32, 4, 64, 1, True, torch.float32, torch.device("cpu"))
+
+
+def test_plan_json_round_trip_and_table(tmp_path, monkeypatch):
+    p = Plan(compute_dtype=torch.float16, gemm_qkv=2, attn_plan=1, cuda_graph=False, label="x")
+    assert Plan.from_json(json.loads(json.dumps(p.to_json()))) == p
+    key = plans_mod.shape_key(4, 2048, 1024, 16, 4096, 4, True, torch.bfloat16, "gfx950")
+    assert key == "b4_s2048_d1024_h16_f4096_l4_causal_bfloat16@gfx950"
+    f = tmp_path / "plans.json"
+    monkeypatch.setattr(plans_mod, "_PLAN_FILE", f)
+    monkeypatch.setattr(plans_mod, "_cache", None)
+    plans_mod.save_plans({key: p})
+    plans_mod.save_plans({"other@gfx950": Plan(label="y")})
+    table = plans_mod._load_tuned()
+    assert table[key] == p and table["other@gfx950"].label == "y"
+    # an unreadable table is ignored, never fatal
+    f.write_text("{not json")
+    monkeypatch.setattr(plans_mod, "_cache", None)
+    assert plans_mod._load_tuned() == {}
+
+
+def test_plan_validation_rejects_fallback_backends():
+    with pytest.raises(ValueError, match="only 'hip'"):
+        Plan(attn="sdpa").validate()
+    with pytest.raises(ValueError, match="float32 residual"):
+        Plan(residual_dtype=torch.float16).validate()
+    Plan().validate()
+
+
+def test_override_and_env_knobs(monkeypatch):
+    forced = Plan(label="forced")
+    plans_mod.set_override(forced)
+    try:
+        assert plans_mod.select_plan(1, 1, 8, 1, 8, 1, True, torch.float32,
+                                     torch.device("cpu")) is forced
+    finally:
+        plans_mod.set_override(None)
+    monkeypatch.setattr(plans_mod, "device_arch", lambda d: "gfx950")
+    monkeypatch.setattr(plans_mod, "_cache", {})
+    dev = torch.device("cuda", 0)
+    base = plans_mod.select_plan(4, 2048, 1024, 16, 4096, 4, True, torch.bfloat16, dev)
+    assert base.cuda_graph and base.compute_dtype == torch.bfloat16 and base.residual_epilogue
+    big = plans_mod.select_plan(64, 4096, 1024, 16, 4096, 4, True, torch.bfloat16, dev)
+    assert not big.cuda_graph  # x above 64 MiB: no whole-forward graph
+    monkeypatch.setenv("TJ_NO_GRAPH", "1")
+    monkeypatch.setenv("TJ_DEFERRED_RESIDUAL", "1")
+    p = plans_mod.select_plan(4, 2048, 1024, 16, 4096, 4, True, torch.bfloat16, dev)
+    assert not p.cuda_graph and not p.residual_epilogue
+
+
+def test_mask_classification():
+    cfg = TransformerConfig(2, 6, 32, 4, 64, 1, True)
+    eng = Engine(UserOptimizedTransformer(cfg))
+    assert eng._mask_mode(None) == MASK_NONE
+    assert eng._mask_mode(torch.ones(2, 6, dtype=torch.bool)) == MASK_NONE
+    prefix = torch.arange(6)[None, :] < torch.tensor([[3], [6]])
+    assert eng._mask_mode(prefix) == MASK_PREFIX
+    general = prefix.clone()
+    general[0, 1] = False
+    assert eng._mask_mode(general) == MASK_GENERAL
+    # memoised on identity
+    assert eng._mask_modes.get(prefix) == MASK_PREFIX
+    cfg_nc = TransformerConfig(2, 6, 32, 4, 64, 1, False)
+    eng_nc = Engine(UserOptimizedTransformer(cfg_nc))
+    assert eng_nc._mask_mode(prefix) == MASK_GENERAL  # no causal: keys must be masked
+
+
+def test_graph_capture_failure_degrades_to_eager(capsys):
+    cache = GraphCache()
+    # capture cannot happen on the CPU; the cache records None and warns once
+    g = cache.get(("k",), lambda x, m: x, torch.zeros(2), None)
+    assert g is None and len(cache) == 1
+    assert cache.get(("k",), lambda x, m: x, torch.zeros(2), None) is None
+
+
+def test_engine_cached_on_module_without_touching_state_dict():
+    cfg = TransformerConfig(1, 4, 32, 4, 64, 1, True)
+    m = UserOptimizedTransformer(cfg)
+    before = set(m.state_dict())
+    e = tjkernels.get_engine(m)
+    assert tjkernels.get_engine(m) is e
+    assert set(m.state_dict()) == before
+    tjkernels.reset_engines(m)
+    assert tjkernels.get_engine(m) is not e
+
+
+def test_tj_disable_calls_parent_forward(monkeypatch):
+    """TJ_DISABLE=1 defers to the parent class (the harness's baseline)."""
+    class Parent(torch.nn.Module):
+        def __init__(self, cfg):
+            super().__init__()
+            self.config = cfg
+            self.w = torch.nn.Parameter(torch.zeros(1))
+
+        def forward(self, x, mask=None):
+            return x + 1
+
+    class Hook(Parent):
+        def forward(self, x, mask=None):
+            return tjkernels.forward(self, x, mask)
+
+    monkeypatch.setenv("TJ_DISABLE", "1")
+    h = Hook(TransformerConfig(1, 2, 4, 1, 4, 1, True))
+    assert torch.equal(h(torch.zeros(1, 2, 4)), torch.ones(1, 2, 4))

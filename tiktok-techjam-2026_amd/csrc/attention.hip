@@ -1,0 +1,383 @@
+// FlashAttention-2 forward on the packed [B, S, 3, H, hd] QKV buffer.
+//
+// Computes softmax(Q K^T * scale) V per (batch, head) with an fp32 online
+// softmax in base 2, reading Q/K/V in place through strides and writing the
+// context as [B*S, H*hd] (head h at columns h*hd ...), the layout the
+// out-projection consumes.  Replaces the Triton kernel
+// tjkernels/kernels/attention.py:34-125 (launcher :189-226) and, through
+// the `lengths` / `key_mask` arguments, the SDPA fallback used for padded
+// non-causal and general masks (tjkernels/engine.py:184-203,216-228).
+//
+// CDNA4 mapping.  A workgroup is 4 waves; each wave owns NQ blocks of 32
+// queries.  Both products are computed transposed so that every per-query
+// quantity lives in a single lane:
+//     S^T = K Q^T       (MFMA A = K rows from LDS, B = Q held in registers)
+//     O^T += V^T P^T    (MFMA A = V^T rows from LDS, B = P from registers)
+// In the 32x32 accumulator layout lane l owns column l%32, i.e. one query,
+// so the row max/sum of the softmax are in-lane reductions plus a single
+// exchange with lane l^32, and the O rescale by exp2(m_old - m_new) is a
+// per-lane scalar.  The K rows of each 32-key block are read in an order
+// that swaps bits 2 and 3 of the key index; with that order, the eight S^T
+// registers a lane feeds into one 16-key PV step cover 8 consecutive keys,
+// so the matching V^T fragment is one 16-byte LDS read.  V is transposed
+// while it is staged into LDS (pairs of keys packed per 32-bit word).
+//
+// K/V tiles are 64 keys, double-buffered in LDS with a 16-byte row pad;
+// global loads for tile t+1 are issued before the math of tile t.  Causal
+// workgroups only visit key tiles up to their last query, and a wave skips
+// the math of tiles entirely above its own diagonal.  Workgroups are issued
+// longest-first (the last query blocks have the most key tiles).
+
+#include "tjk_common.h"
+
+namespace tjk {
+
+__device__ __forceinline__ int swap_bits_2_3(int x) {
+  return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1);
+}
+
+template <typename T> struct PairPack;
+template <> struct PairPack<bf16> {
+  // two 8-element rows (keys k, k+1) -> 8 words {row0[e], row1[e]}
+  static __device__ __forceinline__ void write(bf16* dst, int ld, uint4 r0, uint4 r1) {
+    const uint32_t a[4] = {r0.x, r0.y, r0.z, r0.w};
+    const uint32_t b[4] = {r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t lo = (a[w] & 0xffffu) | (b[w] << 16);
+      const uint32_t hi = (a[w] >> 16) | (b[w] & 0xffff0000u);
+      *reinterpret_cast<uint32_t*>(dst + (2 * w) * ld) = lo;
+      *reinterpret_cast<uint32_t*>(dst + (2 * w + 1) * ld) = hi;
+    }
+  }
+};
+template <> struct PairPack<f16> {
+  static __device__ __forceinline__ void write(f16* dst, int ld, uint4 r0, uint4 r1) {
+    PairPack<bf16>::write(reinterpret_cast<bf16*>(dst), ld, r0, r1);
+  }
+};
+template <> struct PairPack<float> {
+  static __device__ __forceinline__ void write(float* dst, int ld, uint4 r0, uint4 r1) {
+    const uint32_t a[4] = {r0.x, r0.y, r0.z, r0.w};
+    const uint32_t b[4] = {r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) *reinterpret_cast<uint2*>(dst + e * ld) = make_uint2(a[e], b[e]);
+  }
+};
+
+template <typename T, int HDP, int NQ>
+__global__ __launch_bounds__(256) void flash_fwd_kernel(
+    const T* __restrict__ qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh,
+    T* __restrict__ out, int64_t ld_out, int B, int S, int H, int hd, float scale_log2,
+    int causal, const int32_t* __restrict__ lengths, const uint8_t* __restrict__ key_mask, int nqb) {
+  constexpr int NW = 4;
+  constexpr int BMQ = NW * NQ * 32;     // queries per workgroup
+  constexpr int BNK = 64;               // keys per tile
+  constexpr int VEC = 16 / sizeof(T);   // elements per 16-byte chunk
+  constexpr int LDK = HDP + VEC;        // K tile row pitch (elements)
+  constexpr int LDV = BNK + VEC;        // V^T tile row pitch (elements)
+  constexpr int KC = HDP / 16;          // 16-deep steps along hd
+  constexpr int HB = HDP / 32;          // 32-row blocks of hd in O^T
+  constexpr int CH = HDP / VEC;         // 16-byte chunks per K/V row
+  constexpr int KITEMS = BNK * CH;      // K chunks per tile
+  constexpr int VITEMS = (BNK / 2) * CH;  // (key pair, chunk) items per tile
+  static_assert(KITEMS % 256 == 0, "K tile must split evenly over 256 threads");
+
+  __shared__ __attribute__((aligned(16))) T sK[2][BNK * LDK];
+  __shared__ __attribute__((aligned(16))) T sV[2][HDP * LDV];
+
+  const int BH = B * H;
+  const int rank = blockIdx.x / BH, bh = blockIdx.x % BH;
+  const int qb = causal ? nqb - 1 - rank : rank;
+  const int b = bh / H, h = bh % H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hi = lane >> 5;
+
+  const T* qbase = qkv + (int64_t)b * sb + (int64_t)h * sh;
+  const T* kbase = qbase + sc;
+  const T* vbase = qbase + 2 * sc;
+
+  int kv_len = S;
+  if (lengths != nullptr) kv_len = min(kv_len, max(lengths[b], 0));
+  const int q0 = qb * BMQ;
+  const int wq0 = q0 + wave * NQ * 32;
+  int kend = causal ? min(q0 + BMQ, S) : S;
+  kend = min(kend, kv_len);
+  const int nkt = (kend + BNK - 1) / BNK;
+
+  // ---- Q fragments (B operand of S^T): lane holds Q[q][16c + 8*hi + 0..7]
+  typename Mfma<T>::frag qf[NQ][KC];
+#pragma unroll
+  for (int j = 0; j < NQ; ++j) {
+    const int q = wq0 + j * 32 + l32;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      const int col = 16 * c + 8 * hi;
+      if (q < S && col < hd) {
+        qf[j][c] = Mfma<T>::load(qbase + (int64_t)q * ss + col);
+      } else {
+        float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        qf[j][c] = Mfma<T>::pack(z);
+      }
+    }
+  }
+
+  // ---- staging of one K/V tile through registers
+  constexpr int KPT = KITEMS / 256;
+  constexpr int VPT = (VITEMS + 255) / 256;
+  uint4 rk[KPT], rv0[VPT], rv1[VPT];
+  auto load_kv = [&](int kt) {
+    const int k0 = kt * BNK;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int it = tid + i * 256, key = it / CH, c = it % CH;
+      const int gk = k0 + key, col = c * VEC;
+      rk[i] = (gk < S && col < hd) ? *reinterpret_cast<const uint4*>(kbase + (int64_t)gk * ss + col)
+                                  : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int it = tid + i * 256;
+      const int p = it % (BNK / 2), c = it / (BNK / 2);
+      const int gk = k0 + 2 * p, col = c * VEC;
+      const bool ok = it < VITEMS && col < hd;
+      rv0[i] = (ok && gk < S) ? *reinterpret_cast<const uint4*>(vbase + (int64_t)gk * ss + col)
+                              : make_uint4(0, 0, 0, 0);
+      rv1[i] = (ok && gk + 1 < S) ? *reinterpret_cast<const uint4*>(vbase + (int64_t)(gk + 1) * ss + col)
+                                  : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store_kv = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int it = tid + i * 256, key = it / CH, c = it % CH;
+      *reinterpret_cast<uint4*>(&sK[buf][key * LDK + c * VEC]) = rk[i];
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int it = tid + i * 256;
+      if (it < VITEMS) {
+        const int p = it % (BNK / 2), c = it / (BNK / 2);
+        PairPack<T>::write(&sV[buf][(c * VEC) * LDV + 2 * p], LDV, rv0[i], rv1[i]);
+      }
+    }
+  };
+
+  f32x16 o[NQ][HB];
+  float m_run[NQ], l_run[NQ];
+#pragma unroll
+  for (int j = 0; j < NQ; ++j) {
+    m_run[j] = -INFINITY;
+    l_run[j] = 0.f;
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[j][hb][r] = 0.f;
+  }
+
+  if (nkt > 0) {
+    load_kv(0);
+    store_kv(0);
+  }
+  __syncthreads();
+
+  const int krow = swap_bits_2_3(l32);  // K row this lane feeds into S^T
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nkt) load_kv(kt + 1);
+    const int k0 = kt * BNK;
+    const bool wave_active = !causal || k0 <= wq0 + NQ * 32 - 1;
+    if (wave_active) {
+      // ---- S^T = K Q^T for two 32-key blocks
+      f32x16 s[NQ][2];
+#pragma unroll
+      for (int j = 0; j < NQ; ++j)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[j][kb][r] = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const T* kp = &sK[cur][(kb * 32 + krow) * LDK + 8 * hi];
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+          const typename Mfma<T>::frag kf = Mfma<T>::load(kp + 16 * c);
+#pragma unroll
+          for (int j = 0; j < NQ; ++j) Mfma<T>::mma(s[j][kb], kf, qf[j][c]);
+        }
+      }
+
+      // ---- masking: register r of block kb is key k0 + kb*32 + 16*(r/8) + 8*hi + r%8
+      const bool tail = k0 + BNK > kend;
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) {
+        const int q = wq0 + j * 32 + l32;
+        const bool diag = causal && k0 + BNK - 1 > wq0 + j * 32;
+        if (tail || diag || key_mask != nullptr) {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int key = k0 + kb * 32 + 16 * (r >> 3) + 8 * hi + (r & 7);
+              bool dead = key >= kend || (causal && key > q);
+              if (key_mask != nullptr && !dead) dead = key_mask[(int64_t)b * S + key] == 0;
+              if (dead) s[j][kb][r] = -INFINITY;
+            }
+        }
+      }
+
+      // ---- online softmax (base 2) and P fragments
+      typename Mfma<T>::frag pf[NQ][4];
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[j][kb][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run[j], mx);
+        const float m_use = m_new == -INFINITY ? 0.f : m_new * scale_log2;
+        const float alpha = __builtin_amdgcn_exp2f(m_run[j] * scale_log2 - m_use);
+        float rs = 0.f;
+        float p[2][16];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            p[kb][r] = __builtin_amdgcn_exp2f(fmaf(s[j][kb][r], scale_log2, -m_use));
+            rs += p[kb][r];
+          }
+        l_run[j] = l_run[j] * alpha + rs;
+        m_run[j] = m_new;
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[j][hb][r] *= alpha;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) pf[j][st] = Mfma<T>::pack(&p[st >> 1][8 * (st & 1)]);
+      }
+
+      // ---- O^T += V^T P^T: 16-key step st covers keys 16*st + 8*hi + 0..7
+#pragma unroll
+      for (int hb = 0; hb < HB; ++hb) {
+        const T* vp = &sV[cur][(hb * 32 + l32) * LDV + 8 * hi];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const typename Mfma<T>::frag vf = Mfma<T>::load(vp + 16 * st);
+#pragma unroll
+          for (int j = 0; j < NQ; ++j) Mfma<T>::mma(o[j][hb], vf, pf[j][st]);
+        }
+      }
+    }
+    if (kt + 1 < nkt) store_kv(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- normalise and store: register r of block hb is hd row hb*32 + 8*(r/4) + 4*hi + r%4
+#pragma unroll
+  for (int j = 0; j < NQ; ++j) {
+    const int q = wq0 + j * 32 + l32;
+    const float l = l_run[j] + __shfl_xor(l_run[j], 32, 64);
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    if (q >= S) continue;
+    T* orow = out + ((int64_t)b * S + q) * ld_out + (int64_t)h * hd;
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int col = hb * 32 + 8 * g + 4 * hi;
+        if (col < hd) {
+          const float4 v = make_float4(o[j][hb][4 * g] * inv, o[j][hb][4 * g + 1] * inv,
+                                       o[j][hb][4 * g + 2] * inv, o[j][hb][4 * g + 3] * inv);
+          *reinterpret_cast<typename Quad<T>::raw*>(orow + col) = Quad<T>::from(v);
+        }
+      }
+  }
+}
+
+template <typename T, int HDP, int NQ>
+static int launch_flash(const void* qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh, void* out,
+                        int64_t ld_out, int B, int S, int H, int hd, float scale_log2, int causal,
+                        const int32_t* lengths, const uint8_t* key_mask, hipStream_t st) {
+  constexpr int BMQ = 4 * NQ * 32;
+  const int nqb = (S + BMQ - 1) / BMQ;
+  const int64_t nblk = (int64_t)nqb * B * H;
+  if (nblk > INT32_MAX) return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd: grid too large");
+  hipLaunchKernelGGL((flash_fwd_kernel<T, HDP, NQ>), dim3((unsigned)nblk), dim3(256), 0, st,
+                     (const T*)qkv, sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal,
+                     lengths, key_mask, nqb);
+  return check_launch("tjk_flash_fwd");
+}
+
+template <typename T, int HDP>
+static int flash_nq(int plan, const void* qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh, void* out,
+                    int64_t ld_out, int B, int S, int H, int hd, float scale_log2, int causal,
+                    const int32_t* lengths, const uint8_t* key_mask, hipStream_t st) {
+  if (plan == 1)
+    return launch_flash<T, HDP, 2>(qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
+                                   key_mask, st);
+  return launch_flash<T, HDP, 1>(qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
+                                 key_mask, st);
+}
+
+template <typename T>
+static int flash_typed(int plan, const void* qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh, void* out,
+                       int64_t ld_out, int B, int S, int H, int hd, float scale_log2, int causal,
+                       const int32_t* lengths, const uint8_t* key_mask, hipStream_t st) {
+  if (hd <= 32)
+    return flash_nq<T, 32>(plan, qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
+                           key_mask, st);
+  if (hd <= 64)
+    return flash_nq<T, 64>(plan, qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
+                           key_mask, st);
+  return flash_nq<T, 128>(plan, qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
+                          key_mask, st);
+}
+
+}  // namespace tjk
+
+using namespace tjk;
+
+extern "C" int tjk_flash_plan_count(int dtype) {
+  if (dtype != TJK_F32 && dtype != TJK_F16 && dtype != TJK_BF16)
+    return fail(TJK_EINVAL, "tjk_flash_plan_count: bad dtype %d", dtype);
+  return 2;
+}
+
+extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s,
+                             int64_t stride_c, int64_t stride_h,
+                             void* out, int64_t ld_out,
+                             int batch, int seq, int heads, int head_dim, float scale,
+                             int causal, const int32_t* lengths, const uint8_t* key_mask,
+                             int dtype, int plan_id, void* stream) {
+  if (batch < 0 || seq < 0 || heads <= 0 || head_dim <= 0)
+    return fail(TJK_EINVAL, "tjk_flash_fwd: bad shape B=%d S=%d H=%d hd=%d", batch, seq, heads, head_dim);
+  if (batch == 0 || seq == 0) return TJK_OK;
+  if (!qkv || !out) return fail(TJK_EINVAL, "tjk_flash_fwd: null pointer");
+  if (dtype != TJK_F32 && dtype != TJK_F16 && dtype != TJK_BF16) return fail(TJK_EINVAL, "tjk_flash_fwd: bad dtype %d", dtype);
+  if (head_dim > 128 || head_dim % 8)
+    return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd: head_dim=%d must be a multiple of 8 and <= 128", head_dim);
+  if (plan_id < -1 || plan_id > 1) return fail(TJK_EINVAL, "tjk_flash_fwd: plan %d out of range", plan_id);
+  const int vec = 16 / dtype_size(dtype);
+  if (stride_b % vec || stride_s % vec || stride_c % vec || stride_h % vec)
+    return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd: strides must be multiples of %d elements", vec);
+  if (ld_out < (int64_t)heads * head_dim || ld_out % 4) return fail(TJK_EINVAL, "tjk_flash_fwd: bad ld_out");
+  if (((uintptr_t)qkv & 15) || ((uintptr_t)out & (4 * dtype_size(dtype) - 1)))
+    return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd: misaligned pointer");
+  if (!(scale > 0.f)) return fail(TJK_EINVAL, "tjk_flash_fwd: scale must be positive");
+  if (plan_id == -1) plan_id = (seq >= 1024 && dtype != TJK_F32) ? 1 : 0;
+  const float scale_log2 = scale * 1.4426950408889634f;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case TJK_F32:
+      return flash_typed<float>(plan_id, qkv, stride_b, stride_s, stride_c, stride_h, out, ld_out, batch, seq,
+                                heads, head_dim, scale_log2, causal, lengths, key_mask, st);
+    case TJK_F16:
+      return flash_typed<f16>(plan_id, qkv, stride_b, stride_s, stride_c, stride_h, out, ld_out, batch, seq,
+                              heads, head_dim, scale_log2, causal, lengths, key_mask, st);
+    default:
+      return flash_typed<bf16>(plan_id, qkv, stride_b, stride_s, stride_c, stride_h, out, ld_out, batch, seq,
+                               heads, head_dim, scale_log2, causal, lengths, key_mask, st);
+  }
+}

@@ -1,0 +1,230 @@
+// Fused residual-add + LayerNorm (HBM-bound row kernel) and the ABI's
+// bookkeeping entry points (version, last error).
+//
+// One wave64 owns one row.  Lane l handles the 4-element chunks
+// l, l+64, l+128, ... of the row, so every load/store instruction of a wave
+// covers 64 consecutive chunks (fully coalesced 512 B/1 KB transactions).
+// The row is held in registers: x = res (+ delta) in fp32, the fp32 residual
+// is optionally written back, mean and biased variance are two wave
+// reductions over the register copy (two-pass, like the reference kernel
+// tjkernels/kernels/layernorm.py:63-66), then gamma/beta are applied and
+// the output is written in its own dtype.  A row mask (the final-LN zeroing
+// of tjkernels/engine.py:267-268) writes padded rows as exact zeros.
+
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "tjk_common.h"
+
+namespace tjk {
+
+static thread_local char g_err[512];
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(static_cast<int>(e), "%s: launch failed: %s", what, hipGetErrorString(e));
+  return TJK_OK;
+}
+
+template <typename TRes, typename TDelta, typename TOut, int MAXCH>
+__global__ __launch_bounds__(256) void add_layernorm_kernel(
+    const TRes* res, int64_t ld_res,  // may alias res_out (in-place update)
+    const TDelta* __restrict__ delta, int64_t ld_delta,
+    float* res_out, int64_t ld_res_out,
+    TOut* __restrict__ out, int64_t ld_out,
+    const float* __restrict__ gamma, const float* __restrict__ beta,
+    int64_t rows, int n, float eps, const uint8_t* __restrict__ row_mask) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nch = n >> 2;
+
+  float4 x[MAXCH];
+  const TRes* rrow = res + row * ld_res;
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < MAXCH; ++j) {
+    const int c = lane + 64 * j;
+    if (c < nch) {
+      x[j] = Quad<TRes>::to(reinterpret_cast<const typename Quad<TRes>::raw*>(rrow)[c]);
+    } else {
+      x[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  if (delta != nullptr) {
+    const TDelta* drow = delta + row * ld_delta;
+#pragma unroll
+    for (int j = 0; j < MAXCH; ++j) {
+      const int c = lane + 64 * j;
+      if (c < nch) {
+        float4 d = Quad<TDelta>::to(reinterpret_cast<const typename Quad<TDelta>::raw*>(drow)[c]);
+        x[j].x += d.x; x[j].y += d.y; x[j].z += d.z; x[j].w += d.w;
+      }
+    }
+  }
+  if (res_out != nullptr) {
+    float4* orow = reinterpret_cast<float4*>(res_out + row * ld_res_out);
+#pragma unroll
+    for (int j = 0; j < MAXCH; ++j) {
+      const int c = lane + 64 * j;
+      if (c < nch) orow[c] = x[j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < MAXCH; ++j) s += (x[j].x + x[j].y) + (x[j].z + x[j].w);
+  const float inv_n = 1.0f / (float)n;
+  const float mean = wave_sum(s) * inv_n;
+  float q = 0.f;
+#pragma unroll
+  for (int j = 0; j < MAXCH; ++j) {
+    const int c = lane + 64 * j;
+    if (c < nch) {
+      const float a = x[j].x - mean, b = x[j].y - mean, cc = x[j].z - mean, d = x[j].w - mean;
+      q += (a * a + b * b) + (cc * cc + d * d);
+    }
+  }
+  const float var = wave_sum(q) * inv_n;
+  const float rstd = 1.0f / sqrtf(var + eps);
+  const bool zero = row_mask != nullptr && row_mask[row] == 0;
+
+  typename Quad<TOut>::raw* yrow = reinterpret_cast<typename Quad<TOut>::raw*>(out + row * ld_out);
+  const float4* g4 = reinterpret_cast<const float4*>(gamma);
+  const float4* b4 = reinterpret_cast<const float4*>(beta);
+#pragma unroll
+  for (int j = 0; j < MAXCH; ++j) {
+    const int c = lane + 64 * j;
+    if (c < nch) {
+      float4 y;
+      if (zero) {
+        y = make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        const float4 g = g4[c], b = b4[c];
+        y.x = (x[j].x - mean) * rstd * g.x + b.x;
+        y.y = (x[j].y - mean) * rstd * g.y + b.y;
+        y.z = (x[j].z - mean) * rstd * g.z + b.z;
+        y.w = (x[j].w - mean) * rstd * g.w + b.w;
+      }
+      yrow[c] = Quad<TOut>::from(y);
+    }
+  }
+}
+
+template <typename TRes, typename TDelta, typename TOut>
+static int launch_ln(const void* res, int64_t ld_res, const void* delta, int64_t ld_delta,
+                     float* res_out, int64_t ld_res_out, void* out, int64_t ld_out,
+                     const float* gamma, const float* beta, int64_t rows, int n, float eps,
+                     const uint8_t* row_mask, hipStream_t stream) {
+  const int nch = n / 4;
+  dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+#define TJK_LN_CASE(MC)                                                                      \
+  if (nch <= 64 * MC) {                                                                      \
+    hipLaunchKernelGGL((add_layernorm_kernel<TRes, TDelta, TOut, MC>), grid, block, 0, stream, \
+                       (const TRes*)res, ld_res, (const TDelta*)delta, ld_delta, res_out,    \
+                       ld_res_out, (TOut*)out, ld_out, gamma, beta, rows, n, eps, row_mask); \
+    return check_launch("tjk_add_layernorm");                                                \
+  }
+  TJK_LN_CASE(1)
+  TJK_LN_CASE(2)
+  TJK_LN_CASE(4)
+  TJK_LN_CASE(8)
+  TJK_LN_CASE(16)
+  TJK_LN_CASE(32)
+#undef TJK_LN_CASE
+  return fail(TJK_EUNSUPPORTED, "tjk_add_layernorm: n=%d exceeds 8192", n);
+}
+
+template <typename TRes, typename TDelta>
+static int dispatch_out(int out_dtype, const void* res, int64_t ld_res, const void* delta,
+                        int64_t ld_delta, float* res_out, int64_t ld_res_out, void* out,
+                        int64_t ld_out, const float* gamma, const float* beta, int64_t rows,
+                        int n, float eps, const uint8_t* row_mask, hipStream_t stream) {
+  switch (out_dtype) {
+    case TJK_F32:
+      return launch_ln<TRes, TDelta, float>(res, ld_res, delta, ld_delta, res_out, ld_res_out, out, ld_out,
+                                            gamma, beta, rows, n, eps, row_mask, stream);
+    case TJK_F16:
+      return launch_ln<TRes, TDelta, f16>(res, ld_res, delta, ld_delta, res_out, ld_res_out, out, ld_out,
+                                          gamma, beta, rows, n, eps, row_mask, stream);
+    case TJK_BF16:
+      return launch_ln<TRes, TDelta, bf16>(res, ld_res, delta, ld_delta, res_out, ld_res_out, out, ld_out,
+                                           gamma, beta, rows, n, eps, row_mask, stream);
+  }
+  return fail(TJK_EINVAL, "tjk_add_layernorm: bad out dtype %d", out_dtype);
+}
+
+template <typename TRes>
+static int dispatch_delta(int delta_dtype, int out_dtype, const void* res, int64_t ld_res,
+                          const void* delta, int64_t ld_delta, float* res_out, int64_t ld_res_out,
+                          void* out, int64_t ld_out, const float* gamma, const float* beta,
+                          int64_t rows, int n, float eps, const uint8_t* row_mask,
+                          hipStream_t stream) {
+  switch (delta_dtype) {
+    case TJK_F32:
+      return dispatch_out<TRes, float>(out_dtype, res, ld_res, delta, ld_delta, res_out, ld_res_out, out,
+                                       ld_out, gamma, beta, rows, n, eps, row_mask, stream);
+    case TJK_F16:
+      return dispatch_out<TRes, f16>(out_dtype, res, ld_res, delta, ld_delta, res_out, ld_res_out, out,
+                                     ld_out, gamma, beta, rows, n, eps, row_mask, stream);
+    case TJK_BF16:
+      return dispatch_out<TRes, bf16>(out_dtype, res, ld_res, delta, ld_delta, res_out, ld_res_out, out,
+                                      ld_out, gamma, beta, rows, n, eps, row_mask, stream);
+  }
+  return fail(TJK_EINVAL, "tjk_add_layernorm: bad delta dtype %d", delta_dtype);
+}
+
+}  // namespace tjk
+
+using namespace tjk;
+
+extern "C" int tjk_abi_version(void) { return TJK_ABI_VERSION; }
+
+extern "C" const char* tjk_last_error_string(void) { return g_err; }
+
+extern "C" int tjk_add_layernorm(const void* res, int res_dtype, int64_t ld_res,
+                                 const void* delta, int delta_dtype, int64_t ld_delta,
+                                 float* res_out, int64_t ld_res_out,
+                                 void* out, int out_dtype, int64_t ld_out,
+                                 const float* gamma, const float* beta,
+                                 int64_t rows, int64_t n, float eps,
+                                 const uint8_t* row_mask, void* stream) {
+  g_err[0] = 0;
+  if (rows < 0 || n <= 0) return fail(TJK_EINVAL, "tjk_add_layernorm: bad shape rows=%lld n=%lld", (long long)rows, (long long)n);
+  if (rows == 0) return TJK_OK;
+  if (!res || !out || !gamma || !beta) return fail(TJK_EINVAL, "tjk_add_layernorm: null pointer");
+  if (n % 4 != 0) return fail(TJK_EUNSUPPORTED, "tjk_add_layernorm: n=%lld not a multiple of 4", (long long)n);
+  if (n > 8192) return fail(TJK_EUNSUPPORTED, "tjk_add_layernorm: n=%lld exceeds 8192", (long long)n);
+  if (ld_res < n || ld_out < n || (delta && ld_delta < n) || (res_out && ld_res_out < n))
+    return fail(TJK_EINVAL, "tjk_add_layernorm: leading dimension smaller than n");
+  if (ld_res % 4 || ld_out % 4 || (delta && ld_delta % 4) || (res_out && ld_res_out % 4))
+    return fail(TJK_EUNSUPPORTED, "tjk_add_layernorm: leading dimensions must be multiples of 4");
+  {
+    // Chunks are 4 elements: 8-byte aligned for 2-byte types, 16 for fp32.
+    const uintptr_t need_res = 4 * dtype_size(res_dtype) - 1, need_out = 4 * dtype_size(out_dtype) - 1;
+    const uintptr_t need_delta = 4 * dtype_size(delta ? delta_dtype : res_dtype) - 1;
+    if (((uintptr_t)res & need_res) || ((uintptr_t)out & need_out) || ((uintptr_t)delta & need_delta) ||
+        ((uintptr_t)res_out & 15) || ((uintptr_t)gamma & 15) || ((uintptr_t)beta & 15))
+      return fail(TJK_EUNSUPPORTED, "tjk_add_layernorm: misaligned pointer");
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int dd = delta ? delta_dtype : res_dtype;
+  switch (res_dtype) {
+    case TJK_F32:
+      return dispatch_delta<float>(dd, out_dtype, res, ld_res, delta, ld_delta, res_out, ld_res_out, out,
+                                   ld_out, gamma, beta, rows, (int)n, eps, row_mask, s);
+    case TJK_F16:
+      return dispatch_delta<f16>(dd, out_dtype, res, ld_res, delta, ld_delta, res_out, ld_res_out, out,
+                                 ld_out, gamma, beta, rows, (int)n, eps, row_mask, s);
+    case TJK_BF16:
+      return dispatch_delta<bf16>(dd, out_dtype, res, ld_res, delta, ld_delta, res_out, ld_res_out, out,
+                                  ld_out, gamma, beta, rows, (int)n, eps, row_mask, s);
+  }
+  return fail(TJK_EINVAL, "tjk_add_layernorm: bad res dtype %d", res_dtype);
+}

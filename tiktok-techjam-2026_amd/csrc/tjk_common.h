@@ -1,0 +1,162 @@
+// Shared definitions for the gfx950 kernels behind the tjk C-ABI.
+//
+// Element types, 16-byte chunk helpers, MFMA fragment traits and the
+// thread-local error string returned by tjk_last_error_string().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/tjk.h"
+
+namespace tjk {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Records a formatted message for tjk_last_error_string() and returns `code`.
+int fail(int code, const char* fmt, ...);
+
+// Maps a hipError_t to the C-ABI status (positive = HIP error code).
+inline int hip_status(hipError_t e) {
+  return e == hipSuccess ? TJK_OK : static_cast<int>(e);
+}
+
+// Launch-error check shared by every entry point.
+int check_launch(const char* what);
+
+inline int dtype_size(int dt) { return dt == TJK_F32 ? 4 : 2; }
+
+// ---------------------------------------------------------------- scalars
+
+template <typename T> __device__ __forceinline__ float to_f32(T v) { return static_cast<float>(v); }
+template <typename T> __device__ __forceinline__ T from_f32(float v) { return static_cast<T>(v); }
+
+// Four consecutive elements <-> float4 (8 bytes for 2-byte types, 16 for fp32).
+template <typename T> struct Quad;
+template <> struct Quad<float> {
+  typedef float4 raw;
+  static __device__ __forceinline__ float4 to(raw r) { return r; }
+  static __device__ __forceinline__ raw from(float4 v) { return v; }
+};
+template <> struct Quad<bf16> {
+  typedef uint2 raw;
+  static __device__ __forceinline__ float4 to(raw r) {
+    float4 v;
+    v.x = __uint_as_float(r.x << 16);
+    v.y = __uint_as_float(r.x & 0xffff0000u);
+    v.z = __uint_as_float(r.y << 16);
+    v.w = __uint_as_float(r.y & 0xffff0000u);
+    return v;
+  }
+  static __device__ __forceinline__ raw from(float4 v) {
+    bf16 a = static_cast<bf16>(v.x), b = static_cast<bf16>(v.y);
+    bf16 c = static_cast<bf16>(v.z), d = static_cast<bf16>(v.w);
+    raw r;
+    r.x = (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+    r.y = (uint32_t)__builtin_bit_cast(uint16_t, c) | ((uint32_t)__builtin_bit_cast(uint16_t, d) << 16);
+    return r;
+  }
+};
+template <> struct Quad<f16> {
+  typedef uint2 raw;
+  static __device__ __forceinline__ float4 to(raw r) {
+    f16 a = __builtin_bit_cast(f16, (uint16_t)(r.x & 0xffff));
+    f16 b = __builtin_bit_cast(f16, (uint16_t)(r.x >> 16));
+    f16 c = __builtin_bit_cast(f16, (uint16_t)(r.y & 0xffff));
+    f16 d = __builtin_bit_cast(f16, (uint16_t)(r.y >> 16));
+    return make_float4((float)a, (float)b, (float)c, (float)d);
+  }
+  static __device__ __forceinline__ raw from(float4 v) {
+    f16 a = (f16)v.x, b = (f16)v.y, c = (f16)v.z, d = (f16)v.w;
+    raw r;
+    r.x = (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+    r.y = (uint32_t)__builtin_bit_cast(uint16_t, c) | ((uint32_t)__builtin_bit_cast(uint16_t, d) << 16);
+    return r;
+  }
+};
+
+// ------------------------------------------------------------ MFMA traits
+//
+// A "fragment" is the slice of one 32x32 MFMA operand that one lane owns for
+// a 16-deep contraction step: 8 consecutive elements along K.  For 2-byte
+// types that is one v_mfma_f32_32x32x16_{bf16,f16}; for fp32 it is eight
+// v_mfma_f32_32x32x2_f32, sub-step j contracting element j of every lane.
+// Any assignment of K indices to (lane half, element) is valid as long as
+// both operands use the same one, which every caller below does.
+//
+// The 32x32 fp32 accumulator layout (all 32x32 MFMAs): lane l, register r
+// holds row 8*(r/4) + 4*(l/32) + (r%4), column l%32.
+
+template <typename T> struct Mfma;
+
+template <> struct Mfma<bf16> {
+  typedef bf16x8 frag;
+  static constexpr int kVec = 8;  // elements per 16-byte chunk
+  static __device__ __forceinline__ void mma(f32x16& acc, const frag& a, const frag& b) {
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
+  }
+  static __device__ __forceinline__ frag load(const bf16* p) {  // 16-byte aligned
+    return *reinterpret_cast<const frag*>(p);
+  }
+  static __device__ __forceinline__ frag pack(const float* v) {
+    frag f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = static_cast<bf16>(v[i]);
+    return f;
+  }
+};
+
+template <> struct Mfma<f16> {
+  typedef f16x8 frag;
+  static constexpr int kVec = 8;
+  static __device__ __forceinline__ void mma(f32x16& acc, const frag& a, const frag& b) {
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc, 0, 0, 0);
+  }
+  static __device__ __forceinline__ frag load(const f16* p) {
+    return *reinterpret_cast<const frag*>(p);
+  }
+  static __device__ __forceinline__ frag pack(const float* v) {
+    frag f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = static_cast<f16>(v[i]);
+    return f;
+  }
+};
+
+template <> struct Mfma<float> {
+  typedef f32x8 frag;
+  static constexpr int kVec = 4;
+  static __device__ __forceinline__ void mma(f32x16& acc, const frag& a, const frag& b) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[j], b[j], acc, 0, 0, 0);
+  }
+  static __device__ __forceinline__ frag load(const float* p) {  // 16-byte aligned
+    float4 lo = *reinterpret_cast<const float4*>(p);
+    float4 hi = *reinterpret_cast<const float4*>(p + 4);
+    frag f;
+    f[0] = lo.x; f[1] = lo.y; f[2] = lo.z; f[3] = lo.w;
+    f[4] = hi.x; f[5] = hi.y; f[6] = hi.z; f[7] = hi.w;
+    return f;
+  }
+  static __device__ __forceinline__ frag pack(const float* v) {
+    frag f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = v[i];
+    return f;
+  }
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+}  // namespace tjk

@@ -1,0 +1,163 @@
+"""Tensor-level wrappers over the tjk C-ABI.
+
+Each op checks devices/layouts it relies on, passes raw device pointers and
+``torch.cuda.current_stream().cuda_stream`` (so the launch lands on the
+caller's stream, including under hipGraph capture), and raises ``TjkError``
+on a non-zero status.  None of them allocates on the hot path except where
+an output tensor is requested with ``out=None``.
+
+Mirrors of the reference's kernel dispatch layer
+(tjkernels/kernels/__init__.py:48-101), minus its torch fallbacks.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RESIDUAL, TjkError, check  # noqa: F401
+
+
+def _code(t: torch.Tensor) -> int:
+    try:
+        return _lib.DTYPE_CODES[t.dtype]
+    except KeyError:
+        raise TjkError(f"unsupported dtype {t.dtype}") from None
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _require_gpu(*ts: Optional[torch.Tensor]) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise TjkError("tjkernels ops need ROCm device tensors (no CPU path)")
+
+
+def _rowmajor(t: torch.Tensor, name: str) -> int:
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise TjkError(f"{name} must be a 2-D row-major view, got shape {tuple(t.shape)} "
+                       f"strides {t.stride()}")
+    return t.stride(0)
+
+
+def add_layernorm(res: torch.Tensor, delta: Optional[torch.Tensor],
+                  gamma: torch.Tensor, beta: torch.Tensor, eps: float,
+                  out: torch.Tensor, res_out: Optional[torch.Tensor] = None,
+                  row_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """x = res (+ delta) in fp32; res_out <- x (optional, fp32); out <- LN(x)
+    (rows with row_mask == 0 written as 0).  Mirrors fused_add_layernorm,
+    tjkernels/kernels/__init__.py:48-70."""
+    _require_gpu(res, delta, gamma, beta, out, res_out, row_mask)
+    rows, n = res.shape
+    if res_out is not None and res_out.dtype != torch.float32:
+        raise TjkError("res_out must be float32")
+    if gamma.dtype != torch.float32 or beta.dtype != torch.float32:
+        raise TjkError("gamma/beta must be float32")
+    if row_mask is not None and (row_mask.dtype not in (torch.bool, torch.uint8)
+                                 or row_mask.numel() != rows or not row_mask.is_contiguous()):
+        raise TjkError("row_mask must be a contiguous bool/uint8 tensor with one entry per row")
+    lib = _lib.load()
+    status = lib.tjk_add_layernorm(
+        res.data_ptr(), _code(res), _rowmajor(res, "res"),
+        _ptr(delta), _code(delta) if delta is not None else 0,
+        _rowmajor(delta, "delta") if delta is not None else 0,
+        _ptr(res_out), _rowmajor(res_out, "res_out") if res_out is not None else 0,
+        out.data_ptr(), _code(out), _rowmajor(out, "out"),
+        gamma.data_ptr(), beta.data_ptr(), rows, n, float(eps),
+        _ptr(row_mask), _stream(res))
+    check(status, "tjk_add_layernorm")
+    return out
+
+
+def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], out: torch.Tensor,
+         epilogue: int = EPI_BIAS, plan: int = -1) -> torch.Tensor:
+    """out = epi(a @ w.T + bias); w in nn.Linear [N, K] layout.
+    With EPI_BIAS_RESIDUAL, ``out`` is an fp32 residual updated in place."""
+    _require_gpu(a, w, bias, out)
+    m, k = a.shape
+    n, k2 = w.shape
+    if k != k2 or out.shape[0] != m or out.shape[1] != n:
+        raise TjkError(f"gemm shape mismatch a{tuple(a.shape)} w{tuple(w.shape)} out{tuple(out.shape)}")
+    if w.dtype != a.dtype or (bias is not None and bias.dtype != a.dtype):
+        raise TjkError("gemm operands must share a dtype")
+    if epilogue == EPI_BIAS_RESIDUAL:
+        if out.dtype != torch.float32:
+            raise TjkError("residual epilogue needs a float32 out")
+    elif out.dtype != a.dtype:
+        raise TjkError("gemm out must have the operands' dtype")
+    lib = _lib.load()
+    status = lib.tjk_gemm_bias(a.data_ptr(), _rowmajor(a, "a"), w.data_ptr(), _rowmajor(w, "w"),
+                               _ptr(bias), out.data_ptr(), _rowmajor(out, "out"), m, n, k,
+                               _code(a), epilogue, plan, _stream(a))
+    check(status, "tjk_gemm_bias")
+    return out
+
+
+def flash_attention(qkv: torch.Tensor, out: torch.Tensor, causal: bool = True,
+                    scale: Optional[float] = None, lengths: Optional[torch.Tensor] = None,
+                    key_mask: Optional[torch.Tensor] = None, plan: int = -1) -> torch.Tensor:
+    """qkv: [B, S, 3, H, hd] (any strides with a unit hd stride) -> out [B*S, H*hd].
+    Mirrors flash_attention, tjkernels/kernels/attention.py:189-226, plus the
+    masked cases the reference sends to SDPA (tjkernels/engine.py:184-203)."""
+    _require_gpu(qkv, out, lengths, key_mask)
+    if qkv.dim() != 5 or qkv.shape[2] != 3 or qkv.stride(4) != 1:
+        raise TjkError(f"qkv must be [B, S, 3, H, hd] with unit hd stride, got {tuple(qkv.shape)}")
+    b, s, _, h, hd = qkv.shape
+    if out.shape[0] != b * s or out.shape[1] < h * hd or out.dtype != qkv.dtype:
+        raise TjkError("bad attention output buffer")
+    if lengths is not None and (lengths.dtype != torch.int32 or lengths.numel() != b):
+        raise TjkError("lengths must be int32 [B]")
+    if key_mask is not None and (key_mask.dtype not in (torch.bool, torch.uint8)
+                                 or tuple(key_mask.shape) != (b, s) or not key_mask.is_contiguous()):
+        raise TjkError("key_mask must be a contiguous bool/uint8 [B, S] tensor")
+    sb, ss, sc, sh, _ = qkv.stride()
+    lib = _lib.load()
+    status = lib.tjk_flash_fwd(qkv.data_ptr(), sb, ss, sc, sh, out.data_ptr(), _rowmajor(out, "out"),
+                               b, s, h, hd, float(hd ** -0.5 if scale is None else scale),
+                               int(bool(causal)), _ptr(lengths), _ptr(key_mask), _code(qkv), plan,
+                               _stream(qkv))
+    check(status, "tjk_flash_fwd")
+    return out
+
+
+def ffn(h: torch.Tensor, w1: torch.Tensor, b1: Optional[torch.Tensor], w2: torch.Tensor,
+        b2: Optional[torch.Tensor], out: torch.Tensor, workspace: torch.Tensor,
+        epilogue: int = EPI_BIAS, plans: int = -1) -> torch.Tensor:
+    """out (+)= gelu_erf(h W1^T + b1) W2^T + b2; mirrors fused_ffn,
+    tjkernels/kernels/__init__.py:80-89.  ``plans`` packs the two GEMM tile
+    plans as p1 | p2 << 8 (-1 = both automatic)."""
+    _require_gpu(h, w1, b1, w2, b2, out, workspace)
+    t, d = h.shape
+    f = w1.shape[0]
+    need = _lib.load().tjk_ffn_workspace_bytes(t, f, _code(h))
+    if workspace.numel() * workspace.element_size() < need:
+        raise TjkError(f"ffn workspace too small ({need} bytes needed)")
+    if plans == -1:
+        plans = 0xffff
+    status = _lib.load().tjk_ffn(h.data_ptr(), _rowmajor(h, "h"), w1.data_ptr(), _ptr(b1), w2.data_ptr(),
+                                 _ptr(b2), out.data_ptr(), _rowmajor(out, "out"), workspace.data_ptr(),
+                                 t, d, f, _code(h), epilogue, plans, _stream(h))
+    check(status, "tjk_ffn")
+    return out
+
+
+def gemm_plans(dtype: torch.dtype):
+    """[(plan_id, block_m, block_n, waves)] available for ``dtype``."""
+    import ctypes
+    lib = _lib.load()
+    code = _lib.DTYPE_CODES[dtype]
+    out = []
+    for i in range(lib.tjk_gemm_plan_count(code)):
+        bm, bn, wv = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        check(lib.tjk_gemm_plan_info(code, i, ctypes.byref(bm), ctypes.byref(bn), ctypes.byref(wv)),
+              "tjk_gemm_plan_info")
+        out.append((i, bm.value, bn.value, wv.value))
+    return out
