@@ -109,6 +109,13 @@ def _breakdown(engine, x, mask, plan):
     finally:
         for name, fn in orig.items():
             setattr(ops, name, fn)
+    # A plain copy of known size (256 MiB read + 256 MiB written): its rocprof
+    # FETCH_SIZE / WRITE_SIZE readings calibrate the HBM-traffic counters.
+    src = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device=x.device)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
     for label, flops, s0, s1 in events:
         c = classes.setdefault(label, {"ms": 0.0, "launches": 0, "flops": 0.0})
         c["ms"] += s0.elapsed_time(s1)

@@ -113,24 +113,40 @@ def _gemm_case(device, m, n, k, dt, epi, plan, seed=0):
     _close(out, ref, rtol, 1e-4 if dt != torch.float32 else 1e-5)
 
 
-@pytest.mark.parametrize("plan", range(6))
+# Plans of the staged kernel take any K % 8 == 0; direct-to-LDS plans need
+# K % 64 == 0 (bf16/fp16) and reject other K with TJK_EUNSUPPORTED.
+STAGED16, DTL16, DTL16_K32 = range(0, 6), range(6, 12), ()
+STAGED32, DTL32 = range(0, 2), range(2, 5)
+
+
+@pytest.mark.parametrize("plan", list(STAGED16) + list(DTL16))
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 def test_gemm_plans(device, plan, dt):
-    # ragged M and N (not tile multiples), K not a multiple of BK
-    _gemm_case(device, 300, 200, 96, dt, ops.EPI_BIAS, plan)
+    # ragged M and N (not tile multiples)
     _gemm_case(device, 513, 1028, 1088, dt, ops.EPI_BIAS, plan)
+    _gemm_case(device, 64, 32, 64, dt, ops.EPI_BIAS, plan)
+    if plan in STAGED16 or plan in DTL16_K32:  # K = 96 is a multiple of 32, not of 64
+        _gemm_case(device, 300, 200, 96, dt, ops.EPI_BIAS, plan)
+    else:
+        with pytest.raises(ops.TjkError, match="needs k"):
+            _gemm_case(device, 300, 200, 96, dt, ops.EPI_BIAS, plan)
+    if plan in DTL16_K32:
+        with pytest.raises(ops.TjkError, match="needs k"):
+            _gemm_case(device, 64, 64, 40, dt, ops.EPI_BIAS, plan)
 
 
-@pytest.mark.parametrize("plan", [0, 1])
+@pytest.mark.parametrize("plan", list(STAGED32) + list(DTL32))
 def test_gemm_fp32_plans(device, plan):
-    _gemm_case(device, 300, 200, 96, torch.float32, ops.EPI_BIAS, plan)
-    _gemm_case(device, 257, 516, 260, torch.float32, ops.EPI_BIAS, plan)
+    _gemm_case(device, 257, 516, 256, torch.float32, ops.EPI_BIAS, plan)
+    if plan in STAGED32:
+        _gemm_case(device, 300, 200, 96, torch.float32, ops.EPI_BIAS, plan)
 
 
 @pytest.mark.parametrize("epi", [ops.EPI_BIAS_GELU, ops.EPI_BIAS_RESIDUAL])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
 def test_gemm_epilogues(device, epi, dt):
     _gemm_case(device, 256, 384, 512, dt, epi, -1)
+    _gemm_case(device, 200, 388, 96, dt, epi, -1)
 
 
 def test_gemm_headline_shapes(device):

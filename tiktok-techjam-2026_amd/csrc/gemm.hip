@@ -44,6 +44,58 @@ __device__ __forceinline__ int xcd_remap(int bid, int nb) {
   return x < rem ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
 }
 
+
+// Epilogue shared by both GEMM kernels.  The accumulators hold C^T blocks:
+// for block (i, j), lane (l32, hi) owns output row m = mw + 32 j + l32 and,
+// for g = 0..3, the four consecutive columns n = nw + 32 i + 8 g + 4 hi.
+template <typename T, int EPI, int FM, int FN>
+__device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* __restrict__ bias,
+                                         void* __restrict__ Cv, int64_t ldc, int M, int N, int mw, int nw,
+                                         int l32, int hi) {
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+    const int m = mw + j * 32 + l32;
+    if (m >= M) continue;
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = nw + i * 32 + g * 8 + hi * 4;
+        if (n >= N) continue;
+        float4 v = make_float4(acc[i][j][4 * g + 0], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                               acc[i][j][4 * g + 3]);
+        if (bias != nullptr) {
+          const float4 bv = Quad<T>::to(*reinterpret_cast<const typename Quad<T>::raw*>(bias + n));
+          v.x += bv.x; v.y += bv.y; v.z += bv.z; v.w += bv.w;
+        }
+        if (EPI == TJK_EPI_BIAS_GELU) {
+          v.x = gelu_erf(v.x); v.y = gelu_erf(v.y); v.z = gelu_erf(v.z); v.w = gelu_erf(v.w);
+        }
+        if (EPI == TJK_EPI_BIAS_RESIDUAL) {
+          float4* r = reinterpret_cast<float4*>(static_cast<float*>(Cv) + (int64_t)m * ldc + n);
+          float4 o = *r;
+          o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
+          *r = o;
+        } else {
+          T* c = static_cast<T*>(Cv) + (int64_t)m * ldc + n;
+          *reinterpret_cast<typename Quad<T>::raw*>(c) = Quad<T>::from(v);
+        }
+      }
+    }
+  }
+}
+
+// Tile coordinates of workgroup `bid`: XCD-contiguous ranges of a
+// GROUP_M-grouped raster over (tiles_m x tiles_n).
+__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int& pid_m, int& pid_n) {
+  const int t = xcd_remap(bid, tiles_m * tiles_n);
+  const int group = t / (kGroupM * tiles_n);
+  const int first_m = group * kGroupM;
+  const int gsize = min(tiles_m - first_m, kGroupM);
+  pid_m = first_m + (t % (kGroupM * tiles_n)) % gsize;
+  pid_n = (t % (kGroupM * tiles_n)) / gsize;
+}
+
 template <typename T, int BM, int BN, int WM, int WN, int EPI>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
     const T* __restrict__ A, int64_t lda, const T* __restrict__ W, int64_t ldw,
@@ -68,14 +120,8 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
   const int l32 = lane & 31, hi = lane >> 5;
 
   // ---- tile coordinates: XCD-contiguous ranges of a grouped order
-  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  const int nb = tiles_m * tiles_n;
-  const int t = xcd_remap(blockIdx.x, nb);
-  const int group = t / (kGroupM * tiles_n);
-  const int first_m = group * kGroupM;
-  const int gsize = min(tiles_m - first_m, kGroupM);
-  const int pid_m = first_m + (t % (kGroupM * tiles_n)) % gsize;
-  const int pid_n = (t % (kGroupM * tiles_n)) / gsize;
+  int pid_m, pid_n;
+  tile_coords(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, pid_m, pid_n);
   const int m0 = pid_m * BM, n0 = pid_n * BN;
 
   // ---- global -> register staging
@@ -145,59 +191,216 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
     __syncthreads();
   }
 
-  // ---- epilogue: lane owns C[m, n..n+3] for each (i, j, g)
+  epilogue<T, EPI, FM, FN>(acc, bias, Cv, ldc, M, N, m0 + wm * WTM, n0 + wn * WTN, l32, hi);
+}
+
+// ------------------------------------------------------- direct-to-LDS GEMM
+//
+// Same math and epilogue as gemm_kernel, with the operand tiles moved by
+// gfx950's LDS DMA (buffer_load_dwordx4 ... lds): each wave instruction
+// copies 64 x 16 B straight from global memory into 1 KB of LDS, so tiles
+// never pass through VGPRs.  Rows beyond M (or N) fall outside the buffer
+// descriptor's range and arrive as zeros, which removes every bounds branch
+// from the main loop.
+//
+// LDS holds STAGES tiles in a ring; a tile row is BKB bytes of K (64 or
+// 128) with no padding.  The 16-byte chunk c of row r is stored at chunk
+// c ^ swz(r), which spreads the ds_read_b128 fragment reads of 16
+// consecutive rows over all banks (for 32- and 64-bank LDS alike).
+//
+// Pipeline, one barrier per tile: before computing tile k a wave waits until
+// its own DMAs for tile k have landed (s_waitcnt vmcnt(N), N = DMAs of the
+// STAGES-2 younger tiles still allowed in flight) and then meets the others
+// at s_barrier; it then issues the DMA of tile k+STAGES-1 into the slot tile
+// k-1 just vacated and runs tile k's MFMAs.  So every DMA has STAGES-1
+// tiles of MFMA work to land.  The DMA is issued on every iteration, past
+// the end pointed outside the buffer range (it moves nothing), which keeps
+// the body one basic block; scheduling directives then interleave the
+// MFMAs with the next step's ds_reads and with the DMA issues.
+// Requires K % (BKB / sizeof(T)) == 0 and 16-byte aligned rows.
+
+template <int BKB> __device__ __forceinline__ int swz(int r);
+template <> __device__ __forceinline__ int swz<128>(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+template <> __device__ __forceinline__ int swz<64>(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Byte offset that lies beyond any buffer descriptor range used here.
+constexpr int kPastEnd = 0x7fff0000;
+
+template <typename T, int BM, int BN, int WM, int WN, int BKB, int STAGES, int EPI>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_dtl_kernel(
+    const T* __restrict__ A, int64_t lda, const T* __restrict__ W, int64_t ldw,
+    const T* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K) {
+  constexpr bool SCHED = sizeof(T) == 2;
+  constexpr int NW = WM * WN;
+  constexpr int BK = BKB / sizeof(T);            // K elements per tile
+  constexpr int CPR = BKB / 16;                  // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;                  // rows per DMA instruction
+  constexpr int KS = BK / 16;                    // 16-deep MFMA steps per tile
+  constexpr int CPS = sizeof(T) == 2 ? 2 : 4;    // chunks per 16-deep step
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int FM = WTM / 32, FN = WTN / 32;
+  constexpr int STAGE = (BM + BN) * BKB;         // bytes per LDS stage
+  constexpr int DA = BM / (RPI * NW), DW = BN / (RPI * NW);
+  constexpr int NDMA = DA + DW;                  // DMA instructions per wave per tile
+  static_assert(DA * RPI * NW == BM && DW * RPI * NW == BN, "tile rows must split over the waves");
+  static_assert(STAGES >= 2 && (STAGES - 2) * NDMA <= 63, "vmcnt range");
+
+  __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int l32 = lane & 31, hi = lane >> 5;
+
+  int pid_m, pid_n;
+  tile_coords(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, pid_m, pid_n);
+  const int m0 = pid_m * BM, n0 = pid_n * BN;
+
+  // Buffer descriptors over this tile's rows; reads past row M (N) return 0.
+  const int64_t a_rows = min((int64_t)BM, (int64_t)(M - m0));
+  const int64_t w_rows = min((int64_t)BN, (int64_t)(N - n0));
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(A + (int64_t)m0 * lda), (short)0, (int)(a_rows * lda * (int64_t)sizeof(T)), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(W + (int64_t)n0 * ldw), (short)0, (int)(w_rows * ldw * (int64_t)sizeof(T)), 0x00020000);
+
+  // DMA instruction i of this wave fills LDS rows (i*NW + wave)*RPI + 0..RPI-1;
+  // lane l lands at byte 16*l of that 1 KB: row +l/CPR, physical chunk l%CPR,
+  // so it fetches logical chunk (l%CPR) ^ swz(row).
+  uint32_t voff_a[DA], voff_w[DW];
 #pragma unroll
-  for (int j = 0; j < FM; ++j) {
-    const int m = m0 + wm * WTM + j * 32 + l32;
-    if (m >= M) continue;
+  for (int i = 0; i < DA; ++i) {
+    const int r = (i * NW + wave) * RPI + lane / CPR;
+    voff_a[i] = (uint32_t)(r * lda * (int64_t)sizeof(T)) + (uint32_t)(((lane % CPR) ^ swz<BKB>(r)) << 4);
+  }
 #pragma unroll
-    for (int i = 0; i < FN; ++i) {
+  for (int i = 0; i < DW; ++i) {
+    const int r = (i * NW + wave) * RPI + lane / CPR;
+    voff_w[i] = (uint32_t)(r * ldw * (int64_t)sizeof(T)) + (uint32_t)(((lane % CPR) ^ swz<BKB>(r)) << 4);
+  }
+  const int nk = K / BK;
+  auto issue = [&](int kt) {  // DMA of tile kt into its ring slot (nothing past the end)
+    char* sb = smem + (kt % STAGES) * STAGE;
+    const uint32_t kb = kt < nk ? (uint32_t)(kt * BKB) : (uint32_t)kPastEnd;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int n = n0 + wn * WTN + i * 32 + g * 8 + hi * 4;
-        if (n >= N) continue;
-        float4 v = make_float4(acc[i][j][4 * g + 0], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                               acc[i][j][4 * g + 3]);
-        if (bias != nullptr) {
-          const float4 bv = Quad<T>::to(*reinterpret_cast<const typename Quad<T>::raw*>(bias + n));
-          v.x += bv.x; v.y += bv.y; v.z += bv.z; v.w += bv.w;
-        }
-        if (EPI == TJK_EPI_BIAS_GELU) {
-          v.x = gelu_erf(v.x); v.y = gelu_erf(v.y); v.z = gelu_erf(v.z); v.w = gelu_erf(v.w);
-        }
-        if (EPI == TJK_EPI_BIAS_RESIDUAL) {
-          float4* r = reinterpret_cast<float4*>(static_cast<float*>(Cv) + (int64_t)m * ldc + n);
-          float4 o = *r;
-          o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
-          *r = o;
-        } else {
-          T* c = static_cast<T*>(Cv) + (int64_t)m * ldc + n;
-          *reinterpret_cast<typename Quad<T>::raw*>(c) = Quad<T>::from(v);
-        }
+    for (int i = 0; i < DA; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)(sb + (i * NW + wave) * 1024), 16,
+                                               (uint32_t)(voff_a[i] + kb), 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < DW; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_void*)(sb + BM * BKB + (i * NW + wave) * 1024), 16,
+                                               (uint32_t)(voff_w[i] + kb), 0, 0, 0);
+  };
+
+  // Fragment reads: row (base + l32), logical chunk c at physical c ^ swz(l32).
+  const int sw = swz<BKB>(l32);
+  auto frag_at = [&](const char* rowbase, int ks) -> typename Mfma<T>::frag {
+    if constexpr (sizeof(T) == 2) {
+      return *reinterpret_cast<const typename Mfma<T>::frag*>(rowbase + (((CPS * ks + hi) ^ sw) << 4));
+    } else {
+      const float4 lo = *reinterpret_cast<const float4*>(rowbase + (((CPS * ks + 2 * hi) ^ sw) << 4));
+      const float4 up = *reinterpret_cast<const float4*>(rowbase + (((CPS * ks + 2 * hi + 1) ^ sw) << 4));
+      typename Mfma<T>::frag f;
+      f[0] = lo.x; f[1] = lo.y; f[2] = lo.z; f[3] = lo.w;
+      f[4] = up.x; f[5] = up.y; f[6] = up.z; f[7] = up.w;
+      return f;
+    }
+  };
+
+  f32x16 acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+#pragma unroll
+  for (int t = 0; t < STAGES - 1; ++t) issue(t);
+  typename Mfma<T>::frag fa[2][FM], fw[2][FN];
+  for (int kt = 0; kt < nk; ++kt) {
+    // My DMAs of tile kt have landed, then everyone's (and tile kt-1 is
+    // retired by every wave).  Inline asm with a memory clobber keeps the
+    // compiler from moving LDS accesses across either instruction; a
+    // __syncthreads() would instead wait for every DMA in flight.
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((STAGES - 2) * NDMA) : "memory");
+    asm volatile("s_barrier" ::: "memory");
+    const char* st = smem + (kt % STAGES) * STAGE;
+    const char* sa = st + (wm * WTM + l32) * BKB;
+    const char* sw_ = st + BM * BKB + (wn * WTN + l32) * BKB;
+#pragma unroll
+    for (int j = 0; j < FM; ++j) fa[0][j] = frag_at(sa + j * 32 * BKB, 0);
+#pragma unroll
+    for (int i = 0; i < FN; ++i) fw[0][i] = frag_at(sw_ + i * 32 * BKB, 0);
+    issue(kt + STAGES - 1);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int b = ks & 1;
+      if (ks + 1 < KS) {
+#pragma unroll
+        for (int j = 0; j < FM; ++j) fa[b ^ 1][j] = frag_at(sa + j * 32 * BKB, ks + 1);
+#pragma unroll
+        for (int i = 0; i < FN; ++i) fw[b ^ 1][i] = frag_at(sw_ + i * 32 * BKB, ks + 1);
       }
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) Mfma<T>::mma(acc[i][j], fw[b][i], fa[b][j]);
+    }
+    if constexpr (SCHED) {
+      constexpr int NMF = FN * FM, NDS = FN + FM;
+      __builtin_amdgcn_sched_group_barrier(0x100, NDS, 0);  // step-0 fragments
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int m = 0; m < NMF; ++m) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (ks == 0 && m < NDMA) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+          if (ks + 1 < KS && m >= NMF - NDS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
     }
   }
+
+  epilogue<T, EPI, FM, FN>(acc, bias, Cv, ldc, M, N, m0 + wm * WTM, n0 + wn * WTN, l32, hi);
 }
 
 // ------------------------------------------------------------------ plans
 
+enum { kStaged = 0, kDtl = 1 };
+
 struct GemmPlan {
-  int bm, bn, wm, wn;
+  int kind, bm, bn, wm, wn, bkb, stages;
+  double eff;  // prior used by auto_plan
 };
 
-// 2-byte types (bf16/fp16), BK = 64.
+// 2-byte types (bf16/fp16), BK = 64.  Measured on MI355X (bf16, C4/C5
+// projections): the 64x64-wave-tile plan 7 is best while there are too few
+// 256x256 tiles to fill two rounds of the 256 CUs, the 8-wave 256x256 plan 8
+// beyond that.  (A 4-stage ring of 64-byte rows was tried and dropped: it
+// measured 50% LDS bank-conflict cycles and no gain.)
 static const GemmPlan kPlans16[] = {
-    {256, 256, 2, 2},  // 0: wave tile 128x128 (LDS 144 KB, 1 WG/CU)
-    {256, 128, 2, 2},  // 1: wave tile 128x64
-    {128, 256, 2, 2},  // 2: wave tile 64x128
-    {128, 128, 2, 2},  // 3: wave tile 64x64 (2 WG/CU)
-    {64, 64, 2, 2},    // 4: wave tile 32x32, small shapes
-    {256, 256, 2, 4},  // 5: 8 waves, wave tile 128x64
+    {kStaged, 256, 256, 2, 2, 128, 2, 0.50},  // 0
+    {kStaged, 256, 128, 2, 2, 128, 2, 0.45},  // 1
+    {kStaged, 128, 256, 2, 2, 128, 2, 0.45},  // 2
+    {kStaged, 128, 128, 2, 2, 128, 2, 0.55},  // 3
+    {kStaged, 64, 64, 2, 2, 128, 2, 0.40},    // 4  small shapes / K % 64 != 0
+    {kStaged, 256, 256, 2, 4, 128, 2, 0.55},  // 5
+    {kDtl, 256, 256, 2, 2, 128, 2, 0.85},     // 6  wave tile 128x128, 1 WG/CU
+    {kDtl, 128, 128, 2, 2, 128, 2, 0.90},     // 7  wave tile 64x64, 2 WG/CU
+    {kDtl, 256, 256, 2, 4, 128, 2, 1.00},     // 8  8 waves, wave tile 128x64
+    {kDtl, 64, 64, 2, 2, 128, 2, 0.45},       // 9  small shapes
+    {kDtl, 256, 128, 2, 2, 128, 2, 0.75},     // 10 wave tile 128x64
+    {kDtl, 128, 256, 2, 2, 128, 2, 0.75},     // 11 wave tile 64x128
 };
-// fp32, BK = 32.
+// fp32.
 static const GemmPlan kPlans32[] = {
-    {128, 128, 2, 2},  // 0
-    {64, 64, 2, 2},    // 1
+    {kStaged, 128, 128, 2, 2, 128, 2, 0.6},  // 0
+    {kStaged, 64, 64, 2, 2, 128, 2, 0.4},    // 1
+    {kDtl, 128, 128, 2, 2, 128, 2, 1.0},     // 2
+    {kDtl, 256, 128, 2, 2, 128, 2, 1.0},     // 3
+    {kDtl, 64, 64, 2, 2, 128, 2, 0.5},       // 4
 };
 
 template <typename T>
@@ -210,21 +413,31 @@ static const GemmPlan* plans(int* count) {
   return kPlans16;
 }
 
-// Picks the tile that minimises (number of full-chip rounds) x (tile cost),
-// with a per-tile efficiency prior favouring the larger wave tiles.
+static bool dtl_ok(const GemmPlan& p, int64_t k, int64_t lda, int64_t ldw, int es) {
+  return k % (p.bkb / es) == 0 && (lda * es) % 16 == 0 && (ldw * es) % 16 == 0;
+}
+
+// Default tile choice.  For shapes the direct-to-LDS kernel takes, the
+// measured rule above; otherwise (odd K, misaligned rows) the staged plan
+// minimising (full-chip rounds of 256 workgroups) x (tile area / prior).
 template <typename T>
-static int auto_plan(int64_t M, int64_t N) {
+static int auto_plan(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) {
   int count;
   const GemmPlan* p = plans<T>(&count);
-  static const double eff16[] = {1.0, 0.85, 0.85, 0.6, 0.3, 0.9};
-  static const double eff32[] = {1.0, 0.6};
-  const double* eff = sizeof(T) == 4 ? eff32 : eff16;
+  if (sizeof(T) == 2 && dtl_ok(p[7], K, lda, ldw, sizeof(T))) {
+    const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
+    const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+    if (t256 >= 512) return 8;
+    if (t128 >= 128) return 7;
+    return 9;
+  }
   int best = 0;
   double best_cost = 1e300;
   for (int i = 0; i < count; ++i) {
+    if (p[i].kind == kDtl && !dtl_ok(p[i], K, lda, ldw, sizeof(T))) continue;
     const int64_t tiles = ((M + p[i].bm - 1) / p[i].bm) * ((N + p[i].bn - 1) / p[i].bn);
     const int64_t rounds = (tiles + 255) / 256;
-    const double cost = (double)rounds * p[i].bm * p[i].bn / eff[i];
+    const double cost = (double)rounds * p[i].bm * p[i].bn / p[i].eff;
     if (cost < best_cost * 0.999) {
       best_cost = cost;
       best = i;
@@ -233,23 +446,45 @@ static int auto_plan(int64_t M, int64_t N) {
   return best;
 }
 
-template <typename T, int BM, int BN, int WM, int WN>
+// Kernel selection by plan kind through a specialised struct (the host stub
+// of a kernel launched under `if constexpr` is not always emitted).
+template <int KIND> struct Launcher;
+template <> struct Launcher<kStaged> {
+  template <typename T, int BM, int BN, int WM, int WN, int EPI>
+  static void go(dim3 grid, hipStream_t s, const void* a, int64_t lda, const void* w, int64_t ldw,
+                 const void* bias, void* c, int64_t ldc, int M, int N, int K) {
+    hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WM, WN, EPI>), grid, dim3(WM * WN * 64), 0, s, (const T*)a, lda,
+                       (const T*)w, ldw, (const T*)bias, c, ldc, M, N, K);
+  }
+};
+template <int BKB, int STAGES> struct DtlLauncher {
+  template <typename T, int BM, int BN, int WM, int WN, int EPI>
+  static void go(dim3 grid, hipStream_t s, const void* a, int64_t lda, const void* w, int64_t ldw,
+                 const void* bias, void* c, int64_t ldc, int M, int N, int K) {
+    hipLaunchKernelGGL((gemm_dtl_kernel<T, BM, BN, WM, WN, BKB, STAGES, EPI>), grid, dim3(WM * WN * 64), 0, s,
+                       (const T*)a, lda, (const T*)w, ldw, (const T*)bias, c, ldc, M, N, K);
+  }
+};
+
+template <typename L, typename T, int BM, int BN, int WM, int WN, int EPI>
+static void launch_one(dim3 grid, hipStream_t s, const void* a, int64_t lda, const void* w, int64_t ldw,
+                       const void* bias, void* c, int64_t ldc, int M, int N, int K) {
+  L::template go<T, BM, BN, WM, WN, EPI>(grid, s, a, lda, w, ldw, bias, c, ldc, M, N, K);
+}
+
+template <typename L, typename T, int BM, int BN, int WM, int WN>
 static void launch_epi(int epi, const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias,
                        void* c, int64_t ldc, int M, int N, int K, hipStream_t s) {
-  const int nb = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  dim3 grid(nb), block(WM * WN * 64);
+  const dim3 grid(((M + BM - 1) / BM) * ((N + BN - 1) / BN));
   switch (epi) {
     case TJK_EPI_BIAS:
-      hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WM, WN, TJK_EPI_BIAS>), grid, block, 0, s, (const T*)a, lda,
-                         (const T*)w, ldw, (const T*)bias, c, ldc, M, N, K);
+      launch_one<L, T, BM, BN, WM, WN, TJK_EPI_BIAS>(grid, s, a, lda, w, ldw, bias, c, ldc, M, N, K);
       break;
     case TJK_EPI_BIAS_GELU:
-      hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WM, WN, TJK_EPI_BIAS_GELU>), grid, block, 0, s, (const T*)a,
-                         lda, (const T*)w, ldw, (const T*)bias, c, ldc, M, N, K);
+      launch_one<L, T, BM, BN, WM, WN, TJK_EPI_BIAS_GELU>(grid, s, a, lda, w, ldw, bias, c, ldc, M, N, K);
       break;
     default:
-      hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WM, WN, TJK_EPI_BIAS_RESIDUAL>), grid, block, 0, s,
-                         (const T*)a, lda, (const T*)w, ldw, (const T*)bias, c, ldc, M, N, K);
+      launch_one<L, T, BM, BN, WM, WN, TJK_EPI_BIAS_RESIDUAL>(grid, s, a, lda, w, ldw, bias, c, ldc, M, N, K);
       break;
   }
 }
@@ -257,21 +492,35 @@ static void launch_epi(int epi, const void* a, int64_t lda, const void* w, int64
 template <typename T>
 static int run_gemm(int plan, int epi, const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias,
                     void* c, int64_t ldc, int M, int N, int K, hipStream_t s) {
+  typedef Launcher<kStaged> St;
+  typedef DtlLauncher<128, 2> D2;
+#define TJK_GEMM_CASE(ID, L, BM, BN, WM, WN) \
+  case ID: launch_epi<L, T, BM, BN, WM, WN>(epi, a, lda, w, ldw, bias, c, ldc, M, N, K, s); break;
   if constexpr (sizeof(T) == 4) {
     switch (plan) {
-      case 0: launch_epi<T, 128, 128, 2, 2>(epi, a, lda, w, ldw, bias, c, ldc, M, N, K, s); break;
-      default: launch_epi<T, 64, 64, 2, 2>(epi, a, lda, w, ldw, bias, c, ldc, M, N, K, s); break;
+      TJK_GEMM_CASE(0, St, 128, 128, 2, 2)
+      TJK_GEMM_CASE(1, St, 64, 64, 2, 2)
+      TJK_GEMM_CASE(2, D2, 128, 128, 2, 2)
+      TJK_GEMM_CASE(3, D2, 256, 128, 2, 2)
+      TJK_GEMM_CASE(4, D2, 64, 64, 2, 2)
     }
   } else {
     switch (plan) {
-      case 0: launch_epi<T, 256, 256, 2, 2>(epi, a, lda, w, ldw, bias, c, ldc, M, N, K, s); break;
-      case 1: launch_epi<T, 256, 128, 2, 2>(epi, a, lda, w, ldw, bias, c, ldc, M, N, K, s); break;
-      case 2: launch_epi<T, 128, 256, 2, 2>(epi, a, lda, w, ldw, bias, c, ldc, M, N, K, s); break;
-      case 3: launch_epi<T, 128, 128, 2, 2>(epi, a, lda, w, ldw, bias, c, ldc, M, N, K, s); break;
-      case 4: launch_epi<T, 64, 64, 2, 2>(epi, a, lda, w, ldw, bias, c, ldc, M, N, K, s); break;
-      default: launch_epi<T, 256, 256, 2, 4>(epi, a, lda, w, ldw, bias, c, ldc, M, N, K, s); break;
+      TJK_GEMM_CASE(0, St, 256, 256, 2, 2)
+      TJK_GEMM_CASE(1, St, 256, 128, 2, 2)
+      TJK_GEMM_CASE(2, St, 128, 256, 2, 2)
+      TJK_GEMM_CASE(3, St, 128, 128, 2, 2)
+      TJK_GEMM_CASE(4, St, 64, 64, 2, 2)
+      TJK_GEMM_CASE(5, St, 256, 256, 2, 4)
+      TJK_GEMM_CASE(6, D2, 256, 256, 2, 2)
+      TJK_GEMM_CASE(7, D2, 128, 128, 2, 2)
+      TJK_GEMM_CASE(8, D2, 256, 256, 2, 4)
+      TJK_GEMM_CASE(9, D2, 64, 64, 2, 2)
+      TJK_GEMM_CASE(10, D2, 256, 128, 2, 2)
+      TJK_GEMM_CASE(11, D2, 128, 256, 2, 2)
     }
   }
+#undef TJK_GEMM_CASE
   return check_launch("tjk_gemm_bias");
 }
 
@@ -279,9 +528,14 @@ template <typename T>
 static int gemm_checked(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias, void* c,
                         int64_t ldc, int64_t m, int64_t n, int64_t k, int epi, int plan, hipStream_t s) {
   int count;
-  plans<T>(&count);
+  const GemmPlan* p = plans<T>(&count);
   if (plan < -1 || plan >= count) return fail(TJK_EINVAL, "tjk_gemm_bias: plan %d out of range [-1,%d)", plan, count);
-  if (plan == -1) plan = auto_plan<T>(m, n);
+  if (plan == -1) plan = auto_plan<T>(m, n, k, lda, ldw);
+  if (p[plan].kind == kDtl && !dtl_ok(p[plan], k, lda, ldw, sizeof(T)))
+    return fail(TJK_EUNSUPPORTED, "tjk_gemm_bias: plan %d needs k %% %d == 0", plan, (int)(p[plan].bkb / sizeof(T)));
+  if (p[plan].kind == kDtl && ((int64_t)p[plan].bm * lda * (int64_t)sizeof(T) > INT32_MAX ||
+                               (int64_t)p[plan].bn * ldw * (int64_t)sizeof(T) > INT32_MAX))
+    return fail(TJK_EUNSUPPORTED, "tjk_gemm_bias: leading dimension too large for plan %d", plan);
   return run_gemm<T>(plan, epi, a, lda, w, ldw, bias, c, ldc, (int)m, (int)n, (int)k, s);
 }
 

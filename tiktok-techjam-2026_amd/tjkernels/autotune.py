@@ -1,0 +1,230 @@
+"""Accuracy-gated autotuner: writes tuned plans into ``plans.json``.
+
+    python -m tjkernels.autotune --workloads C2,C3,C4,C5 [--margin 0.85] [--dry-run]
+
+Mirrors the reference's tuner (bench/autotune.py:61-246): it searches for
+the fastest plan whose outputs stay inside a tightened version of the
+accuracy budget, and records it per shape key.  A plan is admitted only
+if, over the trial seeds and two held-out seeds (777, 4242), no element uses
+more than ``margin`` of its own budget ``max(atol, rtol*|ref|)``
+(bench/autotune.py:61-68); if the heuristic plan is inadmissible the tuner
+escalates to fp32 compute (:203-217); a knob change is kept only if the plan
+stays admissible and gets at least 2% faster (:229-234).
+
+MI355X specifics:
+
+* the accuracy reference is this build's own IEEE fp32 plan run on the GPU
+  on the same inputs (the tests pin that plan to the CPU oracle at 1e-4, far
+  inside the 2e-2 budgets), so the tuner needs no CPU oracle at run time;
+* the GEMM tile plans are tuned per projection by timing every valid plan on
+  the exact (M, N, K, epilogue) of that projection with HIP events, which is
+  cheap and independent of the other knobs; the plan-level knobs (attention
+  plan, residual epilogue, hipGraph) are then tuned by coordinate descent on
+  whole-forward latency measured as the harness does (events on the current
+  stream around the module call).
+"""
+
+from __future__ import annotations
+
+import argparse
+import statistics
+from dataclasses import replace
+from typing import Dict, List, Optional, Tuple
+
+import torch
+
+from . import ops
+from .modules import UserOptimizedTransformer
+from .plans import Plan, default_plan, device_arch, save_plans, set_override, shape_key
+from .workloads import WORKLOADS, Workload, make_inputs, make_state_dict
+
+HELD_OUT_SEEDS = [777, 4242]
+
+
+def budget(dtype: torch.dtype) -> Tuple[float, float]:
+    """(atol, rtol) of the per-element budget for a model dtype."""
+    return (1e-4, 1e-4) if dtype == torch.float32 else (2e-2, 2e-2)
+
+
+def budget_usage(ref: torch.Tensor, got: torch.Tensor, atol: float, rtol: float) -> float:
+    err = (got.float() - ref.float()).abs_()
+    bud = ref.float().abs().mul_(rtol).clamp_min_(atol)
+    return float(err.div_(bud).max())
+
+
+def _time_ms(fn, iters: int, warmup: int = 3) -> float:
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(iters):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        samples.append((e0, e1))
+    torch.cuda.synchronize()
+    return statistics.median(a.elapsed_time(b) for a, b in samples)
+
+
+def tune_gemm(m: int, n: int, k: int, dtype: torch.dtype, epilogue: int,
+              iters: int = 20) -> Tuple[int, Dict[int, float]]:
+    """Fastest valid tile plan for one projection shape; returns (plan, {plan: ms})."""
+    dev = torch.device("cuda", torch.cuda.current_device())
+    a = torch.randn(m, k, device=dev).to(dtype)
+    w = (torch.randn(n, k, device=dev) * 0.02).to(dtype)
+    b = torch.zeros(n, device=dev, dtype=dtype)
+    out = torch.zeros(m, n, device=dev, dtype=torch.float32 if epilogue == ops.EPI_BIAS_RESIDUAL else dtype)
+    times: Dict[int, float] = {}
+    for pid, *_ in ops.gemm_plans(dtype):
+        try:
+            ops.gemm(a, w, b, out, epilogue, pid)
+        except ops.TjkError:
+            continue  # plan does not take this K
+        times[pid] = _time_ms(lambda: ops.gemm(a, w, b, out, epilogue, pid), iters)
+    best = min(times, key=times.get)
+    return best, times
+
+
+class _Evaluator:
+    def __init__(self, w: Workload, trials: int, iters: int) -> None:
+        self.w = w
+        self.dev = torch.device("cuda", torch.cuda.current_device())
+        self.sd = make_state_dict(w, seed=0)
+        self.atol, self.rtol = budget(w.dtype)
+        self.iters = iters
+        seeds = list(range(1, trials + 1)) + HELD_OUT_SEEDS
+        self.inputs = []
+        for s in seeds:
+            x, mask, _ = make_inputs(w, seed=s)
+            self.inputs.append((x.to(self.dev, w.dtype), mask.to(self.dev)))
+        xb, mb, _ = make_inputs(w, seed=100001)
+        self.bench_input = (xb.to(self.dev, w.dtype), mb.to(self.dev))
+        self.refs = [self._run(Plan(compute_dtype=torch.float32, cuda_graph=False,
+                                    label="fp32-reference"), x, m)
+                     for x, m in self.inputs]
+
+    def _model(self) -> UserOptimizedTransformer:
+        m = UserOptimizedTransformer(self.w.config)
+        m.load_state_dict(self.sd, strict=True)
+        return m.to(device=self.dev, dtype=self.w.dtype).eval()
+
+    def _run(self, plan: Plan, x, mask) -> torch.Tensor:
+        set_override(plan)
+        try:
+            with torch.inference_mode():
+                return self._model()(x, mask)
+        finally:
+            set_override(None)
+
+    def evaluate(self, plan: Plan) -> Dict[str, object]:
+        set_override(plan)
+        try:
+            model = self._model()
+            usage = 0.0
+            with torch.inference_mode():
+                for (x, m), ref in zip(self.inputs, self.refs):
+                    got = model(x, m)
+                    if not torch.isfinite(got).all():
+                        return {"plan": plan, "admissible": False, "usage": float("inf")}
+                    usage = max(usage, budget_usage(ref, got, self.atol, self.rtol))
+                xb, mb = self.bench_input
+                ms = _time_ms(lambda: model(xb, mb), self.iters)
+        except ops.TjkError as exc:
+            return {"plan": plan, "admissible": False, "error": str(exc)[:160]}
+        finally:
+            set_override(None)
+        return {"plan": plan, "latency_ms": ms, "usage": usage}
+
+
+def tune_workload(w: Workload, trials: int = 2, margin: float = 0.85, iters: int = 30,
+                  verbose: bool = True) -> Optional[Tuple[str, Plan, Dict[str, object]]]:
+    dev = torch.device("cuda", torch.cuda.current_device())
+    base = replace(default_plan(w.batch, w.seq, w.d_model, w.heads, w.ffn_dim, w.layers,
+                                w.causal, w.dtype, dev), label="autotuned")
+    ev = _Evaluator(w, trials, iters)
+
+    def admissible(r):
+        return "latency_ms" in r and r["usage"] <= margin
+
+    def show(tag, r):
+        if verbose:
+            if "latency_ms" in r:
+                flag = "ok " if admissible(r) else "REJ"
+                print(f"    {tag:<28} {flag} {r['latency_ms']:8.3f} ms  budget={r['usage']:.0%}", flush=True)
+            else:
+                print(f"    {tag:<28} ERR {r.get('error', 'non-finite output')}", flush=True)
+
+    cur = ev.evaluate(base)
+    show("heuristic", cur)
+    if not admissible(cur) and base.compute_dtype != torch.float32:
+        esc = ev.evaluate(replace(base, compute_dtype=torch.float32, label="autotuned-fp32"))
+        show("escalate-fp32", esc)
+        if admissible(esc):
+            cur = esc
+    if not admissible(cur):
+        return None
+
+    # per-projection tile plans, timed in isolation at the exact shapes
+    plan = cur["plan"]
+    t, d, f = w.tokens, w.d_model, w.ffn_dim
+    cdt = plan.compute_dtype
+    res_epi = ops.EPI_BIAS_RESIDUAL if plan.residual_epilogue else ops.EPI_BIAS
+    picks = {}
+    for knob, (m, n, k, epi) in {"gemm_qkv": (t, 3 * d, d, ops.EPI_BIAS),
+                                 "gemm_out": (t, d, d, res_epi),
+                                 "gemm_ffn1": (t, f, d, ops.EPI_BIAS_GELU),
+                                 "gemm_ffn2": (t, d, f, res_epi)}.items():
+        best, times = tune_gemm(m, n, k, cdt, epi)
+        picks[knob] = best
+        if verbose:
+            top = sorted(times.items(), key=lambda kv: kv[1])[:3]
+            print(f"    {knob:<10} {m}x{n}x{k}: " +
+                  ", ".join(f"p{p}={ms * 1e3:.1f}us" for p, ms in top), flush=True)
+    cand = ev.evaluate(replace(plan, **picks))
+    show("tuned gemm tiles", cand)
+    if admissible(cand) and cand["latency_ms"] < cur["latency_ms"]:
+        cur = cand
+
+    # coordinate descent over the plan-level knobs
+    for knob, values in (("attn_plan", [0, 1]), ("residual_epilogue", [True, False]),
+                         ("cuda_graph", [True, False])):
+        for v in values:
+            if getattr(cur["plan"], knob) == v:
+                continue
+            probe = ev.evaluate(replace(cur["plan"], **{knob: v}))
+            show(f"{knob}={v}", probe)
+            if admissible(probe) and probe["latency_ms"] < cur["latency_ms"] * 0.98:
+                cur = probe
+    key = shape_key(w.batch, w.seq, w.d_model, w.heads, w.ffn_dim, w.layers, w.causal,
+                    w.dtype, device_arch(dev))
+    return key, cur["plan"], cur
+
+
+def main(argv: Optional[List[str]] = None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--workloads", default="C2,C3,C4,C5")
+    ap.add_argument("--trials", type=int, default=2)
+    ap.add_argument("--margin", type=float, default=0.85)
+    ap.add_argument("--iters", type=int, default=30)
+    ap.add_argument("--dry-run", action="store_true")
+    args = ap.parse_args(argv)
+    tuned: Dict[str, Plan] = {}
+    for name in args.workloads.split(","):
+        w = WORKLOADS[name]
+        print(f"{w.describe()}", flush=True)
+        out = tune_workload(w, args.trials, args.margin, args.iters)
+        if out is None:
+            print("    no admissible plan; heuristic left in place", flush=True)
+            continue
+        key, plan, res = out
+        tuned[key] = plan
+        print(f"    -> {res['latency_ms']:.3f} ms budget={res['usage']:.0%} {plan.to_json()}", flush=True)
+    if tuned and not args.dry_run:
+        save_plans(tuned)
+        print(f"wrote {len(tuned)} plan(s) to plans.json", flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
