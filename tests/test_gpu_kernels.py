@@ -188,7 +188,7 @@ def test_flash_shapes(device, dt, hd, seq, causal):
     g = _gen(hd * 1000 + seq)
     qkv = torch.randn(b, seq, 3, h, hd, generator=g).to(dt)
     ref = _attn_ref(qkv, causal)
-    for plan in (0, 1):
+    for plan in (0, 1, 2):
         out = torch.full((b * seq, h * hd), float("nan"), dtype=dt, device=device)
         ops.flash_attention(qkv.to(device), out, causal=causal, plan=plan)
         torch.cuda.synchronize()
@@ -205,17 +205,19 @@ def test_flash_key_mask_and_lengths(device, dt):
     key_mask[:, 0] = True
     for causal in (True, False):
         ref = _attn_ref(qkv, causal, key_mask)
-        out = torch.empty(b * s, h * hd, dtype=dt, device=device)
-        ops.flash_attention(qkv.to(device), out, causal=causal, key_mask=key_mask.to(device))
-        torch.cuda.synchronize()
-        _close(out, ref, 1e-5 if dt == torch.float32 else 1e-2, 1e-5 if dt == torch.float32 else 1e-2)
+        for plan in (0, 1):
+            out = torch.empty(b * s, h * hd, dtype=dt, device=device)
+            ops.flash_attention(qkv.to(device), out, causal=causal, key_mask=key_mask.to(device), plan=plan)
+            torch.cuda.synchronize()
+            _close(out, ref, 1e-5 if dt == torch.float32 else 1e-2, 1e-5 if dt == torch.float32 else 1e-2)
     lengths = torch.tensor([150, 1, 77], dtype=torch.int32)
     pm = torch.arange(s)[None, :] < lengths[:, None].long()
     ref = _attn_ref(qkv, False, pm)
-    out = torch.empty(b * s, h * hd, dtype=dt, device=device)
-    ops.flash_attention(qkv.to(device), out, causal=False, lengths=lengths.to(device))
-    torch.cuda.synchronize()
-    _close(out, ref, 1e-5 if dt == torch.float32 else 1e-2, 1e-5 if dt == torch.float32 else 1e-2)
+    for plan in (0, 1):
+        out = torch.empty(b * s, h * hd, dtype=dt, device=device)
+        ops.flash_attention(qkv.to(device), out, causal=False, lengths=lengths.to(device), plan=plan)
+        torch.cuda.synchronize()
+        _close(out, ref, 1e-5 if dt == torch.float32 else 1e-2, 1e-5 if dt == torch.float32 else 1e-2)
 
 
 def test_flash_closed_forms(device):
@@ -242,7 +244,12 @@ def test_flash_packed_layout_headline(device):
     out = torch.empty(b * s, h * hd, device=device, dtype=torch.bfloat16)
     ops.flash_attention(q5, out, causal=True)
     torch.cuda.synchronize()
-    sel = [0, 1, 777, 2047]
+    sel = [0, 1, 63, 64, 127, 128, 777, 2047]
     ref = _attn_ref(q5[:1].cpu(), True).view(s, h * hd)
     got = out.view(b, s, h * hd)[0].cpu()
     _close(got[sel], ref[sel], 1e-2, 1e-2)
+    # the pipelined and the plain kernel agree on every row
+    out1 = torch.empty_like(out)
+    ops.flash_attention(q5, out1, causal=True, plan=1)
+    torch.cuda.synchronize()
+    assert (out.float() - out1.float()).abs().max().item() < 2e-2

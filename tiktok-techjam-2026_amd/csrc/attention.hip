@@ -65,7 +65,7 @@ template <> struct PairPack<float> {
   }
 };
 
-template <typename T, int HDP, int NQ>
+template <typename T, int HDP, int NQ, bool KEYMASK>
 __global__ __launch_bounds__(256) void flash_fwd_kernel(
     const T* __restrict__ qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh,
     T* __restrict__ out, int64_t ld_out, int B, int S, int H, int hd, float scale_log2,
@@ -207,26 +207,39 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(
         }
       }
 
-      // ---- masking: register r of block kb is key k0 + kb*32 + 16*(r/8) + 8*hi + r%8
+      // ---- masking: register r of block kb is key k0 + kb*32 + 16*(r/8) + 8*hi + r%8.
+      // Selects, not branches; only tiles that straddle the causal diagonal
+      // or the end of the keys pay for them (a wave-uniform test).
       const bool tail = k0 + BNK > kend;
 #pragma unroll
       for (int j = 0; j < NQ; ++j) {
         const int q = wq0 + j * 32 + l32;
         const bool diag = causal && k0 + BNK - 1 > wq0 + j * 32;
-        if (tail || diag || key_mask != nullptr) {
+        if (tail || diag) {
+          const int lim = causal ? min(q + 1, kend) : kend;  // keys < lim are admissible
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const int key = k0 + kb * 32 + 16 * (r >> 3) + 8 * hi + (r & 7);
-              bool dead = key >= kend || (causal && key > q);
-              if (key_mask != nullptr && !dead) dead = key_mask[(int64_t)b * S + key] == 0;
-              if (dead) s[j][kb][r] = -INFINITY;
+              s[j][kb][r] = key < lim ? s[j][kb][r] : -INFINITY;
+            }
+        }
+        if constexpr (KEYMASK) {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int key = k0 + kb * 32 + 16 * (r >> 3) + 8 * hi + (r & 7);
+              const bool keep = key < kend && key_mask[(int64_t)b * S + key] != 0;
+              s[j][kb][r] = keep ? s[j][kb][r] : -INFINITY;
             }
         }
       }
 
-      // ---- online softmax (base 2) and P fragments
+      // ---- online softmax (base 2) and P fragments.  The O rescale is
+      // skipped when no lane's running max moved (alpha == 1 everywhere),
+      // which is the common case once a row has seen its largest scores.
       typename Mfma<T>::frag pf[NQ][4];
 #pragma unroll
       for (int j = 0; j < NQ; ++j) {
@@ -250,10 +263,12 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(
           }
         l_run[j] = l_run[j] * alpha + rs;
         m_run[j] = m_new;
+        if (__any(alpha != 1.0f)) {
 #pragma unroll
-        for (int hb = 0; hb < HB; ++hb)
+          for (int hb = 0; hb < HB; ++hb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) o[j][hb][r] *= alpha;
+            for (int r = 0; r < 16; ++r) o[j][hb][r] *= alpha;
+        }
 #pragma unroll
         for (int st = 0; st < 4; ++st) pf[j][st] = Mfma<T>::pack(&p[st >> 1][8 * (st & 1)]);
       }
@@ -296,6 +311,290 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(
   }
 }
 
+// ------------------------------------------------ software-pipelined variant
+//
+// Same math and output as flash_fwd_kernel (one 32-query block per wave),
+// for 2-byte types, with the per-tile dependency chain
+//     S = K Q^T  ->  softmax(S)  ->  O += V P
+// broken across tiles: the MFMAs of S for tile t+1 are issued before the
+// softmax of tile t, so the matrix cores work while the VALU does the
+// softmax.  That needs K of tile t+1 resident while V of tile t is still
+// read, so K/V tiles live in a 3-deep LDS ring; the global loads of tile
+// t+2 go out at the start of iteration t.  K/V are read through buffer
+// descriptors that end at this head's last key, so keys past S arrive as 0
+// without a bounds branch.  Tiles that need no masking (every key below the
+// workgroup's first query and inside the sequence) run a branch-free loop;
+// the diagonal / tail tiles run a second loop with masks and per-wave skips.
+
+constexpr uint32_t kFaPastEnd = 0x7fff0000u;
+
+template <typename T, int HDP, bool KEYMASK>
+__global__ __launch_bounds__(256) void flash_pipe_kernel(
+    const T* __restrict__ qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh,
+    T* __restrict__ out, int64_t ld_out, int B, int S, int H, int hd, float scale_log2,
+    int causal, const int32_t* __restrict__ lengths, const uint8_t* __restrict__ key_mask, int nqb) {
+  static_assert(sizeof(T) == 2, "2-byte element types only");
+  constexpr int BMQ = 128, BNK = 64, NST = 3, VEC = 8;
+  constexpr int LDK = HDP + VEC, LDV = BNK + VEC;
+  constexpr int KC = HDP / 16, HB = HDP / 32, CH = HDP / VEC;
+  constexpr int KITEMS = BNK * CH, VITEMS = (BNK / 2) * CH;
+  constexpr int KPT = KITEMS / 256, VPT = (VITEMS + 255) / 256;
+  static_assert(KITEMS % 256 == 0, "K tile must split evenly over 256 threads");
+
+  __shared__ __attribute__((aligned(16))) T sK[NST][BNK * LDK];
+  __shared__ __attribute__((aligned(16))) T sV[NST][HDP * LDV];
+
+  const int BH = B * H;
+  const int rank = blockIdx.x / BH, bh = blockIdx.x % BH;
+  const int qb = causal ? nqb - 1 - rank : rank;
+  const int b = bh / H, h = bh % H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hi = lane >> 5;
+
+  const T* qbase = qkv + (int64_t)b * sb + (int64_t)h * sh;
+  int kv_len = S;
+  if (lengths != nullptr) kv_len = min(kv_len, max(lengths[b], 0));
+  const int q0 = qb * BMQ;
+  const int wq0 = q0 + wave * 32;
+  int kend = causal ? min(q0 + BMQ, S) : S;
+  kend = min(kend, kv_len);
+  const int nkt = (kend + BNK - 1) / BNK;
+
+  // Q fragments (B operand of S^T): lane holds Q[q][16c + 8*hi + 0..7]
+  typename Mfma<T>::frag qf[KC];
+  {
+    const int q = wq0 + l32;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      const int col = 16 * c + 8 * hi;
+      if (q < S && col < hd) {
+        qf[c] = Mfma<T>::load(qbase + (int64_t)q * ss + col);
+      } else {
+        float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        qf[c] = Mfma<T>::pack(z);
+      }
+    }
+  }
+
+  // K / V rows of this (b, h) through buffer descriptors ending at key S-1.
+  const uint32_t row_bytes = (uint32_t)(ss * (int64_t)sizeof(T));
+  const int span = (int)(((int64_t)(S - 1) * ss + hd) * (int64_t)sizeof(T));
+  const __amdgpu_buffer_rsrc_t rsk = __builtin_amdgcn_make_buffer_rsrc((void*)(qbase + sc), (short)0, span, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc((void*)(qbase + 2 * sc), (short)0, span, 0x00020000);
+  uint4 rk[KPT], rv0[VPT], rv1[VPT];
+  auto load_kv = [&](int t) {  // tiles past the end read as zeros
+    const uint32_t tb = t < nkt ? (uint32_t)t * BNK * row_bytes : kFaPastEnd;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int it = tid + i * 256, key = it / CH, c = it % CH;
+      const uint32_t off = tb + (uint32_t)key * row_bytes + (uint32_t)(c * 16);
+      uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsk, off, 0, 0));
+      rk[i] = c * VEC < hd ? v : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int it = tid + i * 256;
+      const int p = it % (BNK / 2), c = it / (BNK / 2);
+      const uint32_t off = tb + (uint32_t)(2 * p) * row_bytes + (uint32_t)(c * 16);
+      uint4 v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsv, off, 0, 0));
+      uint4 v1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsv, off + row_bytes, 0, 0));
+      const bool ok = c * VEC < hd;
+      rv0[i] = ok ? v0 : make_uint4(0, 0, 0, 0);
+      rv1[i] = ok ? v1 : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store_kv = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int it = tid + i * 256, key = it / CH, c = it % CH;
+      *reinterpret_cast<uint4*>(&sK[st][key * LDK + c * VEC]) = rk[i];
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int it = tid + i * 256;
+      if (VITEMS % 256 == 0 || it < VITEMS) {
+        const int p = it % (BNK / 2), c = it / (BNK / 2);
+        PairPack<T>::write(&sV[st][(c * VEC) * LDV + 2 * p], LDV, rv0[i], rv1[i]);
+      }
+    }
+  };
+
+  const int krow = swap_bits_2_3(l32);
+  auto qk = [&](int st, f32x16 (&sa)[2]) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sa[kb][r] = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const T* kp = &sK[st][(kb * 32 + krow) * LDK + 8 * hi];
+#pragma unroll
+      for (int c = 0; c < KC; ++c) Mfma<T>::mma(sa[kb], Mfma<T>::load(kp + 16 * c), qf[c]);
+    }
+  };
+
+  f32x16 o[HB];
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[hb][r] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  // softmax of one tile's scores (already masked) and O += V P
+  auto softmax_pv = [&](int st, f32x16 (&sa)[2], bool interleave) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sa[kb][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new * scale_log2;
+    const float alpha = __builtin_amdgcn_exp2f(m_run * scale_log2 - m_use);
+    float rs = 0.f;
+    float p[2][16];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        p[kb][r] = __builtin_amdgcn_exp2f(fmaf(sa[kb][r], scale_log2, -m_use));
+        rs += p[kb][r];
+      }
+    l_run = l_run * alpha + rs;
+    m_run = m_new;
+    typename Mfma<T>::frag pf[4];
+#pragma unroll
+    for (int stp = 0; stp < 4; ++stp) pf[stp] = Mfma<T>::pack(&p[stp >> 1][8 * (stp & 1)]);
+    if (interleave) {
+      // Spread the next tile's S MFMAs (issued just before this call, same
+      // basic block) over the softmax VALU work so both pipes stay busy.
+      __builtin_amdgcn_sched_group_barrier(0x020, KPT + 2 * VPT, 0);  // global loads of tile t+2
+#pragma unroll
+      for (int i = 0; i < 2 * KC; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // K fragment
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // S MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 10, 0); // softmax VALU
+      }
+    }
+    if (__any(alpha != 1.0f)) {
+#pragma unroll
+      for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[hb][r] *= alpha;
+    }
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+      const T* vp = &sV[st][(hb * 32 + l32) * LDV + 8 * hi];
+#pragma unroll
+      for (int stp = 0; stp < 4; ++stp) Mfma<T>::mma(o[hb], Mfma<T>::load(vp + 16 * stp), pf[stp]);
+    }
+  };
+
+  // register r of block kb is key k0 + kb*32 + 16*(r/8) + 8*hi + r%8
+  auto mask_tile = [&](int t, f32x16 (&sa)[2]) {
+    const int k0 = t * BNK, q = wq0 + l32;
+    const int lim = causal ? min(q + 1, kend) : kend;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = k0 + kb * 32 + 16 * (r >> 3) + 8 * hi + (r & 7);
+        bool keep = key < lim;
+        if constexpr (KEYMASK) keep = keep && key_mask[(int64_t)b * S + min(key, S - 1)] != 0;
+        sa[kb][r] = keep ? sa[kb][r] : -INFINITY;
+      }
+  };
+
+  load_kv(0);
+  store_kv(0);
+  load_kv(1);
+  store_kv(1);
+  __syncthreads();
+
+  f32x16 scur[2];
+  if (nkt > 0) qk(0, scur);
+  // Interior tiles: every key below the workgroup's first query and inside
+  // the sequence, and a next tile exists.
+  int n_int = KEYMASK ? 0 : min(causal ? q0 / BNK : nkt, min(kend / BNK, nkt - 1));
+  n_int = max(n_int, 0);
+  int t = 0;
+  f32x16 salt[2];
+  for (; t + 1 < n_int; t += 2) {  // two tiles per trip: scores ping-pong scur <-> salt
+    load_kv(t + 2);
+    qk((t + 1) % NST, salt);
+    softmax_pv(t % NST, scur, true);
+    store_kv((t + 2) % NST);
+    __syncthreads();
+    load_kv(t + 3);
+    qk((t + 2) % NST, scur);
+    softmax_pv((t + 1) % NST, salt, true);
+    store_kv((t + 3) % NST);
+    __syncthreads();
+  }
+  if (t < n_int) {
+    load_kv(t + 2);
+    qk((t + 1) % NST, salt);
+    softmax_pv(t % NST, scur, true);
+    store_kv((t + 2) % NST);
+    __syncthreads();
+    scur[0] = salt[0];
+    scur[1] = salt[1];
+    ++t;
+  }
+  for (; t < nkt; ++t) {
+    load_kv(t + 2);
+    f32x16 snext[2];
+    const bool act_next = t + 1 < nkt && (!causal || (t + 1) * BNK <= wq0 + 31);
+    if (act_next) qk((t + 1) % NST, snext);
+    const bool act = !causal || t * BNK <= wq0 + 31;
+    if (act) {
+      mask_tile(t, scur);
+      softmax_pv(t % NST, scur, false);
+    }
+    store_kv((t + 2) % NST);
+    __syncthreads();
+    if (act_next) {
+      scur[0] = snext[0];
+      scur[1] = snext[1];
+    }
+  }
+
+  // normalise and store: register r of block hb is hd row hb*32 + 8*(r/4) + 4*hi + r%4
+  const int q = wq0 + l32;
+  const float l = l_run + __shfl_xor(l_run, 32, 64);
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  if (q < S) {
+    T* orow = out + ((int64_t)b * S + q) * ld_out + (int64_t)h * hd;
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int col = hb * 32 + 8 * g + 4 * hi;
+        if (col < hd) {
+          const float4 v = make_float4(o[hb][4 * g] * inv, o[hb][4 * g + 1] * inv, o[hb][4 * g + 2] * inv,
+                                       o[hb][4 * g + 3] * inv);
+          *reinterpret_cast<typename Quad<T>::raw*>(orow + col) = Quad<T>::from(v);
+        }
+      }
+  }
+}
+
+template <typename T, int HDP>
+static int launch_pipe(const void* qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh, void* out,
+                       int64_t ld_out, int B, int S, int H, int hd, float scale_log2, int causal,
+                       const int32_t* lengths, const uint8_t* key_mask, hipStream_t st) {
+  const int nqb = (S + 127) / 128;
+  const int64_t nblk = (int64_t)nqb * B * H;
+  if (nblk > INT32_MAX) return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd: grid too large");
+  if (key_mask != nullptr)
+    hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, true>), dim3((unsigned)nblk), dim3(256), 0, st, (const T*)qkv,
+                       sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, lengths, key_mask, nqb);
+  else
+    hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, false>), dim3((unsigned)nblk), dim3(256), 0, st, (const T*)qkv,
+                       sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, lengths, key_mask, nqb);
+  return check_launch("tjk_flash_fwd");
+}
+
 template <typename T, int HDP, int NQ>
 static int launch_flash(const void* qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh, void* out,
                         int64_t ld_out, int B, int S, int H, int hd, float scale_log2, int causal,
@@ -304,17 +603,27 @@ static int launch_flash(const void* qkv, int64_t sb, int64_t ss, int64_t sc, int
   const int nqb = (S + BMQ - 1) / BMQ;
   const int64_t nblk = (int64_t)nqb * B * H;
   if (nblk > INT32_MAX) return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd: grid too large");
-  hipLaunchKernelGGL((flash_fwd_kernel<T, HDP, NQ>), dim3((unsigned)nblk), dim3(256), 0, st,
-                     (const T*)qkv, sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal,
-                     lengths, key_mask, nqb);
+  if (key_mask != nullptr)
+    hipLaunchKernelGGL((flash_fwd_kernel<T, HDP, NQ, true>), dim3((unsigned)nblk), dim3(256), 0, st,
+                       (const T*)qkv, sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal,
+                       lengths, key_mask, nqb);
+  else
+    hipLaunchKernelGGL((flash_fwd_kernel<T, HDP, NQ, false>), dim3((unsigned)nblk), dim3(256), 0, st,
+                       (const T*)qkv, sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal,
+                       lengths, key_mask, nqb);
   return check_launch("tjk_flash_fwd");
 }
 
 template <typename T, int HDP>
-static int flash_nq(int plan, const void* qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh, void* out,
-                    int64_t ld_out, int B, int S, int H, int hd, float scale_log2, int causal,
-                    const int32_t* lengths, const uint8_t* key_mask, hipStream_t st) {
-  if (plan == 1)
+static int flash_plan(int plan, const void* qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh, void* out,
+                      int64_t ld_out, int B, int S, int H, int hd, float scale_log2, int causal,
+                      const int32_t* lengths, const uint8_t* key_mask, hipStream_t st) {
+  if constexpr (sizeof(T) == 2) {
+    if (plan == 0)
+      return launch_pipe<T, HDP>(qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
+                                 key_mask, st);
+  }
+  if (plan == 2)
     return launch_flash<T, HDP, 2>(qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
                                    key_mask, st);
   return launch_flash<T, HDP, 1>(qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
@@ -326,13 +635,13 @@ static int flash_typed(int plan, const void* qkv, int64_t sb, int64_t ss, int64_
                        int64_t ld_out, int B, int S, int H, int hd, float scale_log2, int causal,
                        const int32_t* lengths, const uint8_t* key_mask, hipStream_t st) {
   if (hd <= 32)
-    return flash_nq<T, 32>(plan, qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
-                           key_mask, st);
+    return flash_plan<T, 32>(plan, qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
+                             key_mask, st);
   if (hd <= 64)
-    return flash_nq<T, 64>(plan, qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
-                           key_mask, st);
-  return flash_nq<T, 128>(plan, qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
-                          key_mask, st);
+    return flash_plan<T, 64>(plan, qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
+                             key_mask, st);
+  return flash_plan<T, 128>(plan, qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
+                            key_mask, st);
 }
 
 }  // namespace tjk
@@ -342,7 +651,7 @@ using namespace tjk;
 extern "C" int tjk_flash_plan_count(int dtype) {
   if (dtype != TJK_F32 && dtype != TJK_F16 && dtype != TJK_BF16)
     return fail(TJK_EINVAL, "tjk_flash_plan_count: bad dtype %d", dtype);
-  return 2;
+  return 3;
 }
 
 extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s,
@@ -358,7 +667,7 @@ extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s
   if (dtype != TJK_F32 && dtype != TJK_F16 && dtype != TJK_BF16) return fail(TJK_EINVAL, "tjk_flash_fwd: bad dtype %d", dtype);
   if (head_dim > 128 || head_dim % 8)
     return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd: head_dim=%d must be a multiple of 8 and <= 128", head_dim);
-  if (plan_id < -1 || plan_id > 1) return fail(TJK_EINVAL, "tjk_flash_fwd: plan %d out of range", plan_id);
+  if (plan_id < -1 || plan_id > 2) return fail(TJK_EINVAL, "tjk_flash_fwd: plan %d out of range", plan_id);
   const int vec = 16 / dtype_size(dtype);
   if (stride_b % vec || stride_s % vec || stride_c % vec || stride_h % vec)
     return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd: strides must be multiples of %d elements", vec);
@@ -366,7 +675,13 @@ extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s
   if (((uintptr_t)qkv & 15) || ((uintptr_t)out & (4 * dtype_size(dtype) - 1)))
     return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd: misaligned pointer");
   if (!(scale > 0.f)) return fail(TJK_EINVAL, "tjk_flash_fwd: scale must be positive");
-  if (plan_id == -1) plan_id = (seq >= 1024 && dtype != TJK_F32) ? 1 : 0;
+  // plan 0: software-pipelined kernel (2-byte types, byte offsets within a
+  // head's K/V span must fit 31 bits); plans 1/2: one / two 32-query blocks
+  // per wave without cross-tile pipelining (every dtype).  Plan 1 measured
+  // fastest at S >= 2048 on MI355X, plan 0 at short sequences (S = 512).
+  const bool pipe_ok = dtype != TJK_F32 && ((int64_t)seq * stride_s + head_dim) * dtype_size(dtype) < INT32_MAX;
+  if (plan_id == -1) plan_id = (pipe_ok && seq <= 1024) ? 0 : 1;
+  if (plan_id == 0 && !pipe_ok) plan_id = 1;
   const float scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   switch (dtype) {
