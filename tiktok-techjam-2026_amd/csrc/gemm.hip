@@ -26,6 +26,8 @@
 //     workgroup i to XCD i % 8) walks a contiguous range of a GROUP_M-grouped
 //     tile order, keeping the A rows and W columns it reuses in its own L2.
 
+#include <type_traits>
+
 #include "tjk_common.h"
 
 namespace tjk {
@@ -48,37 +50,87 @@ __device__ __forceinline__ int xcd_remap(int bid, int nb) {
 // Epilogue shared by both GEMM kernels.  The accumulators hold C^T blocks:
 // for block (i, j), lane (l32, hi) owns output row m = mw + 32 j + l32 and,
 // for g = 0..3, the four consecutive columns n = nw + 32 i + 8 g + 4 hi.
+// Stored straight from that layout, every store instruction would scatter
+// 8-16 byte pieces over 32 rows (32 L2 requests per instruction), which
+// measured slower than the whole K=1024 main loop.  Instead each wave
+// applies bias / GELU in registers, transposes one 32-row block at a time
+// through a private LDS region (row pitch padded by one 16-byte piece) and
+// writes whole row segments: 16 bytes per lane, WTN contiguous elements per
+// row.  The residual epilogue stages fp32 and does its read-modify-write of
+// the fp32 residual with the same row-contiguous pieces.
+template <typename T, int EPI, int FN>
+struct EpiStage {
+  typedef typename std::conditional<EPI == TJK_EPI_BIAS_RESIDUAL, float, T>::type S;  // staged type
+  static constexpr int WTN = FN * 32;
+  static constexpr int SV = 16 / (int)sizeof(S);  // elements per 16-byte piece
+  static constexpr int PITCH = WTN + SV;          // staged row pitch (elements)
+  static constexpr int BYTES = 32 * PITCH * (int)sizeof(S);  // LDS bytes per wave
+};
+
 template <typename T, int EPI, int FM, int FN>
 __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* __restrict__ bias,
                                          void* __restrict__ Cv, int64_t ldc, int M, int N, int mw, int nw,
-                                         int l32, int hi) {
+                                         int lane, char* __restrict__ stage) {
+  typedef EpiStage<T, EPI, FN> E;
+  typedef typename E::S S;
+  constexpr int LPR = E::WTN / E::SV;  // lanes per staged row on the read side
+  constexpr int RPI = 64 / LPR;        // rows per read instruction
+  static_assert(LPR <= 64 && 64 % LPR == 0, "row split");
+  S* st = reinterpret_cast<S*>(stage);
+  const int l32 = lane & 31, hi = lane >> 5;
+  // 16-byte output pieces need a 16-byte aligned C and a leading dimension
+  // that keeps every row 16-byte aligned; otherwise pieces go out as halves.
+  const bool a16 = ((uintptr_t)Cv & 15) == 0 && (ldc % E::SV) == 0;
+
+  float4 bv[FN][4];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int n = nw + i * 32 + g * 8 + hi * 4;
+      bv[i][g] = (bias != nullptr && n < N)
+                     ? Quad<T>::to(*reinterpret_cast<const typename Quad<T>::raw*>(bias + n))
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
-    const int m = mw + j * 32 + l32;
-    if (m >= M) continue;
 #pragma unroll
-    for (int i = 0; i < FN; ++i) {
+    for (int i = 0; i < FN; ++i)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int n = nw + i * 32 + g * 8 + hi * 4;
-        if (n >= N) continue;
-        float4 v = make_float4(acc[i][j][4 * g + 0], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                               acc[i][j][4 * g + 3]);
-        if (bias != nullptr) {
-          const float4 bv = Quad<T>::to(*reinterpret_cast<const typename Quad<T>::raw*>(bias + n));
-          v.x += bv.x; v.y += bv.y; v.z += bv.z; v.w += bv.w;
-        }
+        float4 v = make_float4(acc[i][j][4 * g + 0] + bv[i][g].x, acc[i][j][4 * g + 1] + bv[i][g].y,
+                               acc[i][j][4 * g + 2] + bv[i][g].z, acc[i][j][4 * g + 3] + bv[i][g].w);
         if (EPI == TJK_EPI_BIAS_GELU) {
           v.x = gelu_erf(v.x); v.y = gelu_erf(v.y); v.z = gelu_erf(v.z); v.w = gelu_erf(v.w);
         }
-        if (EPI == TJK_EPI_BIAS_RESIDUAL) {
+        S* dst = st + l32 * E::PITCH + i * 32 + g * 8 + hi * 4;
+        if constexpr (EPI == TJK_EPI_BIAS_RESIDUAL)
+          *reinterpret_cast<float4*>(dst) = v;
+        else
+          *reinterpret_cast<typename Quad<T>::raw*>(dst) = Quad<T>::from(v);
+      }
+#pragma unroll
+    for (int r0 = 0; r0 < 32; r0 += RPI) {
+      const int rr = r0 + lane / LPR, cc = (lane % LPR) * E::SV;
+      const int m = mw + 32 * j + rr, n = nw + cc;
+      const uint4 piece = *reinterpret_cast<const uint4*>(st + rr * E::PITCH + cc);
+      if (m < M && n < N) {
+        if constexpr (EPI == TJK_EPI_BIAS_RESIDUAL) {
+          // fp32 pieces never straddle N (N % 4 == 0)
           float4* r = reinterpret_cast<float4*>(static_cast<float*>(Cv) + (int64_t)m * ldc + n);
+          const float4 a = __builtin_bit_cast(float4, piece);
           float4 o = *r;
-          o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
+          o.x += a.x; o.y += a.y; o.z += a.z; o.w += a.w;
           *r = o;
         } else {
           T* c = static_cast<T*>(Cv) + (int64_t)m * ldc + n;
-          *reinterpret_cast<typename Quad<T>::raw*>(c) = Quad<T>::from(v);
+          if (E::SV == 4 || (a16 && n + E::SV <= N)) {
+            *reinterpret_cast<uint4*>(c) = piece;
+          } else {  // 2-byte types: halves of 4 elements (N % 4 == 0)
+            *reinterpret_cast<uint2*>(c) = make_uint2(piece.x, piece.y);
+            if (n + 4 < N) *reinterpret_cast<uint2*>(c + 4) = make_uint2(piece.z, piece.w);
+          }
         }
       }
     }
@@ -191,7 +243,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
     __syncthreads();
   }
 
-  epilogue<T, EPI, FM, FN>(acc, bias, Cv, ldc, M, N, m0 + wm * WTM, n0 + wn * WTN, l32, hi);
+  // The loop ends on a barrier, so the operand tiles are dead: reuse LDS.
+  static_assert(NT / 64 * EpiStage<T, EPI, FN>::BYTES <= (int)sizeof(smem), "epilogue staging exceeds LDS");
+  epilogue<T, EPI, FM, FN>(acc, bias, Cv, ldc, M, N, m0 + wm * WTM, n0 + wn * WTN, lane,
+                           reinterpret_cast<char*>(&smem[0][0]) + wave * EpiStage<T, EPI, FN>::BYTES);
 }
 
 // ------------------------------------------------------- direct-to-LDS GEMM
@@ -363,7 +418,13 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_dtl_kernel(
     }
   }
 
-  epilogue<T, EPI, FM, FN>(acc, bias, Cv, ldc, M, N, m0 + wm * WTM, n0 + wn * WTN, l32, hi);
+  // Reuse LDS for the epilogue once every DMA (including the ones issued
+  // past the last tile) has landed and every wave is done reading.
+  static_assert(NW * EpiStage<T, EPI, FN>::BYTES <= STAGES * STAGE, "epilogue staging exceeds LDS");
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  epilogue<T, EPI, FM, FN>(acc, bias, Cv, ldc, M, N, m0 + wm * WTM, n0 + wn * WTN, lane,
+                           smem + wave * EpiStage<T, EPI, FN>::BYTES);
 }
 
 // ------------------------------------------------------------------ plans
