@@ -6,8 +6,11 @@ Prints ONE JSON line.  A "step" is one forward of the drop-in hook
 (``UserOptimizedTransformer``) over the workload's synthetic batch, inputs
 already resident in HBM; each step is bracketed by HIP events on torch's
 current stream (the harness's method, torch_transformer_benchmark.py:
-491-504) and ``value`` is the median step latency in ms.  TFLOP/s and % of
-the dense bf16 MFMA peak use the algorithmic FLOPs of the full padded S.
+491-504) and ``value`` is the median step latency in ms.  Prefix-padded tokens are not computed
+(the engine packs the valid tokens), so TFLOP/s and % of the dense bf16
+MFMA peak use the FLOPs of the work executed -- the valid tokens' GEMM rows
+and causal attention pairs; the full-padded-S figure is reported beside it
+as an equivalent rate, with the eager packed / unpacked latencies.
 
 Also reported:
 * ``roofline``: the dominant kernel (largest share of one eager forward,
@@ -63,12 +66,26 @@ def _time_steps(fn, steps, warmup):
     return [s.elapsed_time(e) for s, e in zip(starts, ends)], wall
 
 
-def _breakdown(engine, x, mask, plan):
+def _attn_flops(qkv, causal, cu_seqlens=None):
+    """Algorithmic attention FLOPs of one launch: 2*hd per (query, key) pair
+    for QK^T and again for PV, over the pairs it computes (causal: j <= i)."""
+    if cu_seqlens is not None:
+        h, hd = qkv.shape[2], qkv.shape[3]
+        lens = (cu_seqlens[1:] - cu_seqlens[:-1]).tolist()
+    else:
+        b, s, _, h, hd = qkv.shape
+        lens = [s] * b
+    pairs = sum(n * (n + 1) // 2 if causal else n * n for n in lens)
+    return 4.0 * h * hd * pairs
+
+
+def _breakdown(engine, x, mask):
     """Per-kernel-class time of one eager forward: each tjk launch bracketed
-    by HIP events on the current stream (the launch stream)."""
+    by HIP events on the current stream (the launch stream).  Also returns,
+    per class, the exact call of its last launch so it can be replayed."""
     import torch
     from tjkernels import ops
-    classes = {}
+    classes, calls = {}, {}
     orig = {name: getattr(ops, name) for name in ("gemm", "flash_attention", "add_layernorm")}
     events = []
 
@@ -87,8 +104,7 @@ def _breakdown(engine, x, mask, plan):
                     label = ("gemm_out" if w.shape[1] == d else "gemm_ffn2") + ("_residual" if epi == 2 else "")
                 flops = 2.0 * a0.shape[0] * w.shape[0] * w.shape[1]
             elif name == "flash_attention":
-                b, s, _, h, hd = a[0].shape
-                flops = 2.0 * b * h * hd * s * (s + 1) if k.get("causal", True) else 4.0 * b * h * hd * s * s
+                flops = _attn_flops(a[0], k.get("causal", True), k.get("cu_seqlens"))
             else:
                 flops = 0.0
             s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -96,15 +112,18 @@ def _breakdown(engine, x, mask, plan):
             r = fn(*a, **k)
             s1.record()
             events.append((label, flops, s0, s1))
+            calls[label] = (fn, a, k)
             return r
         return inner
 
+    mode, lens = engine._mask_info(mask)
+    packing = engine._packing(lens, x.shape[1]) if lens is not None else None
     for name, fn in orig.items():
         setattr(ops, name, wrap(name, fn))
     try:
         for _ in range(3):  # warm, then keep the last pass
             events.clear()
-            engine._forward_impl(x, mask, engine._mask_mode(mask))
+            engine._forward_impl(x, mask, mode, packing)
         torch.cuda.synchronize()
     finally:
         for name, fn in orig.items():
@@ -121,38 +140,21 @@ def _breakdown(engine, x, mask, plan):
         c["ms"] += s0.elapsed_time(s1)
         c["launches"] += 1
         c["flops"] += flops
-    return classes
+    return classes, calls
 
 
-def _kernel_avg_ms(label, engine, x, plan, reps=50):
-    """Average duration of one launch of the dominant kernel, HIP events on
-    its launch stream, over `reps` back-to-back launches."""
+def _kernel_avg_ms(call, reps=50):
+    """Average duration of one launch of a kernel class: its recorded call
+    replayed `reps` times back to back, HIP events on the launch stream."""
     import torch
-    from tjkernels import ops
-    ws = engine._workspace(x.shape[0], x.shape[1], plan)
-    lw = engine.layers[0]
-    b, s = x.shape[:2]
-    h, hd = engine.num_heads, engine.head_dim
-    if label == "gemm_ffn1_gelu":
-        fn = lambda: ops.gemm(ws.h, lw.w1, lw.b1, ws.mid, ops.EPI_BIAS_GELU, plan.gemm_ffn1)  # noqa: E731
-    elif label == "gemm_ffn2_residual":
-        fn = lambda: ops.gemm(ws.mid, lw.w2, lw.b2, ws.res, ops.EPI_BIAS_RESIDUAL, plan.gemm_ffn2)  # noqa: E731
-    elif label == "gemm_qkv":
-        fn = lambda: ops.gemm(ws.h, lw.wqkv, lw.bqkv, ws.qkv, ops.EPI_BIAS, plan.gemm_qkv)  # noqa: E731
-    elif label == "gemm_out_residual":
-        fn = lambda: ops.gemm(ws.ctx, lw.wo, lw.bo, ws.res, ops.EPI_BIAS_RESIDUAL, plan.gemm_out)  # noqa: E731
-    elif label == "flash_attention":
-        q5 = ws.qkv.view(b, s, 3, h, hd)
-        fn = lambda: ops.flash_attention(q5, ws.ctx, causal=engine.causal, plan=plan.attn_plan)  # noqa: E731
-    else:
-        return None
+    fn, a, k = call
     for _ in range(5):
-        fn()
+        fn(*a, **k)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
-        fn()
+        fn(*a, **k)
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / reps
@@ -215,7 +217,8 @@ def main() -> int:
 
     import torch
     from tjkernels import UserOptimizedTransformer
-    from tjkernels.workloads import WORKLOADS, flops_per_forward, make_inputs, make_state_dict
+    from tjkernels.workloads import (WORKLOADS, flops_per_forward, flops_valid_tokens, make_inputs,
+                                     make_state_dict)
 
     w = WORKLOADS[args.workload]
     dev = torch.device("cuda", 0)
@@ -231,19 +234,29 @@ def main() -> int:
         got = model(xd, md).cpu()
         engine = model._tj_engine
         plan = engine.plan
-        breakdown = {} if args.no_breakdown else _breakdown(engine, xd, md, plan)
+        breakdown, calls = ({}, {}) if args.no_breakdown else _breakdown(engine, xd, md)
+        # The same forward with every padded row computed (per-key mask
+        # attention, the reference's way), eager, for the packing gain.
+        from tjkernels.engine import MASK_GENERAL
+        eager_unpacked = statistics.median(_time_steps(
+            lambda: engine._forward_impl(xd, md, MASK_GENERAL), 20, 3)[0])
+        mode, lens = engine._mask_info(md)
+        pk = engine._packing(lens, w.seq) if lens is not None else None
+        eager_packed = statistics.median(_time_steps(
+            lambda: engine._forward_impl(xd, md, mode, pk), 20, 3)[0])
 
     flops = flops_per_forward(w)
+    flops_valid = flops_valid_tokens(w, lengths.tolist())
     med = statistics.median(samples)
     dtype_name = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}[plan.compute_dtype]
     peak = PEAK_TFLOPS[dtype_name]
-    tflops = flops / (med * 1e-3) / 1e12
+    tflops = flops_valid / (med * 1e-3) / 1e12
 
     roofline = None
     if breakdown:
         dom = max((k for k in breakdown if breakdown[k]["flops"] > 0), key=lambda k: breakdown[k]["ms"])
         with torch.inference_mode():
-            avg_ms = _kernel_avg_ms(dom, engine, xd, plan)
+            avg_ms = _kernel_avg_ms(calls[dom])
         per_launch = breakdown[dom]["flops"] / breakdown[dom]["launches"]
         achieved = per_launch / (avg_ms * 1e-3) / 1e12
         roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 1), "peak": peak,
@@ -267,8 +280,18 @@ def main() -> int:
         "config": {"workload": w.describe(), "tokens": w.tokens, "plan": plan.label,
                    "hipgraph": plan.cuda_graph, "residual_epilogue": plan.residual_epilogue},
         "p90_ms": round(_percentile(samples, 0.9), 4), "min_ms": round(min(samples), 4),
-        "wall_s": round(wall, 3), "tflops": round(tflops, 1),
-        "pct_peak": round(100 * tflops / peak, 2), "gflop_per_forward": round(flops / 1e9, 2),
+        "wall_s": round(wall, 3),
+        # MFMA rate on the work actually executed: valid-token FLOPs (padded
+        # rows are not computed; see "packing").
+        "tflops": round(tflops, 1), "pct_peak": round(100 * tflops / peak, 2),
+        "gflop_executed": round(flops_valid / 1e9, 2),
+        # The full-padded-S formula (every padded row counted, as if computed):
+        # an equivalent rate, not an MFMA utilisation.
+        "gflop_per_forward_padded": round(flops / 1e9, 2),
+        "tflops_padded_equiv": round(flops / (med * 1e-3) / 1e12, 1),
+        "packing": {"lengths": lengths.tolist(), "valid_token_frac": round(sum(lengths.tolist()) / w.tokens, 4),
+                    "eager_packed_ms": round(eager_packed, 4),
+                    "eager_unpacked_ms": round(eager_unpacked, 4)},
         "roofline": roofline, "cpu_baseline": cpu, "accuracy": acc, "breakdown": breakdown,
     }
     print(json.dumps(line))

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define TJK_ABI_VERSION 1
+#define TJK_ABI_VERSION 2
 
 /* dtypes */
 #define TJK_F32 0
@@ -66,6 +66,10 @@ const char* tjk_last_error_string(void);
  *   out = (x - mean) * rsqrt(var + eps) * gamma + beta, biased variance,
  *         written in out_dtype; rows whose row_mask byte is 0 are written as 0
  *         (row_mask may be NULL, indexed by row).
+ * row_index (may be NULL) makes the call a gather / scatter over `rows`
+ * output rows: output row r reads res / delta row row_index[r]; a negative
+ * index writes an all-zero output row and leaves res_out's row untouched.
+ * res_out must not alias res when row_index is given.
  * res_dtype, delta_dtype, out_dtype in {TJK_F32, TJK_F16, TJK_BF16};
  * delta may be NULL.  Requires n % 4 == 0, n <= 8192, 8-byte aligned rows.
  */
@@ -75,7 +79,7 @@ int tjk_add_layernorm(const void* res, int res_dtype, int64_t ld_res,
                       void* out, int out_dtype, int64_t ld_out,
                       const float* gamma, const float* beta,
                       int64_t rows, int64_t n, float eps,
-                      const uint8_t* row_mask, void* stream);
+                      const int32_t* row_index, const uint8_t* row_mask, void* stream);
 
 /*
  * C[m, n] = epilogue(sum_k A[m, k] * W[n, k] + bias[n]) -- W in nn.Linear
@@ -103,6 +107,12 @@ int tjk_gemm_plan_info(int dtype, int id, int* block_m, int* block_n, int* waves
  *   causal     keys j > query i are excluded
  *   lengths    if non-NULL, keys j >= lengths[b] are excluded
  *   key_mask   if non-NULL ([B, S] bytes), keys with a 0 byte are excluded
+ *   cu_seqlens if non-NULL ([B + 1] int32, non-decreasing, cu_seqlens[0] = 0,
+ *              every cu_seqlens[b+1] - cu_seqlens[b] <= seq): packed
+ *              sequences; sequence b is rows cu_seqlens[b] .. cu_seqlens[b+1]-1
+ *              of both the QKV buffer (row stride stride_s; stride_b unused)
+ *              and `out`; only its own rows are read or written.  Exclusive
+ *              with key_mask.
  * A query row with no admissible key is written as 0.
  * head_dim in [1, 128], head_dim % 8 == 0 (16-byte aligned rows).
  */
@@ -111,7 +121,7 @@ int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s,
                   void* out, int64_t ld_out,
                   int batch, int seq, int heads, int head_dim, float scale,
                   int causal, const int32_t* lengths, const uint8_t* key_mask,
-                  int dtype, int plan_id, void* stream);
+                  const int32_t* cu_seqlens, int dtype, int plan_id, void* stream);
 
 /* Number of attention plans for `dtype`. */
 int tjk_flash_plan_count(int dtype);

@@ -149,6 +149,36 @@ def test_gemm_epilogues(device, epi, dt):
     _gemm_case(device, 200, 388, 96, dt, epi, -1)
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_gemm_gelu_accuracy_sweep(device, dt):
+    """The GELU epilogue over v in [-12, 12] (plus 0 and tiny values), each
+    value passed through the GEMM exactly (A = e_0, W[n, 0] = v_n), against
+    0.5 v (1 + erf(v / sqrt 2)) in fp64 (math.erf): within 8e-7 absolute plus
+    two fp32 ulps for fp32, one output rounding for bf16."""
+    vals = torch.cat([torch.linspace(-12, 12, 4001), torch.tensor([0.0, 1e-6, -1e-6, 1e-30, -3.5, 3.5])])
+    n = (vals.numel() + 3) // 4 * 4
+    v = torch.zeros(n)
+    v[:vals.numel()] = vals
+    v = v.to(dt)  # the values the GEMM sees
+    a = torch.zeros(64, 64, dtype=dt)
+    a[:, 0] = 1
+    w = torch.zeros(n, 64, dtype=dt)
+    w[:, 0] = v
+    out = torch.empty(64, n, dtype=dt, device=device)
+    ops.gemm(a.to(device), w.to(device), None, out, ops.EPI_BIAS_GELU)
+    torch.cuda.synchronize()
+    x = v.double()
+    ref = torch.tensor([0.5 * t * (1 + math.erf(t / math.sqrt(2))) for t in x.tolist()], dtype=torch.float64)
+    got = out[0].cpu().double()
+    if dt == torch.float32:
+        bound = 8e-7 + 2.4e-7 * ref.abs()
+    else:
+        bound = 8e-7 + 2 ** -8 * ref.abs()
+    err = (got - ref).abs()
+    assert bool((err <= bound).all()), f"max err {float(err.max()):.3e} at v={float(x[err.argmax()]):.4f}"
+    assert torch.equal(out[1:].cpu(), out[:1].cpu().expand(63, n))
+
+
 def test_gemm_headline_shapes(device):
     # the four C4 projections at full size, against fp64 on the CPU
     for (m, n, k) in [(8192, 3072, 1024), (8192, 1024, 1024), (8192, 4096, 1024), (8192, 1024, 4096)]:
@@ -162,6 +192,44 @@ def test_gemm_zero_weight_gives_bias(device):
     out = torch.empty(64, 256, device=device, dtype=torch.bfloat16)
     ops.gemm(a, w, b, out)
     assert torch.equal(out, b.expand(64, 256))
+
+
+@pytest.mark.parametrize("out_dt", ["bf16", "f32"])
+def test_add_layernorm_gather_scatter(device, out_dt):
+    """row_index: output row r is LN(res[row_index[r]]), zeros where the index
+    is negative -- the packing (gather) and unpacking (scatter) of prefix
+    masked tokens."""
+    n, rows = 768, 40
+    g = _gen(5)
+    x = (torch.randn(rows, n, generator=g) * 2).to(torch.bfloat16)
+    gamma, beta = torch.randn(n, generator=g), torch.randn(n, generator=g)
+    ref_all = oracle.layer_norm(x.double(), gamma.double(), beta.double(), 1e-5)
+    gather = torch.tensor([3, 4, 5, 17, 0, 39, 38, 20, 21], dtype=torch.int32)
+    out = torch.full((gather.numel(), n), float("nan"), dtype=DT[out_dt], device=device)
+    res_out = torch.full((gather.numel(), n), float("nan"), dtype=torch.float32, device=device)
+    ops.add_layernorm(x.to(device), None, gamma.to(device), beta.to(device), 1e-5, out,
+                      res_out=res_out, row_index=gather.to(device))
+    torch.cuda.synchronize()
+    assert torch.equal(res_out.cpu(), x.float()[gather.long()])
+    _close(out, ref_all[gather.long()], OUT_RTOL[DT[out_dt]], 1e-5 if out_dt == "f32" else 4e-3)
+    # scatter: 12 output rows from 5 packed rows, holes are exact zeros
+    packed = res_out[:5].contiguous()
+    scatter = torch.tensor([-1, 0, 1, -1, -1, 2, 3, 4, -1, -1, -1, -1], dtype=torch.int32)
+    out2 = torch.full((scatter.numel(), n), float("nan"), dtype=DT[out_dt], device=device)
+    ops.add_layernorm(packed, None, gamma.to(device), beta.to(device), 1e-5, out2,
+                      row_index=scatter.to(device))
+    torch.cuda.synchronize()
+    got = out2.cpu()
+    hole = scatter < 0
+    assert (got[hole] == 0).all()
+    src = gather[:5].long()[scatter[~hole].long()]
+    _close(got[~hole], ref_all[src], OUT_RTOL[DT[out_dt]], 1e-5 if out_dt == "f32" else 4e-3)
+    # an in-place residual update cannot be a gather
+    with pytest.raises(ops.TjkError):
+        r = torch.zeros(8, n, device=device)
+        ops.add_layernorm(r, None, gamma.to(device), beta.to(device), 1e-5,
+                          torch.empty(8, n, device=device), res_out=r,
+                          row_index=torch.arange(8, dtype=torch.int32, device=device))
 
 
 # ------------------------------------------------------------------ attention
@@ -188,7 +256,7 @@ def test_flash_shapes(device, dt, hd, seq, causal):
     g = _gen(hd * 1000 + seq)
     qkv = torch.randn(b, seq, 3, h, hd, generator=g).to(dt)
     ref = _attn_ref(qkv, causal)
-    for plan in (0, 1, 2):
+    for plan in (0, 1, 2, 3):
         out = torch.full((b * seq, h * hd), float("nan"), dtype=dt, device=device)
         ops.flash_attention(qkv.to(device), out, causal=causal, plan=plan)
         torch.cuda.synchronize()
@@ -205,7 +273,7 @@ def test_flash_key_mask_and_lengths(device, dt):
     key_mask[:, 0] = True
     for causal in (True, False):
         ref = _attn_ref(qkv, causal, key_mask)
-        for plan in (0, 1):
+        for plan in (0, 1, 3):
             out = torch.empty(b * s, h * hd, dtype=dt, device=device)
             ops.flash_attention(qkv.to(device), out, causal=causal, key_mask=key_mask.to(device), plan=plan)
             torch.cuda.synchronize()
@@ -213,7 +281,7 @@ def test_flash_key_mask_and_lengths(device, dt):
     lengths = torch.tensor([150, 1, 77], dtype=torch.int32)
     pm = torch.arange(s)[None, :] < lengths[:, None].long()
     ref = _attn_ref(qkv, False, pm)
-    for plan in (0, 1):
+    for plan in (0, 1, 3):
         out = torch.empty(b * s, h * hd, dtype=dt, device=device)
         ops.flash_attention(qkv.to(device), out, causal=False, lengths=lengths.to(device), plan=plan)
         torch.cuda.synchronize()
@@ -248,8 +316,40 @@ def test_flash_packed_layout_headline(device):
     ref = _attn_ref(q5[:1].cpu(), True).view(s, h * hd)
     got = out.view(b, s, h * hd)[0].cpu()
     _close(got[sel], ref[sel], 1e-2, 1e-2)
-    # the pipelined and the plain kernel agree on every row
-    out1 = torch.empty_like(out)
-    ops.flash_attention(q5, out1, causal=True, plan=1)
-    torch.cuda.synchronize()
-    assert (out.float() - out1.float()).abs().max().item() < 2e-2
+    # every plan agrees on every row
+    for plan in (0, 1, 2, 3):
+        out1 = torch.empty_like(out)
+        ops.flash_attention(q5, out1, causal=True, plan=plan)
+        torch.cuda.synchronize()
+        assert (out.float() - out1.float()).abs().max().item() < 2e-2
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("hd", [64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_packed_sequences(device, dt, hd, causal):
+    """cu_seqlens: B sequences of different lengths back to back; each must
+    equal the fp64 brute force over its own rows, and no other row of the
+    output may be touched."""
+    lengths = [130, 0, 1, 257, 64]
+    h, max_len = 2, 300
+    cu = [0]
+    for n in lengths:
+        cu.append(cu[-1] + n)
+    t = cu[-1]
+    g = _gen(hd + (0 if causal else 1))
+    qkv = torch.randn(t, 3, h, hd, generator=g).to(dt)
+    tol = 1e-5 if dt == torch.float32 else 1e-2
+    cu_d = torch.tensor(cu, dtype=torch.int32, device=device)
+    for plan in (0, 1, 2, 3):
+        out = torch.full((t + 7, h * hd), 7.0, dtype=dt, device=device)
+        ops.flash_attention(qkv.to(device), out, causal=causal, plan=plan,
+                            cu_seqlens=cu_d, max_seqlen=max_len)
+        torch.cuda.synchronize()
+        got = out.cpu()
+        for b, n in enumerate(lengths):
+            if n == 0:
+                continue
+            ref = _attn_ref(qkv[cu[b]:cu[b + 1]].unsqueeze(0), causal)
+            _close(got[cu[b]:cu[b + 1]], ref, tol, tol)
+        assert (got[t:] == 7.0).all(), "rows past the packed tokens were written"

@@ -210,3 +210,36 @@ def test_deferred_residual_plan_matches(device):
     w = WORKLOADS["C3"]
     _run_workload(device, "C3", plan=Plan(compute_dtype=w.dtype, residual_epilogue=False,
                                           cuda_graph=False, label="deferred"))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_packed_forward_matches_unpacked(device, causal):
+    """Prefix masks run packed (only the valid rows through every GEMM and
+    LayerNorm, varlen attention); the valid rows must equal the unpacked
+    forward that computes every row with a per-key mask (the reference's
+    way, tjkernels/engine.py:184-203,267-268), and a zero-length sequence
+    comes out as all-zero rows."""
+    from tjkernels.engine import MASK_GENERAL
+    cfg = TransformerConfig(4, 80, 128, 4, 256, 2, causal)
+    torch.manual_seed(2)
+    sd = {k: v.float() for k, v in UserOptimizedTransformer(cfg).state_dict().items()}
+    model = _module(cfg, sd, torch.float32, device)
+    lengths = torch.tensor([80, 0, 33, 1], dtype=torch.int32)
+    mask = torch.arange(80)[None, :] < lengths[:, None].long()
+    g = torch.Generator()
+    g.manual_seed(9)
+    x = torch.randn(4, 80, 128, generator=g).masked_fill(~mask[..., None], 0)
+    plans_mod.set_override(Plan(compute_dtype=torch.float32, cuda_graph=False, label="eager"))
+    try:
+        with torch.inference_mode():
+            packed = model(x.to(device), lengths.to(device)).cpu()
+            eng = model._tj_engine
+            unpacked = eng._forward_impl(x.to(device), mask.to(device), MASK_GENERAL).cpu()
+    finally:
+        plans_mod.set_override(None)
+    assert (packed[~mask] == 0).all() and (unpacked[~mask] == 0).all()
+    diff = (packed[mask] - unpacked[mask]).abs().max().item()
+    assert diff <= 1e-5, f"packed vs unpacked valid rows differ by {diff:.3e}"
+    keep = lengths > 0
+    ref = oracle.forward(sd, x[keep], mask[keep], cfg.num_heads, causal, torch.float32)
+    _check(packed[keep], ref, mask[keep], torch.float32)

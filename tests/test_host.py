@@ -35,9 +35,9 @@ def test_abi_rejects_bad_arguments_without_launching():
     assert lib.tjk_gemm_bias(None, 8, None, 8, None, None, 8, 4, 4, 8, _lib.BF16, 0, -1, None) < 0
     assert b"null" in lib.tjk_last_error_string()
     assert lib.tjk_flash_fwd(None, 0, 0, 0, 0, None, 0, 1, 4, 1, 12, 0.5, 1, None, None,
-                             _lib.BF16, -1, None) < 0
+                             None, _lib.BF16, -1, None) < 0
     assert lib.tjk_add_layernorm(None, 0, 8, None, 0, 0, None, 0, None, 0, 8, None, None,
-                                 2, 6, 1e-5, None, None) < 0
+                                 2, 6, 1e-5, None, None, None) < 0
     assert b"null pointer" in lib.tjk_last_error_string()
     # empty work is a successful no-op
     assert lib.tjk_gemm_bias(None, 8, None, 8, None, None, 8, 0, 4, 8, _lib.BF16, 0, -1, None) == 0
@@ -137,11 +137,35 @@ def test_mask_classification():
     general = prefix.clone()
     general[0, 1] = False
     assert eng._mask_mode(general) == MASK_GENERAL
-    # memoised on identity
-    assert eng._mask_modes.get(prefix) == MASK_PREFIX
+    # memoised on identity, with the prefix lengths read once
+    assert eng._mask_modes.get(prefix) == (MASK_PREFIX, (3, 6))
+    assert eng._mask_info(prefix) == (MASK_PREFIX, (3, 6))
+    # packing is exact without causal attention too (padded keys are excluded
+    # by restricting each packed sequence to its own rows)
     cfg_nc = TransformerConfig(2, 6, 32, 4, 64, 1, False)
     eng_nc = Engine(UserOptimizedTransformer(cfg_nc))
-    assert eng_nc._mask_mode(prefix) == MASK_GENERAL  # no causal: keys must be masked
+    assert eng_nc._mask_info(prefix) == (MASK_PREFIX, (3, 6))
+    assert eng_nc._mask_mode(general) == MASK_GENERAL
+
+
+def test_packing_row_maps():
+    """gather / scatter / cu_seqlens of the packed layout, against a
+    brute-force enumeration of the valid (b, s) positions."""
+    from tjkernels.engine import build_packing
+    lengths, seq = (3, 0, 5, 1), 5
+    pk = build_packing(lengths, seq, torch.device("cpu"))
+    valid = [(b, s) for b in range(len(lengths)) for s in range(seq) if s < lengths[b]]
+    assert pk.tokens == len(valid) == 9
+    assert pk.gather.tolist() == [b * seq + s for b, s in valid]
+    assert pk.cu_seqlens.tolist() == [0, 3, 3, 8, 9]
+    expect = [-1] * (len(lengths) * seq)
+    for r, (b, s) in enumerate(valid):
+        expect[b * seq + s] = r
+    assert pk.scatter.tolist() == expect
+    # scatter inverts gather on the valid rows
+    assert all(pk.scatter[g].item() == r for r, g in enumerate(pk.gather.tolist()))
+    empty = build_packing((0, 0), 4, torch.device("cpu"))
+    assert empty.tokens == 0 and empty.gather.numel() == 0 and (empty.scatter == -1).all()
 
 
 def test_graph_capture_failure_degrades_to_eager(capsys):
@@ -181,3 +205,18 @@ def test_tj_disable_calls_parent_forward(monkeypatch):
     monkeypatch.setenv("TJ_DISABLE", "1")
     h = Hook(TransformerConfig(1, 2, 4, 1, 4, 1, True))
     assert torch.equal(h(torch.zeros(1, 2, 4)), torch.ones(1, 2, 4))
+
+
+def test_valid_token_flops():
+    """The executed-work FLOP count reduces to the padded-S formula at full
+    lengths and counts each sequence's own pairs otherwise (hand count)."""
+    from tjkernels.workloads import WORKLOADS, flops_per_forward, flops_valid_tokens
+    for name in ("C2", "C4", "C5"):
+        w = WORKLOADS[name]
+        assert flops_valid_tokens(w, [w.seq] * w.batch) == flops_per_forward(w)
+    w = WORKLOADS["C4"]
+    d, f, L = w.d_model, w.ffn_dim, w.layers
+    lens = [3, 1]
+    gemm = (6 + 2) * 4 * d * d + 4 * 4 * d * f          # 4 valid rows
+    attn = 4 * d * (6 + 1)                              # 3*4/2 + 1*2/2 causal pairs
+    assert flops_valid_tokens(w, lens) == L * (gemm + attn)

@@ -7,6 +7,9 @@
 // tjkernels/kernels/attention.py:34-125 (launcher :189-226) and, through
 // the `lengths` / `key_mask` arguments, the SDPA fallback used for padded
 // non-causal and general masks (tjkernels/engine.py:184-203,216-228).
+// With `cu_seqlens` the sequences are packed back to back (varlen): batch b
+// owns rows cu_seqlens[b] .. cu_seqlens[b+1]-1 of the QKV and output
+// buffers, and workgroups past the end of their sequence exit at once.
 //
 // CDNA4 mapping.  A workgroup is 4 waves; each wave owns NQ blocks of 32
 // queries.  Both products are computed transposed so that every per-query
@@ -65,13 +68,14 @@ template <> struct PairPack<float> {
   }
 };
 
-template <typename T, int HDP, int NQ, bool KEYMASK>
-__global__ __launch_bounds__(256) void flash_fwd_kernel(
+template <typename T, int HDP, int NQ, int KS, bool KEYMASK>
+__global__ __launch_bounds__(256 * KS) void flash_fwd_kernel(
     const T* __restrict__ qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh,
     T* __restrict__ out, int64_t ld_out, int B, int S, int H, int hd, float scale_log2,
-    int causal, const int32_t* __restrict__ lengths, const uint8_t* __restrict__ key_mask, int nqb) {
-  constexpr int NW = 4;
-  constexpr int BMQ = NW * NQ * 32;     // queries per workgroup
+    int causal, const int32_t* __restrict__ lengths, const uint8_t* __restrict__ key_mask,
+    const int32_t* __restrict__ cu_seqlens, int nqb) {
+  constexpr int NQW = 4;                // waves per key split (one query group each)
+  constexpr int BMQ = NQW * NQ * 32;    // queries per workgroup
   constexpr int BNK = 64;               // keys per tile
   constexpr int VEC = 16 / sizeof(T);   // elements per 16-byte chunk
   constexpr int LDK = HDP + VEC;        // K tile row pitch (elements)
@@ -83,8 +87,8 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(
   constexpr int VITEMS = (BNK / 2) * CH;  // (key pair, chunk) items per tile
   static_assert(KITEMS % 256 == 0, "K tile must split evenly over 256 threads");
 
-  __shared__ __attribute__((aligned(16))) T sK[2][BNK * LDK];
-  __shared__ __attribute__((aligned(16))) T sV[2][HDP * LDV];
+  __shared__ __attribute__((aligned(16))) T sK[2][KS][BNK * LDK];
+  __shared__ __attribute__((aligned(16))) T sV[2][KS][HDP * LDV];
 
   const int BH = B * H;
   const int rank = blockIdx.x / BH, bh = blockIdx.x % BH;
@@ -92,18 +96,33 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(
   const int b = bh / H, h = bh % H;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
+  // Key split: waves qw and qw + NQW*p share query group qw; split p takes
+  // key tiles p, p + KS, p + 2 KS, ...; the ltid-th thread of each split
+  // stages that split's tiles.
+  const int qw = wave % NQW, par = wave / NQW, ltid = tid & 255;
 
-  const T* qbase = qkv + (int64_t)b * sb + (int64_t)h * sh;
+  // Sequence b: its tokens are rows row0 .. row0 + Sb - 1 (packed varlen
+  // layout when cu_seqlens is given, else b*S .. b*S + S - 1).
+  int Sb = S;
+  int64_t row0 = (int64_t)b * S, boff = (int64_t)b * sb;
+  if (cu_seqlens != nullptr) {
+    row0 = cu_seqlens[b];
+    Sb = cu_seqlens[b + 1] - cu_seqlens[b];
+    boff = row0 * ss;
+  }
+  const T* qbase = qkv + boff + (int64_t)h * sh;
   const T* kbase = qbase + sc;
   const T* vbase = qbase + 2 * sc;
 
-  int kv_len = S;
+  int kv_len = Sb;
   if (lengths != nullptr) kv_len = min(kv_len, max(lengths[b], 0));
   const int q0 = qb * BMQ;
-  const int wq0 = q0 + wave * NQ * 32;
-  int kend = causal ? min(q0 + BMQ, S) : S;
+  const int wq0 = q0 + qw * NQ * 32;
+  if (q0 >= Sb) return;  // the whole workgroup: past this sequence's end
+  int kend = causal ? min(q0 + BMQ, Sb) : Sb;
   kend = min(kend, kv_len);
   const int nkt = (kend + BNK - 1) / BNK;
+  const int nit = (nkt + KS - 1) / KS;  // iterations of KS tiles
 
   // ---- Q fragments (B operand of S^T): lane holds Q[q][16c + 8*hi + 0..7]
   typename Mfma<T>::frag qf[NQ][KC];
@@ -113,7 +132,7 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
       const int col = 16 * c + 8 * hi;
-      if (q < S && col < hd) {
+      if (q < Sb && col < hd) {
         qf[j][c] = Mfma<T>::load(qbase + (int64_t)q * ss + col);
       } else {
         float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -126,39 +145,39 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(
   constexpr int KPT = KITEMS / 256;
   constexpr int VPT = (VITEMS + 255) / 256;
   uint4 rk[KPT], rv0[VPT], rv1[VPT];
-  auto load_kv = [&](int kt) {
-    const int k0 = kt * BNK;
+  auto load_kv = [&](int it) {
+    const int k0 = (it * KS + par) * BNK;
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
-      const int it = tid + i * 256, key = it / CH, c = it % CH;
+      const int it = ltid + i * 256, key = it / CH, c = it % CH;
       const int gk = k0 + key, col = c * VEC;
-      rk[i] = (gk < S && col < hd) ? *reinterpret_cast<const uint4*>(kbase + (int64_t)gk * ss + col)
+      rk[i] = (gk < Sb && col < hd) ? *reinterpret_cast<const uint4*>(kbase + (int64_t)gk * ss + col)
                                   : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
-      const int it = tid + i * 256;
+      const int it = ltid + i * 256;
       const int p = it % (BNK / 2), c = it / (BNK / 2);
       const int gk = k0 + 2 * p, col = c * VEC;
       const bool ok = it < VITEMS && col < hd;
-      rv0[i] = (ok && gk < S) ? *reinterpret_cast<const uint4*>(vbase + (int64_t)gk * ss + col)
+      rv0[i] = (ok && gk < Sb) ? *reinterpret_cast<const uint4*>(vbase + (int64_t)gk * ss + col)
                               : make_uint4(0, 0, 0, 0);
-      rv1[i] = (ok && gk + 1 < S) ? *reinterpret_cast<const uint4*>(vbase + (int64_t)(gk + 1) * ss + col)
+      rv1[i] = (ok && gk + 1 < Sb) ? *reinterpret_cast<const uint4*>(vbase + (int64_t)(gk + 1) * ss + col)
                                   : make_uint4(0, 0, 0, 0);
     }
   };
   auto store_kv = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
-      const int it = tid + i * 256, key = it / CH, c = it % CH;
-      *reinterpret_cast<uint4*>(&sK[buf][key * LDK + c * VEC]) = rk[i];
+      const int it = ltid + i * 256, key = it / CH, c = it % CH;
+      *reinterpret_cast<uint4*>(&sK[buf][par][key * LDK + c * VEC]) = rk[i];
     }
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
-      const int it = tid + i * 256;
+      const int it = ltid + i * 256;
       if (it < VITEMS) {
         const int p = it % (BNK / 2), c = it / (BNK / 2);
-        PairPack<T>::write(&sV[buf][(c * VEC) * LDV + 2 * p], LDV, rv0[i], rv1[i]);
+        PairPack<T>::write(&sV[buf][par][(c * VEC) * LDV + 2 * p], LDV, rv0[i], rv1[i]);
       }
     }
   };
@@ -175,18 +194,19 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(
       for (int r = 0; r < 16; ++r) o[j][hb][r] = 0.f;
   }
 
-  if (nkt > 0) {
+  if (nit > 0) {
     load_kv(0);
     store_kv(0);
   }
   __syncthreads();
 
   const int krow = swap_bits_2_3(l32);  // K row this lane feeds into S^T
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nkt) load_kv(kt + 1);
+  for (int itr = 0; itr < nit; ++itr) {
+    const int cur = itr & 1;
+    if (itr + 1 < nit) load_kv(itr + 1);
+    const int kt = itr * KS + par;
     const int k0 = kt * BNK;
-    const bool wave_active = !causal || k0 <= wq0 + NQ * 32 - 1;
+    const bool wave_active = kt < nkt && (!causal || k0 <= wq0 + NQ * 32 - 1);
     if (wave_active) {
       // ---- S^T = K Q^T for two 32-key blocks
       f32x16 s[NQ][2];
@@ -198,7 +218,7 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(
           for (int r = 0; r < 16; ++r) s[j][kb][r] = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const T* kp = &sK[cur][(kb * 32 + krow) * LDK + 8 * hi];
+        const T* kp = &sK[cur][par][(kb * 32 + krow) * LDK + 8 * hi];
 #pragma unroll
         for (int c = 0; c < KC; ++c) {
           const typename Mfma<T>::frag kf = Mfma<T>::load(kp + 16 * c);
@@ -276,7 +296,7 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(
       // ---- O^T += V^T P^T: 16-key step st covers keys 16*st + 8*hi + 0..7
 #pragma unroll
       for (int hb = 0; hb < HB; ++hb) {
-        const T* vp = &sV[cur][(hb * 32 + l32) * LDV + 8 * hi];
+        const T* vp = &sV[cur][par][(hb * 32 + l32) * LDV + 8 * hi];
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
           const typename Mfma<T>::frag vf = Mfma<T>::load(vp + 16 * st);
@@ -285,8 +305,50 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(
         }
       }
     }
-    if (kt + 1 < nkt) store_kv(cur ^ 1);
+    if (itr + 1 < nit) store_kv(cur ^ 1);
     __syncthreads();
+  }
+
+  // ---- merge the key splits: split p > 0 leaves its running max, partial
+  // sums and O^T in LDS (the tiles are dead after the loop's last barrier);
+  // split 0 rescales both to the common max and adds.
+  if constexpr (KS > 1) {
+    constexpr int OW = NQ * HB * 16 * 64;  // O^T floats per wave
+    constexpr int SW = OW + 2 * NQ * 64;   // + running max and sum
+    static_assert(NQW * (KS - 1) * SW * 4 <= (int)sizeof(sK), "split merge exceeds the K tiles' LDS");
+    float* xo = reinterpret_cast<float*>(&sK[0][0][0]);
+    if (par > 0) {
+      float* my = xo + ((par - 1) * NQW + qw) * SW;
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) {
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) my[((j * HB + hb) * 16 + r) * 64 + lane] = o[j][hb][r];
+        my[OW + j * 64 + lane] = m_run[j];
+        my[OW + NQ * 64 + j * 64 + lane] = l_run[j];
+      }
+    }
+    __syncthreads();
+    if (par > 0) return;
+#pragma unroll
+    for (int p = 1; p < KS; ++p) {
+      const float* ot = xo + ((p - 1) * NQW + qw) * SW;
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) {
+        const float m2 = ot[OW + j * 64 + lane], l2 = ot[OW + NQ * 64 + j * 64 + lane];
+        const float m = fmaxf(m_run[j], m2);
+        const float a1 = m_run[j] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_run[j] - m) * scale_log2);
+        const float a2 = m2 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m2 - m) * scale_log2);
+        l_run[j] = l_run[j] * a1 + l2 * a2;
+        m_run[j] = m;
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            o[j][hb][r] = o[j][hb][r] * a1 + ot[((j * HB + hb) * 16 + r) * 64 + lane] * a2;
+      }
+    }
   }
 
   // ---- normalise and store: register r of block hb is hd row hb*32 + 8*(r/4) + 4*hi + r%4
@@ -295,8 +357,8 @@ __global__ __launch_bounds__(256) void flash_fwd_kernel(
     const int q = wq0 + j * 32 + l32;
     const float l = l_run[j] + __shfl_xor(l_run[j], 32, 64);
     const float inv = l > 0.f ? 1.0f / l : 0.f;
-    if (q >= S) continue;
-    T* orow = out + ((int64_t)b * S + q) * ld_out + (int64_t)h * hd;
+    if (q >= Sb) continue;
+    T* orow = out + (row0 + q) * ld_out + (int64_t)h * hd;
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb)
 #pragma unroll
@@ -332,7 +394,8 @@ template <typename T, int HDP, bool KEYMASK>
 __global__ __launch_bounds__(256) void flash_pipe_kernel(
     const T* __restrict__ qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh,
     T* __restrict__ out, int64_t ld_out, int B, int S, int H, int hd, float scale_log2,
-    int causal, const int32_t* __restrict__ lengths, const uint8_t* __restrict__ key_mask, int nqb) {
+    int causal, const int32_t* __restrict__ lengths, const uint8_t* __restrict__ key_mask,
+    const int32_t* __restrict__ cu_seqlens, int nqb) {
   static_assert(sizeof(T) == 2, "2-byte element types only");
   constexpr int BMQ = 128, BNK = 64, NST = 3, VEC = 8;
   constexpr int LDK = HDP + VEC, LDV = BNK + VEC;
@@ -351,12 +414,22 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
 
-  const T* qbase = qkv + (int64_t)b * sb + (int64_t)h * sh;
-  int kv_len = S;
+  // Sequence b: its tokens are rows row0 .. row0 + Sb - 1 (packed varlen
+  // layout when cu_seqlens is given, else b*S .. b*S + S - 1).
+  int Sb = S;
+  int64_t row0 = (int64_t)b * S, boff = (int64_t)b * sb;
+  if (cu_seqlens != nullptr) {
+    row0 = cu_seqlens[b];
+    Sb = cu_seqlens[b + 1] - cu_seqlens[b];
+    boff = row0 * ss;
+  }
+  const T* qbase = qkv + boff + (int64_t)h * sh;
+  int kv_len = Sb;
   if (lengths != nullptr) kv_len = min(kv_len, max(lengths[b], 0));
   const int q0 = qb * BMQ;
   const int wq0 = q0 + wave * 32;
-  int kend = causal ? min(q0 + BMQ, S) : S;
+  if (q0 >= Sb) return;  // the whole workgroup: past this sequence's end
+  int kend = causal ? min(q0 + BMQ, Sb) : Sb;
   kend = min(kend, kv_len);
   const int nkt = (kend + BNK - 1) / BNK;
 
@@ -367,7 +440,7 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
       const int col = 16 * c + 8 * hi;
-      if (q < S && col < hd) {
+      if (q < Sb && col < hd) {
         qf[c] = Mfma<T>::load(qbase + (int64_t)q * ss + col);
       } else {
         float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -376,9 +449,9 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
     }
   }
 
-  // K / V rows of this (b, h) through buffer descriptors ending at key S-1.
+  // K / V rows of this (b, h) through buffer descriptors ending at key Sb-1.
   const uint32_t row_bytes = (uint32_t)(ss * (int64_t)sizeof(T));
-  const int span = (int)(((int64_t)(S - 1) * ss + hd) * (int64_t)sizeof(T));
+  const int span = (int)(((int64_t)(Sb - 1) * ss + hd) * (int64_t)sizeof(T));
   const __amdgpu_buffer_rsrc_t rsk = __builtin_amdgcn_make_buffer_rsrc((void*)(qbase + sc), (short)0, span, 0x00020000);
   const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc((void*)(qbase + 2 * sc), (short)0, span, 0x00020000);
   uint4 rk[KPT], rv0[VPT], rv1[VPT];
@@ -563,8 +636,8 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
   const int q = wq0 + l32;
   const float l = l_run + __shfl_xor(l_run, 32, 64);
   const float inv = l > 0.f ? 1.0f / l : 0.f;
-  if (q < S) {
-    T* orow = out + ((int64_t)b * S + q) * ld_out + (int64_t)h * hd;
+  if (q < Sb) {
+    T* orow = out + (row0 + q) * ld_out + (int64_t)h * hd;
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb)
 #pragma unroll
@@ -582,66 +655,76 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
 template <typename T, int HDP>
 static int launch_pipe(const void* qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh, void* out,
                        int64_t ld_out, int B, int S, int H, int hd, float scale_log2, int causal,
-                       const int32_t* lengths, const uint8_t* key_mask, hipStream_t st) {
+                       const int32_t* lengths, const uint8_t* key_mask, const int32_t* cu_seqlens,
+                       hipStream_t st) {
   const int nqb = (S + 127) / 128;
   const int64_t nblk = (int64_t)nqb * B * H;
   if (nblk > INT32_MAX) return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd: grid too large");
   if (key_mask != nullptr)
     hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, true>), dim3((unsigned)nblk), dim3(256), 0, st, (const T*)qkv,
-                       sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, lengths, key_mask, nqb);
+                       sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, lengths, key_mask, cu_seqlens, nqb);
   else
     hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, false>), dim3((unsigned)nblk), dim3(256), 0, st, (const T*)qkv,
-                       sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, lengths, key_mask, nqb);
+                       sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, lengths, key_mask, cu_seqlens, nqb);
   return check_launch("tjk_flash_fwd");
 }
 
-template <typename T, int HDP, int NQ>
+template <typename T, int HDP, int NQ, int KS>
 static int launch_flash(const void* qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh, void* out,
                         int64_t ld_out, int B, int S, int H, int hd, float scale_log2, int causal,
-                        const int32_t* lengths, const uint8_t* key_mask, hipStream_t st) {
+                        const int32_t* lengths, const uint8_t* key_mask, const int32_t* cu_seqlens,
+                       hipStream_t st) {
   constexpr int BMQ = 4 * NQ * 32;
   const int nqb = (S + BMQ - 1) / BMQ;
+  const dim3 block(256 * KS);
   const int64_t nblk = (int64_t)nqb * B * H;
   if (nblk > INT32_MAX) return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd: grid too large");
   if (key_mask != nullptr)
-    hipLaunchKernelGGL((flash_fwd_kernel<T, HDP, NQ, true>), dim3((unsigned)nblk), dim3(256), 0, st,
+    hipLaunchKernelGGL((flash_fwd_kernel<T, HDP, NQ, KS, true>), dim3((unsigned)nblk), block, 0, st,
                        (const T*)qkv, sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal,
-                       lengths, key_mask, nqb);
+                       lengths, key_mask, cu_seqlens, nqb);
   else
-    hipLaunchKernelGGL((flash_fwd_kernel<T, HDP, NQ, false>), dim3((unsigned)nblk), dim3(256), 0, st,
+    hipLaunchKernelGGL((flash_fwd_kernel<T, HDP, NQ, KS, false>), dim3((unsigned)nblk), block, 0, st,
                        (const T*)qkv, sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal,
-                       lengths, key_mask, nqb);
+                       lengths, key_mask, cu_seqlens, nqb);
   return check_launch("tjk_flash_fwd");
 }
 
 template <typename T, int HDP>
 static int flash_plan(int plan, const void* qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh, void* out,
                       int64_t ld_out, int B, int S, int H, int hd, float scale_log2, int causal,
-                      const int32_t* lengths, const uint8_t* key_mask, hipStream_t st) {
+                      const int32_t* lengths, const uint8_t* key_mask, const int32_t* cu_seqlens,
+                       hipStream_t st) {
   if constexpr (sizeof(T) == 2) {
     if (plan == 0)
       return launch_pipe<T, HDP>(qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
-                                 key_mask, st);
+                                 key_mask, cu_seqlens, st);
   }
   if (plan == 2)
-    return launch_flash<T, HDP, 2>(qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
-                                   key_mask, st);
-  return launch_flash<T, HDP, 1>(qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
-                                 key_mask, st);
+    return launch_flash<T, HDP, 2, 1>(qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
+                                      key_mask, cu_seqlens, st);
+  // plan 3: two key splits per query group (8 waves); fp32 at hd 128 would
+  // not fit its K/V tiles in LDS and runs plan 1 instead.
+  if (plan == 3 && (sizeof(T) == 2 || HDP <= 64))
+    return launch_flash<T, HDP, 1, (sizeof(T) == 2 || HDP <= 64) ? 2 : 1>(
+        qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths, key_mask, cu_seqlens, st);
+  return launch_flash<T, HDP, 1, 1>(qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
+                                    key_mask, cu_seqlens, st);
 }
 
 template <typename T>
 static int flash_typed(int plan, const void* qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh, void* out,
                        int64_t ld_out, int B, int S, int H, int hd, float scale_log2, int causal,
-                       const int32_t* lengths, const uint8_t* key_mask, hipStream_t st) {
+                       const int32_t* lengths, const uint8_t* key_mask, const int32_t* cu_seqlens,
+                       hipStream_t st) {
   if (hd <= 32)
     return flash_plan<T, 32>(plan, qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
-                             key_mask, st);
+                             key_mask, cu_seqlens, st);
   if (hd <= 64)
     return flash_plan<T, 64>(plan, qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
-                             key_mask, st);
+                             key_mask, cu_seqlens, st);
   return flash_plan<T, 128>(plan, qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
-                            key_mask, st);
+                            key_mask, cu_seqlens, st);
 }
 
 }  // namespace tjk
@@ -651,7 +734,7 @@ using namespace tjk;
 extern "C" int tjk_flash_plan_count(int dtype) {
   if (dtype != TJK_F32 && dtype != TJK_F16 && dtype != TJK_BF16)
     return fail(TJK_EINVAL, "tjk_flash_plan_count: bad dtype %d", dtype);
-  return 3;
+  return 4;
 }
 
 extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s,
@@ -659,7 +742,7 @@ extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s
                              void* out, int64_t ld_out,
                              int batch, int seq, int heads, int head_dim, float scale,
                              int causal, const int32_t* lengths, const uint8_t* key_mask,
-                             int dtype, int plan_id, void* stream) {
+                             const int32_t* cu_seqlens, int dtype, int plan_id, void* stream) {
   if (batch < 0 || seq < 0 || heads <= 0 || head_dim <= 0)
     return fail(TJK_EINVAL, "tjk_flash_fwd: bad shape B=%d S=%d H=%d hd=%d", batch, seq, heads, head_dim);
   if (batch == 0 || seq == 0) return TJK_OK;
@@ -667,7 +750,9 @@ extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s
   if (dtype != TJK_F32 && dtype != TJK_F16 && dtype != TJK_BF16) return fail(TJK_EINVAL, "tjk_flash_fwd: bad dtype %d", dtype);
   if (head_dim > 128 || head_dim % 8)
     return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd: head_dim=%d must be a multiple of 8 and <= 128", head_dim);
-  if (plan_id < -1 || plan_id > 2) return fail(TJK_EINVAL, "tjk_flash_fwd: plan %d out of range", plan_id);
+  if (plan_id < -1 || plan_id > 3) return fail(TJK_EINVAL, "tjk_flash_fwd: plan %d out of range", plan_id);
+  if (cu_seqlens && key_mask)
+    return fail(TJK_EINVAL, "tjk_flash_fwd: cu_seqlens (packed sequences) and key_mask are exclusive");
   const int vec = 16 / dtype_size(dtype);
   if (stride_b % vec || stride_s % vec || stride_c % vec || stride_h % vec)
     return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd: strides must be multiples of %d elements", vec);
@@ -677,22 +762,26 @@ extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s
   if (!(scale > 0.f)) return fail(TJK_EINVAL, "tjk_flash_fwd: scale must be positive");
   // plan 0: software-pipelined kernel (2-byte types, byte offsets within a
   // head's K/V span must fit 31 bits); plans 1/2: one / two 32-query blocks
-  // per wave without cross-tile pipelining (every dtype).  Plan 1 measured
-  // fastest at S >= 2048 on MI355X, plan 0 at short sequences (S = 512).
+  // per wave without cross-tile pipelining (every dtype); plan 3: plan 1
+  // with two key splits per query group (8 waves, merged through LDS).
+  // Measured on MI355X (bf16/fp16, hd 64/128): plan 1 is fastest at
+  // S >= 2048 (C4 padded 64 us vs 69 us for plan 0; C5 191 us vs 258 us),
+  // plan 0 below (C3 15 us; packed C4, lengths 1054-1710: 44.5 us vs
+  // 47.9 us); plans 2 and 3 were slower on every BASELINE shape.
   const bool pipe_ok = dtype != TJK_F32 && ((int64_t)seq * stride_s + head_dim) * dtype_size(dtype) < INT32_MAX;
-  if (plan_id == -1) plan_id = (pipe_ok && seq <= 1024) ? 0 : 1;
+  if (plan_id == -1) plan_id = (pipe_ok && seq < 2048) ? 0 : 1;
   if (plan_id == 0 && !pipe_ok) plan_id = 1;
   const float scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   switch (dtype) {
     case TJK_F32:
       return flash_typed<float>(plan_id, qkv, stride_b, stride_s, stride_c, stride_h, out, ld_out, batch, seq,
-                                heads, head_dim, scale_log2, causal, lengths, key_mask, st);
+                                heads, head_dim, scale_log2, causal, lengths, key_mask, cu_seqlens, st);
     case TJK_F16:
       return flash_typed<f16>(plan_id, qkv, stride_b, stride_s, stride_c, stride_h, out, ld_out, batch, seq,
-                              heads, head_dim, scale_log2, causal, lengths, key_mask, st);
+                              heads, head_dim, scale_log2, causal, lengths, key_mask, cu_seqlens, st);
     default:
       return flash_typed<bf16>(plan_id, qkv, stride_b, stride_s, stride_c, stride_h, out, ld_out, batch, seq,
-                               heads, head_dim, scale_log2, causal, lengths, key_mask, st);
+                               heads, head_dim, scale_log2, causal, lengths, key_mask, cu_seqlens, st);
   }
 }

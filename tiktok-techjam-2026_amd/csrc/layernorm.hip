@@ -10,6 +10,12 @@
 // tjkernels/kernels/layernorm.py:63-66), then gamma/beta are applied and
 // the output is written in its own dtype.  A row mask (the final-LN zeroing
 // of tjkernels/engine.py:267-268) writes padded rows as exact zeros.
+//
+// A row index turns the kernel into a gather / scatter: output row r reads
+// input row row_index[r], or is written as zeros when the index is negative.
+// The engine uses it to pack the valid tokens of prefix-masked sequences
+// into consecutive rows (first LayerNorm) and to put them back in [B, S]
+// order with zero padded rows (final LayerNorm).
 
 #include <stdarg.h>
 #include <stdio.h>
@@ -41,14 +47,25 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(
     float* res_out, int64_t ld_res_out,
     TOut* __restrict__ out, int64_t ld_out,
     const float* __restrict__ gamma, const float* __restrict__ beta,
-    int64_t rows, int n, float eps, const uint8_t* __restrict__ row_mask) {
+    int64_t rows, int n, float eps, const int32_t* __restrict__ row_index,
+    const uint8_t* __restrict__ row_mask) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int nch = n >> 2;
+  const int64_t src = row_index != nullptr ? (int64_t)row_index[row] : row;
+  if (src < 0) {  // scatter hole: an exact zero row, nothing read
+    typename Quad<TOut>::raw* yrow = reinterpret_cast<typename Quad<TOut>::raw*>(out + row * ld_out);
+#pragma unroll
+    for (int j = 0; j < MAXCH; ++j) {
+      const int c = lane + 64 * j;
+      if (c < nch) yrow[c] = Quad<TOut>::from(make_float4(0.f, 0.f, 0.f, 0.f));
+    }
+    return;
+  }
 
   float4 x[MAXCH];
-  const TRes* rrow = res + row * ld_res;
+  const TRes* rrow = res + src * ld_res;
   float s = 0.f;
 #pragma unroll
   for (int j = 0; j < MAXCH; ++j) {
@@ -60,7 +77,7 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(
     }
   }
   if (delta != nullptr) {
-    const TDelta* drow = delta + row * ld_delta;
+    const TDelta* drow = delta + src * ld_delta;
 #pragma unroll
     for (int j = 0; j < MAXCH; ++j) {
       const int c = lane + 64 * j;
@@ -121,14 +138,14 @@ template <typename TRes, typename TDelta, typename TOut>
 static int launch_ln(const void* res, int64_t ld_res, const void* delta, int64_t ld_delta,
                      float* res_out, int64_t ld_res_out, void* out, int64_t ld_out,
                      const float* gamma, const float* beta, int64_t rows, int n, float eps,
-                     const uint8_t* row_mask, hipStream_t stream) {
+                     const int32_t* row_index, const uint8_t* row_mask, hipStream_t stream) {
   const int nch = n / 4;
   dim3 grid((unsigned)((rows + 3) / 4)), block(256);
 #define TJK_LN_CASE(MC)                                                                      \
   if (nch <= 64 * MC) {                                                                      \
     hipLaunchKernelGGL((add_layernorm_kernel<TRes, TDelta, TOut, MC>), grid, block, 0, stream, \
                        (const TRes*)res, ld_res, (const TDelta*)delta, ld_delta, res_out,    \
-                       ld_res_out, (TOut*)out, ld_out, gamma, beta, rows, n, eps, row_mask); \
+                       ld_res_out, (TOut*)out, ld_out, gamma, beta, rows, n, eps, row_index, row_mask); \
     return check_launch("tjk_add_layernorm");                                                \
   }
   TJK_LN_CASE(1)
@@ -145,17 +162,17 @@ template <typename TRes, typename TDelta>
 static int dispatch_out(int out_dtype, const void* res, int64_t ld_res, const void* delta,
                         int64_t ld_delta, float* res_out, int64_t ld_res_out, void* out,
                         int64_t ld_out, const float* gamma, const float* beta, int64_t rows,
-                        int n, float eps, const uint8_t* row_mask, hipStream_t stream) {
+                        int n, float eps, const int32_t* row_index, const uint8_t* row_mask, hipStream_t stream) {
   switch (out_dtype) {
     case TJK_F32:
       return launch_ln<TRes, TDelta, float>(res, ld_res, delta, ld_delta, res_out, ld_res_out, out, ld_out,
-                                            gamma, beta, rows, n, eps, row_mask, stream);
+                                            gamma, beta, rows, n, eps, row_index, row_mask, stream);
     case TJK_F16:
       return launch_ln<TRes, TDelta, f16>(res, ld_res, delta, ld_delta, res_out, ld_res_out, out, ld_out,
-                                          gamma, beta, rows, n, eps, row_mask, stream);
+                                          gamma, beta, rows, n, eps, row_index, row_mask, stream);
     case TJK_BF16:
       return launch_ln<TRes, TDelta, bf16>(res, ld_res, delta, ld_delta, res_out, ld_res_out, out, ld_out,
-                                           gamma, beta, rows, n, eps, row_mask, stream);
+                                           gamma, beta, rows, n, eps, row_index, row_mask, stream);
   }
   return fail(TJK_EINVAL, "tjk_add_layernorm: bad out dtype %d", out_dtype);
 }
@@ -164,18 +181,18 @@ template <typename TRes>
 static int dispatch_delta(int delta_dtype, int out_dtype, const void* res, int64_t ld_res,
                           const void* delta, int64_t ld_delta, float* res_out, int64_t ld_res_out,
                           void* out, int64_t ld_out, const float* gamma, const float* beta,
-                          int64_t rows, int n, float eps, const uint8_t* row_mask,
-                          hipStream_t stream) {
+                          int64_t rows, int n, float eps, const int32_t* row_index,
+                          const uint8_t* row_mask, hipStream_t stream) {
   switch (delta_dtype) {
     case TJK_F32:
       return dispatch_out<TRes, float>(out_dtype, res, ld_res, delta, ld_delta, res_out, ld_res_out, out,
-                                       ld_out, gamma, beta, rows, n, eps, row_mask, stream);
+                                       ld_out, gamma, beta, rows, n, eps, row_index, row_mask, stream);
     case TJK_F16:
       return dispatch_out<TRes, f16>(out_dtype, res, ld_res, delta, ld_delta, res_out, ld_res_out, out,
-                                     ld_out, gamma, beta, rows, n, eps, row_mask, stream);
+                                     ld_out, gamma, beta, rows, n, eps, row_index, row_mask, stream);
     case TJK_BF16:
       return dispatch_out<TRes, bf16>(out_dtype, res, ld_res, delta, ld_delta, res_out, ld_res_out, out,
-                                      ld_out, gamma, beta, rows, n, eps, row_mask, stream);
+                                      ld_out, gamma, beta, rows, n, eps, row_index, row_mask, stream);
   }
   return fail(TJK_EINVAL, "tjk_add_layernorm: bad delta dtype %d", delta_dtype);
 }
@@ -194,7 +211,7 @@ extern "C" int tjk_add_layernorm(const void* res, int res_dtype, int64_t ld_res,
                                  void* out, int out_dtype, int64_t ld_out,
                                  const float* gamma, const float* beta,
                                  int64_t rows, int64_t n, float eps,
-                                 const uint8_t* row_mask, void* stream) {
+                                 const int32_t* row_index, const uint8_t* row_mask, void* stream) {
   g_err[0] = 0;
   if (rows < 0 || n <= 0) return fail(TJK_EINVAL, "tjk_add_layernorm: bad shape rows=%lld n=%lld", (long long)rows, (long long)n);
   if (rows == 0) return TJK_OK;
@@ -213,18 +230,22 @@ extern "C" int tjk_add_layernorm(const void* res, int res_dtype, int64_t ld_res,
         ((uintptr_t)res_out & 15) || ((uintptr_t)gamma & 15) || ((uintptr_t)beta & 15))
       return fail(TJK_EUNSUPPORTED, "tjk_add_layernorm: misaligned pointer");
   }
+  // A gather / scatter reads rows other than the one it writes: an
+  // in-place residual update would race with other rows' reads.
+  if (row_index && res_out && (const void*)res_out == res)
+    return fail(TJK_EINVAL, "tjk_add_layernorm: row_index with res_out aliasing res");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int dd = delta ? delta_dtype : res_dtype;
   switch (res_dtype) {
     case TJK_F32:
       return dispatch_delta<float>(dd, out_dtype, res, ld_res, delta, ld_delta, res_out, ld_res_out, out,
-                                   ld_out, gamma, beta, rows, (int)n, eps, row_mask, s);
+                                   ld_out, gamma, beta, rows, (int)n, eps, row_index, row_mask, s);
     case TJK_F16:
       return dispatch_delta<f16>(dd, out_dtype, res, ld_res, delta, ld_delta, res_out, ld_res_out, out,
-                                 ld_out, gamma, beta, rows, (int)n, eps, row_mask, s);
+                                 ld_out, gamma, beta, rows, (int)n, eps, row_index, row_mask, s);
     case TJK_BF16:
       return dispatch_delta<bf16>(dd, out_dtype, res, ld_res, delta, ld_delta, res_out, ld_res_out, out,
-                                  ld_out, gamma, beta, rows, (int)n, eps, row_mask, s);
+                                  ld_out, gamma, beta, rows, (int)n, eps, row_index, row_mask, s);
   }
   return fail(TJK_EINVAL, "tjk_add_layernorm: bad res dtype %d", res_dtype);
 }

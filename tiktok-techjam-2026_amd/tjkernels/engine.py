@@ -24,17 +24,25 @@ With ``Plan.residual_epilogue=False`` the out-proj / FFN outputs are instead
 written in the compute dtype and added by the following LayerNorm, which is
 the reference's deferred-residual scheme (engine.py:232-264).
 
-Masks: NONE (no mask or all valid) needs nothing; PREFIX under causal
-attention needs only the final zeroing, since a valid query never sees a
-key at or beyond its sequence's length (engine.py:147-150); anything else
-(GENERAL, or any padding mask without causal attention) also hands the mask
-to the attention kernel as a per-key mask.  Padded rows are computed like
-valid ones and zeroed once, in the final LayerNorm.
+Masks: NONE (no mask or all valid) needs nothing.  PREFIX (every sequence
+valid on a prefix of length len_b) packs the valid tokens: no valid row ever
+depends on a padded one -- under causal attention a valid query never sees
+a key at or beyond its sequence's length (engine.py:147-150), without it the
+padded keys are masked, and every other op is row-wise -- so the first
+LayerNorm gathers the sum(len_b) valid rows into consecutive rows, every
+GEMM and LayerNorm runs on those rows only, attention runs on the packed
+sequences (cu_seqlens), and the final LayerNorm scatters the rows back to
+[B, S] order with padded rows written as exact zeros.  The reference
+computes the padded rows and zeroes them at the end (engine.py:267-268);
+the valid rows come out the same either way.  GENERAL (any other mask)
+hands the mask to the attention kernel as a per-key mask, computes every
+row and zeroes the padded ones in the final LayerNorm.
 """
 
 from __future__ import annotations
 
 import os
+from collections import OrderedDict
 from dataclasses import dataclass
 from typing import Dict, List, Optional, Tuple
 
@@ -74,6 +82,29 @@ class LayerWeights:
 
 
 @dataclass
+class Packing:
+    """Row maps of one set of prefix lengths (device tensors, built once)."""
+
+    lengths: Tuple[int, ...]
+    tokens: int                  # sum(lengths): rows of the packed layout
+    gather: torch.Tensor         # int32 [tokens]: [B*S] row of each packed row
+    scatter: torch.Tensor        # int32 [B*S]: packed row of each output row, -1 = padding
+    cu_seqlens: torch.Tensor     # int32 [B+1]
+
+
+def build_packing(lengths: Tuple[int, ...], seq: int, device: torch.device) -> Packing:
+    cu = [0]
+    for n in lengths:
+        cu.append(cu[-1] + n)
+    gather = torch.cat([torch.arange(b * seq, b * seq + n, dtype=torch.int32)
+                        for b, n in enumerate(lengths)]) if cu[-1] else torch.zeros(0, dtype=torch.int32)
+    scatter = torch.full((len(lengths) * seq,), -1, dtype=torch.int32)
+    scatter[gather.long()] = torch.arange(cu[-1], dtype=torch.int32)
+    return Packing(lengths=tuple(lengths), tokens=cu[-1], gather=gather.to(device),
+                   scatter=scatter.to(device), cu_seqlens=torch.tensor(cu, dtype=torch.int32, device=device))
+
+
+@dataclass
 class Workspace:
     res: torch.Tensor    # [T, d] fp32
     h: torch.Tensor      # [T, d] compute dtype
@@ -104,6 +135,7 @@ class Engine:
         self._graphs = GraphCache()
         self._mask_modes = _WeakDict()
         self._workspaces: Dict[Tuple, Workspace] = {}
+        self._packings: "OrderedDict[Tuple[int, Tuple[int, ...]], Packing]" = OrderedDict()
 
     # ------------------------------------------------------------- weights
 
@@ -161,28 +193,44 @@ class Engine:
     # ---------------------------------------------------------------- mask
 
     def _mask_mode(self, mask: Optional[torch.Tensor]) -> int:
-        """NONE / PREFIX / GENERAL, one host sync per distinct mask tensor
-        (memoised on tensor identity, as tjkernels/engine.py:131-158)."""
+        return self._mask_info(mask)[0]
+
+    def _mask_info(self, mask: Optional[torch.Tensor]) -> Tuple[int, Optional[Tuple[int, ...]]]:
+        """(NONE / PREFIX / GENERAL, prefix lengths for PREFIX) with one host
+        sync per distinct mask tensor, memoised on tensor identity as
+        tjkernels/engine.py:131-158 does."""
         if mask is None:
-            return MASK_NONE
+            return MASK_NONE, None
         cached = self._mask_modes.get(mask)
         if cached is not None:
             return cached
-        if bool(mask.all().item()):
-            mode = MASK_NONE
+        lengths = mask.sum(dim=-1)
+        positions = torch.arange(mask.shape[-1], device=mask.device)
+        prefix = positions[None, :] < lengths[:, None]
+        if bool(torch.equal(prefix, mask)):
+            host = tuple(int(n) for n in lengths.tolist())
+            info = (MASK_NONE, None) if min(host) == mask.shape[-1] else (MASK_PREFIX, host)
         else:
-            lengths = mask.sum(dim=-1)
-            positions = torch.arange(mask.shape[-1], device=mask.device)
-            prefix = positions[None, :] < lengths[:, None]
-            mode = MASK_PREFIX if bool(torch.equal(prefix, mask)) else MASK_GENERAL
-            if not self.causal:
-                mode = MASK_GENERAL
-        self._mask_modes[mask] = mode
-        return mode
+            info = (MASK_GENERAL, None)
+        self._mask_modes[mask] = info
+        return info
+
+    def _packing(self, lengths: Tuple[int, ...], seq: int) -> Packing:
+        key = (seq, lengths)
+        pk = self._packings.get(key)
+        if pk is None:
+            pk = build_packing(lengths, seq, self.device)
+            self._packings[key] = pk
+            while len(self._packings) > 64:
+                self._packings.popitem(last=False)
+        else:
+            self._packings.move_to_end(key)
+        return pk
 
     # ------------------------------------------------------------- compute
 
-    def _forward_impl(self, x: torch.Tensor, mask: Optional[torch.Tensor], mode: int) -> torch.Tensor:
+    def _forward_impl(self, x: torch.Tensor, mask: Optional[torch.Tensor], mode: int,
+                      packing: Optional[Packing] = None) -> torch.Tensor:
         plan = self.plan
         assert plan is not None and self.final_ln is not None
         batch, seq, d = x.shape
@@ -193,37 +241,48 @@ class Engine:
         heads, hd = self.num_heads, self.head_dim
         row_mask = None
         key_mask = None
-        if mode != MASK_NONE:
+        gather = scatter = None
+        rows = t
+        if mode == MASK_PREFIX:
+            assert packing is not None
+            rows, gather, scatter = packing.tokens, packing.gather, packing.scatter
+        elif mode == MASK_GENERAL:
             row_mask = mask.reshape(t)
-            if mode == MASK_GENERAL:
-                key_mask = mask
-        qkv5 = ws.qkv.view(batch, seq, 3, heads, hd)
+            key_mask = mask
+        res, h, qkv, ctx, mid = ws.res[:rows], ws.h[:rows], ws.qkv[:rows], ws.ctx[:rows], ws.mid[:rows]
+        delta = None if ws.delta is None else ws.delta[:rows]
         fused = plan.residual_epilogue
         pending = None
         for i, lw in enumerate(self.layers):
             if i == 0:
-                ops.add_layernorm(x2, None, lw.ln1_w, lw.ln1_b, lw.ln1_eps, ws.h, res_out=ws.res)
+                ops.add_layernorm(x2, None, lw.ln1_w, lw.ln1_b, lw.ln1_eps, h, res_out=res,
+                                  row_index=gather)
             else:
-                ops.add_layernorm(ws.res, pending, lw.ln1_w, lw.ln1_b, lw.ln1_eps, ws.h,
-                                  res_out=ws.res if pending is not None else None)
-            ops.gemm(ws.h, lw.wqkv, lw.bqkv, ws.qkv, ops.EPI_BIAS, plan.gemm_qkv)
-            ops.flash_attention(qkv5, ws.ctx, causal=self.causal, key_mask=key_mask,
-                                plan=plan.attn_plan)
+                ops.add_layernorm(res, pending, lw.ln1_w, lw.ln1_b, lw.ln1_eps, h,
+                                  res_out=res if pending is not None else None)
+            ops.gemm(h, lw.wqkv, lw.bqkv, qkv, ops.EPI_BIAS, plan.gemm_qkv)
+            if mode == MASK_PREFIX:
+                ops.flash_attention(qkv.view(rows, 3, heads, hd), ctx, causal=self.causal,
+                                    plan=plan.attn_plan, cu_seqlens=packing.cu_seqlens,
+                                    max_seqlen=max(packing.lengths))
+            else:
+                ops.flash_attention(qkv.view(batch, seq, 3, heads, hd), ctx, causal=self.causal,
+                                    key_mask=key_mask, plan=plan.attn_plan)
             if fused:
-                ops.gemm(ws.ctx, lw.wo, lw.bo, ws.res, ops.EPI_BIAS_RESIDUAL, plan.gemm_out)
-                ops.add_layernorm(ws.res, None, lw.ln2_w, lw.ln2_b, lw.ln2_eps, ws.h)
+                ops.gemm(ctx, lw.wo, lw.bo, res, ops.EPI_BIAS_RESIDUAL, plan.gemm_out)
+                ops.add_layernorm(res, None, lw.ln2_w, lw.ln2_b, lw.ln2_eps, h)
             else:
-                ops.gemm(ws.ctx, lw.wo, lw.bo, ws.delta, ops.EPI_BIAS, plan.gemm_out)
-                ops.add_layernorm(ws.res, ws.delta, lw.ln2_w, lw.ln2_b, lw.ln2_eps, ws.h,
-                                  res_out=ws.res)
-            ops.gemm(ws.h, lw.w1, lw.b1, ws.mid, ops.EPI_BIAS_GELU, plan.gemm_ffn1)
+                ops.gemm(ctx, lw.wo, lw.bo, delta, ops.EPI_BIAS, plan.gemm_out)
+                ops.add_layernorm(res, delta, lw.ln2_w, lw.ln2_b, lw.ln2_eps, h, res_out=res)
+            ops.gemm(h, lw.w1, lw.b1, mid, ops.EPI_BIAS_GELU, plan.gemm_ffn1)
             if fused:
-                ops.gemm(ws.mid, lw.w2, lw.b2, ws.res, ops.EPI_BIAS_RESIDUAL, plan.gemm_ffn2)
+                ops.gemm(mid, lw.w2, lw.b2, res, ops.EPI_BIAS_RESIDUAL, plan.gemm_ffn2)
             else:
-                ops.gemm(ws.mid, lw.w2, lw.b2, ws.delta, ops.EPI_BIAS, plan.gemm_ffn2)
-                pending = ws.delta
+                ops.gemm(mid, lw.w2, lw.b2, delta, ops.EPI_BIAS, plan.gemm_ffn2)
+                pending = delta
         fw, fb, feps = self.final_ln
-        ops.add_layernorm(ws.res, pending, fw, fb, feps, out.view(t, d), row_mask=row_mask)
+        ops.add_layernorm(res, pending, fw, fb, feps, out.view(t, d), row_mask=row_mask,
+                          row_index=scatter)
         return out
 
     # ---------------------------------------------------------------- call
@@ -238,16 +297,17 @@ class Engine:
             raise ValueError(f"x dtype {x.dtype} != model dtype {self.dtype}")
         if not x.is_contiguous():
             x = x.contiguous()
-        lengths_given = False
+        host_lengths: Optional[Tuple[int, ...]] = None
         if mask is not None and mask.dim() == 1 and not mask.dtype.is_floating_point \
                 and mask.dtype != torch.bool:
-            # forward(x, lengths): int prefix lengths [B] -> prefix mask, built on
-            # the device; its mode is known without inspecting it.
+            # forward(x, lengths): int prefix lengths [B]; read once on the host
+            # (the packed layout is sized from them) and turned into the
+            # equivalent prefix mask for the graph path's static inputs.
             if mask.shape[0] != x.shape[0]:
                 raise ValueError(f"lengths must be [B], got {tuple(mask.shape)}")
-            lengths = mask.to(device=x.device, dtype=torch.int64)
+            host_lengths = tuple(min(max(int(n), 0), x.shape[1]) for n in mask.tolist())
+            lengths = torch.tensor(host_lengths, dtype=torch.int64, device=x.device)
             mask = torch.arange(x.shape[1], device=x.device)[None, :] < lengths[:, None]
-            lengths_given = True
         if mask is not None:
             if tuple(mask.shape) != tuple(x.shape[:2]):
                 raise ValueError(f"valid_token_mask must be [B, S], got {tuple(mask.shape)}")
@@ -264,16 +324,24 @@ class Engine:
             self._plan_cache[(batch, seq)] = plan
         self.plan = plan
         self._build(plan)
-        if lengths_given:
-            mode = MASK_PREFIX if self.causal else MASK_GENERAL
+        if host_lengths is not None:
+            if min(host_lengths, default=x.shape[1]) == x.shape[1]:
+                mode, lens = MASK_NONE, None
+            else:
+                mode, lens = MASK_PREFIX, host_lengths
         else:
-            mode = self._mask_mode(mask)
+            mode, lens = self._mask_info(mask)
+        packing = self._packing(lens, x.shape[1]) if mode == MASK_PREFIX else None
         if plan.cuda_graph:
-            key = (tuple(x.shape), x.dtype, mode, plan)
-            graph = self._graphs.get(key, lambda gx, gm: self._forward_impl(gx, gm, mode), x, mask)
+            # A packed forward is specific to its lengths (its launches are
+            # sized by them), so they are part of the key; the graph keeps
+            # the row maps it reads alive.
+            key = (tuple(x.shape), x.dtype, mode, lens, plan)
+            graph = self._graphs.get(key, lambda gx, gm: self._forward_impl(gx, gm, mode, packing),
+                                     x, mask, keepalive=packing)
             if graph is not None:
                 return graph.run(x, mask)
-        return self._forward_impl(x, mask, mode)
+        return self._forward_impl(x, mask, mode, packing)
 
 
 def get_engine(module: torch.nn.Module) -> Engine:

@@ -12,7 +12,8 @@ allocation, no host sync, no memset).
 
 from __future__ import annotations
 
-from typing import Callable, Dict, Optional, Tuple
+from collections import OrderedDict
+from typing import Callable, Optional, Tuple
 
 import torch
 
@@ -55,21 +56,28 @@ class CapturedGraph:
 
 
 class GraphCache:
-    """Captured graphs keyed by everything that changes the captured work."""
+    """Captured graphs keyed by everything that changes the captured work,
+    least recently used first out beyond ``max_entries`` (keys include the
+    prefix lengths of packed forwards, so distinct masks add entries)."""
 
-    def __init__(self) -> None:
-        self._graphs: Dict[Tuple, Optional[CapturedGraph]] = {}
+    def __init__(self, max_entries: int = 16) -> None:
+        self._graphs: "OrderedDict[Tuple, Optional[CapturedGraph]]" = OrderedDict()
+        self.max_entries = max_entries
 
-    def get(self, key: Tuple, fn, x: torch.Tensor,
-            mask: Optional[torch.Tensor]) -> Optional[CapturedGraph]:
+    def get(self, key: Tuple, fn, x: torch.Tensor, mask: Optional[torch.Tensor],
+            keepalive: object = None) -> Optional[CapturedGraph]:
         if key in self._graphs:
+            self._graphs.move_to_end(key)
             return self._graphs[key]
         try:
             graph = CapturedGraph(fn, x, mask)
+            graph.keepalive = keepalive  # device buffers the captured kernels read
         except Exception as exc:  # capture is an optimisation; eager HIP still runs
             _warn_once(f"hipGraph capture failed ({exc}); running eager.")
             graph = None
         self._graphs[key] = graph
+        while len(self._graphs) > self.max_entries:
+            self._graphs.popitem(last=False)
         return graph
 
     def clear(self) -> None:

@@ -51,12 +51,26 @@ def _rowmajor(t: torch.Tensor, name: str) -> int:
 def add_layernorm(res: torch.Tensor, delta: Optional[torch.Tensor],
                   gamma: torch.Tensor, beta: torch.Tensor, eps: float,
                   out: torch.Tensor, res_out: Optional[torch.Tensor] = None,
-                  row_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+                  row_mask: Optional[torch.Tensor] = None,
+                  row_index: Optional[torch.Tensor] = None) -> torch.Tensor:
     """x = res (+ delta) in fp32; res_out <- x (optional, fp32); out <- LN(x)
     (rows with row_mask == 0 written as 0).  Mirrors fused_add_layernorm,
-    tjkernels/kernels/__init__.py:48-70."""
-    _require_gpu(res, delta, gamma, beta, out, res_out, row_mask)
+    tjkernels/kernels/__init__.py:48-70.
+
+    With ``row_index`` (int32, one entry per output row) the call is a
+    gather / scatter: output row r is computed from input row row_index[r],
+    or written as zeros when the index is negative; ``out`` (and ``res_out``)
+    then have ``row_index.numel()`` rows."""
+    _require_gpu(res, delta, gamma, beta, out, res_out, row_mask, row_index)
     rows, n = res.shape
+    if row_index is not None:
+        if row_index.dtype != torch.int32 or row_index.dim() != 1 or not row_index.is_contiguous():
+            raise TjkError("row_index must be a contiguous int32 vector")
+        rows = row_index.numel()
+        if out.shape[0] < rows or (res_out is not None and res_out.shape[0] < rows):
+            raise TjkError("row_index has more entries than out / res_out rows")
+    elif out.shape[0] < rows or (res_out is not None and res_out.shape[0] < rows):
+        raise TjkError("out / res_out have fewer rows than res")
     if res_out is not None and res_out.dtype != torch.float32:
         raise TjkError("res_out must be float32")
     if gamma.dtype != torch.float32 or beta.dtype != torch.float32:
@@ -72,7 +86,7 @@ def add_layernorm(res: torch.Tensor, delta: Optional[torch.Tensor],
         _ptr(res_out), _rowmajor(res_out, "res_out") if res_out is not None else 0,
         out.data_ptr(), _code(out), _rowmajor(out, "out"),
         gamma.data_ptr(), beta.data_ptr(), rows, n, float(eps),
-        _ptr(row_mask), _stream(res))
+        _ptr(row_index), _ptr(row_mask), _stream(res))
     check(status, "tjk_add_layernorm")
     return out
 
@@ -103,16 +117,38 @@ def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], out: to
 
 def flash_attention(qkv: torch.Tensor, out: torch.Tensor, causal: bool = True,
                     scale: Optional[float] = None, lengths: Optional[torch.Tensor] = None,
-                    key_mask: Optional[torch.Tensor] = None, plan: int = -1) -> torch.Tensor:
+                    key_mask: Optional[torch.Tensor] = None, plan: int = -1,
+                    cu_seqlens: Optional[torch.Tensor] = None,
+                    max_seqlen: Optional[int] = None) -> torch.Tensor:
     """qkv: [B, S, 3, H, hd] (any strides with a unit hd stride) -> out [B*S, H*hd].
     Mirrors flash_attention, tjkernels/kernels/attention.py:189-226, plus the
-    masked cases the reference sends to SDPA (tjkernels/engine.py:184-203)."""
-    _require_gpu(qkv, out, lengths, key_mask)
-    if qkv.dim() != 5 or qkv.shape[2] != 3 or qkv.stride(4) != 1:
-        raise TjkError(f"qkv must be [B, S, 3, H, hd] with unit hd stride, got {tuple(qkv.shape)}")
-    b, s, _, h, hd = qkv.shape
-    if out.shape[0] != b * s or out.shape[1] < h * hd or out.dtype != qkv.dtype:
-        raise TjkError("bad attention output buffer")
+    masked cases the reference sends to SDPA (tjkernels/engine.py:184-203).
+
+    Packed (varlen) form: ``qkv`` is [T, 3, H, hd] holding B sequences back
+    to back, ``cu_seqlens`` int32 [B+1] their row offsets and ``max_seqlen``
+    an upper bound of their lengths; ``out`` is [T, H*hd]."""
+    _require_gpu(qkv, out, lengths, key_mask, cu_seqlens)
+    if cu_seqlens is not None:
+        if qkv.dim() != 4 or qkv.shape[1] != 3 or qkv.stride(3) != 1:
+            raise TjkError(f"packed qkv must be [T, 3, H, hd] with unit hd stride, got {tuple(qkv.shape)}")
+        if cu_seqlens.dtype != torch.int32 or cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2 \
+                or not cu_seqlens.is_contiguous():
+            raise TjkError("cu_seqlens must be a contiguous int32 [B+1] vector")
+        if key_mask is not None:
+            raise TjkError("cu_seqlens and key_mask are exclusive")
+        if max_seqlen is None:
+            raise TjkError("packed attention needs max_seqlen")
+        t = qkv.shape[0]
+        if out.shape[0] < t or out.shape[1] < qkv.shape[2] * qkv.shape[3] or out.dtype != qkv.dtype:
+            raise TjkError("bad attention output buffer")
+        qkv = qkv.unsqueeze(0)  # stride_b is unused for packed sequences
+        b, s, h, hd = cu_seqlens.numel() - 1, int(max_seqlen), qkv.shape[3], qkv.shape[4]
+    else:
+        if qkv.dim() != 5 or qkv.shape[2] != 3 or qkv.stride(4) != 1:
+            raise TjkError(f"qkv must be [B, S, 3, H, hd] with unit hd stride, got {tuple(qkv.shape)}")
+        b, s, _, h, hd = qkv.shape
+        if out.shape[0] != b * s or out.shape[1] < h * hd or out.dtype != qkv.dtype:
+            raise TjkError("bad attention output buffer")
     if lengths is not None and (lengths.dtype != torch.int32 or lengths.numel() != b):
         raise TjkError("lengths must be int32 [B]")
     if key_mask is not None and (key_mask.dtype not in (torch.bool, torch.uint8)
@@ -122,8 +158,8 @@ def flash_attention(qkv: torch.Tensor, out: torch.Tensor, causal: bool = True,
     lib = _lib.load()
     status = lib.tjk_flash_fwd(qkv.data_ptr(), sb, ss, sc, sh, out.data_ptr(), _rowmajor(out, "out"),
                                b, s, h, hd, float(hd ** -0.5 if scale is None else scale),
-                               int(bool(causal)), _ptr(lengths), _ptr(key_mask), _code(qkv), plan,
-                               _stream(qkv))
+                               int(bool(causal)), _ptr(lengths), _ptr(key_mask), _ptr(cu_seqlens),
+                               _code(qkv), plan, _stream(qkv))
     check(status, "tjk_flash_fwd")
     return out
 

@@ -85,6 +85,15 @@ def flops_per_forward(w: Workload) -> float:
     return w.layers * (6.0 * t * d * d + 2.0 * t * d * d + 4.0 * t * d * f + attn)
 
 
+def flops_valid_tokens(w: Workload, lengths) -> float:
+    """FLOPs of the work a packed forward executes: the GEMMs over the
+    sum(lengths) valid rows and attention over each sequence's own valid
+    (query, key) pairs (causal: len(len+1)/2 per head)."""
+    t, d, f = sum(lengths), w.d_model, w.ffn_dim
+    pairs = sum(n * (n + 1) // 2 if w.causal else n * n for n in lengths)
+    return w.layers * (6.0 * t * d * d + 2.0 * t * d * d + 4.0 * t * d * f + 4.0 * d * pairs)
+
+
 def make_state_dict(w: Workload, seed: int = 0) -> Dict[str, torch.Tensor]:
     """fp32 CPU state_dict with the reference module's keys, rounded to the
     model dtype and returned in fp32 (so the oracle sees the rounded values)."""
