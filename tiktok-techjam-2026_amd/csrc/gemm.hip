@@ -89,9 +89,9 @@ __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* _
                                          int lane, char* __restrict__ stage) {
   typedef EpiStage<T, EPI, FN> E;
   typedef typename E::S S;
-  constexpr int LPR = E::WTN / E::SV;  // lanes per staged row on the read side
-  constexpr int RPI = 64 / LPR;        // rows per read instruction
-  static_assert(LPR <= 64 && 64 % LPR == 0, "row split");
+  constexpr int LPR = E::WTN / E::SV;  // 16-byte pieces per staged row
+  constexpr int NPC = 32 * LPR;        // pieces per 32-row block
+  constexpr int NIT = (NPC + 63) / 64; // read instructions per block
   S* st = reinterpret_cast<S*>(stage);
   const int l32 = lane & 31, hi = lane >> 5;
   // 16-byte output pieces need a 16-byte aligned C and a leading dimension
@@ -127,8 +127,10 @@ __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* _
           *reinterpret_cast<typename Quad<T>::raw*>(dst) = Quad<T>::from(v);
       }
 #pragma unroll
-    for (int r0 = 0; r0 < 32; r0 += RPI) {
-      const int rr = r0 + lane / LPR, cc = (lane % LPR) * E::SV;
+    for (int it = 0; it < NIT; ++it) {
+      const int pc = lane + 64 * it;  // piece index: row pc / LPR, piece pc % LPR
+      if (NPC % 64 != 0 && pc >= NPC) break;
+      const int rr = pc / LPR, cc = (pc % LPR) * E::SV;
       const int m = mw + 32 * j + rr, n = nw + cc;
       const uint4 piece = *reinterpret_cast<const uint4*>(st + rr * E::PITCH + cc);
       if (m < M && n < N) {
@@ -470,6 +472,10 @@ static const GemmPlan kPlans16[] = {
     {kDtl, 64, 64, 2, 2, 128, 2, 0.45},       // 9  small shapes
     {kDtl, 256, 128, 2, 2, 128, 2, 0.75},     // 10 wave tile 128x64
     {kDtl, 128, 256, 2, 2, 128, 2, 0.75},     // 11 wave tile 64x128
+    {kDtl, 192, 128, 2, 2, 128, 2, 0.80},     // 12 wave tile 96x64, 1 WG/CU
+    {kDtl, 192, 256, 2, 4, 128, 2, 0.90},     // 13 8 waves, wave tile 96x64
+    {kDtl, 192, 384, 2, 4, 128, 2, 0.95},     // 14 8 waves, wave tile 96x96
+    {kDtl, 96, 128, 1, 4, 128, 2, 0.60},      // 15 wave tile 96x32, small M
 };
 // fp32.
 static const GemmPlan kPlans32[] = {
@@ -595,6 +601,10 @@ static int run_gemm(int plan, int epi, const void* a, int64_t lda, const void* w
       TJK_GEMM_CASE(9, D2, 64, 64, 2, 2)
       TJK_GEMM_CASE(10, D2, 256, 128, 2, 2)
       TJK_GEMM_CASE(11, D2, 128, 256, 2, 2)
+      TJK_GEMM_CASE(12, D2, 192, 128, 2, 2)
+      TJK_GEMM_CASE(13, D2, 192, 256, 2, 4)
+      TJK_GEMM_CASE(14, D2, 192, 384, 2, 4)
+      TJK_GEMM_CASE(15, D2, 96, 128, 1, 4)
     }
   }
 #undef TJK_GEMM_CASE

@@ -16,12 +16,13 @@ MI355X specifics:
 * the accuracy reference is this build's own IEEE fp32 plan run on the GPU
   on the same inputs (the tests pin that plan to the CPU oracle at 1e-4, far
   inside the 2e-2 budgets), so the tuner needs no CPU oracle at run time;
-* the GEMM tile plans are tuned per projection by timing every valid plan on
-  the exact (M, N, K, epilogue) of that projection with HIP events, which is
-  cheap and independent of the other knobs; the plan-level knobs (attention
-  plan, residual epilogue, hipGraph) are then tuned by coordinate descent on
-  whole-forward latency measured as the harness does (events on the current
-  stream around the module call).
+* GEMM tile plans are not part of the tuned table: the engine times the tile
+  candidates once per projection shape at run time (``tjkernels.tiles``),
+  because with packed prefix-masked tokens the row count M of every
+  projection follows the input lengths; ``tune_gemm`` remains as a tool;
+  the plan-level knobs (attention plan, residual epilogue, hipGraph) are
+  tuned by coordinate descent on whole-forward latency measured as the
+  harness does (events on the current stream around the module call).
 """
 
 from __future__ import annotations
@@ -165,29 +166,12 @@ def tune_workload(w: Workload, trials: int = 2, margin: float = 0.85, iters: int
     if not admissible(cur):
         return None
 
-    # per-projection tile plans, timed in isolation at the exact shapes
-    plan = cur["plan"]
-    t, d, f = w.tokens, w.d_model, w.ffn_dim
-    cdt = plan.compute_dtype
-    res_epi = ops.EPI_BIAS_RESIDUAL if plan.residual_epilogue else ops.EPI_BIAS
-    picks = {}
-    for knob, (m, n, k, epi) in {"gemm_qkv": (t, 3 * d, d, ops.EPI_BIAS),
-                                 "gemm_out": (t, d, d, res_epi),
-                                 "gemm_ffn1": (t, f, d, ops.EPI_BIAS_GELU),
-                                 "gemm_ffn2": (t, d, f, res_epi)}.items():
-        best, times = tune_gemm(m, n, k, cdt, epi)
-        picks[knob] = best
-        if verbose:
-            top = sorted(times.items(), key=lambda kv: kv[1])[:3]
-            print(f"    {knob:<10} {m}x{n}x{k}: " +
-                  ", ".join(f"p{p}={ms * 1e3:.1f}us" for p, ms in top), flush=True)
-    cand = ev.evaluate(replace(plan, **picks))
-    show("tuned gemm tiles", cand)
-    if admissible(cand) and cand["latency_ms"] < cur["latency_ms"]:
-        cur = cand
+    # GEMM tile plans stay -1: the engine times the tile candidates once per
+    # projection shape at run time (tjkernels.tiles), since with packed
+    # prefix-masked tokens M follows the input lengths.
 
     # coordinate descent over the plan-level knobs
-    for knob, values in (("attn_plan", [0, 1]), ("residual_epilogue", [True, False]),
+    for knob, values in (("attn_plan", [0, 1, 3]), ("residual_epilogue", [True, False]),
                          ("cuda_graph", [True, False])):
         for v in values:
             if getattr(cur["plan"], knob) == v:

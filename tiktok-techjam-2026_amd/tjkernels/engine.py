@@ -48,7 +48,7 @@ from typing import Dict, List, Optional, Tuple
 
 import torch
 
-from . import ops
+from . import ops, tiles
 from .graphs import GraphCache
 from .plans import Plan, select_plan
 
@@ -252,6 +252,13 @@ class Engine:
         res, h, qkv, ctx, mid = ws.res[:rows], ws.h[:rows], ws.qkv[:rows], ws.ctx[:rows], ws.mid[:rows]
         delta = None if ws.delta is None else ws.delta[:rows]
         fused = plan.residual_epilogue
+        # Tile plans: forced by the Plan, else measured once per shape.
+        cdt, d, f = plan.compute_dtype, self.d_model, self.ffn_dim
+        epi_res = ops.EPI_BIAS_RESIDUAL if fused else ops.EPI_BIAS
+        tp_qkv = tiles.gemm_plan(rows, 3 * d, d, cdt, ops.EPI_BIAS, plan.gemm_qkv)
+        tp_out = tiles.gemm_plan(rows, d, d, cdt, epi_res, plan.gemm_out)
+        tp_ffn1 = tiles.gemm_plan(rows, f, d, cdt, ops.EPI_BIAS_GELU, plan.gemm_ffn1)
+        tp_ffn2 = tiles.gemm_plan(rows, d, f, cdt, epi_res, plan.gemm_ffn2)
         pending = None
         for i, lw in enumerate(self.layers):
             if i == 0:
@@ -260,7 +267,7 @@ class Engine:
             else:
                 ops.add_layernorm(res, pending, lw.ln1_w, lw.ln1_b, lw.ln1_eps, h,
                                   res_out=res if pending is not None else None)
-            ops.gemm(h, lw.wqkv, lw.bqkv, qkv, ops.EPI_BIAS, plan.gemm_qkv)
+            ops.gemm(h, lw.wqkv, lw.bqkv, qkv, ops.EPI_BIAS, tp_qkv)
             if mode == MASK_PREFIX:
                 ops.flash_attention(qkv.view(rows, 3, heads, hd), ctx, causal=self.causal,
                                     plan=plan.attn_plan, cu_seqlens=packing.cu_seqlens,
@@ -269,16 +276,16 @@ class Engine:
                 ops.flash_attention(qkv.view(batch, seq, 3, heads, hd), ctx, causal=self.causal,
                                     key_mask=key_mask, plan=plan.attn_plan)
             if fused:
-                ops.gemm(ctx, lw.wo, lw.bo, res, ops.EPI_BIAS_RESIDUAL, plan.gemm_out)
+                ops.gemm(ctx, lw.wo, lw.bo, res, ops.EPI_BIAS_RESIDUAL, tp_out)
                 ops.add_layernorm(res, None, lw.ln2_w, lw.ln2_b, lw.ln2_eps, h)
             else:
-                ops.gemm(ctx, lw.wo, lw.bo, delta, ops.EPI_BIAS, plan.gemm_out)
+                ops.gemm(ctx, lw.wo, lw.bo, delta, ops.EPI_BIAS, tp_out)
                 ops.add_layernorm(res, delta, lw.ln2_w, lw.ln2_b, lw.ln2_eps, h, res_out=res)
-            ops.gemm(h, lw.w1, lw.b1, mid, ops.EPI_BIAS_GELU, plan.gemm_ffn1)
+            ops.gemm(h, lw.w1, lw.b1, mid, ops.EPI_BIAS_GELU, tp_ffn1)
             if fused:
-                ops.gemm(mid, lw.w2, lw.b2, res, ops.EPI_BIAS_RESIDUAL, plan.gemm_ffn2)
+                ops.gemm(mid, lw.w2, lw.b2, res, ops.EPI_BIAS_RESIDUAL, tp_ffn2)
             else:
-                ops.gemm(mid, lw.w2, lw.b2, delta, ops.EPI_BIAS, plan.gemm_ffn2)
+                ops.gemm(mid, lw.w2, lw.b2, delta, ops.EPI_BIAS, tp_ffn2)
                 pending = delta
         fw, fb, feps = self.final_ln
         ops.add_layernorm(res, pending, fw, fb, feps, out.view(t, d), row_mask=row_mask,

@@ -1,0 +1,80 @@
+"""Measured GEMM tile choice per (M, N, K, dtype, epilogue).
+
+With packed prefix-masked tokens the row count M of every projection is
+the number of valid tokens, which changes with the input lengths, and the
+best tile shape depends on how the tile count falls onto the 256 CUs (a
+launch whose last round holds a handful of tiles costs nearly a full
+round).  No fixed table covers that, so the first time a projection shape is
+seen its candidate tile plans are timed on scratch operands of that exact
+shape (HIP events on the current stream) and the fastest is kept for the
+rest of the process.  Every candidate accumulates each output element over
+K in the same order, so the choice changes speed, not results.
+
+This replaces the reference's static per-shape table lookup for the GEMM
+part of a plan (tjkernels/plans.py:147-170); plan ids >= 0 in a ``Plan``
+still force a specific tile.  ``TJ_GEMM_TUNE=0`` falls back to the
+library's own rule (plan -1).
+"""
+
+from __future__ import annotations
+
+import os
+from typing import Dict, Tuple
+
+import torch
+
+from . import _lib, ops
+
+# Direct-to-LDS tile plans worth timing (2-byte types): 128x128, 256x256,
+# 64x64, 192x128, 192x256, 192x384, 96x128.  fp32 uses its own list.
+CANDIDATES_16 = (7, 8, 9, 12, 13, 14, 15)
+CANDIDATES_32 = (2, 3, 4)
+
+_choice: Dict[Tuple, int] = {}
+
+
+def _time_plan(a, w, bias, out, epi, plan, reps) -> float:
+    for _ in range(2):
+        ops.gemm(a, w, bias, out, epi, plan)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        ops.gemm(a, w, bias, out, epi, plan)
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def gemm_plan(m: int, n: int, k: int, dtype: torch.dtype, epilogue: int, forced: int = -1) -> int:
+    """Tile plan for out[m, n] = epi(a[m, k] w[n, k]^T + b); ``forced`` >= 0 wins."""
+    if forced >= 0 or m == 0:
+        return forced
+    if os.environ.get("TJ_GEMM_TUNE") == "0" or torch.cuda.is_current_stream_capturing():
+        return _choice.get((m, n, k, dtype, epilogue), -1)
+    key = (m, n, k, dtype, epilogue)
+    plan = _choice.get(key)
+    if plan is not None:
+        return plan
+    dev = torch.device("cuda", torch.cuda.current_device())
+    g = torch.Generator(device=dev)
+    g.manual_seed(m * 7919 + n * 31 + k)
+    a = torch.randn(m, k, device=dev, generator=g).to(dtype)
+    w = (torch.randn(n, k, device=dev, generator=g) * k ** -0.5).to(dtype)
+    bias = torch.zeros(n, device=dev, dtype=dtype)
+    out = torch.empty(m, n, device=dev,
+                      dtype=torch.float32 if epilogue == ops.EPI_BIAS_RESIDUAL else dtype)
+    reps = 3 if 2.0 * m * n * k > 5e10 else 6
+    best, best_ms = -1, float("inf")
+    for cand in (CANDIDATES_32 if dtype == torch.float32 else CANDIDATES_16):
+        try:
+            ms = _time_plan(a, w, bias, out, epilogue, cand, reps)
+        except _lib.TjkError:  # shape this tile does not take (e.g. K % 64 != 0)
+            continue
+        if ms < best_ms * 0.98:  # prefer the earlier (larger-reuse) candidate on near ties
+            best, best_ms = cand, ms
+    _choice[key] = best
+    return best
+
+
+def reset() -> None:
+    _choice.clear()
