@@ -1,0 +1,156 @@
+"""Per-kernel-class summary of a rocprofv3 run of ``bench.py``.
+
+    python -m tjkernels.rocprof_summary TRACE.csv [--fetch FETCH.csv --write WRITE.csv]
+                                        [--layers 4] [--copy-calib-bytes 268435456]
+
+TRACE.csv is ``*_kernel_trace.csv`` of ``rocprofv3 --kernel-trace``; FETCH /
+WRITE are ``*_counter_collection.csv`` of two ``rocprofv3 --pmc FETCH_SIZE``
+/ ``--pmc WRITE_SIZE`` runs.  Kernels are labelled by their position in the
+forward: the forward's launch sequence is fixed (first LayerNorm, then per
+layer QKV GEMM, attention, out-proj GEMM, LayerNorm, FFN1 GEMM, FFN2 GEMM,
+LayerNorm, and the final LayerNorm), so every complete sequence that starts
+with the first LayerNorm (the one reading the model-dtype input) is split
+into labelled launches.  Sequences are grouped by the first LayerNorm's grid
+(the packed forward has fewer rows than the all-rows one) and each group is
+reported separately.  HBM bytes per launch are FETCH_SIZE and WRITE_SIZE
+(KiB per dispatch) scaled by what the same counters read for the bench's
+plain 256 MiB copy (``__amd_rocclr_copyBuffer`` of 268435456 bytes read and
+written).
+"""
+
+from __future__ import annotations
+
+import argparse
+import collections
+import csv
+from typing import Dict, List, Optional, Tuple
+
+GEMM, FLASH, LN, COPY = "gemm_dtl_kernel", "flash_", "add_layernorm_kernel", "__amd_rocclr_copyBuffer"
+
+
+def _is_first_ln(name: str) -> bool:
+    # add_layernorm_kernel<TRes, TDelta, TOut, ...>: TRes is the model dtype
+    # (bf16 / fp16) for the first LayerNorm, fp32 for every other one.
+    return LN in name and ("add_layernorm_kernelIDF16b" in name or "add_layernorm_kernelIDF16_" in name)
+
+
+def _labels(layers: int) -> List[str]:
+    seq = ["ln_first"]
+    for i in range(layers):
+        if i:
+            seq.append("add_layernorm")
+        seq += ["gemm_qkv", "flash_attention", "gemm_out_residual", "add_layernorm",
+                "gemm_ffn1_gelu", "gemm_ffn2_residual"]
+    seq.append("ln_final")
+    return seq
+
+
+def _grid(r: dict) -> int:
+    return int(r.get("Grid_Size") or r["Grid_Size_X"])
+
+
+def _wg(r: dict) -> int:
+    return int(r.get("Workgroup_Size") or r["Workgroup_Size_X"])
+
+
+def _tjk(name: str) -> bool:
+    return GEMM in name or FLASH in name or LN in name
+
+
+def _forwards(rows: List[dict], layers: int) -> Dict[int, List[List[Tuple[str, dict]]]]:
+    """{first-LN grid: [forward as [(label, row)]]} from dispatch-ordered rows."""
+    labels = _labels(layers)
+    tjk = [r for r in rows if _tjk(r["Kernel_Name"])]
+    out: Dict[int, List[List[Tuple[str, dict]]]] = collections.defaultdict(list)
+    i = 0
+    while i < len(tjk):
+        if _is_first_ln(tjk[i]["Kernel_Name"]) and i + len(labels) <= len(tjk):
+            seq = tjk[i:i + len(labels)]
+            ok = all((GEMM in r["Kernel_Name"]) == lab.startswith("gemm")
+                     and (FLASH in r["Kernel_Name"]) == (lab == "flash_attention")
+                     for lab, r in zip(labels, seq))
+            if ok and not any(_is_first_ln(r["Kernel_Name"]) for r in seq[1:]):
+                out[_grid(seq[0])].append(list(zip(labels, seq)))
+                i += len(labels)
+                continue
+        i += 1
+    return out
+
+
+def _dur_us(r: dict) -> float:
+    return (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+
+
+def _counter(path: str) -> Tuple[List[dict], Optional[float]]:
+    rows = list(csv.DictReader(open(path)))
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    copies = [float(r["Counter_Value"]) for r in rows if r["Kernel_Name"] == COPY]
+    return rows, (max(copies) if copies else None)
+
+
+def summarize(trace: str, layers: int = 4, fetch: Optional[str] = None,
+              write: Optional[str] = None, calib_bytes: float = 268435456.0) -> str:
+    rows = list(csv.DictReader(open(trace)))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    groups = _forwards(rows, layers)
+    lines = []
+    for grid, fwds in sorted(groups.items()):
+        per: Dict[str, List[float]] = collections.defaultdict(list)
+        totals = []
+        for f in fwds:
+            totals.append(sum(_dur_us(r) for _, r in f))
+            for lab, r in f:
+                per[lab].append(_dur_us(r))
+        names = {lab: r["Kernel_Name"] for lab, r in fwds[-1]}
+        grids = {lab: _grid(r) // _wg(r) for lab, r in fwds[-1]}
+        lines.append(f"forward group: first LayerNorm grid {grid} threads, {len(fwds)} forwards, "
+                     f"kernel time per forward {sorted(totals)[len(totals) // 2]:.1f} us (median)")
+        lines.append(f"{'label':<20} {'launches/fwd':>12} {'avg us':>9} {'us/fwd':>9} {'WGs':>6}  kernel")
+        for lab in dict.fromkeys(_labels(layers)):
+            v = per[lab]
+            n = len(v) // len(fwds)
+            lines.append(f"{lab:<20} {n:>12} {sum(v) / len(v):>9.2f} {sum(v) / len(fwds):>9.1f} "
+                         f"{grids[lab]:>6}  {names[lab][:90]}")
+        lines.append("")
+    if fetch and write:
+        lines.append(f"HBM traffic per launch (FETCH_SIZE / WRITE_SIZE, calibrated on the "
+                     f"{calib_bytes / 2**20:.0f} MiB copy)")
+        scaled = {}
+        for tag, path in (("fetch", fetch), ("write", write)):
+            crow, copy_kib = _counter(path)
+            if not copy_kib:
+                lines.append(f"  no calibration copy in {path}")
+                return "\n".join(lines)
+            factor = calib_bytes / (copy_kib * 1024.0)
+            lines.append(f"  {tag}: calibration copy reads {copy_kib:.0f} KiB -> scale x{factor:.3f}")
+            gr = _forwards(crow, layers)
+            grid = min(gr) if gr else None
+            acc: Dict[str, List[float]] = collections.defaultdict(list)
+            for f in gr.get(grid, []):
+                for lab, r in f:
+                    acc[lab].append(float(r["Counter_Value"]) * 1024.0 * factor)
+            scaled[tag] = {lab: sum(v) / len(v) for lab, v in acc.items()}
+        lines.append(f"{'label':<20} {'fetch MB':>9} {'write MB':>9} {'total MB':>9}")
+        for lab in dict.fromkeys(_labels(layers)):
+            fb, wb = scaled["fetch"].get(lab, 0.0), scaled["write"].get(lab, 0.0)
+            lines.append(f"{lab:<20} {fb / 1e6:>9.1f} {wb / 1e6:>9.1f} {(fb + wb) / 1e6:>9.1f}")
+        for lab in dict.fromkeys(_labels(layers)):
+            fb, wb = scaled["fetch"].get(lab, 0.0), scaled["write"].get(lab, 0.0)
+            lines.append(f"traffic_bytes_per_launch[{lab}] {fb + wb:.0f}")
+    return "\n".join(lines)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("trace")
+    ap.add_argument("--fetch")
+    ap.add_argument("--write")
+    ap.add_argument("--layers", type=int, default=4)
+    ap.add_argument("--copy-calib-bytes", type=float, default=268435456.0)
+    args = ap.parse_args()
+    print(summarize(args.trace, args.layers, args.fetch, args.write, args.copy_calib_bytes))
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
