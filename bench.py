@@ -86,7 +86,8 @@ def _breakdown(engine, x, mask):
     import torch
     from tjkernels import ops
     classes, calls = {}, {}
-    orig = {name: getattr(ops, name) for name in ("gemm", "flash_attention", "add_layernorm")}
+    orig = {name: getattr(ops, name) for name in ("gemm", "flash_attention", "flash_attention_sched",
+                                                  "add_layernorm")}
     events = []
 
     def wrap(name, fn):
@@ -105,6 +106,9 @@ def _breakdown(engine, x, mask):
                 flops = 2.0 * a0.shape[0] * w.shape[0] * w.shape[1]
             elif name == "flash_attention":
                 flops = _attn_flops(a[0], k.get("causal", True), k.get("cu_seqlens"))
+            elif name == "flash_attention_sched":
+                label = "flash_attention"
+                flops = _attn_flops(a[0], k.get("causal", True), a[2])
             else:
                 flops = 0.0
             s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

@@ -127,6 +127,35 @@ int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s,
 int tjk_flash_plan_count(int dtype);
 
 /*
+ * Scheduled flash attention over packed sequences (bf16 / fp16): the same
+ * math as tjk_flash_fwd with cu_seqlens, but the workgroups follow a work
+ * list built by the caller (from the host-known lengths), so long query
+ * blocks can start first and be split over their key range.
+ *   work[4*i .. 4*i+3] = { b*heads + h, qb, t_lo | t_hi << 16, slot }
+ *     query block qb (queries 128*qb .. 128*qb+127 of sequence b, head h)
+ *     over key tiles t_lo .. t_hi-1 (64 keys each; t_hi is clipped to the
+ *     block's last causal / in-sequence tile); slot < 0 writes the output
+ *     rows, slot >= 0 writes an fp32 partial (unnormalised O, running max
+ *     and sum per query) into partials slot `slot`
+ *   merges[4*j .. 4*j+3] = { b*heads + h, qb, slot_lo, slot_hi }: a second
+ *     launch combines two partials of one query block (in that order, so the
+ *     result is deterministic) and writes its output rows
+ * Every (query block, key tile) pair of every sequence must be covered
+ * exactly once.  partials holds tjk_flash_partial_bytes(head_dim, n) bytes
+ * for n slots.  max_seqlen bounds every sequence length.  Replaces the
+ * reference's grid of (query block, b*h) programs, attention.py:199-217.
+ */
+int tjk_flash_fwd_sched(const void* qkv, int64_t stride_s, int64_t stride_c, int64_t stride_h,
+                        void* out, int64_t ld_out, int batch, int max_seqlen, int heads,
+                        int head_dim, float scale, int causal, const int32_t* cu_seqlens,
+                        const int32_t* work, int n_work, const int32_t* merges, int n_merges,
+                        float* partials, int dtype, void* stream);
+size_t tjk_flash_partial_bytes(int head_dim, int n_slots);
+/* Workgroups of the scheduled kernel resident per CU (> 0), or a negative /
+ * hipError_t status. */
+int tjk_flash_sched_occupancy(int head_dim, int dtype);
+
+/*
  * Feed-forward block: out = gelu_erf(h W1^T + b1) W2^T + b2 with W1 [f, d],
  * W2 [d, f] (nn.Linear layout).  The [tokens, f] intermediate is rounded to
  * `dtype` (as the reference does) and lives in `workspace`

@@ -353,3 +353,45 @@ def test_flash_packed_sequences(device, dt, hd, causal):
             ref = _attn_ref(qkv[cu[b]:cu[b + 1]].unsqueeze(0), causal)
             _close(got[cu[b]:cu[b + 1]], ref, tol, tol)
         assert (got[t:] == 7.0).all(), "rows past the packed tokens were written"
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("hd", [32, 64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_scheduled(device, dt, hd, causal):
+    """The scheduled kernel (work list, key-split items merged in a second
+    launch) against the fp64 brute force per sequence, with few slots so that
+    most items are split, and against the plain packed kernel."""
+    from tjkernels.schedule import build_schedule
+    lengths = [300, 0, 1, 129, 64, 200]
+    h = 3
+    cu = [0]
+    for n in lengths:
+        cu.append(cu[-1] + n)
+    t = cu[-1]
+    g = _gen(hd * 3 + int(causal))
+    qkv = torch.randn(t, 3, h, hd, generator=g).to(dt)
+    cu_d = torch.tensor(cu, dtype=torch.int32, device=device)
+    # split target = max(total tiles / slots, min_split): (many slots, 2)
+    # splits every item of more than 2 key tiles, (1 slot, 6) splits none
+    for slots, min_split in ((100000, 2), (1, 6)):
+        sched = build_schedule(lengths, h, hd, causal, dt, device, slots=slots, min_split=min_split,
+                               split_factor=1.0)
+        assert (sched.merges.shape[0] > 0) == (min_split == 2)
+        out = torch.full((t + 5, h * hd), 7.0, dtype=dt, device=device)
+        ops.flash_attention_sched(qkv.to(device), out, cu_d, max(lengths), sched, causal=causal)
+        torch.cuda.synchronize()
+        got = out.cpu()
+        for b, n in enumerate(lengths):
+            if n:
+                ref = _attn_ref(qkv[cu[b]:cu[b + 1]].unsqueeze(0), causal)
+                _close(got[cu[b]:cu[b + 1]], ref, 1e-2, 1e-2)
+        assert (got[t:] == 7.0).all(), "rows past the packed tokens were written"
+        plain = torch.empty(t, h * hd, dtype=dt, device=device)
+        ops.flash_attention(qkv.to(device), plain, causal=causal, plan=0, cu_seqlens=cu_d,
+                            max_seqlen=max(lengths))
+        torch.cuda.synchronize()
+        if min_split == 6:  # no split: same kernel, same tiles, bitwise equal
+            assert torch.equal(got[:t], plain.cpu())
+        else:
+            assert (got[:t].float() - plain.cpu().float()).abs().max().item() < 2e-2

@@ -220,3 +220,38 @@ def test_valid_token_flops():
     gemm = (6 + 2) * 4 * d * d + 4 * 4 * d * f          # 4 valid rows
     attn = 4 * d * (6 + 1)                              # 3*4/2 + 1*2/2 causal pairs
     assert flops_valid_tokens(w, lens) == L * (gemm + attn)
+
+
+def test_attention_schedule_covers_every_tile_once():
+    """Every (sequence, head, query block, key tile) pair appears in exactly
+    one work item, split items pair up in the merge list, items are issued
+    longest first, and no item exceeds the split target."""
+    from tjkernels.schedule import BMQ, BNK, build_items
+    for causal in (True, False):
+        lengths, heads, slots = [1380, 1710, 0, 1054, 1, 129], 3, 40
+        work, merges, n_slots = build_items(lengths, heads, causal, slots, split_factor=1.0)
+        seen = {}
+        for cost, bh, qb, lo, hi, slot in work:
+            assert hi - lo == cost and cost > 0
+            for t in range(lo, hi):
+                key = (bh, qb, t)
+                assert key not in seen
+                seen[key] = slot
+        expect = set()
+        for b, n in enumerate(lengths):
+            for qb in range((n + BMQ - 1) // BMQ):
+                kend = min((qb + 1) * BMQ, n) if causal else n
+                for t in range((kend + BNK - 1) // BNK):
+                    for h in range(heads):
+                        expect.add((b * heads + h, qb, t))
+        assert set(seen) == expect
+        costs = [w[0] for w in work]
+        assert costs == sorted(costs, reverse=True)
+        total = sum(costs)
+        target = max(total / slots, 6)
+        assert all(w[0] <= target for w in work if w[5] < 0), "an item above the target was not split"
+        slots_used = sorted(s for m in merges for s in m[2:])
+        assert slots_used == list(range(n_slots))
+        for bh, qb, lo_slot, hi_slot in merges:
+            halves = sorted((w[3], w[4], w[5]) for w in work if w[1] == bh and w[2] == qb)
+            assert [h[2] for h in halves] == [lo_slot, hi_slot] and halves[0][1] == halves[1][0]

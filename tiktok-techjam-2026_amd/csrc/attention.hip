@@ -390,12 +390,13 @@ __global__ __launch_bounds__(256 * KS) void flash_fwd_kernel(
 
 constexpr uint32_t kFaPastEnd = 0x7fff0000u;
 
-template <typename T, int HDP, bool KEYMASK>
+template <typename T, int HDP, bool KEYMASK, bool FULLHD>
 __global__ __launch_bounds__(256) void flash_pipe_kernel(
     const T* __restrict__ qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh,
     T* __restrict__ out, int64_t ld_out, int B, int S, int H, int hd, float scale_log2,
     int causal, const int32_t* __restrict__ lengths, const uint8_t* __restrict__ key_mask,
-    const int32_t* __restrict__ cu_seqlens, int nqb) {
+    const int32_t* __restrict__ cu_seqlens, int nqb,
+    const int4* __restrict__ work, float* __restrict__ partials) {
   static_assert(sizeof(T) == 2, "2-byte element types only");
   constexpr int BMQ = 128, BNK = 64, NST = 3, VEC = 8;
   constexpr int LDK = HDP + VEC, LDV = BNK + VEC;
@@ -408,8 +409,21 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
   __shared__ __attribute__((aligned(16))) T sV[NST][HDP * LDV];
 
   const int BH = B * H;
-  const int rank = blockIdx.x / BH, bh = blockIdx.x % BH;
-  const int qb = causal ? nqb - 1 - rank : rank;
+  // Work item: from the scheduled list (bh, qb, key tiles [t_lo, t_hi),
+  // partial slot or -1), else from the grid (every key tile, longest first).
+  int bh, qb, t_lo = 0, t_hi = 1 << 30, slot = -1;
+  if (work != nullptr) {
+    const int4 it = work[blockIdx.x];
+    bh = it.x;
+    qb = it.y;
+    t_lo = it.z & 0xffff;
+    t_hi = it.z >> 16;
+    slot = it.w;
+  } else {
+    const int rank = blockIdx.x / BH;
+    bh = blockIdx.x % BH;
+    qb = causal ? nqb - 1 - rank : rank;
+  }
   const int b = bh / H, h = bh % H;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
@@ -432,6 +446,7 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
   int kend = causal ? min(q0 + BMQ, Sb) : Sb;
   kend = min(kend, kv_len);
   const int nkt = (kend + BNK - 1) / BNK;
+  t_hi = min(t_hi, nkt);
 
   // Q fragments (B operand of S^T): lane holds Q[q][16c + 8*hi + 0..7]
   typename Mfma<T>::frag qf[KC];
@@ -440,7 +455,7 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
       const int col = 16 * c + 8 * hi;
-      if (q < Sb && col < hd) {
+      if (q < Sb && (FULLHD || col < hd)) {
         qf[c] = Mfma<T>::load(qbase + (int64_t)q * ss + col);
       } else {
         float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -456,13 +471,13 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
   const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc((void*)(qbase + 2 * sc), (short)0, span, 0x00020000);
   uint4 rk[KPT], rv0[VPT], rv1[VPT];
   auto load_kv = [&](int t) {  // tiles past the end read as zeros
-    const uint32_t tb = t < nkt ? (uint32_t)t * BNK * row_bytes : kFaPastEnd;
+    const uint32_t tb = t < t_hi ? (uint32_t)t * BNK * row_bytes : kFaPastEnd;
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int it = tid + i * 256, key = it / CH, c = it % CH;
       const uint32_t off = tb + (uint32_t)key * row_bytes + (uint32_t)(c * 16);
       uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsk, off, 0, 0));
-      rk[i] = c * VEC < hd ? v : make_uint4(0, 0, 0, 0);
+      rk[i] = (FULLHD || c * VEC < hd) ? v : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
@@ -471,7 +486,7 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
       const uint32_t off = tb + (uint32_t)(2 * p) * row_bytes + (uint32_t)(c * 16);
       uint4 v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsv, off, 0, 0));
       uint4 v1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsv, off + row_bytes, 0, 0));
-      const bool ok = c * VEC < hd;
+      const bool ok = FULLHD || c * VEC < hd;
       rv0[i] = ok ? v0 : make_uint4(0, 0, 0, 0);
       rv1[i] = ok ? v1 : make_uint4(0, 0, 0, 0);
     }
@@ -494,16 +509,23 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
 
   const int krow = swap_bits_2_3(l32);
   auto qk = [&](int st, f32x16 (&sa)[2]) {
+    // all K fragment reads of the tile first, then the MFMAs, so the reads'
+    // LDS latency overlaps instead of being waited out before every MFMA
+    typename Mfma<T>::frag kf[2][KC];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const T* kp = &sK[st][(kb * 32 + krow) * LDK + 8 * hi];
+#pragma unroll
+      for (int c = 0; c < KC; ++c) kf[kb][c] = Mfma<T>::load(kp + 16 * c);
+    }
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) sa[kb][r] = 0.f;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const T* kp = &sK[st][(kb * 32 + krow) * LDK + 8 * hi];
+    for (int c = 0; c < KC; ++c)
 #pragma unroll
-      for (int c = 0; c < KC; ++c) Mfma<T>::mma(sa[kb], Mfma<T>::load(kp + 16 * c), qf[c]);
-    }
+      for (int kb = 0; kb < 2; ++kb) Mfma<T>::mma(sa[kb], kf[kb][c], qf[c]);
   };
 
   f32x16 o[HB];
@@ -578,19 +600,19 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
       }
   };
 
-  load_kv(0);
-  store_kv(0);
-  load_kv(1);
-  store_kv(1);
+  load_kv(t_lo);
+  store_kv(t_lo % NST);
+  load_kv(t_lo + 1);
+  store_kv((t_lo + 1) % NST);
   __syncthreads();
 
   f32x16 scur[2];
-  if (nkt > 0) qk(0, scur);
+  if (t_hi > t_lo) qk(t_lo % NST, scur);
   // Interior tiles: every key below the workgroup's first query and inside
-  // the sequence, and a next tile exists.
-  int n_int = KEYMASK ? 0 : min(causal ? q0 / BNK : nkt, min(kend / BNK, nkt - 1));
-  n_int = max(n_int, 0);
-  int t = 0;
+  // the sequence, and a next tile exists in this item's range.
+  int n_int = KEYMASK ? 0 : min(causal ? q0 / BNK : nkt, min(kend / BNK, t_hi - 1));
+  n_int = max(n_int, t_lo);
+  int t = t_lo;
   f32x16 salt[2];
   for (; t + 1 < n_int; t += 2) {  // two tiles per trip: scores ping-pong scur <-> salt
     load_kv(t + 2);
@@ -614,10 +636,10 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
     scur[1] = salt[1];
     ++t;
   }
-  for (; t < nkt; ++t) {
+  for (; t < t_hi; ++t) {
     load_kv(t + 2);
     f32x16 snext[2];
-    const bool act_next = t + 1 < nkt && (!causal || (t + 1) * BNK <= wq0 + 31);
+    const bool act_next = t + 1 < t_hi && (!causal || (t + 1) * BNK <= wq0 + 31);
     if (act_next) qk((t + 1) % NST, snext);
     const bool act = !causal || t * BNK <= wq0 + 31;
     if (act) {
@@ -635,6 +657,23 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
   // normalise and store: register r of block hb is hd row hb*32 + 8*(r/4) + 4*hi + r%4
   const int q = wq0 + l32;
   const float l = l_run + __shfl_xor(l_run, 32, 64);
+  if (slot >= 0) {
+    // Partial of a key-split item: unnormalised O^T, running max and sum per
+    // query, merged with the other half by flash_merge_kernel.
+    float* pb = partials + (int64_t)slot * BMQ * (HDP + 2);
+    float* prow = pb + (int64_t)(wave * 32 + l32) * HDP;
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<float4*>(prow + hb * 32 + 8 * g + 4 * hi) =
+            make_float4(o[hb][4 * g], o[hb][4 * g + 1], o[hb][4 * g + 2], o[hb][4 * g + 3]);
+    if (hi == 0) {
+      pb[BMQ * HDP + wave * 32 + l32] = m_run;
+      pb[BMQ * HDP + BMQ + wave * 32 + l32] = l;
+    }
+    return;
+  }
   const float inv = l > 0.f ? 1.0f / l : 0.f;
   if (q < Sb) {
     T* orow = out + (row0 + q) * ld_out + (int64_t)h * hd;
@@ -643,13 +682,67 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int col = hb * 32 + 8 * g + 4 * hi;
-        if (col < hd) {
+        if (FULLHD || col < hd) {
           const float4 v = make_float4(o[hb][4 * g] * inv, o[hb][4 * g + 1] * inv, o[hb][4 * g + 2] * inv,
                                        o[hb][4 * g + 3] * inv);
           *reinterpret_cast<typename Quad<T>::raw*>(orow + col) = Quad<T>::from(v);
         }
       }
   }
+}
+
+// Merge of key-split work items: item halves lo / hi of query block qb of
+// (b, h) each left an unnormalised O, a running max m (raw score units) and
+// a sum l per query; the output is
+//     (O_lo a_lo + O_hi a_hi) / (l_lo a_lo + l_hi a_hi),  a_x = 2^((m_x - m) s),
+// m = max(m_lo, m_hi), always combined in this order (deterministic).
+template <typename T, int HDP>
+__global__ __launch_bounds__(256) void flash_merge_kernel(
+    const float* __restrict__ partials, const int4* __restrict__ merges, T* __restrict__ out,
+    int64_t ld_out, int H, int hd, float scale_log2, const int32_t* __restrict__ cu_seqlens) {
+  constexpr int BMQ = 128, C4 = HDP / 4;
+  const int4 mg = merges[blockIdx.x];  // (bh, qb, slot_lo, slot_hi)
+  const int b = mg.x / H, h = mg.x % H, q0 = mg.y * BMQ;
+  const int64_t row0 = cu_seqlens[b];
+  const int Sb = cu_seqlens[b + 1] - cu_seqlens[b];
+  const float* lo = partials + (int64_t)mg.z * BMQ * (HDP + 2);
+  const float* hi = partials + (int64_t)mg.w * BMQ * (HDP + 2);
+  for (int idx = threadIdx.x; idx < BMQ * C4; idx += 256) {
+    const int ql = idx / C4, c = (idx % C4) * 4;
+    if (q0 + ql >= Sb || c >= hd) continue;
+    const float m_lo = lo[BMQ * HDP + ql], m_hi = hi[BMQ * HDP + ql];
+    const float m = fmaxf(m_lo, m_hi);
+    const float a_lo = m_lo == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_lo - m) * scale_log2);
+    const float a_hi = m_hi == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_hi - m) * scale_log2);
+    const float l = fmaf(hi[BMQ * HDP + BMQ + ql], a_hi, lo[BMQ * HDP + BMQ + ql] * a_lo);
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    const float4 ol = *reinterpret_cast<const float4*>(lo + (int64_t)ql * HDP + c);
+    const float4 oh = *reinterpret_cast<const float4*>(hi + (int64_t)ql * HDP + c);
+    const float4 v = make_float4(fmaf(oh.x, a_hi, ol.x * a_lo) * inv, fmaf(oh.y, a_hi, ol.y * a_lo) * inv,
+                                 fmaf(oh.z, a_hi, ol.z * a_lo) * inv, fmaf(oh.w, a_hi, ol.w * a_lo) * inv);
+    *reinterpret_cast<typename Quad<T>::raw*>(out + (row0 + q0 + ql) * ld_out + (int64_t)h * hd + c) =
+        Quad<T>::from(v);
+  }
+}
+
+template <typename T, int HDP>
+static int launch_sched(const void* qkv, int64_t ss, int64_t sc, int64_t sh, void* out, int64_t ld_out,
+                        int B, int S, int H, int hd, float scale_log2, int causal, const int32_t* cu_seqlens,
+                        const int32_t* work, int n_work, const int32_t* merges, int n_merges, float* partials,
+                        hipStream_t st) {
+#define TJK_PIPE_SCHED(FULL)                                                                                  \
+  hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, false, FULL>), dim3((unsigned)n_work), dim3(256), 0, st,      \
+                     (const T*)qkv, (int64_t)0, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, \
+                     (const int32_t*)nullptr, (const uint8_t*)nullptr, cu_seqlens, 0,                         \
+                     reinterpret_cast<const int4*>(work), partials)
+  if (hd == HDP) TJK_PIPE_SCHED(true); else TJK_PIPE_SCHED(false);
+#undef TJK_PIPE_SCHED
+  int rc = check_launch("tjk_flash_fwd_sched");
+  if (rc != TJK_OK || n_merges == 0) return rc;
+  hipLaunchKernelGGL((flash_merge_kernel<T, HDP>), dim3((unsigned)n_merges), dim3(256), 0, st,
+                     (const float*)partials, reinterpret_cast<const int4*>(merges), (T*)out, ld_out, H, hd,
+                     scale_log2, cu_seqlens);
+  return check_launch("tjk_flash_fwd_sched (merge)");
 }
 
 template <typename T, int HDP>
@@ -660,12 +753,16 @@ static int launch_pipe(const void* qkv, int64_t sb, int64_t ss, int64_t sc, int6
   const int nqb = (S + 127) / 128;
   const int64_t nblk = (int64_t)nqb * B * H;
   if (nblk > INT32_MAX) return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd: grid too large");
-  if (key_mask != nullptr)
-    hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, true>), dim3((unsigned)nblk), dim3(256), 0, st, (const T*)qkv,
-                       sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, lengths, key_mask, cu_seqlens, nqb);
-  else
-    hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, false>), dim3((unsigned)nblk), dim3(256), 0, st, (const T*)qkv,
-                       sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, lengths, key_mask, cu_seqlens, nqb);
+#define TJK_PIPE(KM, FULL)                                                                                     \
+  hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, KM, FULL>), dim3((unsigned)nblk), dim3(256), 0, st, (const T*)qkv, \
+                     sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, lengths, key_mask,          \
+                     cu_seqlens, nqb, (const int4*)nullptr, (float*)nullptr)
+  if (key_mask != nullptr) {
+    if (hd == HDP) TJK_PIPE(true, true); else TJK_PIPE(true, false);
+  } else {
+    if (hd == HDP) TJK_PIPE(false, true); else TJK_PIPE(false, false);
+  }
+#undef TJK_PIPE
   return check_launch("tjk_flash_fwd");
 }
 
@@ -784,4 +881,64 @@ extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s
       return flash_typed<bf16>(plan_id, qkv, stride_b, stride_s, stride_c, stride_h, out, ld_out, batch, seq,
                                heads, head_dim, scale_log2, causal, lengths, key_mask, cu_seqlens, st);
   }
+}
+
+extern "C" size_t tjk_flash_partial_bytes(int head_dim, int n_slots) {
+  if (head_dim <= 0 || n_slots <= 0) return 0;
+  const int hdp = head_dim <= 32 ? 32 : head_dim <= 64 ? 64 : 128;
+  return (size_t)n_slots * 128 * (hdp + 2) * sizeof(float);
+}
+
+extern "C" int tjk_flash_fwd_sched(const void* qkv, int64_t stride_s, int64_t stride_c, int64_t stride_h,
+                                   void* out, int64_t ld_out, int batch, int max_seqlen, int heads,
+                                   int head_dim, float scale, int causal, const int32_t* cu_seqlens,
+                                   const int32_t* work, int n_work, const int32_t* merges, int n_merges,
+                                   float* partials, int dtype, void* stream) {
+  if (batch < 0 || max_seqlen < 0 || heads <= 0 || head_dim <= 0 || n_work < 0 || n_merges < 0)
+    return fail(TJK_EINVAL, "tjk_flash_fwd_sched: bad shape or counts");
+  if (n_work == 0) return TJK_OK;
+  if (!qkv || !out || !cu_seqlens || !work) return fail(TJK_EINVAL, "tjk_flash_fwd_sched: null pointer");
+  if (n_merges > 0 && (!merges || !partials)) return fail(TJK_EINVAL, "tjk_flash_fwd_sched: merges need partials");
+  if (dtype != TJK_F16 && dtype != TJK_BF16)
+    return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd_sched: 2-byte dtypes only (got %d)", dtype);
+  if (head_dim > 128 || head_dim % 8)
+    return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd_sched: head_dim=%d must be a multiple of 8 and <= 128", head_dim);
+  if (stride_s % 8 || stride_c % 8 || stride_h % 8)
+    return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd_sched: strides must be multiples of 8 elements");
+  if (((int64_t)max_seqlen * stride_s + head_dim) * 2 >= INT32_MAX)
+    return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd_sched: a sequence's K/V span exceeds 31-bit offsets");
+  if (ld_out < (int64_t)heads * head_dim || ld_out % 4) return fail(TJK_EINVAL, "tjk_flash_fwd_sched: bad ld_out");
+  if (((uintptr_t)qkv & 15) || ((uintptr_t)out & 7) || ((uintptr_t)work & 15) || ((uintptr_t)merges & 15) ||
+      ((uintptr_t)partials & 15))
+    return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd_sched: misaligned pointer");
+  if (!(scale > 0.f)) return fail(TJK_EINVAL, "tjk_flash_fwd_sched: scale must be positive");
+  const float scale_log2 = scale * 1.4426950408889634f;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+#define TJK_SCHED(TT, HDP)                                                                                  \
+  return launch_sched<TT, HDP>(qkv, stride_s, stride_c, stride_h, out, ld_out, batch, max_seqlen, heads, \
+                               head_dim, scale_log2, causal, cu_seqlens, work, n_work, merges, n_merges,  \
+                               partials, st)
+  if (dtype == TJK_F16) {
+    if (head_dim <= 32) TJK_SCHED(f16, 32);
+    if (head_dim <= 64) TJK_SCHED(f16, 64);
+    TJK_SCHED(f16, 128);
+  }
+  if (head_dim <= 32) TJK_SCHED(bf16, 32);
+  if (head_dim <= 64) TJK_SCHED(bf16, 64);
+  TJK_SCHED(bf16, 128);
+#undef TJK_SCHED
+}
+
+extern "C" int tjk_flash_sched_occupancy(int head_dim, int dtype) {
+  // Workgroups of the scheduled kernel resident per CU (LDS / register bound).
+  int blocks = 0;
+  hipError_t e = hipErrorInvalidValue;
+  const bool h16 = dtype == TJK_F16;
+#define TJK_OCC(TT, HDP) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, flash_pipe_kernel<TT, HDP, false, true>, 256, 0)
+  if (head_dim <= 32) { if (h16) TJK_OCC(f16, 32); else TJK_OCC(bf16, 32); }
+  else if (head_dim <= 64) { if (h16) TJK_OCC(f16, 64); else TJK_OCC(bf16, 64); }
+  else { if (h16) TJK_OCC(f16, 128); else TJK_OCC(bf16, 128); }
+#undef TJK_OCC
+  if (e != hipSuccess) return fail(hip_status(e), "tjk_flash_sched_occupancy: %s", hipGetErrorString(e));
+  return blocks;
 }

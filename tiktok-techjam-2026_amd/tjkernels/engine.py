@@ -48,7 +48,7 @@ from typing import Dict, List, Optional, Tuple
 
 import torch
 
-from . import ops, tiles
+from . import ops, schedule as sched_mod, tiles
 from .graphs import GraphCache
 from .plans import Plan, select_plan
 
@@ -90,6 +90,7 @@ class Packing:
     gather: torch.Tensor         # int32 [tokens]: [B*S] row of each packed row
     scatter: torch.Tensor        # int32 [B*S]: packed row of each output row, -1 = padding
     cu_seqlens: torch.Tensor     # int32 [B+1]
+    attn: Optional[object] = None  # scheduled-attention work list (built on first use)
 
 
 def build_packing(lengths: Tuple[int, ...], seq: int, device: torch.device) -> Packing:
@@ -259,6 +260,15 @@ class Engine:
         tp_out = tiles.gemm_plan(rows, d, d, cdt, epi_res, plan.gemm_out)
         tp_ffn1 = tiles.gemm_plan(rows, f, d, cdt, ops.EPI_BIAS_GELU, plan.gemm_ffn1)
         tp_ffn2 = tiles.gemm_plan(rows, d, f, cdt, epi_res, plan.gemm_ffn2)
+        # Packed 2-byte attention below 2048 keys follows a longest-first work
+        # list (tjkernels.schedule; attn_plan -1 or 4).  Longer sequences run
+        # the plain plan-1 kernel, measured faster there; other plan ids
+        # force the plain kernel.
+        use_sched = (mode == MASK_PREFIX and cdt != torch.float32 and rows > 0
+                     and (plan.attn_plan == 4 or (plan.attn_plan == -1 and max(packing.lengths) < 2048)))
+        if use_sched and packing.attn is None:
+            packing.attn = sched_mod.build_schedule(packing.lengths, heads, hd, self.causal, cdt,
+                                                    self.device)
         pending = None
         for i, lw in enumerate(self.layers):
             if i == 0:
@@ -268,7 +278,10 @@ class Engine:
                 ops.add_layernorm(res, pending, lw.ln1_w, lw.ln1_b, lw.ln1_eps, h,
                                   res_out=res if pending is not None else None)
             ops.gemm(h, lw.wqkv, lw.bqkv, qkv, ops.EPI_BIAS, tp_qkv)
-            if mode == MASK_PREFIX:
+            if mode == MASK_PREFIX and use_sched:
+                ops.flash_attention_sched(qkv.view(rows, 3, heads, hd), ctx, packing.cu_seqlens,
+                                          max(packing.lengths), packing.attn, causal=self.causal)
+            elif mode == MASK_PREFIX:
                 ops.flash_attention(qkv.view(rows, 3, heads, hd), ctx, causal=self.causal,
                                     plan=plan.attn_plan, cu_seqlens=packing.cu_seqlens,
                                     max_seqlen=max(packing.lengths))

@@ -1,0 +1,89 @@
+"""Work list of the scheduled attention kernel for packed sequences.
+
+The reference launches one program per (query block, b*h) in a fixed grid
+(tjkernels/kernels/attention.py:199-217).  With packed ragged sequences a
+causal query block's cost is its number of key tiles, which ranges from 1 to
+len/64: launched in grid order, the longest blocks set the kernel's length
+while most of the GPU idles at the end.  Here, from the host-known lengths:
+
+* every (b, h, query block of 128) is an item costing its key tiles (64 keys);
+* items are issued longest first (ties broken by (b, h, block) so the list,
+  and hence the result, is a pure function of the lengths);
+* an item costing more than ``split_factor`` times the average work per
+  resident workgroup (and at least ``min_split`` tiles) is split into two
+  halves over its key range; the halves write fp32 partials and a merge
+  launch combines them.
+
+Measured on MI355X at the packed C4 lengths (bf16, hd 64): grid order
+45.6 us, longest first 40.1 us, longest first with every item above the
+average split (192 splits) 51 us -- the kernel is throughput-bound (the
+softmax VALU work of a 64-key tile is about twice its MFMA time), so splits
+only add partial traffic and a launch.  ``split_factor`` = 2 keeps splitting
+for lists dominated by a few very long items.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import List, Sequence, Tuple
+
+import torch
+
+BMQ, BNK = 128, 64
+
+
+@dataclass
+class AttentionSchedule:
+    work: torch.Tensor      # int32 [n_work, 4]: (b*H + h, qb, t_lo | t_hi << 16, slot)
+    merges: torch.Tensor    # int32 [n_merges, 4]: (b*H + h, qb, slot_lo, slot_hi)
+    n_slots: int
+    partials: torch.Tensor  # fp32 scratch for the split halves
+    max_item: int           # largest item, in key tiles
+    total: int              # key tiles over all items
+
+
+def build_items(lengths: Sequence[int], heads: int, causal: bool, slots: int, min_split: int = 6,
+                split_factor: float = 2.0) -> Tuple[List[Tuple[int, int, int, int, int, int]],
+                                                    List[Tuple[int, int, int, int]], int]:
+    items = []
+    for b, n in enumerate(lengths):
+        for qb in range((n + BMQ - 1) // BMQ):
+            kend = min((qb + 1) * BMQ, n) if causal else n
+            nkt = (kend + BNK - 1) // BNK
+            for h in range(heads):
+                items.append((nkt, b * heads + h, qb))
+    total = sum(c for c, _, _ in items)
+    target = max(split_factor * total / max(slots, 1), float(min_split))
+    work, merges, n_slots = [], [], 0
+    for nkt, bh, qb in items:
+        if nkt > target:
+            mid = nkt // 2
+            work.append((mid, bh, qb, 0, mid, n_slots))
+            work.append((nkt - mid, bh, qb, mid, nkt, n_slots + 1))
+            merges.append((bh, qb, n_slots, n_slots + 1))
+            n_slots += 2
+        else:
+            work.append((nkt, bh, qb, 0, nkt, -1))
+    work.sort(key=lambda w: (-w[0], w[1], w[2], w[3]))
+    return work, merges, n_slots
+
+
+def build_schedule(lengths: Sequence[int], heads: int, head_dim: int, causal: bool,
+                   dtype: torch.dtype, device: torch.device, slots: int = 0,
+                   min_split: int = 6, split_factor: float = 2.0) -> AttentionSchedule:
+    """``slots`` (resident workgroups) defaults to CUs x the kernel's occupancy."""
+    from . import _lib
+    lib = _lib.load()
+    if slots <= 0:
+        occ = lib.tjk_flash_sched_occupancy(head_dim, _lib.DTYPE_CODES[dtype])
+        _lib.check(0 if occ > 0 else (occ or -1), "tjk_flash_sched_occupancy")
+        slots = occ * torch.cuda.get_device_properties(device).multi_processor_count
+    work, merges, n_slots = build_items(lengths, heads, causal, slots, min_split, split_factor)
+    w = torch.tensor([(bh, qb, lo | (hi << 16), slot) for _, bh, qb, lo, hi, slot in work] or [(0, 0, 0, -1)],
+                     dtype=torch.int32)[:len(work)]
+    m = torch.tensor(merges or [(0, 0, 0, 0)], dtype=torch.int32)[:len(merges)]
+    nbytes = lib.tjk_flash_partial_bytes(head_dim, max(n_slots, 1))
+    return AttentionSchedule(work=w.contiguous().to(device), merges=m.contiguous().to(device), n_slots=n_slots,
+                             partials=torch.empty(nbytes // 4, dtype=torch.float32, device=device),
+                             max_item=max((c for c, *_ in work), default=0),
+                             total=sum(c for c, *_ in work))
