@@ -184,6 +184,15 @@ def test_graph_equals_eager(device, dtype):
     eager = _module(cfg, UserOptimizedTransformer(cfg).state_dict(), dtype, device)
     graphed = _module(cfg, eager.state_dict(), dtype, device)
     cases = [_inputs(cfg, dtype, seed=50 + i, padding=0.3 * (i % 2)) for i in range(4)]
+    # two non-prefix (GENERAL) masks: the captured attention reads the mask
+    # from a static buffer the engine refreshes before every replay
+    g = torch.Generator()
+    g.manual_seed(7)
+    for _ in range(2):
+        m = torch.rand(cfg.batch_size, cfg.seq_len, generator=g) > 0.3
+        m[:, 0] = True
+        x = torch.randn(cfg.batch_size, cfg.seq_len, cfg.d_model, generator=g).masked_fill(~m[..., None], 0)
+        cases.append((x.to(dtype), m))
     plans_mod.set_override(Plan(compute_dtype=dtype, cuda_graph=False, label="eager"))
     try:
         with torch.inference_mode():

@@ -106,6 +106,33 @@ def build_packing(lengths: Tuple[int, ...], seq: int, device: torch.device) -> P
 
 
 @dataclass
+class _Fwd:
+    """Static context of one forward shape: workspace views of the processed
+    rows, tile plans, masks and the packing it runs on."""
+
+    batch: int
+    seq: int
+    mode: int
+    packing: Optional[Packing]
+    rows: int
+    gather: Optional[torch.Tensor] = None
+    scatter: Optional[torch.Tensor] = None
+    key_mask: Optional[torch.Tensor] = None
+    row_mask: Optional[torch.Tensor] = None
+    res: Optional[torch.Tensor] = None
+    h: Optional[torch.Tensor] = None
+    qkv: Optional[torch.Tensor] = None
+    ctx: Optional[torch.Tensor] = None
+    mid: Optional[torch.Tensor] = None
+    delta: Optional[torch.Tensor] = None
+    tp_qkv: int = -1
+    tp_out: int = -1
+    tp_ffn1: int = -1
+    tp_ffn2: int = -1
+    use_sched: bool = False
+
+
+@dataclass
 class Workspace:
     res: torch.Tensor    # [T, d] fp32
     h: torch.Tensor      # [T, d] compute dtype
@@ -137,6 +164,8 @@ class Engine:
         self._mask_modes = _WeakDict()
         self._workspaces: Dict[Tuple, Workspace] = {}
         self._packings: "OrderedDict[Tuple[int, Tuple[int, ...]], Packing]" = OrderedDict()
+        self._static_masks: Dict[Tuple[int, int], torch.Tensor] = {}
+        self._fwds: Dict[Tuple, "_Fwd"] = {}
 
     # ------------------------------------------------------------- weights
 
@@ -172,6 +201,7 @@ class Engine:
         self.final_ln = (fn.weight.float().contiguous(), fn.bias.float().contiguous(), fn.eps)
         self._built_for = key
         self._graphs.clear()
+        self._fwds.clear()
         self._workspaces.clear()
 
     def _workspace(self, batch: int, seq: int, plan: Plan) -> Workspace:
@@ -230,79 +260,104 @@ class Engine:
 
     # ------------------------------------------------------------- compute
 
-    def _forward_impl(self, x: torch.Tensor, mask: Optional[torch.Tensor], mode: int,
-                      packing: Optional[Packing] = None) -> torch.Tensor:
+    def _prepare(self, batch: int, seq: int, mode: int, packing: Optional[Packing],
+                 mask: Optional[torch.Tensor]) -> "_Fwd":
+        """Everything a forward needs besides x and the output: workspace
+        views, tile plans, the attention schedule.  Launches nothing except
+        the one-time tile timing / schedule build of a new shape."""
         plan = self.plan
         assert plan is not None and self.final_ln is not None
-        batch, seq, d = x.shape
-        t = batch * seq
         ws = self._workspace(batch, seq, plan)
-        x2 = x.reshape(t, d)
-        out = torch.empty((batch, seq, d), dtype=self.dtype, device=x.device)
-        heads, hd = self.num_heads, self.head_dim
-        row_mask = None
-        key_mask = None
-        gather = scatter = None
-        rows = t
+        fw = _Fwd(batch=batch, seq=seq, mode=mode, packing=packing, rows=batch * seq)
         if mode == MASK_PREFIX:
             assert packing is not None
-            rows, gather, scatter = packing.tokens, packing.gather, packing.scatter
+            fw.rows, fw.gather, fw.scatter = packing.tokens, packing.gather, packing.scatter
         elif mode == MASK_GENERAL:
-            row_mask = mask.reshape(t)
-            key_mask = mask
-        res, h, qkv, ctx, mid = ws.res[:rows], ws.h[:rows], ws.qkv[:rows], ws.ctx[:rows], ws.mid[:rows]
-        delta = None if ws.delta is None else ws.delta[:rows]
-        fused = plan.residual_epilogue
+            fw.key_mask = mask
+            fw.row_mask = mask.reshape(-1)
+        rows = fw.rows
+        fw.res, fw.h, fw.qkv, fw.ctx, fw.mid = (ws.res[:rows], ws.h[:rows], ws.qkv[:rows],
+                                                ws.ctx[:rows], ws.mid[:rows])
+        fw.delta = None if ws.delta is None else ws.delta[:rows]
         # Tile plans: forced by the Plan, else measured once per shape.
         cdt, d, f = plan.compute_dtype, self.d_model, self.ffn_dim
-        epi_res = ops.EPI_BIAS_RESIDUAL if fused else ops.EPI_BIAS
-        tp_qkv = tiles.gemm_plan(rows, 3 * d, d, cdt, ops.EPI_BIAS, plan.gemm_qkv)
-        tp_out = tiles.gemm_plan(rows, d, d, cdt, epi_res, plan.gemm_out)
-        tp_ffn1 = tiles.gemm_plan(rows, f, d, cdt, ops.EPI_BIAS_GELU, plan.gemm_ffn1)
-        tp_ffn2 = tiles.gemm_plan(rows, d, f, cdt, epi_res, plan.gemm_ffn2)
+        epi_res = ops.EPI_BIAS_RESIDUAL if plan.residual_epilogue else ops.EPI_BIAS
+        fw.tp_qkv = tiles.gemm_plan(rows, 3 * d, d, cdt, ops.EPI_BIAS, plan.gemm_qkv)
+        fw.tp_out = tiles.gemm_plan(rows, d, d, cdt, epi_res, plan.gemm_out)
+        fw.tp_ffn1 = tiles.gemm_plan(rows, f, d, cdt, ops.EPI_BIAS_GELU, plan.gemm_ffn1)
+        fw.tp_ffn2 = tiles.gemm_plan(rows, d, f, cdt, epi_res, plan.gemm_ffn2)
         # Packed 2-byte attention below 2048 keys follows a longest-first work
         # list (tjkernels.schedule; attn_plan -1 or 4).  Longer sequences run
         # the plain plan-1 kernel, measured faster there; other plan ids
         # force the plain kernel.
-        use_sched = (mode == MASK_PREFIX and cdt != torch.float32 and rows > 0
-                     and (plan.attn_plan == 4 or (plan.attn_plan == -1 and max(packing.lengths) < 2048)))
-        if use_sched and packing.attn is None:
-            packing.attn = sched_mod.build_schedule(packing.lengths, heads, hd, self.causal, cdt,
-                                                    self.device)
+        fw.use_sched = (mode == MASK_PREFIX and cdt != torch.float32 and rows > 0
+                        and (plan.attn_plan == 4 or (plan.attn_plan == -1 and max(packing.lengths) < 2048)))
+        if fw.use_sched and packing.attn is None:
+            packing.attn = sched_mod.build_schedule(packing.lengths, self.num_heads, self.head_dim,
+                                                    self.causal, cdt, self.device)
+        return fw
+
+    def _first(self, fw: "_Fwd", x: torch.Tensor) -> None:
+        """Layer-0 LN1: reads x (packing it under a prefix mask), writes the
+        fp32 residual and h."""
+        lw = self.layers[0]
+        ops.add_layernorm(x.reshape(fw.batch * fw.seq, self.d_model), None, lw.ln1_w, lw.ln1_b,
+                          lw.ln1_eps, fw.h, res_out=fw.res, row_index=fw.gather)
+
+    def _body(self, fw: "_Fwd") -> None:
+        """Every layer between the first LayerNorm and the final one: the
+        part the hipGraph captures (fixed buffers only)."""
+        plan = self.plan
+        heads, hd, rows = self.num_heads, self.head_dim, fw.rows
+        res, h, qkv, ctx, mid, delta = fw.res, fw.h, fw.qkv, fw.ctx, fw.mid, fw.delta
+        fused = plan.residual_epilogue
         pending = None
         for i, lw in enumerate(self.layers):
-            if i == 0:
-                ops.add_layernorm(x2, None, lw.ln1_w, lw.ln1_b, lw.ln1_eps, h, res_out=res,
-                                  row_index=gather)
-            else:
+            if i > 0:
                 ops.add_layernorm(res, pending, lw.ln1_w, lw.ln1_b, lw.ln1_eps, h,
                                   res_out=res if pending is not None else None)
-            ops.gemm(h, lw.wqkv, lw.bqkv, qkv, ops.EPI_BIAS, tp_qkv)
-            if mode == MASK_PREFIX and use_sched:
-                ops.flash_attention_sched(qkv.view(rows, 3, heads, hd), ctx, packing.cu_seqlens,
-                                          max(packing.lengths), packing.attn, causal=self.causal)
-            elif mode == MASK_PREFIX:
+            ops.gemm(h, lw.wqkv, lw.bqkv, qkv, ops.EPI_BIAS, fw.tp_qkv)
+            if fw.use_sched:
+                pk = fw.packing
+                ops.flash_attention_sched(qkv.view(rows, 3, heads, hd), ctx, pk.cu_seqlens,
+                                          max(pk.lengths), pk.attn, causal=self.causal)
+            elif fw.mode == MASK_PREFIX:
+                pk = fw.packing
                 ops.flash_attention(qkv.view(rows, 3, heads, hd), ctx, causal=self.causal,
-                                    plan=plan.attn_plan, cu_seqlens=packing.cu_seqlens,
-                                    max_seqlen=max(packing.lengths))
+                                    plan=plan.attn_plan, cu_seqlens=pk.cu_seqlens,
+                                    max_seqlen=max(pk.lengths))
             else:
-                ops.flash_attention(qkv.view(batch, seq, 3, heads, hd), ctx, causal=self.causal,
-                                    key_mask=key_mask, plan=plan.attn_plan)
+                ops.flash_attention(qkv.view(fw.batch, fw.seq, 3, heads, hd), ctx, causal=self.causal,
+                                    key_mask=fw.key_mask, plan=plan.attn_plan)
             if fused:
-                ops.gemm(ctx, lw.wo, lw.bo, res, ops.EPI_BIAS_RESIDUAL, tp_out)
+                ops.gemm(ctx, lw.wo, lw.bo, res, ops.EPI_BIAS_RESIDUAL, fw.tp_out)
                 ops.add_layernorm(res, None, lw.ln2_w, lw.ln2_b, lw.ln2_eps, h)
             else:
-                ops.gemm(ctx, lw.wo, lw.bo, delta, ops.EPI_BIAS, tp_out)
+                ops.gemm(ctx, lw.wo, lw.bo, delta, ops.EPI_BIAS, fw.tp_out)
                 ops.add_layernorm(res, delta, lw.ln2_w, lw.ln2_b, lw.ln2_eps, h, res_out=res)
-            ops.gemm(h, lw.w1, lw.b1, mid, ops.EPI_BIAS_GELU, tp_ffn1)
+            ops.gemm(h, lw.w1, lw.b1, mid, ops.EPI_BIAS_GELU, fw.tp_ffn1)
             if fused:
-                ops.gemm(mid, lw.w2, lw.b2, res, ops.EPI_BIAS_RESIDUAL, tp_ffn2)
+                ops.gemm(mid, lw.w2, lw.b2, res, ops.EPI_BIAS_RESIDUAL, fw.tp_ffn2)
             else:
-                ops.gemm(mid, lw.w2, lw.b2, delta, ops.EPI_BIAS, tp_ffn2)
-                pending = delta
-        fw, fb, feps = self.final_ln
-        ops.add_layernorm(res, pending, fw, fb, feps, out.view(t, d), row_mask=row_mask,
-                          row_index=scatter)
+                ops.gemm(mid, lw.w2, lw.b2, delta, ops.EPI_BIAS, fw.tp_ffn2)
+                pending = delta  # added by the next LayerNorm (deferred residual)
+
+    def _final(self, fw: "_Fwd", out: torch.Tensor, row_mask: Optional[torch.Tensor]) -> None:
+        """Final LayerNorm into the output, padded rows as exact zeros."""
+        fwt, fb, feps = self.final_ln
+        pending = None if self.plan.residual_epilogue else fw.delta
+        ops.add_layernorm(fw.res, pending, fwt, fb, feps, out.view(fw.batch * fw.seq, self.d_model),
+                          row_mask=row_mask, row_index=fw.scatter)
+
+    def _forward_impl(self, x: torch.Tensor, mask: Optional[torch.Tensor], mode: int,
+                      packing: Optional[Packing] = None) -> torch.Tensor:
+        """Eager forward (no graph)."""
+        batch, seq, d = x.shape
+        fw = self._prepare(batch, seq, mode, packing, mask)
+        out = torch.empty((batch, seq, d), dtype=self.dtype, device=x.device)
+        self._first(fw, x)
+        self._body(fw)
+        self._final(fw, out, fw.row_mask)
         return out
 
     # ---------------------------------------------------------------- call
@@ -353,15 +408,45 @@ class Engine:
             mode, lens = self._mask_info(mask)
         packing = self._packing(lens, x.shape[1]) if mode == MASK_PREFIX else None
         if plan.cuda_graph:
-            # A packed forward is specific to its lengths (its launches are
-            # sized by them), so they are part of the key; the graph keeps
-            # the row maps it reads alive.
-            key = (tuple(x.shape), x.dtype, mode, lens, plan)
-            graph = self._graphs.get(key, lambda gx, gm: self._forward_impl(gx, gm, mode, packing),
-                                     x, mask, keepalive=packing)
-            if graph is not None:
-                return graph.run(x, mask)
+            return self._forward_graph(x, mask, mode, lens, packing)
         return self._forward_impl(x, mask, mode, packing)
+
+    def _forward_graph(self, x: torch.Tensor, mask: Optional[torch.Tensor], mode: int,
+                       lens: Optional[Tuple[int, ...]], packing: Optional[Packing]) -> torch.Tensor:
+        """The first LayerNorm (which reads the caller's x) and the final one
+        (which writes a fresh output tensor) run eagerly; the layers between
+        them replay as one hipGraph on fixed workspace buffers.  So no copy
+        of x into a static input and no clone of a static output is needed
+        (the reference copies in and clones out, graphs.py:57-64); only a
+        GENERAL mask, which the captured attention reads, is copied into a
+        static buffer.  A packed forward is specific to its lengths (its
+        launches are sized by them), so they are part of the key; the graph
+        keeps the row maps and schedule it reads alive."""
+        batch, seq, d = x.shape
+        static_mask = None
+        if mode == MASK_GENERAL:
+            static_mask = self._static_masks.get((batch, seq))
+            if static_mask is None:
+                static_mask = torch.empty((batch, seq), dtype=torch.bool, device=x.device)
+                self._static_masks[(batch, seq)] = static_mask
+        key = (batch, seq, x.dtype, mode, lens, self.plan)
+        fw = self._fwds.get(key)
+        if fw is None:
+            fw = self._prepare(batch, seq, mode, packing, static_mask)
+            self._fwds[key] = fw
+        graph = self._graphs.get(key, lambda: self._body(fw), keepalive=(packing, fw))
+        self._first(fw, x)
+        if graph is not None:
+            if static_mask is not None:
+                static_mask.copy_(mask)
+            graph.replay()
+        else:
+            if static_mask is not None:
+                static_mask.copy_(mask)
+            self._body(fw)
+        out = torch.empty((batch, seq, d), dtype=self.dtype, device=x.device)
+        self._final(fw, out, None if mask is None or mode != MASK_GENERAL else mask.reshape(-1))
+        return out
 
 
 def get_engine(module: torch.nn.Module) -> Engine:

@@ -1,13 +1,16 @@
-"""Whole-forward hipGraph capture.
+"""hipGraph capture of the forward's layer body.
 
 Mirrors the reference's graph layer (tjkernels/graphs.py:30-91): one captured
-forward per (shape, dtype, mask mode); every call copies the live input (and
-mask) into the captured static buffers, replays, and returns a clone of the
-static output, so results are correct for any input and the caller always
-gets a fresh tensor.  On ROCm ``torch.cuda.CUDAGraph`` is a hipGraph; the
-tjk kernels launch on torch's current stream, which is the capture stream
-inside ``torch.cuda.graph``.  Every tjk entry point is capture-safe (no
-allocation, no host sync, no memset).
+graph per (shape, dtype, mask mode, prefix lengths, plan), replayed on every
+call.  The reference captures the whole forward and copies the live input
+into a static buffer and clones the static output (graphs.py:57-64); here
+the engine runs the first LayerNorm (reading the caller's x) and the final
+one (writing a fresh output) eagerly around the replay, so neither copy is
+needed and the caller still always gets a fresh tensor.  On ROCm
+``torch.cuda.CUDAGraph`` is a hipGraph; the tjk kernels launch on torch's
+current stream, which is the capture stream inside ``torch.cuda.graph``.
+Every tjk entry point is capture-safe (no allocation, no host sync, no
+memset).
 """
 
 from __future__ import annotations
@@ -28,31 +31,29 @@ def _warn_once(msg: str) -> None:
 
 
 class CapturedGraph:
-    """One captured forward bound to one input shape / dtype / mask mode."""
+    """One captured launch sequence bound to fixed buffers.
 
-    def __init__(self, fn: Callable[[torch.Tensor, Optional[torch.Tensor]], torch.Tensor],
-                 x: torch.Tensor, mask: Optional[torch.Tensor], warmup: int = 2) -> None:
-        self.static_x = x.clone()
-        self.static_mask = None if mask is None else mask.clone()
-        # Warm up on a side stream (default priority) so lazily created
-        # state exists before capture, as torch requires.
-        side = torch.cuda.Stream(device=x.device)
-        side.wait_stream(torch.cuda.current_stream(x.device))
+    ``fn`` enqueues the work on the current stream and reads / writes only
+    buffers that outlive the graph.  It runs once on a side stream (default
+    priority) so lazily created state exists before capture, as torch
+    requires, then is captured; ``replay`` launches it on the current stream.
+    """
+
+    def __init__(self, fn: Callable[[], None], device: torch.device, warmup: int = 1) -> None:
+        side = torch.cuda.Stream(device=device)
+        side.wait_stream(torch.cuda.current_stream(device))
         with torch.cuda.stream(side):
             for _ in range(warmup):
-                fn(self.static_x, self.static_mask)
-        torch.cuda.current_stream(x.device).wait_stream(side)
-        torch.cuda.synchronize(x.device)
+                fn()
+        torch.cuda.current_stream(device).wait_stream(side)
+        torch.cuda.synchronize(device)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
-            self.static_out = fn(self.static_x, self.static_mask)
+            fn()
+        self.keepalive = None
 
-    def run(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
-        self.static_x.copy_(x)
-        if self.static_mask is not None and mask is not None:
-            self.static_mask.copy_(mask)
+    def replay(self) -> None:
         self.graph.replay()
-        return self.static_out.clone()
 
 
 class GraphCache:
@@ -64,13 +65,15 @@ class GraphCache:
         self._graphs: "OrderedDict[Tuple, Optional[CapturedGraph]]" = OrderedDict()
         self.max_entries = max_entries
 
-    def get(self, key: Tuple, fn, x: torch.Tensor, mask: Optional[torch.Tensor],
+    def get(self, key: Tuple, fn: Callable[[], None], device: Optional[torch.device] = None,
             keepalive: object = None) -> Optional[CapturedGraph]:
         if key in self._graphs:
             self._graphs.move_to_end(key)
             return self._graphs[key]
         try:
-            graph = CapturedGraph(fn, x, mask)
+            if device is None:
+                device = torch.device("cuda", torch.cuda.current_device())
+            graph = CapturedGraph(fn, device)
             graph.keepalive = keepalive  # device buffers the captured kernels read
         except Exception as exc:  # capture is an optimisation; eager HIP still runs
             _warn_once(f"hipGraph capture failed ({exc}); running eager.")
