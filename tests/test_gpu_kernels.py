@@ -115,7 +115,7 @@ def _gemm_case(device, m, n, k, dt, epi, plan, seed=0):
 
 # Plans of the staged kernel take any K % 8 == 0; direct-to-LDS plans need
 # K % 64 == 0 (bf16/fp16) and reject other K with TJK_EUNSUPPORTED.
-STAGED16, DTL16, DTL16_K32 = range(0, 6), range(6, 16), ()
+STAGED16, DTL16, DTL16_K32 = range(0, 6), range(6, 18), ()
 STAGED32, DTL32 = range(0, 2), range(2, 5)
 
 

@@ -301,8 +301,8 @@ typedef __attribute__((address_space(3))) void lds_void;
 // Byte offset that lies beyond any buffer descriptor range used here.
 constexpr int kPastEnd = 0x7fff0000;
 
-template <typename T, int BM, int BN, int WM, int WN, int BKB, int STAGES, int EPI>
-__global__ __launch_bounds__(WM * WN * 64) void gemm_dtl_kernel(
+template <typename T, int BM, int BN, int WM, int WN, int BKB, int STAGES, int EPI, int KSPLIT>
+__global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
     const T* __restrict__ A, int64_t lda, const T* __restrict__ W, int64_t ldw,
     const T* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K) {
   constexpr bool SCHED = sizeof(T) == 2;
@@ -320,12 +320,16 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_dtl_kernel(
   static_assert(DA * RPI * NW == BM && DW * RPI * NW == BN, "tile rows must split over the waves");
   static_assert(STAGES >= 2 && (STAGES - 2) * NDMA <= 63, "vmcnt range");
 
-  __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE];
+  __shared__ __attribute__((aligned(1024))) char smem[KSPLIT * STAGES * STAGE];
 
+  // K split inside the workgroup: KSPLIT groups of WM x WN waves, group kg
+  // streaming K tiles kg, kg + KSPLIT, ... through its own LDS ring; the
+  // groups' accumulators are summed (in group order) before the epilogue.
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, kg = (tid >> 6) / NW, wave = (tid >> 6) % NW;
   const int wm = wave / WN, wn = wave % WN;
   const int l32 = lane & 31, hi = lane >> 5;
+  char* const gsm = smem + kg * (STAGES * STAGE);
 
   int pid_m, pid_n;
   tile_coords(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, pid_m, pid_n);
@@ -354,8 +358,10 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_dtl_kernel(
     voff_w[i] = (uint32_t)(r * ldw * (int64_t)sizeof(T)) + (uint32_t)(((lane % CPR) ^ swz<BKB>(r)) << 4);
   }
   const int nk = K / BK;
-  auto issue = [&](int kt) {  // DMA of tile kt into its ring slot (nothing past the end)
-    char* sb = smem + (kt % STAGES) * STAGE;
+  const int nit = (nk + KSPLIT - 1) / KSPLIT;  // ring steps per group
+  auto issue = [&](int it) {  // DMA of this group's step it into its slot (nothing past the end)
+    char* sb = gsm + (it % STAGES) * STAGE;
+    const int kt = it * KSPLIT + kg;
     const uint32_t kb = kt < nk ? (uint32_t)(kt * BKB) : (uint32_t)kPastEnd;
 #pragma unroll
     for (int i = 0; i < DA; ++i)
@@ -393,14 +399,14 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_dtl_kernel(
 #pragma unroll
   for (int t = 0; t < STAGES - 1; ++t) issue(t);
   typename Mfma<T>::frag fa[2][FM], fw[2][FN];
-  for (int kt = 0; kt < nk; ++kt) {
-    // My DMAs of tile kt have landed, then everyone's (and tile kt-1 is
+  for (int kt = 0; kt < nit; ++kt) {
+    // My DMAs of step kt have landed, then everyone's (and step kt-1 is
     // retired by every wave).  Inline asm with a memory clobber keeps the
     // compiler from moving LDS accesses across either instruction; a
     // __syncthreads() would instead wait for every DMA in flight.
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"((STAGES - 2) * NDMA) : "memory");
     asm volatile("s_barrier" ::: "memory");
-    const char* st = smem + (kt % STAGES) * STAGE;
+    const char* st = gsm + (kt % STAGES) * STAGE;
     const char* sa = st + (wm * WTM + l32) * BKB;
     const char* sw_ = st + BM * BKB + (wn * WTN + l32) * BKB;
 #pragma unroll
@@ -436,13 +442,40 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_dtl_kernel(
     }
   }
 
-  // Reuse LDS for the epilogue once every DMA (including the ones issued
-  // past the last tile) has landed and every wave is done reading.
-  static_assert(NW * EpiStage<T, EPI, FN>::BYTES <= STAGES * STAGE, "epilogue staging exceeds LDS");
+  // Reuse LDS once every DMA (including the ones issued past the last
+  // tile) has landed and every wave is done reading.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+  constexpr int ACCF = FN * FM * 16;                   // accumulator floats per lane
+  constexpr int XCH = (KSPLIT - 1) * NW * ACCF * 64 * 4;  // exchange bytes
+  static_assert(XCH + NW * EpiStage<T, EPI, FN>::BYTES <= KSPLIT * STAGES * STAGE,
+                "K-split exchange + epilogue staging exceed LDS");
+  if constexpr (KSPLIT > 1) {
+    float* xch = reinterpret_cast<float*>(smem);
+    if (kg > 0) {
+      float* my = xch + (int64_t)((kg - 1) * NW + wave) * ACCF * 64;
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) my[((i * FM + j) * 16 + r) * 64 + lane] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (kg > 0) return;
+#pragma unroll
+    for (int p = 1; p < KSPLIT; ++p) {
+      const float* ot = xch + (int64_t)((p - 1) * NW + wave) * ACCF * 64;
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] += ot[((i * FM + j) * 16 + r) * 64 + lane];
+    }
+  }
   epilogue<T, EPI, FM, FN>(acc, bias, Cv, ldc, M, N, m0 + wm * WTM, n0 + wn * WTN, lane,
-                           smem + wave * EpiStage<T, EPI, FN>::BYTES);
+                           smem + XCH + wave * EpiStage<T, EPI, FN>::BYTES);
 }
 
 // ------------------------------------------------------------------ plans
@@ -451,7 +484,8 @@ enum { kStaged = 0, kDtl = 1 };
 
 struct GemmPlan {
   int kind, bm, bn, wm, wn, bkb, stages;
-  double eff;  // prior used by auto_plan
+  double eff;      // prior used by auto_plan
+  int ksplit = 1;  // K groups per workgroup (direct-to-LDS kernel)
 };
 
 // 2-byte types (bf16/fp16), BK = 64.  Measured on MI355X (bf16, C4/C5
@@ -476,6 +510,13 @@ static const GemmPlan kPlans16[] = {
     {kDtl, 192, 256, 2, 4, 128, 2, 0.90},     // 13 8 waves, wave tile 96x64
     {kDtl, 192, 384, 2, 4, 128, 2, 0.95},     // 14 8 waves, wave tile 96x96
     {kDtl, 96, 128, 1, 4, 128, 2, 0.60},      // 15 wave tile 96x32, small M
+    // 16, 17: two K groups of 4 waves per workgroup (K tiles alternate between
+    // the groups' LDS rings, partial sums added before the epilogue).  At the
+    // packed C4 N=1024 projections they measured slower than plan 15 (FFN2
+    // 60.4 vs 57.8 us): those GEMMs are partly bound by re-reading A from
+    // the MALL, which splitting K does not change.
+    {kDtl, 192, 128, 2, 2, 128, 2, 0.85, 2},  // 16 wave tile 96x64
+    {kDtl, 128, 128, 2, 2, 128, 2, 0.85, 2},  // 17 wave tile 64x64
 };
 // fp32.
 static const GemmPlan kPlans32[] = {
@@ -540,12 +581,13 @@ template <> struct Launcher<kStaged> {
                        (const T*)w, ldw, (const T*)bias, c, ldc, M, N, K);
   }
 };
-template <int BKB, int STAGES> struct DtlLauncher {
+template <int BKB, int STAGES, int KSPLIT = 1> struct DtlLauncher {
   template <typename T, int BM, int BN, int WM, int WN, int EPI>
   static void go(dim3 grid, hipStream_t s, const void* a, int64_t lda, const void* w, int64_t ldw,
                  const void* bias, void* c, int64_t ldc, int M, int N, int K) {
-    hipLaunchKernelGGL((gemm_dtl_kernel<T, BM, BN, WM, WN, BKB, STAGES, EPI>), grid, dim3(WM * WN * 64), 0, s,
-                       (const T*)a, lda, (const T*)w, ldw, (const T*)bias, c, ldc, M, N, K);
+    hipLaunchKernelGGL((gemm_dtl_kernel<T, BM, BN, WM, WN, BKB, STAGES, EPI, KSPLIT>), grid,
+                       dim3(WM * WN * KSPLIT * 64), 0, s, (const T*)a, lda, (const T*)w, ldw, (const T*)bias, c,
+                       ldc, M, N, K);
   }
 };
 
@@ -577,6 +619,7 @@ static int run_gemm(int plan, int epi, const void* a, int64_t lda, const void* w
                     void* c, int64_t ldc, int M, int N, int K, hipStream_t s) {
   typedef Launcher<kStaged> St;
   typedef DtlLauncher<128, 2> D2;
+  typedef DtlLauncher<128, 2, 2> D2K2;
 #define TJK_GEMM_CASE(ID, L, BM, BN, WM, WN) \
   case ID: launch_epi<L, T, BM, BN, WM, WN>(epi, a, lda, w, ldw, bias, c, ldc, M, N, K, s); break;
   if constexpr (sizeof(T) == 4) {
@@ -605,6 +648,8 @@ static int run_gemm(int plan, int epi, const void* a, int64_t lda, const void* w
       TJK_GEMM_CASE(13, D2, 192, 256, 2, 4)
       TJK_GEMM_CASE(14, D2, 192, 384, 2, 4)
       TJK_GEMM_CASE(15, D2, 96, 128, 1, 4)
+      TJK_GEMM_CASE(16, D2K2, 192, 128, 2, 2)
+      TJK_GEMM_CASE(17, D2K2, 128, 128, 2, 2)
     }
   }
 #undef TJK_GEMM_CASE
@@ -647,7 +692,7 @@ extern "C" int tjk_gemm_plan_info(int dtype, int id, int* block_m, int* block_n,
   if (id < 0 || id >= count) return fail(TJK_EINVAL, "tjk_gemm_plan_info: plan %d out of range", id);
   if (block_m) *block_m = p[id].bm;
   if (block_n) *block_n = p[id].bn;
-  if (waves) *waves = p[id].wm * p[id].wn;
+  if (waves) *waves = p[id].wm * p[id].wn * p[id].ksplit;
   return TJK_OK;
 }
 

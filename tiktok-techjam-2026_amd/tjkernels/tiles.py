@@ -8,7 +8,9 @@ round).  No fixed table covers that, so the first time a projection shape is
 seen its candidate tile plans are timed on scratch operands of that exact
 shape (HIP events on the current stream) and the fastest is kept for the
 rest of the process.  Every candidate accumulates each output element over
-K in the same order, so the choice changes speed, not results.
+K in the same order, so the choice changes speed, not results.  (The
+K-split plans 16 / 17 add two half-K partial sums instead; they measured
+no faster on the BASELINE shapes and are only used when a Plan forces them.)
 
 This replaces the reference's static per-shape table lookup for the GEMM
 part of a plan (tjkernels/plans.py:147-170); plan ids >= 0 in a ``Plan``
