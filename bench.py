@@ -84,7 +84,7 @@ def _breakdown(engine, x, mask):
     by HIP events on the current stream (the launch stream).  Also returns,
     per class, the exact call of its last launch so it can be replayed."""
     import torch
-    from tjkernels import ops
+    from tjkernels import ops, timing
     classes, calls = {}, {}
     orig = {name: getattr(ops, name) for name in ("gemm", "flash_attention", "flash_attention_sched",
                                                   "add_layernorm")}
@@ -127,6 +127,10 @@ def _breakdown(engine, x, mask):
     try:
         for _ in range(3):  # warm, then keep the last pass
             events.clear()
+            torch.cuda.synchronize()
+            # queue the whole forward behind a spin kernel so each launch's
+            # events read its GPU time, not the host's launch overhead
+            timing.queue_ahead(5.0)
             engine._forward_impl(x, mask, mode, packing)
         torch.cuda.synchronize()
     finally:
@@ -149,19 +153,15 @@ def _breakdown(engine, x, mask):
 
 def _kernel_avg_ms(call, reps=50):
     """Average duration of one launch of a kernel class: its recorded call
-    replayed `reps` times back to back, HIP events on the launch stream."""
+    replayed `reps` times back to back (queued behind a spin kernel, so the
+    host's launch rate does not enter), HIP events on the launch stream."""
     import torch
+    from tjkernels import timing
     fn, a, k = call
     for _ in range(5):
         fn(*a, **k)
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        fn(*a, **k)
-    e1.record()
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / reps
+    return timing.launch_ms(lambda: fn(*a, **k), reps)
 
 
 def _traffic(label):
@@ -249,6 +249,7 @@ def main() -> int:
         eager_packed = statistics.median(_time_steps(
             lambda: engine._forward_impl(xd, md, mode, pk), 20, 3)[0])
 
+    from tjkernels import tiles
     flops = flops_per_forward(w)
     flops_valid = flops_valid_tokens(w, lengths.tolist())
     med = statistics.median(samples)
@@ -297,6 +298,9 @@ def main() -> int:
                     "eager_packed_ms": round(eager_packed, 4),
                     "eager_unpacked_ms": round(eager_unpacked, 4)},
         "roofline": roofline, "cpu_baseline": cpu, "accuracy": acc, "breakdown": breakdown,
+        # measured tile plan per projection shape (M x N x K, epilogue)
+        "gemm_tiles": {f"{m}x{n}x{k}/epi{e}": p for (m, n, k, _, e), p in sorted(tiles._choice.items(),
+                                                                              key=lambda kv: kv[0][:3])},
     }
     print(json.dumps(line))
     return 0

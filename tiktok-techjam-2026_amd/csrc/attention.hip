@@ -533,7 +533,12 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
   for (int hb = 0; hb < HB; ++hb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[hb][r] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
+  // m_off: the exponent offset (log2 units) the running O and l are taken
+  // relative to.  It is raised only when a query's scores exceed it by more
+  // than kLazyRescale, so most tiles skip the O rescale; p <= 2^kLazyRescale
+  // is harmless in fp32 and in the 2-byte P.
+  constexpr float kLazyRescale = 8.0f;
+  float m_off = -INFINITY, l_run = 0.f;
 
   // softmax of one tile's scores (already masked) and O += V P
   auto softmax_pv = [&](int st, f32x16 (&sa)[2], bool interleave) {
@@ -542,24 +547,30 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sa[kb][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new * scale_log2;
-    const float alpha = __builtin_amdgcn_exp2f(m_run * scale_log2 - m_use);
-    float rs = 0.f;
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;  // both lanes of a query agree
+    if (__any(mx > m_off + kLazyRescale)) {
+      const float m_new = fmaxf(m_off, mx);
+      const float alpha = m_off == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_off - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[hb][r] *= alpha;
+      m_off = m_new;
+    }
+    const float base = m_off == -INFINITY ? 0.f : m_off;
     float p[2][16];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        p[kb][r] = __builtin_amdgcn_exp2f(fmaf(sa[kb][r], scale_log2, -m_use));
-        rs += p[kb][r];
-      }
-    l_run = l_run * alpha + rs;
-    m_run = m_new;
+      for (int r = 0; r < 16; ++r) p[kb][r] = __builtin_amdgcn_exp2f(fmaf(sa[kb][r], scale_log2, -base));
     typename Mfma<T>::frag pf[4];
 #pragma unroll
     for (int stp = 0; stp < 4; ++stp) pf[stp] = Mfma<T>::pack(&p[stp >> 1][8 * (stp & 1)]);
+    // row sums of the rounded P (exactly the weights the PV product uses),
+    // two per instruction
+#pragma unroll
+    for (int stp = 0; stp < 4; ++stp) l_run = Mfma<T>::sum8(pf[stp], l_run);
     if (interleave) {
       // Spread the next tile's S MFMAs (issued just before this call, same
       // basic block) over the softmax VALU work so both pipes stay busy.
@@ -570,12 +581,6 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // S MFMA
         __builtin_amdgcn_sched_group_barrier(0x002, 10, 0); // softmax VALU
       }
-    }
-    if (__any(alpha != 1.0f)) {
-#pragma unroll
-      for (int hb = 0; hb < HB; ++hb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[hb][r] *= alpha;
     }
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb) {
@@ -669,7 +674,7 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
         *reinterpret_cast<float4*>(prow + hb * 32 + 8 * g + 4 * hi) =
             make_float4(o[hb][4 * g], o[hb][4 * g + 1], o[hb][4 * g + 2], o[hb][4 * g + 3]);
     if (hi == 0) {
-      pb[BMQ * HDP + wave * 32 + l32] = m_run;
+      pb[BMQ * HDP + wave * 32 + l32] = m_off;
       pb[BMQ * HDP + BMQ + wave * 32 + l32] = l;
     }
     return;
@@ -692,9 +697,9 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
 }
 
 // Merge of key-split work items: item halves lo / hi of query block qb of
-// (b, h) each left an unnormalised O, a running max m (raw score units) and
+// (b, h) each left an unnormalised O, its exponent offset m (log2 units) and
 // a sum l per query; the output is
-//     (O_lo a_lo + O_hi a_hi) / (l_lo a_lo + l_hi a_hi),  a_x = 2^((m_x - m) s),
+//     (O_lo a_lo + O_hi a_hi) / (l_lo a_lo + l_hi a_hi),  a_x = 2^(m_x - m),
 // m = max(m_lo, m_hi), always combined in this order (deterministic).
 template <typename T, int HDP>
 __global__ __launch_bounds__(256) void flash_merge_kernel(
@@ -712,8 +717,8 @@ __global__ __launch_bounds__(256) void flash_merge_kernel(
     if (q0 + ql >= Sb || c >= hd) continue;
     const float m_lo = lo[BMQ * HDP + ql], m_hi = hi[BMQ * HDP + ql];
     const float m = fmaxf(m_lo, m_hi);
-    const float a_lo = m_lo == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_lo - m) * scale_log2);
-    const float a_hi = m_hi == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_hi - m) * scale_log2);
+    const float a_lo = m_lo == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_lo - m);
+    const float a_hi = m_hi == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_hi - m);
     const float l = fmaf(hi[BMQ * HDP + BMQ + ql], a_hi, lo[BMQ * HDP + BMQ + ql] * a_lo);
     const float inv = l > 0.f ? 1.0f / l : 0.f;
     const float4 ol = *reinterpret_cast<const float4*>(lo + (int64_t)ql * HDP + c);

@@ -110,6 +110,17 @@ template <> struct Mfma<bf16> {
     for (int i = 0; i < 8; ++i) f[i] = static_cast<bf16>(v[i]);
     return f;
   }
+  // acc + sum of the 8 elements, two per v_dot2c_f32_bf16
+  static __device__ __forceinline__ float sum8(const frag& f, float acc) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 one = {static_cast<bf16>(1.0f), static_cast<bf16>(1.0f)};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bf16x2 pr = {f[2 * i], f[2 * i + 1]};
+      acc = __builtin_amdgcn_fdot2_f32_bf16(pr, one, acc, false);
+    }
+    return acc;
+  }
 };
 
 template <> struct Mfma<f16> {
@@ -126,6 +137,17 @@ template <> struct Mfma<f16> {
 #pragma unroll
     for (int i = 0; i < 8; ++i) f[i] = static_cast<f16>(v[i]);
     return f;
+  }
+  // acc + sum of the 8 elements, two per v_dot2c_f32_f16
+  static __device__ __forceinline__ float sum8(const frag& f, float acc) {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    const f16x2 one = {static_cast<f16>(1.0f), static_cast<f16>(1.0f)};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f16x2 pr = {f[2 * i], f[2 * i + 1]};
+      acc = __builtin_amdgcn_fdot2(pr, one, acc, false);
+    }
+    return acc;
   }
 };
 
@@ -150,6 +172,11 @@ template <> struct Mfma<float> {
 #pragma unroll
     for (int i = 0; i < 8; ++i) f[i] = v[i];
     return f;
+  }
+  static __device__ __forceinline__ float sum8(const frag& f, float acc) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc += f[i];
+    return acc;
   }
 };
 

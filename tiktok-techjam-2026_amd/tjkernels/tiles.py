@@ -25,7 +25,7 @@ from typing import Dict, Tuple
 
 import torch
 
-from . import _lib, ops
+from . import _lib, ops, timing
 
 # Direct-to-LDS tile plans worth timing (2-byte types): 128x128, 256x256,
 # 64x64, 192x128, 192x256, 192x384, 96x128.  fp32 uses its own list.
@@ -36,13 +36,7 @@ _choice: Dict[Tuple, int] = {}
 
 
 def _time_plan(a, w, bias, out, epi, plan, reps) -> float:
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        ops.gemm(a, w, bias, out, epi, plan)
-    e1.record()
-    e1.synchronize()
-    return e0.elapsed_time(e1) / reps
+    return timing.launch_ms(lambda: ops.gemm(a, w, bias, out, epi, plan), reps)
 
 
 def gemm_plan(m: int, n: int, k: int, dtype: torch.dtype, epilogue: int, forced: int = -1) -> int:
@@ -63,7 +57,8 @@ def gemm_plan(m: int, n: int, k: int, dtype: torch.dtype, epilogue: int, forced:
     bias = torch.zeros(n, device=dev, dtype=dtype)
     out = torch.empty(m, n, device=dev,
                       dtype=torch.float32 if epilogue == ops.EPI_BIAS_RESIDUAL else dtype)
-    reps = 3 if 2.0 * m * n * k > 5e10 else 6
+    # about 0.4 ms of GPU work per measurement (estimated at 500 TFLOP/s)
+    reps = max(3, min(24, int(0.4e-3 / (2.0 * m * n * k / 500e12))))
     cands = []
     for cand in (CANDIDATES_32 if dtype == torch.float32 else CANDIDATES_16):
         try:
