@@ -281,15 +281,15 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
 // c ^ swz(r), which spreads the ds_read_b128 fragment reads of 16
 // consecutive rows over all banks (for 32- and 64-bank LDS alike).
 //
-// Pipeline, one barrier per tile: before computing tile k a wave waits until
-// its own DMAs for tile k have landed (s_waitcnt vmcnt(N), N = DMAs of the
-// STAGES-2 younger tiles still allowed in flight) and then meets the others
-// at s_barrier; it then issues the DMA of tile k+STAGES-1 into the slot tile
-// k-1 just vacated and runs tile k's MFMAs.  So every DMA has STAGES-1
-// tiles of MFMA work to land.  The DMA is issued on every iteration, past
-// the end pointed outside the buffer range (it moves nothing), which keeps
-// the body one basic block; scheduling directives then interleave the
-// MFMAs with the next step's ds_reads and with the DMA issues.
+// Pipeline, one barrier per tile, placed before the tile's last 16-deep
+// step: by then every fragment of tile k is in registers, so after the
+// barrier (which also certifies that tile k+1 has landed) a wave issues the
+// DMA of tile k+STAGES into tile k's slot and reads tile k+1's first
+// fragments while the last step's MFMAs run.  Every DMA has STAGES-1 tiles
+// of MFMA work to land, and no wave waits for LDS right after the barrier.
+// The DMA is issued on every iteration, past the end pointed outside the
+// buffer range (it moves nothing), which keeps the body one basic block;
+// scheduling directives interleave the MFMAs with the next step's ds_reads.
 // Requires K % (BKB / sizeof(T)) == 0 and 16-byte aligned rows.
 
 template <int BKB> __device__ __forceinline__ int swz(int r);
@@ -318,7 +318,7 @@ __global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
   constexpr int DA = BM / (RPI * NW), DW = BN / (RPI * NW);
   constexpr int NDMA = DA + DW;                  // DMA instructions per wave per tile
   static_assert(DA * RPI * NW == BM && DW * RPI * NW == BN, "tile rows must split over the waves");
-  static_assert(STAGES >= 2 && (STAGES - 2) * NDMA <= 63, "vmcnt range");
+  static_assert(STAGES >= 2 && (STAGES - 1) * NDMA <= 63, "vmcnt range");
 
   __shared__ __attribute__((aligned(1024))) char smem[KSPLIT * STAGES * STAGE];
 
@@ -359,18 +359,23 @@ __global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
   }
   const int nk = K / BK;
   const int nit = (nk + KSPLIT - 1) / KSPLIT;  // ring steps per group
-  auto issue = [&](int it) {  // DMA of this group's step it into its slot (nothing past the end)
+  // DMA instruction q (q < DA: A rows, else W rows) of this group's step it
+  // into its slot; past the last step it points outside the range and
+  // moves nothing.
+  auto dma = [&](int it, int q) {
     char* sb = gsm + (it % STAGES) * STAGE;
     const int kt = it * KSPLIT + kg;
     const uint32_t kb = kt < nk ? (uint32_t)(kt * BKB) : (uint32_t)kPastEnd;
+    if (q < DA)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)(sb + (q * NW + wave) * 1024), 16,
+                                               (uint32_t)(voff_a[q] + kb), 0, 0, 0);
+    else
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_void*)(sb + BM * BKB + ((q - DA) * NW + wave) * 1024),
+                                               16, (uint32_t)(voff_w[q - DA] + kb), 0, 0, 0);
+  };
+  auto issue = [&](int it) {
 #pragma unroll
-    for (int i = 0; i < DA; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)(sb + (i * NW + wave) * 1024), 16,
-                                               (uint32_t)(voff_a[i] + kb), 0, 0, 0);
-#pragma unroll
-    for (int i = 0; i < DW; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_void*)(sb + BM * BKB + (i * NW + wave) * 1024), 16,
-                                               (uint32_t)(voff_w[i] + kb), 0, 0, 0);
+    for (int q = 0; q < NDMA; ++q) dma(it, q);
   };
 
   // Fragment reads: row (base + l32), logical chunk c at physical c ^ swz(l32).
@@ -396,49 +401,66 @@ __global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+  // Prologue: tiles 0 .. STAGES-1 in flight; tile 0 landed everywhere.
 #pragma unroll
-  for (int t = 0; t < STAGES - 1; ++t) issue(t);
+  for (int t = 0; t < STAGES; ++t) issue(t);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"((STAGES - 1) * NDMA) : "memory");
+  asm volatile("s_barrier" ::: "memory");
+  static_assert(KS % 2 == 0, "fragment double buffer alternates per 16-deep step");
+  constexpr int NMF = FN * FM, NDS = FN + FM;  // MFMAs and fragment reads per step
+  constexpr int NSLOT = NMF > NDS ? NMF : NDS;
   typename Mfma<T>::frag fa[2][FM], fw[2][FN];
-  for (int kt = 0; kt < nit; ++kt) {
-    // My DMAs of step kt have landed, then everyone's (and step kt-1 is
-    // retired by every wave).  Inline asm with a memory clobber keeps the
-    // compiler from moving LDS accesses across either instruction; a
-    // __syncthreads() would instead wait for every DMA in flight.
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((STAGES - 2) * NDMA) : "memory");
-    asm volatile("s_barrier" ::: "memory");
-    const char* st = gsm + (kt % STAGES) * STAGE;
-    const char* sa = st + (wm * WTM + l32) * BKB;
-    const char* sw_ = st + BM * BKB + (wn * WTN + l32) * BKB;
+  {
+    const char* sa = gsm + (wm * WTM + l32) * BKB;
+    const char* sw_ = gsm + BM * BKB + (wn * WTN + l32) * BKB;
 #pragma unroll
     for (int j = 0; j < FM; ++j) fa[0][j] = frag_at(sa + j * 32 * BKB, 0);
 #pragma unroll
     for (int i = 0; i < FN; ++i) fw[0][i] = frag_at(sw_ + i * 32 * BKB, 0);
-    issue(kt + STAGES - 1);
+  }
+  // The loop body is emitted in source order (scheduling fences between the
+  // pieces): MFMA m of a step is followed by fragment read m of the next
+  // step (m < FM + FN), and after the barrier by DMA instructions, so the
+  // LDS reads and DMA issues hide under the MFMAs of the step before the
+  // one that needs them.
+  for (int kt = 0; kt < nit; ++kt) {
+    const char* st = gsm + (kt % STAGES) * STAGE;
+    const char* sa = st + (wm * WTM + l32) * BKB;
+    const char* sw_ = st + BM * BKB + (wn * WTN + l32) * BKB;
+    const char* nx = gsm + ((kt + 1) % STAGES) * STAGE;
+    const char* na = nx + (wm * WTM + l32) * BKB;
+    const char* nw = nx + BM * BKB + (wn * WTN + l32) * BKB;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const int b = ks & 1;
-      if (ks + 1 < KS) {
-#pragma unroll
-        for (int j = 0; j < FM; ++j) fa[b ^ 1][j] = frag_at(sa + j * 32 * BKB, ks + 1);
-#pragma unroll
-        for (int i = 0; i < FN; ++i) fw[b ^ 1][i] = frag_at(sw_ + i * 32 * BKB, ks + 1);
+      const bool last = ks + 1 == KS;
+      // fragments of the next step: this tile's step ks+1, or after the
+      // barrier the next tile's step 0
+      const char* ra = last ? na : sa;
+      const char* rw = last ? nw : sw_;
+      const int rks = last ? 0 : ks + 1;
+      if (last) {
+        // Before the last step's MFMAs (its fragments are in registers): my
+        // reads of this slot are complete and my DMAs of step kt+1 have
+        // landed, then everyone's.  The slot is then free for step
+        // kt+STAGES.  Inline asm with a memory clobber keeps the compiler
+        // from moving LDS accesses across either instruction.
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((STAGES - 2) * NDMA) : "memory");
+        asm volatile("s_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
-      for (int i = 0; i < FN; ++i)
+      for (int m = 0; m < NSLOT; ++m) {
+        if (m < NMF) Mfma<T>::mma(acc[m / FM][m % FM], fw[b][m / FM], fa[b][m % FM]);
+        if (m < FM) fa[b ^ 1][m] = frag_at(ra + m * 32 * BKB, rks);
+        else if (m < NDS) fw[b ^ 1][m - FM] = frag_at(rw + (m - FM) * 32 * BKB, rks);
+        if (last) {
 #pragma unroll
-        for (int j = 0; j < FM; ++j) Mfma<T>::mma(acc[i][j], fw[b][i], fa[b][j]);
-    }
-    if constexpr (SCHED) {
-      constexpr int NMF = FN * FM, NDS = FN + FM;
-      __builtin_amdgcn_sched_group_barrier(0x100, NDS, 0);  // step-0 fragments
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int m = 0; m < NMF; ++m) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          if (ks == 0 && m < NDMA) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-          if (ks + 1 < KS && m >= NMF - NDS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          for (int q = m * NDMA / NSLOT; q < (m + 1) * NDMA / NSLOT; ++q) dma(kt + STAGES, q);
         }
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
 
