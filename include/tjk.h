@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define TJK_ABI_VERSION 2
+#define TJK_ABI_VERSION 3
 
 /* dtypes */
 #define TJK_F32 0
@@ -94,6 +94,25 @@ int tjk_gemm_bias(const void* a, int64_t lda, const void* w, int64_t ldw,
                   const void* bias, void* c, int64_t ldc,
                   int64_t m, int64_t n, int64_t k,
                   int dtype, int epilogue, int plan_id, void* stream);
+
+/*
+ * tjk_gemm_bias with a caller-provided workspace, which the stream-K plans
+ * need (tjk_gemm_bias returns TJK_EINVAL for them).  workspace_bytes >=
+ * tjk_gemm_workspace_bytes(dtype, plan_id), 256-byte aligned, zero-filled
+ * before its first use; every completed call leaves its flag area zero
+ * again.  Calls sharing one workspace must not run concurrently (one
+ * stream, or ordered streams).  Stream-K results are deterministic for a
+ * given device (the K partition depends on the shape and the CU count).
+ * Replaces the same torch.addmm call sites as tjk_gemm_bias.
+ */
+int tjk_gemm_bias_ws(const void* a, int64_t lda, const void* w, int64_t ldw,
+                     const void* bias, void* c, int64_t ldc,
+                     int64_t m, int64_t n, int64_t k,
+                     int dtype, int epilogue, int plan_id,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes plan_id needs on the current device (0: none). */
+size_t tjk_gemm_workspace_bytes(int dtype, int plan_id);
 
 /* Number of GEMM tile plans for `dtype`, and the tile of plan `id`. */
 int tjk_gemm_plan_count(int dtype);

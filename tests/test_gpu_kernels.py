@@ -135,6 +135,66 @@ def test_gemm_plans(device, plan, dt):
             _gemm_case(device, 64, 64, 40, dt, ops.EPI_BIAS, plan)
 
 
+# Stream-K plans: persistent grid, K-split partial tiles folded by the
+# tile's finisher in a fixed order.
+SK16 = range(18, 24)
+
+
+@pytest.mark.parametrize("plan", list(SK16))
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_gemm_stream_k_plans(device, plan, dt):
+    _gemm_case(device, 513, 1028, 1088, dt, ops.EPI_BIAS, plan)   # ragged M and N
+    _gemm_case(device, 64, 32, 64, dt, ops.EPI_BIAS, plan)        # one tile, one K tile
+    _gemm_case(device, 700, 256, 4096, dt, ops.EPI_BIAS, plan)    # few tiles, each split many ways
+    with pytest.raises(ops.TjkError, match="needs k"):
+        _gemm_case(device, 300, 200, 96, dt, ops.EPI_BIAS, plan)
+
+
+@pytest.mark.parametrize("plan", [18, 20, 22])
+@pytest.mark.parametrize("epi", [ops.EPI_BIAS_GELU, ops.EPI_BIAS_RESIDUAL])
+def test_gemm_stream_k_epilogues(device, plan, epi):
+    # the residual is added exactly once per element by the tile's finisher
+    _gemm_case(device, 5430, 1024, 1024, torch.bfloat16, epi, plan)
+    _gemm_case(device, 1000, 516, 2048, torch.bfloat16, epi, plan)
+
+
+@pytest.mark.parametrize("plan", [18, 22])
+def test_gemm_stream_k_with_data_parallel_rounds(device, plan):
+    # more than two full rounds of tiles: whole tiles first, stream-K after
+    _gemm_case(device, 5000, 7000, 128, torch.bfloat16, ops.EPI_BIAS, plan)
+
+
+def test_gemm_stream_k_deterministic_and_flags_cleared(device):
+    g = _gen(5)
+    a = torch.randn(5430, 4096, generator=g).bfloat16().to(device)
+    w = (torch.randn(1024, 4096, generator=g) / 64).bfloat16().to(device)
+    b = torch.randn(1024, generator=g).bfloat16().to(device)
+    r0 = torch.randn(5430, 1024, generator=g).to(device)
+    outs = []
+    for _ in range(3):
+        out = r0.clone()
+        ops.gemm(a, w, b, out, ops.EPI_BIAS_RESIDUAL, 18)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    ws = ops.gemm_workspace(device)
+    header = ws[:2049 * 4].view(torch.int32).cpu()
+    assert int(header.abs().sum()) == 0  # every flag cleared, no timed-out wait
+
+
+def test_gemm_stream_k_requires_workspace(device):
+    from tjkernels import _lib
+    lib = _lib.load()
+    a = torch.zeros(64, 64, dtype=torch.bfloat16, device=device)
+    out = torch.zeros(64, 64, dtype=torch.bfloat16, device=device)
+    st = lib.tjk_gemm_bias(a.data_ptr(), 64, a.data_ptr(), 64, None, out.data_ptr(), 64, 64, 64, 64,
+                           _lib.BF16, ops.EPI_BIAS, 18, None)
+    assert st < 0 and b"workspace" in lib.tjk_last_error_string()
+    small = torch.zeros(1024, dtype=torch.uint8, device=device)
+    with pytest.raises(ops.TjkError, match="workspace"):
+        ops.gemm(a, a, None, out, ops.EPI_BIAS, 18, workspace=small)
+
+
 @pytest.mark.parametrize("plan", list(STAGED32) + list(DTL32))
 def test_gemm_fp32_plans(device, plan):
     _gemm_case(device, 257, 516, 256, torch.float32, ops.EPI_BIAS, plan)

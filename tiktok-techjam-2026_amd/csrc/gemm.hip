@@ -83,10 +83,19 @@ struct EpiStage {
   static constexpr int BYTES = 32 * PITCH * (int)sizeof(S);  // LDS bytes per wave
 };
 
-template <typename T, int EPI, int FM, int FN>
+//
+// `parts` (stream-K finishers only) supplies parts.n fp32 partial tiles of
+// the same output tile, laid out like the accumulators; they are added in
+// order to acc + bias before the activation.
+struct NoParts {
+  static constexpr int n = 0;
+  __device__ f32x4 get(int, int) const { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+};
+
+template <typename T, int EPI, int FM, int FN, typename Parts = NoParts>
 __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* __restrict__ bias,
                                          void* __restrict__ Cv, int64_t ldc, int M, int N, int mw, int nw,
-                                         int lane, char* __restrict__ stage) {
+                                         int lane, char* __restrict__ stage, const Parts& parts = Parts()) {
   typedef EpiStage<T, EPI, FN> E;
   typedef typename E::S S;
   constexpr int LPR = E::WTN / E::SV;  // 16-byte pieces per staged row
@@ -111,12 +120,34 @@ __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* _
 
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
+    // this row block's partials, all loads of one partial in flight at once
+    f32x4 ps[FN][4];
+    if (parts.n > 0) {
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) ps[i][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int q = 0; q < parts.n; ++q) {
+        f32x4 ld[FN][4];
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) ld[i][g] = parts.get(q, (i * FM + j) * 4 + g);
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) ps[i][g] += ld[i][g];
+      }
+    }
 #pragma unroll
     for (int i = 0; i < FN; ++i)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         float4 v = make_float4(acc[i][j][4 * g + 0] + bv[i][g].x, acc[i][j][4 * g + 1] + bv[i][g].y,
                                acc[i][j][4 * g + 2] + bv[i][g].z, acc[i][j][4 * g + 3] + bv[i][g].w);
+        if (parts.n > 0) {
+          v.x += ps[i][g][0]; v.y += ps[i][g][1]; v.z += ps[i][g][2]; v.w += ps[i][g][3];
+        }
         if (EPI == TJK_EPI_BIAS_GELU) {
           v.x = gelu_erf(v.x); v.y = gelu_erf(v.y); v.z = gelu_erf(v.z); v.w = gelu_erf(v.w);
         }
@@ -301,39 +332,55 @@ typedef __attribute__((address_space(3))) void lds_void;
 // Byte offset that lies beyond any buffer descriptor range used here.
 constexpr int kPastEnd = 0x7fff0000;
 
-template <typename T, int BM, int BN, int WM, int WN, int BKB, int STAGES, int EPI, int KSPLIT>
-__global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
-    const T* __restrict__ A, int64_t lda, const T* __restrict__ W, int64_t ldw,
-    const T* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K) {
-  constexpr bool SCHED = sizeof(T) == 2;
-  constexpr int NW = WM * WN;
-  constexpr int BK = BKB / sizeof(T);            // K elements per tile
-  constexpr int CPR = BKB / 16;                  // 16-byte chunks per row
-  constexpr int RPI = 64 / CPR;                  // rows per DMA instruction
-  constexpr int KS = BK / 16;                    // 16-deep MFMA steps per tile
-  constexpr int CPS = sizeof(T) == 2 ? 2 : 4;    // chunks per 16-deep step
-  constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int FM = WTM / 32, FN = WTN / 32;
-  constexpr int STAGE = (BM + BN) * BKB;         // bytes per LDS stage
-  constexpr int DA = BM / (RPI * NW), DW = BN / (RPI * NW);
-  constexpr int NDMA = DA + DW;                  // DMA instructions per wave per tile
+// Tile geometry shared by the direct-to-LDS kernels.
+template <typename T, int BM, int BN, int WM, int WN, int BKB, int STAGES, int KSPLIT>
+struct DtlGeom {
+  static constexpr int NW = WM * WN;
+  static constexpr int BK = BKB / sizeof(T);          // K elements per tile
+  static constexpr int CPR = BKB / 16;                // 16-byte chunks per row
+  static constexpr int RPI = 64 / CPR;                // rows per DMA instruction
+  static constexpr int KS = BK / 16;                  // 16-deep MFMA steps per tile
+  static constexpr int CPS = sizeof(T) == 2 ? 2 : 4;  // chunks per 16-deep step
+  static constexpr int WTM = BM / WM, WTN = BN / WN;
+  static constexpr int FM = WTM / 32, FN = WTN / 32;
+  static constexpr int STAGE = (BM + BN) * BKB;       // bytes per LDS stage
+  static constexpr int DA = BM / (RPI * NW), DW = BN / (RPI * NW);
+  static constexpr int NDMA = DA + DW;                // DMA instructions per wave per tile
+  static constexpr int LDS = KSPLIT * STAGES * STAGE; // ring bytes
   static_assert(DA * RPI * NW == BM && DW * RPI * NW == BN, "tile rows must split over the waves");
   static_assert(STAGES >= 2 && (STAGES - 1) * NDMA <= 63, "vmcnt range");
+  static_assert(KS % 2 == 0, "fragment double buffer alternates per 16-deep step");
+};
 
-  __shared__ __attribute__((aligned(1024))) char smem[KSPLIT * STAGES * STAGE];
+// acc += A[m0 : m0+BM, K tiles kt0..kt1) * W[n0 : n0+BN, same]^T for this
+// wave's sub-tile (K-split group kg takes K tiles kt0 + kg, kt0 + kg +
+// KSPLIT, ...).  On return every DMA has landed and the workgroup has met at
+// a barrier, so the LDS ring may be reused.  (smem is deliberately not
+// __restrict__: with it the compiler stops telling the LDS DMA writes and
+// the fragment reads of different ring slots apart and waits for every DMA
+// before each ds_read.)
+template <typename T, int BM, int BN, int WM, int WN, int BKB, int STAGES, int KSPLIT>
+__device__ __forceinline__ void dtl_accumulate(
+    char* smem, const T* __restrict__ A, int64_t lda, const T* __restrict__ W, int64_t ldw,
+    int M, int N, int m0, int n0, int kt0, int kt1,
+    f32x16 (&acc)[DtlGeom<T, BM, BN, WM, WN, BKB, STAGES, KSPLIT>::FN][DtlGeom<T, BM, BN, WM, WN, BKB, STAGES, KSPLIT>::FM]) {
+  typedef DtlGeom<T, BM, BN, WM, WN, BKB, STAGES, KSPLIT> G;
+  constexpr int NW = G::NW, KS = G::KS, CPR = G::CPR, RPI = G::RPI, CPS = G::CPS;
+  constexpr int WTM = G::WTM, WTN = G::WTN, FM = G::FM, FN = G::FN, STAGE = G::STAGE;
+  constexpr int DA = G::DA, NDMA = G::NDMA;
+  constexpr int DW = G::DW;
 
   // K split inside the workgroup: KSPLIT groups of WM x WN waves, group kg
-  // streaming K tiles kg, kg + KSPLIT, ... through its own LDS ring; the
-  // groups' accumulators are summed (in group order) before the epilogue.
-  const int tid = threadIdx.x;
+  // streaming its K tiles through its own LDS ring.  The thread id passes an
+  // empty asm so that, inside a persistent kernel's tile loop, nothing
+  // derived from it is hoisted out of that loop (which keeps the per-lane
+  // DMA and fragment addresses of every call live at once).
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
   const int lane = tid & 63, kg = (tid >> 6) / NW, wave = (tid >> 6) % NW;
   const int wm = wave / WN, wn = wave % WN;
   const int l32 = lane & 31, hi = lane >> 5;
   char* const gsm = smem + kg * (STAGES * STAGE);
-
-  int pid_m, pid_n;
-  tile_coords(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, pid_m, pid_n);
-  const int m0 = pid_m * BM, n0 = pid_n * BN;
 
   // Buffer descriptors over this tile's rows; reads past row M (N) return 0.
   const int64_t a_rows = min((int64_t)BM, (int64_t)(M - m0));
@@ -357,25 +404,20 @@ __global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
     const int r = (i * NW + wave) * RPI + lane / CPR;
     voff_w[i] = (uint32_t)(r * ldw * (int64_t)sizeof(T)) + (uint32_t)(((lane % CPR) ^ swz<BKB>(r)) << 4);
   }
-  const int nk = K / BK;
-  const int nit = (nk + KSPLIT - 1) / KSPLIT;  // ring steps per group
+  const int nit = (kt1 - kt0 + KSPLIT - 1) / KSPLIT;  // ring steps per group
   // DMA instruction q (q < DA: A rows, else W rows) of this group's step it
-  // into its slot; past the last step it points outside the range and
-  // moves nothing.
+  // into its slot; past the segment it points outside the range and moves
+  // nothing.
   auto dma = [&](int it, int q) {
     char* sb = gsm + (it % STAGES) * STAGE;
-    const int kt = it * KSPLIT + kg;
-    const uint32_t kb = kt < nk ? (uint32_t)(kt * BKB) : (uint32_t)kPastEnd;
+    const int kt = kt0 + it * KSPLIT + kg;
+    const uint32_t kb = kt < kt1 ? (uint32_t)(kt * BKB) : (uint32_t)kPastEnd;
     if (q < DA)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)(sb + (q * NW + wave) * 1024), 16,
                                                (uint32_t)(voff_a[q] + kb), 0, 0, 0);
     else
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_void*)(sb + BM * BKB + ((q - DA) * NW + wave) * 1024),
                                                16, (uint32_t)(voff_w[q - DA] + kb), 0, 0, 0);
-  };
-  auto issue = [&](int it) {
-#pragma unroll
-    for (int q = 0; q < NDMA; ++q) dma(it, q);
   };
 
   // Fragment reads: row (base + l32), logical chunk c at physical c ^ swz(l32).
@@ -393,20 +435,13 @@ __global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
     }
   };
 
-  f32x16 acc[FN][FM];
-#pragma unroll
-  for (int i = 0; i < FN; ++i)
-#pragma unroll
-    for (int j = 0; j < FM; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
   // Prologue: tiles 0 .. STAGES-1 in flight; tile 0 landed everywhere.
 #pragma unroll
-  for (int t = 0; t < STAGES; ++t) issue(t);
+  for (int t = 0; t < STAGES; ++t)
+#pragma unroll
+    for (int q = 0; q < NDMA; ++q) dma(t, q);
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"((STAGES - 1) * NDMA) : "memory");
   asm volatile("s_barrier" ::: "memory");
-  static_assert(KS % 2 == 0, "fragment double buffer alternates per 16-deep step");
   constexpr int NMF = FN * FM, NDS = FN + FM;  // MFMAs and fragment reads per step
   constexpr int NSLOT = NMF > NDS ? NMF : NDS;
   typename Mfma<T>::frag fa[2][FM], fw[2][FN];
@@ -468,11 +503,44 @@ __global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
   // tile) has landed and every wave is done reading.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+}
+
+template <typename T, int FM, int FN>
+__device__ __forceinline__ void zero_acc(f32x16 (&acc)[FN][FM]) {
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+}
+
+template <typename T, int BM, int BN, int WM, int WN, int BKB, int STAGES, int EPI, int KSPLIT>
+__global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
+    const T* __restrict__ A, int64_t lda, const T* __restrict__ W, int64_t ldw,
+    const T* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K) {
+  typedef DtlGeom<T, BM, BN, WM, WN, BKB, STAGES, KSPLIT> G;
+  constexpr int NW = G::NW, FM = G::FM, FN = G::FN;
+  __shared__ __attribute__((aligned(1024))) char smem[G::LDS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, kg = (tid >> 6) / NW, wave = (tid >> 6) % NW;
+  const int wm = wave / WN, wn = wave % WN;
+
+  int pid_m, pid_n;
+  tile_coords(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, pid_m, pid_n);
+  const int m0 = pid_m * BM, n0 = pid_n * BN;
+
+  f32x16 acc[FN][FM];
+  zero_acc<T, FM, FN>(acc);
+  dtl_accumulate<T, BM, BN, WM, WN, BKB, STAGES, KSPLIT>(smem, A, lda, W, ldw, M, N, m0, n0, 0, K / G::BK, acc);
+
   constexpr int ACCF = FN * FM * 16;                   // accumulator floats per lane
   constexpr int XCH = (KSPLIT - 1) * NW * ACCF * 64 * 4;  // exchange bytes
-  static_assert(XCH + NW * EpiStage<T, EPI, FN>::BYTES <= KSPLIT * STAGES * STAGE,
+  static_assert(XCH + NW * EpiStage<T, EPI, FN>::BYTES <= G::LDS,
                 "K-split exchange + epilogue staging exceed LDS");
   if constexpr (KSPLIT > 1) {
+    // the groups' accumulators are summed (in group order) before the epilogue
     float* xch = reinterpret_cast<float*>(smem);
     if (kg > 0) {
       float* my = xch + (int64_t)((kg - 1) * NW + wave) * ACCF * 64;
@@ -496,13 +564,205 @@ __global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
           for (int r = 0; r < 16; ++r) acc[i][j][r] += ot[((i * FM + j) * 16 + r) * 64 + lane];
     }
   }
-  epilogue<T, EPI, FM, FN>(acc, bias, Cv, ldc, M, N, m0 + wm * WTM, n0 + wn * WTN, lane,
+  epilogue<T, EPI, FM, FN>(acc, bias, Cv, ldc, M, N, m0 + wm * G::WTM, n0 + wn * G::WTN, lane,
                            smem + XCH + wave * EpiStage<T, EPI, FN>::BYTES);
+}
+
+// ------------------------------------------------------------ stream-K GEMM
+//
+// Persistent variant for shapes whose tile count fills the CUs badly.  The
+// grid is one resident wave of G workgroups (CUs x occupancy).  The tiles of
+// the GROUP_M raster are split in two parts:
+//   * the first dp_tiles are whole tiles dealt round-robin over the grid;
+//   * the rest are cut into units of one K tile (BK deep), and the units
+//     (tile-major) are divided into G contiguous ranges of equal length.
+// A workgroup walks its range from the end backwards, one segment (the
+// part of its range inside one tile) at a time:
+//   * a segment that is a whole tile goes straight to the epilogue;
+//   * a segment that ends before the tile's last K tile (always the first
+//     one a workgroup meets) writes its fp32 partial accumulators through to
+//     memory in its workspace slot, waits for the stores, and raises its
+//     flag;
+//   * the segment that holds the tile's last K tile (always the last one a
+//     workgroup meets) polls the flags of the lower workgroups that hold the
+//     rest of the tile, and its epilogue adds their partials (device-coherent
+//     loads, nearest first) before clearing their flags.
+// Producers never wait, and a finisher only waits for workgroups with lower
+// logical ids that publish before doing anything else, so every wait ends
+// while the grid is resident; each wait is still bounded (kSkSpinLimit
+// polls) and a timeout is counted in the workspace's error word instead of
+// hanging.  Results are deterministic for a given grid size: the partition
+// and the summation order depend only on (M, N, K, G).  Flags are left at
+// zero for the next call.  Calls sharing one workspace must not overlap.
+//
+// Measured on MI355X at the packed C4 projections these plans are slower
+// than the best direct-to-LDS tile (e.g. FFN2 5430x1024x4096: 67.7 us vs
+// 55 us): a CU moves ~50 GB/s, so publishing a 192-256 KB partial costs
+// 3-5 us and a finisher's epilogue with two partials 7-18 us, which eats
+// the quantization gain.  They win where the data-parallel rounds dominate
+// (8192^3: 1337 TFLOP/s vs 1300 for plan 8).
+
+constexpr int kMaxSkGrid = 2048;
+// Cache-policy bits of buffer loads / stores on gfx950 (sc0 = 1, sc1 = 16):
+// sc1 makes an access device-coherent, sc0 sc1 on a store writes through.
+constexpr int kCpolSc1 = 16, kCpolSc0Sc1 = 17;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kSkSpinLimit = 1 << 22;
+
+struct SkParams {
+  int tiles_m, tiles_n;
+  int dp_tiles;   // whole tiles dealt round-robin over the grid
+  int sk_units;   // K-tile units of the remaining tiles
+  int nk;         // K tiles per output tile
+};
+
+// Workspace: int flags[kMaxSkGrid], int error, padding to 16 KB, then one
+// BM x BN fp32 partial per workgroup.
+constexpr size_t kSkHeader = 16384;
+static_assert((kMaxSkGrid + 1) * 4 <= (int)kSkHeader, "flag area");
+
+__device__ __forceinline__ void raster_coords(int t, int tiles_m, int tiles_n, int& pid_m, int& pid_n) {
+  const int group = t / (kGroupM * tiles_n);
+  const int first_m = group * kGroupM;
+  const int gsize = min(tiles_m - first_m, kGroupM);
+  pid_m = first_m + (t % (kGroupM * tiles_n)) % gsize;
+  pid_n = (t % (kGroupM * tiles_n)) / gsize;
+}
+
+template <typename T, int BM, int BN, int WM, int WN, int BKB, int STAGES, int EPI>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_sk_kernel(
+    const T* __restrict__ A, int64_t lda, const T* __restrict__ W, int64_t ldw,
+    const T* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, SkParams p,
+    char* __restrict__ workspace) {
+  typedef DtlGeom<T, BM, BN, WM, WN, BKB, STAGES, 1> G;
+  constexpr int NW = G::NW, FM = G::FM, FN = G::FN;
+  static_assert(NW * EpiStage<T, EPI, FN>::BYTES <= G::LDS, "epilogue staging exceeds LDS");
+  __shared__ __attribute__((aligned(1024))) char smem[G::LDS];
+
+  const int tid = threadIdx.x;
+  // Logical workgroup id: XCD-contiguous (the hardware deals workgroup ids
+  // round-robin over the 8 XCDs), so each XCD walks a contiguous range of
+  // units -- neighbouring tiles that share operand rows and columns in its
+  // L2 -- and a producer / finisher pair is mostly on one XCD.  Correctness
+  // does not depend on the placement: partials move write-through and are
+  // read device-coherent.
+  const int grid = gridDim.x, c = xcd_remap(blockIdx.x, grid);
+  int* const flags = reinterpret_cast<int*>(workspace);
+  float* const partials = reinterpret_cast<float*>(workspace + kSkHeader);
+  constexpr int TILE_F4 = BM * BN / 4;  // float4s per partial
+  // this wave's part of a partial: [i][j][r / 4][lane] float4s
+  // Partials move through the device-coherent path instead of whole-cache
+  // maintenance: stores write through to memory (sc0 sc1), loads are
+  // device-coherent (sc1), so no L2 writeback or invalidate is needed
+  // around the flags (a cache-wide invalidate per finisher would evict the
+  // operand tiles of every workgroup on its XCD).  Byte offset of float4
+  // `idx` of this wave / lane in owner's slot:
+  const __amdgpu_buffer_rsrc_t prs =
+      __builtin_amdgcn_make_buffer_rsrc(partials, (short)0, 0x7fffffff, 0x00020000);
+  auto part_off = [&](int owner, int wave, int lane) {
+    return (owner * TILE_F4 + wave * (FN * FM * 4 * 64) + lane) * 16;
+  };
+  struct SkParts {
+    __amdgpu_buffer_rsrc_t r;
+    int base, stride, n;
+    __device__ f32x4 get(int q, int idx) const {
+      return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, base + q * stride + idx * 64 * 16,
+                                                                             0, kCpolSc1));
+    }
+  };
+
+  // Work items, one call site each for the main loop and the epilogue (so
+  // the accumulators stay in registers): first this workgroup's
+  // data-parallel tiles, then its stream-K segments from the range end
+  // backwards.
+  const int dp_first = c;
+  const int n_dp = dp_first < p.dp_tiles ? (p.dp_tiles - dp_first + grid - 1) / grid : 0;
+  const int base = p.sk_units / grid, rem = p.sk_units % grid;
+  const int u_begin = c * base + min(c, rem);
+  const int u_end = u_begin + base + (c < rem ? 1 : 0);
+  const int big = rem * (base + 1);  // units held by the workgroups with base + 1 of them
+
+  f32x16 acc[FN][FM];
+  int u = u_end;
+  for (int item = 0;; ++item) {
+    int t, kt0, kt1, lo = 0, first_owner = c;
+    if (item < n_dp) {
+      t = dp_first + item * grid;
+      kt0 = 0;
+      kt1 = p.nk;
+    } else {
+      if (u <= u_begin) break;
+      const int tl = (u - 1) / p.nk, tu0 = tl * p.nk;
+      lo = max(u_begin, tu0);
+      t = p.dp_tiles + tl;
+      kt0 = lo - tu0;
+      kt1 = u - tu0;
+      // owner of the tile's first unit: the lowest workgroup holding a part
+      first_owner = tu0 < big ? tu0 / (base + 1) : rem + (tu0 - big) / base;
+      u = lo;
+    }
+    if (item > 0) __syncthreads();  // the previous epilogue's staging reads are done
+    int ltid = threadIdx.x;          // per-item copy, not hoisted (see dtl_accumulate)
+    asm volatile("" : "+v"(ltid));
+    const int lane = ltid & 63, wave = ltid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    int pid_m, pid_n;
+    raster_coords(t, p.tiles_m, p.tiles_n, pid_m, pid_n);
+    zero_acc<T, FM, FN>(acc);
+    dtl_accumulate<T, BM, BN, WM, WN, BKB, STAGES, 1>(smem, A, lda, W, ldw, M, N, pid_m * BM, pid_n * BN, kt0,
+                                                      kt1, acc);
+    if (kt1 < p.nk) {
+      // producer: publish the partial
+      const int dst = part_off(c, wave, lane);
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            f32x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * r4 + e];
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), prs,
+                                                   dst + ((i * FM + j) * 4 + r4) * 64 * 16, 0, kCpolSc0Sc1);
+          }
+      // every wave's write-through stores have completed, then the flag
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (tid == 0) __hip_atomic_store(&flags[c], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      continue;
+    }
+    // Finisher (holds the tile's last K tile but not its first): the lower
+    // workgroups holding the rest published their partials as their first
+    // item, so by now the waits are normally over.  The epilogue adds the
+    // partials nearest first.
+    // The polls are relaxed device-coherent loads; the partials are then
+    // read with device-coherent loads as well.
+    const int nparts = (kt0 > 0) ? c - first_owner : 0;
+    for (int o = c - 1; o >= c - nparts; --o) {
+      int spins = 0;
+      while (__hip_atomic_load(&flags[o], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
+        if (++spins > kSkSpinLimit) {
+          if (tid == 0) __hip_atomic_fetch_add(&flags[kMaxSkGrid], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    const SkParts parts{prs, nparts > 0 ? part_off(c - 1, wave, lane) : 0, -TILE_F4 * 16, nparts};
+    epilogue<T, EPI, FM, FN>(acc, bias, Cv, ldc, M, N, pid_m * BM + wm * G::WTM, pid_n * BN + wn * G::WTN, lane,
+                             smem + wave * EpiStage<T, EPI, FN>::BYTES, parts);
+    if (nparts > 0) {
+      __syncthreads();  // every wave has read the partials
+      for (int q = tid; q < nparts; q += WM * WN * 64)
+        __hip_atomic_store(&flags[c - 1 - q], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 // ------------------------------------------------------------------ plans
 
-enum { kStaged = 0, kDtl = 1 };
+enum { kStaged = 0, kDtl = 1, kSk = 2 };
 
 struct GemmPlan {
   int kind, bm, bn, wm, wn, bkb, stages;
@@ -539,6 +799,14 @@ static const GemmPlan kPlans16[] = {
     // the MALL, which splitting K does not change.
     {kDtl, 192, 128, 2, 2, 128, 2, 0.85, 2},  // 16 wave tile 96x64
     {kDtl, 128, 128, 2, 2, 128, 2, 0.85, 2},  // 17 wave tile 64x64
+    // 18-23: stream-K (persistent grid, K-split partial tiles; need a
+    // workspace of tjk_gemm_workspace_bytes()).
+    {kSk, 256, 256, 2, 4, 128, 2, 1.00},      // 18 8 waves, wave tile 128x64
+    {kSk, 256, 256, 2, 2, 128, 2, 1.00},      // 19 wave tile 128x128
+    {kSk, 192, 256, 2, 4, 128, 2, 1.00},      // 20 8 waves, wave tile 96x64
+    {kSk, 192, 384, 2, 4, 128, 2, 1.00},      // 21 8 waves, wave tile 96x96
+    {kSk, 192, 128, 2, 2, 128, 2, 1.00},      // 22 wave tile 96x64
+    {kSk, 128, 128, 2, 2, 128, 2, 1.00},      // 23 wave tile 64x64
 };
 // fp32.
 static const GemmPlan kPlans32[] = {
@@ -580,6 +848,7 @@ static int auto_plan(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) 
   int best = 0;
   double best_cost = 1e300;
   for (int i = 0; i < count; ++i) {
+    if (p[i].kind == kSk) continue;
     if (p[i].kind == kDtl && !dtl_ok(p[i], K, lda, ldw, sizeof(T))) continue;
     const int64_t tiles = ((M + p[i].bm - 1) / p[i].bm) * ((N + p[i].bn - 1) / p[i].bn);
     const int64_t rounds = (tiles + 255) / 256;
@@ -594,56 +863,134 @@ static int auto_plan(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) 
 
 // Kernel selection by plan kind through a specialised struct (the host stub
 // of a kernel launched under `if constexpr` is not always emitted).
+struct GemmArgs {
+  const void* a; int64_t lda; const void* w; int64_t ldw; const void* bias; void* c; int64_t ldc;
+  int M, N, K; void* ws; size_t ws_bytes; hipStream_t s;
+};
 template <int KIND> struct Launcher;
 template <> struct Launcher<kStaged> {
   template <typename T, int BM, int BN, int WM, int WN, int EPI>
-  static void go(dim3 grid, hipStream_t s, const void* a, int64_t lda, const void* w, int64_t ldw,
-                 const void* bias, void* c, int64_t ldc, int M, int N, int K) {
-    hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WM, WN, EPI>), grid, dim3(WM * WN * 64), 0, s, (const T*)a, lda,
-                       (const T*)w, ldw, (const T*)bias, c, ldc, M, N, K);
+  static int go(const GemmArgs& g) {
+    const dim3 grid(((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN));
+    hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WM, WN, EPI>), grid, dim3(WM * WN * 64), 0, g.s, (const T*)g.a,
+                       g.lda, (const T*)g.w, g.ldw, (const T*)g.bias, g.c, g.ldc, g.M, g.N, g.K);
+    return TJK_OK;
   }
 };
 template <int BKB, int STAGES, int KSPLIT = 1> struct DtlLauncher {
   template <typename T, int BM, int BN, int WM, int WN, int EPI>
-  static void go(dim3 grid, hipStream_t s, const void* a, int64_t lda, const void* w, int64_t ldw,
-                 const void* bias, void* c, int64_t ldc, int M, int N, int K) {
+  static int go(const GemmArgs& g) {
+    const dim3 grid(((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN));
     hipLaunchKernelGGL((gemm_dtl_kernel<T, BM, BN, WM, WN, BKB, STAGES, EPI, KSPLIT>), grid,
-                       dim3(WM * WN * KSPLIT * 64), 0, s, (const T*)a, lda, (const T*)w, ldw, (const T*)bias, c,
-                       ldc, M, N, K);
+                       dim3(WM * WN * KSPLIT * 64), 0, g.s, (const T*)g.a, g.lda, (const T*)g.w, g.ldw,
+                       (const T*)g.bias, g.c, g.ldc, g.M, g.N, g.K);
+    return TJK_OK;
   }
 };
 
-template <typename L, typename T, int BM, int BN, int WM, int WN, int EPI>
-static void launch_one(dim3 grid, hipStream_t s, const void* a, int64_t lda, const void* w, int64_t ldw,
-                       const void* bias, void* c, int64_t ldc, int M, int N, int K) {
-  L::template go<T, BM, BN, WM, WN, EPI>(grid, s, a, lda, w, ldw, bias, c, ldc, M, N, K);
+// Resident grid of a persistent kernel on the current device: CUs x
+// workgroups per CU (queried once per kernel and device), at most kMaxSkGrid.
+template <typename F>
+static int resident_grid(F kernel, int threads) {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel), threads, 0) !=
+      hipSuccess)
+    return 0;
+  const int g = min(max(cus * per_cu, 1), kMaxSkGrid);
+  if (dev < 64) cached[dev] = g;
+  return g;
 }
 
+template <int BKB, int STAGES> struct SkLauncher {
+  template <typename T, int BM, int BN, int WM, int WN, int EPI>
+  static int grid() {
+    return resident_grid(gemm_sk_kernel<T, BM, BN, WM, WN, BKB, STAGES, EPI>, WM * WN * 64);
+  }
+  template <typename T, int BM, int BN, int WM, int WN>
+  static size_t workspace_bytes() {
+    const int g = max(max(grid<T, BM, BN, WM, WN, TJK_EPI_BIAS>(), grid<T, BM, BN, WM, WN, TJK_EPI_BIAS_GELU>()),
+                      grid<T, BM, BN, WM, WN, TJK_EPI_BIAS_RESIDUAL>());
+    return g > 0 ? kSkHeader + (size_t)g * BM * BN * sizeof(float) : 0;
+  }
+  template <typename T, int BM, int BN, int WM, int WN, int EPI>
+  static int go(const GemmArgs& g) {
+    const int G = grid<T, BM, BN, WM, WN, EPI>();
+    if (G <= 0) return fail(TJK_EUNSUPPORTED, "tjk_gemm_bias: no resident grid for the stream-K plan");
+    if (!g.ws) return fail(TJK_EINVAL, "tjk_gemm_bias: stream-K plan needs a workspace (tjk_gemm_bias_ws)");
+    const size_t need = kSkHeader + (size_t)G * BM * BN * sizeof(float);
+    if (g.ws_bytes < need || ((uintptr_t)g.ws & 255))
+      return fail(TJK_EINVAL, "tjk_gemm_bias: stream-K workspace needs %zu bytes, 256-byte aligned (got %zu)", need,
+                  g.ws_bytes);
+    constexpr int BK = BKB / sizeof(T);
+    SkParams p;
+    p.tiles_m = (g.M + BM - 1) / BM;
+    p.tiles_n = (g.N + BN - 1) / BN;
+    p.nk = g.K / BK;
+    const int tiles = p.tiles_m * p.tiles_n;
+    // whole rounds stay data-parallel except the last full one, which joins
+    // the partial round in the stream-K part (no K segment shorter than
+    // about a tile's worth per workgroup)
+    if (tiles % G == 0) p.dp_tiles = tiles;
+    else if (tiles < G) p.dp_tiles = 0;
+    else p.dp_tiles = (tiles / G - 1) * G;
+    const int64_t units = (int64_t)(tiles - p.dp_tiles) * p.nk;
+    if (units > INT32_MAX) return fail(TJK_EUNSUPPORTED, "tjk_gemm_bias: too many stream-K units");
+    p.sk_units = (int)units;
+    hipLaunchKernelGGL((gemm_sk_kernel<T, BM, BN, WM, WN, BKB, STAGES, EPI>), dim3(G), dim3(WM * WN * 64), 0, g.s,
+                       (const T*)g.a, g.lda, (const T*)g.w, g.ldw, (const T*)g.bias, g.c, g.ldc, g.M, g.N, p,
+                       (char*)g.ws);
+    return TJK_OK;
+  }
+};
+
 template <typename L, typename T, int BM, int BN, int WM, int WN>
-static void launch_epi(int epi, const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias,
-                       void* c, int64_t ldc, int M, int N, int K, hipStream_t s) {
-  const dim3 grid(((M + BM - 1) / BM) * ((N + BN - 1) / BN));
+static int launch_epi(int epi, const GemmArgs& g) {
   switch (epi) {
-    case TJK_EPI_BIAS:
-      launch_one<L, T, BM, BN, WM, WN, TJK_EPI_BIAS>(grid, s, a, lda, w, ldw, bias, c, ldc, M, N, K);
-      break;
-    case TJK_EPI_BIAS_GELU:
-      launch_one<L, T, BM, BN, WM, WN, TJK_EPI_BIAS_GELU>(grid, s, a, lda, w, ldw, bias, c, ldc, M, N, K);
-      break;
-    default:
-      launch_one<L, T, BM, BN, WM, WN, TJK_EPI_BIAS_RESIDUAL>(grid, s, a, lda, w, ldw, bias, c, ldc, M, N, K);
-      break;
+    case TJK_EPI_BIAS: return L::template go<T, BM, BN, WM, WN, TJK_EPI_BIAS>(g);
+    case TJK_EPI_BIAS_GELU: return L::template go<T, BM, BN, WM, WN, TJK_EPI_BIAS_GELU>(g);
+    default: return L::template go<T, BM, BN, WM, WN, TJK_EPI_BIAS_RESIDUAL>(g);
+  }
+}
+
+typedef Launcher<kStaged> St;
+typedef DtlLauncher<128, 2> D2;
+typedef DtlLauncher<128, 2, 2> D2K2;
+typedef SkLauncher<128, 2> SK2;
+
+// Stream-K plans of the 2-byte table: (id, BM, BN, WM, WN).
+#define TJK_SK_PLANS(X)      \
+  X(18, SK2, 256, 256, 2, 4) \
+  X(19, SK2, 256, 256, 2, 2) \
+  X(20, SK2, 192, 256, 2, 4) \
+  X(21, SK2, 192, 384, 2, 4) \
+  X(22, SK2, 192, 128, 2, 2) \
+  X(23, SK2, 128, 128, 2, 2)
+
+template <typename T>
+static size_t sk_workspace_bytes(int plan) {
+  if constexpr (sizeof(T) == 4) {
+    return 0;
+  } else {
+    switch (plan) {
+#define TJK_SK_WS(ID, L, BM, BN, WM, WN) \
+  case ID: return L::template workspace_bytes<T, BM, BN, WM, WN>();
+      TJK_SK_PLANS(TJK_SK_WS)
+#undef TJK_SK_WS
+    }
+    return 0;
   }
 }
 
 template <typename T>
-static int run_gemm(int plan, int epi, const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias,
-                    void* c, int64_t ldc, int M, int N, int K, hipStream_t s) {
-  typedef Launcher<kStaged> St;
-  typedef DtlLauncher<128, 2> D2;
-  typedef DtlLauncher<128, 2, 2> D2K2;
+static int run_gemm(int plan, int epi, const GemmArgs& g) {
+  int rc = TJK_OK;
 #define TJK_GEMM_CASE(ID, L, BM, BN, WM, WN) \
-  case ID: launch_epi<L, T, BM, BN, WM, WN>(epi, a, lda, w, ldw, bias, c, ldc, M, N, K, s); break;
+  case ID: rc = launch_epi<L, T, BM, BN, WM, WN>(epi, g); break;
   if constexpr (sizeof(T) == 4) {
     switch (plan) {
       TJK_GEMM_CASE(0, St, 128, 128, 2, 2)
@@ -672,25 +1019,29 @@ static int run_gemm(int plan, int epi, const void* a, int64_t lda, const void* w
       TJK_GEMM_CASE(15, D2, 96, 128, 1, 4)
       TJK_GEMM_CASE(16, D2K2, 192, 128, 2, 2)
       TJK_GEMM_CASE(17, D2K2, 128, 128, 2, 2)
+      TJK_SK_PLANS(TJK_GEMM_CASE)
     }
   }
 #undef TJK_GEMM_CASE
+  if (rc != TJK_OK) return rc;
   return check_launch("tjk_gemm_bias");
 }
 
 template <typename T>
 static int gemm_checked(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias, void* c,
-                        int64_t ldc, int64_t m, int64_t n, int64_t k, int epi, int plan, hipStream_t s) {
+                        int64_t ldc, int64_t m, int64_t n, int64_t k, int epi, int plan, void* ws,
+                        size_t ws_bytes, hipStream_t s) {
   int count;
   const GemmPlan* p = plans<T>(&count);
   if (plan < -1 || plan >= count) return fail(TJK_EINVAL, "tjk_gemm_bias: plan %d out of range [-1,%d)", plan, count);
   if (plan == -1) plan = auto_plan<T>(m, n, k, lda, ldw);
-  if (p[plan].kind == kDtl && !dtl_ok(p[plan], k, lda, ldw, sizeof(T)))
+  if (p[plan].kind != kStaged && !dtl_ok(p[plan], k, lda, ldw, sizeof(T)))
     return fail(TJK_EUNSUPPORTED, "tjk_gemm_bias: plan %d needs k %% %d == 0", plan, (int)(p[plan].bkb / sizeof(T)));
-  if (p[plan].kind == kDtl && ((int64_t)p[plan].bm * lda * (int64_t)sizeof(T) > INT32_MAX ||
-                               (int64_t)p[plan].bn * ldw * (int64_t)sizeof(T) > INT32_MAX))
+  if (p[plan].kind != kStaged && ((int64_t)p[plan].bm * lda * (int64_t)sizeof(T) > INT32_MAX ||
+                                  (int64_t)p[plan].bn * ldw * (int64_t)sizeof(T) > INT32_MAX))
     return fail(TJK_EUNSUPPORTED, "tjk_gemm_bias: leading dimension too large for plan %d", plan);
-  return run_gemm<T>(plan, epi, a, lda, w, ldw, bias, c, ldc, (int)m, (int)n, (int)k, s);
+  const GemmArgs g{a, lda, w, ldw, bias, c, ldc, (int)m, (int)n, (int)k, ws, ws_bytes, s};
+  return run_gemm<T>(plan, epi, g);
 }
 
 }  // namespace tjk
@@ -718,10 +1069,26 @@ extern "C" int tjk_gemm_plan_info(int dtype, int id, int* block_m, int* block_n,
   return TJK_OK;
 }
 
+extern "C" size_t tjk_gemm_workspace_bytes(int dtype, int plan_id) {
+  switch (dtype) {
+    case TJK_F16: return sk_workspace_bytes<f16>(plan_id);
+    case TJK_BF16: return sk_workspace_bytes<bf16>(plan_id);
+    default: return 0;
+  }
+}
+
 extern "C" int tjk_gemm_bias(const void* a, int64_t lda, const void* w, int64_t ldw,
                              const void* bias, void* c, int64_t ldc,
                              int64_t m, int64_t n, int64_t k,
                              int dtype, int epilogue, int plan_id, void* stream) {
+  return tjk_gemm_bias_ws(a, lda, w, ldw, bias, c, ldc, m, n, k, dtype, epilogue, plan_id, nullptr, 0, stream);
+}
+
+extern "C" int tjk_gemm_bias_ws(const void* a, int64_t lda, const void* w, int64_t ldw,
+                                const void* bias, void* c, int64_t ldc,
+                                int64_t m, int64_t n, int64_t k,
+                                int dtype, int epilogue, int plan_id,
+                                void* workspace, size_t workspace_bytes, void* stream) {
   if (m < 0 || n < 0 || k < 0) return fail(TJK_EINVAL, "tjk_gemm_bias: negative shape");
   if (m == 0 || n == 0) return TJK_OK;
   if (!a || !w || !c) return fail(TJK_EINVAL, "tjk_gemm_bias: null pointer");
@@ -740,9 +1107,15 @@ extern "C" int tjk_gemm_bias(const void* a, int64_t lda, const void* w, int64_t 
     return fail(TJK_EUNSUPPORTED, "tjk_gemm_bias: misaligned pointer");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (dtype) {
-    case TJK_F32: return gemm_checked<float>(a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, plan_id, s);
-    case TJK_F16: return gemm_checked<f16>(a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, plan_id, s);
-    default: return gemm_checked<bf16>(a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, plan_id, s);
+    case TJK_F32:
+      return gemm_checked<float>(a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, plan_id, workspace,
+                                 workspace_bytes, s);
+    case TJK_F16:
+      return gemm_checked<f16>(a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, plan_id, workspace,
+                               workspace_bytes, s);
+    default:
+      return gemm_checked<bf16>(a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, plan_id, workspace,
+                                workspace_bytes, s);
   }
 }
 

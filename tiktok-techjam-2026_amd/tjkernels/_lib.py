@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede the library load; see module docstring)
 
 LIB_PATH = Path(__file__).with_name("libtjk.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 F32, F16, BF16 = 0, 1, 2
 EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RESIDUAL = 0, 1, 2
@@ -33,6 +33,9 @@ _SIGNATURES = {
                                  _vp, _vp, _i64, _i64, _f32, _vp, _vp, _vp]),
     "tjk_gemm_bias": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64,
                              _i32, _i32, _i32, _vp]),
+    "tjk_gemm_bias_ws": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64,
+                                _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp]),
+    "tjk_gemm_workspace_bytes": (ctypes.c_size_t, [_i32, _i32]),
     "tjk_gemm_plan_count": (_i32, [_i32]),
     "tjk_gemm_plan_info": (_i32, [_i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32),
                                   ctypes.POINTER(_i32)]),

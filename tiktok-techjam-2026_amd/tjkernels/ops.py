@@ -91,10 +91,49 @@ def add_layernorm(res: torch.Tensor, delta: Optional[torch.Tensor],
     return out
 
 
+_ws_need = {}    # (dtype code, plan) -> workspace bytes on this device (0: none)
+_ws_shared = {}  # device index -> zero-filled uint8 workspace for the stream-K plans
+
+
+def gemm_workspace(device: torch.device) -> torch.Tensor:
+    """The per-device workspace the stream-K GEMM plans share: sized for the
+    largest of them, zero-filled once (every completed call leaves its flag
+    area zero).  Calls using it must be ordered (one stream), which the
+    engine's forward is."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _ws_shared.get(idx)
+    if ws is None:
+        lib = _lib.load()
+        with torch.cuda.device(idx):
+            need = max([lib.tjk_gemm_workspace_bytes(code, p)
+                        for code in (_lib.DTYPE_CODES[torch.bfloat16], _lib.DTYPE_CODES[torch.float16])
+                        for p in range(lib.tjk_gemm_plan_count(code))] + [0])
+            ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=torch.device("cuda", idx))
+        _ws_shared[idx] = ws
+    return ws
+
+
+def _workspace_for(a: torch.Tensor, plan: int, workspace: Optional[torch.Tensor]):
+    if plan < 0:
+        return None
+    key = (_code(a), plan, a.device.index)
+    need = _ws_need.get(key)
+    if need is None:
+        with torch.cuda.device(a.device):
+            need = _lib.load().tjk_gemm_workspace_bytes(_code(a), plan)
+        _ws_need[key] = need
+    if need == 0:
+        return None
+    return workspace if workspace is not None else gemm_workspace(a.device)
+
+
 def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], out: torch.Tensor,
-         epilogue: int = EPI_BIAS, plan: int = -1) -> torch.Tensor:
+         epilogue: int = EPI_BIAS, plan: int = -1,
+         workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
     """out = epi(a @ w.T + bias); w in nn.Linear [N, K] layout.
-    With EPI_BIAS_RESIDUAL, ``out`` is an fp32 residual updated in place."""
+    With EPI_BIAS_RESIDUAL, ``out`` is an fp32 residual updated in place.
+    Stream-K plans use ``workspace`` (uint8, zero-filled before its first
+    use) or, by default, the device's shared one (``gemm_workspace``)."""
     _require_gpu(a, w, bias, out)
     m, k = a.shape
     n, k2 = w.shape
@@ -108,9 +147,11 @@ def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], out: to
     elif out.dtype != a.dtype:
         raise TjkError("gemm out must have the operands' dtype")
     lib = _lib.load()
-    status = lib.tjk_gemm_bias(a.data_ptr(), _rowmajor(a, "a"), w.data_ptr(), _rowmajor(w, "w"),
-                               _ptr(bias), out.data_ptr(), _rowmajor(out, "out"), m, n, k,
-                               _code(a), epilogue, plan, _stream(a))
+    ws = _workspace_for(a, plan, workspace)
+    status = lib.tjk_gemm_bias_ws(a.data_ptr(), _rowmajor(a, "a"), w.data_ptr(), _rowmajor(w, "w"),
+                                  _ptr(bias), out.data_ptr(), _rowmajor(out, "out"), m, n, k,
+                                  _code(a), epilogue, plan, _ptr(ws),
+                                  ws.numel() if ws is not None else 0, _stream(a))
     check(status, "tjk_gemm_bias")
     return out
 
