@@ -153,22 +153,27 @@ int tjk_flash_plan_count(int dtype);
  *   work[4*i .. 4*i+3] = { b*heads + h, qb, t_lo | t_hi << 16, slot }
  *     query block qb (queries 128*qb .. 128*qb+127 of sequence b, head h)
  *     over key tiles t_lo .. t_hi-1 (64 keys each; t_hi is clipped to the
- *     block's last causal / in-sequence tile); slot < 0 writes the output
- *     rows, slot >= 0 writes an fp32 partial (unnormalised O, running max
- *     and sum per query) into partials slot `slot`
- *   merges[4*j .. 4*j+3] = { b*heads + h, qb, slot_lo, slot_hi }: a second
- *     launch combines two partials of one query block (in that order, so the
- *     result is deterministic) and writes its output rows
+ *     block's last causal / in-sequence tile); slot -1 writes the output
+ *     rows; a query block split over its key range is two items: the first
+ *     (slot s >= 0) publishes an fp32 partial (unnormalised O, exponent
+ *     offset and sum per query) in partials slot s, the second (slot -2-s)
+ *     waits for it, merges it into its own ((O_hi a_hi + O_lo a_lo) /
+ *     (l_hi a_hi + l_lo a_lo), in that order, so results are deterministic)
+ *     and writes the output rows.  The first half must precede the second in
+ *     the list (workgroups are dispatched in list order).
  * Every (query block, key tile) pair of every sequence must be covered
- * exactly once.  partials holds tjk_flash_partial_bytes(head_dim, n) bytes
- * for n slots.  max_seqlen bounds every sequence length.  Replaces the
- * reference's grid of (query block, b*h) programs, attention.py:199-217.
+ * exactly once.  partials holds tjk_flash_partial_bytes(head_dim, n_slots)
+ * bytes: the n_slots partials, an error word (timed-out waits) and one flag
+ * per slot, zero-filled before the first call; every completed call leaves
+ * the flags zero.  Calls sharing a partials buffer must not overlap.
+ * max_seqlen bounds every sequence length.  Replaces the reference's grid of
+ * (query block, b*h) programs, attention.py:199-217.
  */
 int tjk_flash_fwd_sched(const void* qkv, int64_t stride_s, int64_t stride_c, int64_t stride_h,
                         void* out, int64_t ld_out, int batch, int max_seqlen, int heads,
                         int head_dim, float scale, int causal, const int32_t* cu_seqlens,
-                        const int32_t* work, int n_work, const int32_t* merges, int n_merges,
-                        float* partials, int dtype, void* stream);
+                        const int32_t* work, int n_work, float* partials, int n_slots,
+                        int dtype, void* stream);
 size_t tjk_flash_partial_bytes(int head_dim, int n_slots);
 /* Workgroups of the scheduled kernel resident per CU (> 0), or a negative /
  * hipError_t status. */

@@ -177,8 +177,38 @@ def test_gemm_stream_k_deterministic_and_flags_cleared(device):
         outs.append(out)
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
-    ws = ops.gemm_workspace(device)
-    header = ws[:2049 * 4].view(torch.int32).cpu()
+    header = ops.gemm_workspace(device)[:32768].view(torch.int32).cpu()
+    assert int(header.abs().sum()) == 0  # every flag cleared, no timed-out wait
+
+
+# Split-K residual plans: two workgroups per tile, one per half of K, the
+# second adding its half after the first (residual epilogue only).
+K2_16 = (24, 25)
+
+
+@pytest.mark.parametrize("plan", K2_16)
+def test_gemm_split_k_residual(device, plan):
+    for m, n, k in ((5430, 1024, 4096), (513, 1028, 1088), (64, 32, 64), (1000, 516, 128)):
+        _gemm_case(device, m, n, k, torch.bfloat16, ops.EPI_BIAS_RESIDUAL, plan)
+    _gemm_case(device, 700, 256, 2048, torch.float16, ops.EPI_BIAS_RESIDUAL, plan)
+    with pytest.raises(ops.TjkError, match="residual"):
+        _gemm_case(device, 256, 256, 256, torch.bfloat16, ops.EPI_BIAS, plan)
+
+
+def test_gemm_split_k_deterministic_and_flags_cleared(device):
+    g = _gen(6)
+    a = torch.randn(5430, 1024, generator=g).bfloat16().to(device)
+    w = (torch.randn(1024, 1024, generator=g) / 32).bfloat16().to(device)
+    b = torch.randn(1024, generator=g).bfloat16().to(device)
+    r0 = torch.randn(5430, 1024, generator=g).to(device)
+    outs = []
+    for plan in (24, 24, 24, 25, 25):
+        out = r0.clone()
+        ops.gemm(a, w, b, out, ops.EPI_BIAS_RESIDUAL, plan)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2]) and torch.equal(outs[3], outs[4])
+    header = ops.gemm_workspace(device)[:32768].view(torch.int32).cpu()
     assert int(header.abs().sum()) == 0  # every flag cleared, no timed-out wait
 
 
@@ -419,9 +449,10 @@ def test_flash_packed_sequences(device, dt, hd, causal):
 @pytest.mark.parametrize("hd", [32, 64, 128])
 @pytest.mark.parametrize("causal", [True, False])
 def test_flash_scheduled(device, dt, hd, causal):
-    """The scheduled kernel (work list, key-split items merged in a second
-    launch) against the fp64 brute force per sequence, with few slots so that
-    most items are split, and against the plain packed kernel."""
+    """The scheduled kernel (work list; key-split items whose second half
+    merges the first's partial) against the fp64 brute force per sequence,
+    with many slots so that most items are split, and against the plain
+    packed kernel.  The flags end cleared and no wait timed out."""
     from tjkernels.schedule import build_schedule
     lengths = [300, 0, 1, 129, 64, 200]
     h = 3
@@ -437,7 +468,7 @@ def test_flash_scheduled(device, dt, hd, causal):
     for slots, min_split in ((100000, 2), (1, 6)):
         sched = build_schedule(lengths, h, hd, causal, dt, device, slots=slots, min_split=min_split,
                                split_factor=1.0)
-        assert (sched.merges.shape[0] > 0) == (min_split == 2)
+        assert (sched.n_slots > 0) == (min_split == 2)
         out = torch.full((t + 5, h * hd), 7.0, dtype=dt, device=device)
         ops.flash_attention_sched(qkv.to(device), out, cu_d, max(lengths), sched, causal=causal)
         torch.cuda.synchronize()
@@ -455,3 +486,11 @@ def test_flash_scheduled(device, dt, hd, causal):
             assert torch.equal(got[:t], plain.cpu())
         else:
             assert (got[:t].float() - plain.cpu().float()).abs().max().item() < 2e-2
+            # the partial slots are followed by the error word and the flags
+            hdp = 32 if hd <= 32 else 64 if hd <= 64 else 128
+            tail = sched.partials.view(torch.int32)[sched.n_slots * 128 * (hdp + 2):].cpu()
+            assert int(tail.abs().sum()) == 0, "a flag was left set or a wait timed out"
+            again = torch.full((t + 5, h * hd), 7.0, dtype=dt, device=device)
+            ops.flash_attention_sched(qkv.to(device), again, cu_d, max(lengths), sched, causal=causal)
+            torch.cuda.synchronize()
+            assert torch.equal(again.cpu(), got), "split merge is not deterministic"

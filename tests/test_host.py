@@ -224,12 +224,13 @@ def test_valid_token_flops():
 
 def test_attention_schedule_covers_every_tile_once():
     """Every (sequence, head, query block, key tile) pair appears in exactly
-    one work item, split items pair up in the merge list, items are issued
-    longest first, and no item exceeds the split target."""
+    one work item, split items pair up (first half before second, adjacent
+    key ranges), items are issued longest first, and no unsplit item exceeds
+    the split target."""
     from tjkernels.schedule import BMQ, BNK, build_items
     for causal in (True, False):
-        lengths, heads, slots = [1380, 1710, 0, 1054, 1, 129], 3, 40
-        work, merges, n_slots = build_items(lengths, heads, causal, slots, split_factor=1.0)
+        lengths, heads, slots = [1380, 1710, 0, 1054, 1, 129], 3, 100
+        work, n_slots = build_items(lengths, heads, causal, slots, split_factor=1.0)
         seen = {}
         for cost, bh, qb, lo, hi, slot in work:
             assert hi - lo == cost and cost > 0
@@ -249,9 +250,12 @@ def test_attention_schedule_covers_every_tile_once():
         assert costs == sorted(costs, reverse=True)
         total = sum(costs)
         target = max(total / slots, 6)
-        assert all(w[0] <= target for w in work if w[5] < 0), "an item above the target was not split"
-        slots_used = sorted(s for m in merges for s in m[2:])
-        assert slots_used == list(range(n_slots))
-        for bh, qb, lo_slot, hi_slot in merges:
-            halves = sorted((w[3], w[4], w[5]) for w in work if w[1] == bh and w[2] == qb)
-            assert [h[2] for h in halves] == [lo_slot, hi_slot] and halves[0][1] == halves[1][0]
+        assert all(w[0] <= target for w in work if w[5] == -1), "an item above the target was not split"
+        assert n_slots > 0 or not causal
+        for s_ in range(n_slots):
+            first = [i for i, w in enumerate(work) if w[5] == s_]
+            second = [i for i, w in enumerate(work) if w[5] == -2 - s_]
+            assert len(first) == 1 and len(second) == 1
+            a, b = work[first[0]], work[second[0]]
+            assert first[0] < second[0], "a second half is issued before its first half"
+            assert (a[1], a[2]) == (b[1], b[2]) and a[3] == 0 and a[4] == b[3]

@@ -389,6 +389,11 @@ __global__ __launch_bounds__(256 * KS) void flash_fwd_kernel(
 // the diagonal / tail tiles run a second loop with masks and per-wave skips.
 
 constexpr uint32_t kFaPastEnd = 0x7fff0000u;
+// Cache-policy bits of buffer loads / stores (sc0 = 1, sc1 = 16): sc1 makes
+// an access device-coherent, sc0 sc1 on a store writes through to memory.
+constexpr int kFaSc1 = 16, kFaSc0Sc1 = 17;
+constexpr int kFaSpinLimit = 1 << 22;  // polls of a split item's flag before giving up
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 template <typename T, int HDP, bool KEYMASK, bool FULLHD>
 __global__ __launch_bounds__(256) void flash_pipe_kernel(
@@ -396,7 +401,7 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
     T* __restrict__ out, int64_t ld_out, int B, int S, int H, int hd, float scale_log2,
     int causal, const int32_t* __restrict__ lengths, const uint8_t* __restrict__ key_mask,
     const int32_t* __restrict__ cu_seqlens, int nqb,
-    const int4* __restrict__ work, float* __restrict__ partials) {
+    const int4* __restrict__ work, float* __restrict__ partials, int* __restrict__ flags) {
   static_assert(sizeof(T) == 2, "2-byte element types only");
   constexpr int BMQ = 128, BNK = 64, NST = 3, VEC = 8;
   constexpr int LDK = HDP + VEC, LDV = BNK + VEC;
@@ -410,7 +415,10 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
 
   const int BH = B * H;
   // Work item: from the scheduled list (bh, qb, key tiles [t_lo, t_hi),
-  // partial slot or -1), else from the grid (every key tile, longest first).
+  // slot), else from the grid (every key tile, longest first).  slot -1: a
+  // whole item; slot s >= 0: the first half of a key-split item, which
+  // publishes its partial in slot s; slot -2 - s: the second half, which
+  // merges partial s into its own before the store.
   int bh, qb, t_lo = 0, t_hi = 1 << 30, slot = -1;
   if (work != nullptr) {
     const int4 it = work[blockIdx.x];
@@ -662,24 +670,68 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
   // normalise and store: register r of block hb is hd row hb*32 + 8*(r/4) + 4*hi + r%4
   const int q = wq0 + l32;
   const float l = l_run + __shfl_xor(l_run, 32, 64);
+  // Partial slot s: O^T rows [query][HDP] fp32, then m[BMQ], then l[BMQ].
+  // The halves of a split item are different workgroups, possibly on
+  // different XCDs: the partial is written through to memory (sc0 sc1) and
+  // read device-coherently (sc1), with a flag per slot in between.
+  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(partials, (short)0, 0x7fffffff, 0x00020000);
+  auto pslot = [&](int sl) { return sl * (BMQ * (HDP + 2)) * 4; };  // byte offset
+  const int prow = (wave * 32 + l32) * HDP * 4;
   if (slot >= 0) {
-    // Partial of a key-split item: unnormalised O^T, running max and sum per
-    // query, merged with the other half by flash_merge_kernel.
-    float* pb = partials + (int64_t)slot * BMQ * (HDP + 2);
-    float* prow = pb + (int64_t)(wave * 32 + l32) * HDP;
+    const int pb = pslot(slot);
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb)
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<float4*>(prow + hb * 32 + 8 * g + 4 * hi) =
-            make_float4(o[hb][4 * g], o[hb][4 * g + 1], o[hb][4 * g + 2], o[hb][4 * g + 3]);
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 v = {o[hb][4 * g], o[hb][4 * g + 1], o[hb][4 * g + 2], o[hb][4 * g + 3]};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), prs,
+                                               pb + prow + (hb * 32 + 8 * g + 4 * hi) * 4, 0, kFaSc0Sc1);
+      }
     if (hi == 0) {
-      pb[BMQ * HDP + wave * 32 + l32] = m_off;
-      pb[BMQ * HDP + BMQ + wave * 32 + l32] = l;
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, m_off), prs,
+                                            pb + (BMQ * HDP + wave * 32 + l32) * 4, 0, kFaSc0Sc1);
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, l), prs,
+                                            pb + (BMQ * HDP + BMQ + wave * 32 + l32) * 4, 0, kFaSc0Sc1);
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial is in memory
+    __syncthreads();
+    if (tid == 0) __hip_atomic_store(&flags[slot], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
-  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  float lm = l;
+  if (slot <= -2) {
+    // Second half: wait for the first (bounded polls; a timeout is counted
+    // in the error word after the flags), then
+    //   O = O_hi a_hi + O_lo a_lo,  l = l_hi a_hi + l_lo a_lo,
+    //   a_x = 2^(m_x - max(m_lo, m_hi)),  in this order every time.
+    const int ps = -2 - slot, pb = pslot(ps);
+    int spins = 0;
+    while (__hip_atomic_load(&flags[ps], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
+      if (++spins > kFaSpinLimit) {
+        if (tid == 0) __hip_atomic_fetch_add(&flags[-1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    const float m_lo = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(prs, pb + (BMQ * HDP + wave * 32 + l32) * 4, 0, kFaSc1));
+    const float l_lo = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(prs, pb + (BMQ * HDP + BMQ + wave * 32 + l32) * 4, 0, kFaSc1));
+    const float m = fmaxf(m_lo, m_off);
+    const float a_lo = m_lo == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_lo - m);
+    const float a_hi = m_off == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_off - m);
+    lm = fmaf(l, a_hi, l_lo * a_lo);
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 v = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, pb + prow + (hb * 32 + 8 * g + 4 * hi) * 4, 0, kFaSc1));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[hb][4 * g + e] = fmaf(o[hb][4 * g + e], a_hi, v[e] * a_lo);
+      }
+  }
+  const float inv = lm > 0.f ? 1.0f / lm : 0.f;
   if (q < Sb) {
     T* orow = out + (row0 + q) * ld_out + (int64_t)h * hd;
 #pragma unroll
@@ -694,60 +746,25 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
         }
       }
   }
-}
-
-// Merge of key-split work items: item halves lo / hi of query block qb of
-// (b, h) each left an unnormalised O, its exponent offset m (log2 units) and
-// a sum l per query; the output is
-//     (O_lo a_lo + O_hi a_hi) / (l_lo a_lo + l_hi a_hi),  a_x = 2^(m_x - m),
-// m = max(m_lo, m_hi), always combined in this order (deterministic).
-template <typename T, int HDP>
-__global__ __launch_bounds__(256) void flash_merge_kernel(
-    const float* __restrict__ partials, const int4* __restrict__ merges, T* __restrict__ out,
-    int64_t ld_out, int H, int hd, float scale_log2, const int32_t* __restrict__ cu_seqlens) {
-  constexpr int BMQ = 128, C4 = HDP / 4;
-  const int4 mg = merges[blockIdx.x];  // (bh, qb, slot_lo, slot_hi)
-  const int b = mg.x / H, h = mg.x % H, q0 = mg.y * BMQ;
-  const int64_t row0 = cu_seqlens[b];
-  const int Sb = cu_seqlens[b + 1] - cu_seqlens[b];
-  const float* lo = partials + (int64_t)mg.z * BMQ * (HDP + 2);
-  const float* hi = partials + (int64_t)mg.w * BMQ * (HDP + 2);
-  for (int idx = threadIdx.x; idx < BMQ * C4; idx += 256) {
-    const int ql = idx / C4, c = (idx % C4) * 4;
-    if (q0 + ql >= Sb || c >= hd) continue;
-    const float m_lo = lo[BMQ * HDP + ql], m_hi = hi[BMQ * HDP + ql];
-    const float m = fmaxf(m_lo, m_hi);
-    const float a_lo = m_lo == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_lo - m);
-    const float a_hi = m_hi == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_hi - m);
-    const float l = fmaf(hi[BMQ * HDP + BMQ + ql], a_hi, lo[BMQ * HDP + BMQ + ql] * a_lo);
-    const float inv = l > 0.f ? 1.0f / l : 0.f;
-    const float4 ol = *reinterpret_cast<const float4*>(lo + (int64_t)ql * HDP + c);
-    const float4 oh = *reinterpret_cast<const float4*>(hi + (int64_t)ql * HDP + c);
-    const float4 v = make_float4(fmaf(oh.x, a_hi, ol.x * a_lo) * inv, fmaf(oh.y, a_hi, ol.y * a_lo) * inv,
-                                 fmaf(oh.z, a_hi, ol.z * a_lo) * inv, fmaf(oh.w, a_hi, ol.w * a_lo) * inv);
-    *reinterpret_cast<typename Quad<T>::raw*>(out + (row0 + q0 + ql) * ld_out + (int64_t)h * hd + c) =
-        Quad<T>::from(v);
+  if (slot <= -2) {
+    __syncthreads();  // every wave has read the partial
+    if (tid == 0) __hip_atomic_store(&flags[-2 - slot], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
 template <typename T, int HDP>
 static int launch_sched(const void* qkv, int64_t ss, int64_t sc, int64_t sh, void* out, int64_t ld_out,
                         int B, int S, int H, int hd, float scale_log2, int causal, const int32_t* cu_seqlens,
-                        const int32_t* work, int n_work, const int32_t* merges, int n_merges, float* partials,
-                        hipStream_t st) {
+                        const int32_t* work, int n_work, float* partials, int n_slots, hipStream_t st) {
+  int* flags = n_slots > 0 ? reinterpret_cast<int*>(partials + (size_t)n_slots * 128 * (HDP + 2)) + 1 : nullptr;
 #define TJK_PIPE_SCHED(FULL)                                                                                  \
   hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, false, FULL>), dim3((unsigned)n_work), dim3(256), 0, st,      \
                      (const T*)qkv, (int64_t)0, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, \
                      (const int32_t*)nullptr, (const uint8_t*)nullptr, cu_seqlens, 0,                         \
-                     reinterpret_cast<const int4*>(work), partials)
+                     reinterpret_cast<const int4*>(work), partials, flags)
   if (hd == HDP) TJK_PIPE_SCHED(true); else TJK_PIPE_SCHED(false);
 #undef TJK_PIPE_SCHED
-  int rc = check_launch("tjk_flash_fwd_sched");
-  if (rc != TJK_OK || n_merges == 0) return rc;
-  hipLaunchKernelGGL((flash_merge_kernel<T, HDP>), dim3((unsigned)n_merges), dim3(256), 0, st,
-                     (const float*)partials, reinterpret_cast<const int4*>(merges), (T*)out, ld_out, H, hd,
-                     scale_log2, cu_seqlens);
-  return check_launch("tjk_flash_fwd_sched (merge)");
+  return check_launch("tjk_flash_fwd_sched");
 }
 
 template <typename T, int HDP>
@@ -761,7 +778,7 @@ static int launch_pipe(const void* qkv, int64_t sb, int64_t ss, int64_t sc, int6
 #define TJK_PIPE(KM, FULL)                                                                                     \
   hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, KM, FULL>), dim3((unsigned)nblk), dim3(256), 0, st, (const T*)qkv, \
                      sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, lengths, key_mask,          \
-                     cu_seqlens, nqb, (const int4*)nullptr, (float*)nullptr)
+                     cu_seqlens, nqb, (const int4*)nullptr, (float*)nullptr, (int*)nullptr)
   if (key_mask != nullptr) {
     if (hd == HDP) TJK_PIPE(true, true); else TJK_PIPE(true, false);
   } else {
@@ -891,19 +908,21 @@ extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s
 extern "C" size_t tjk_flash_partial_bytes(int head_dim, int n_slots) {
   if (head_dim <= 0 || n_slots <= 0) return 0;
   const int hdp = head_dim <= 32 ? 32 : head_dim <= 64 ? 64 : 128;
-  return (size_t)n_slots * 128 * (hdp + 2) * sizeof(float);
+  // partial slots, then the error word and one flag per slot
+  return (size_t)n_slots * 128 * (hdp + 2) * sizeof(float) + (size_t)(n_slots + 1) * sizeof(int);
 }
 
 extern "C" int tjk_flash_fwd_sched(const void* qkv, int64_t stride_s, int64_t stride_c, int64_t stride_h,
                                    void* out, int64_t ld_out, int batch, int max_seqlen, int heads,
                                    int head_dim, float scale, int causal, const int32_t* cu_seqlens,
-                                   const int32_t* work, int n_work, const int32_t* merges, int n_merges,
-                                   float* partials, int dtype, void* stream) {
-  if (batch < 0 || max_seqlen < 0 || heads <= 0 || head_dim <= 0 || n_work < 0 || n_merges < 0)
+                                   const int32_t* work, int n_work, float* partials, int n_slots,
+                                   int dtype, void* stream) {
+  if (batch < 0 || max_seqlen < 0 || heads <= 0 || head_dim <= 0 || n_work < 0 || n_slots < 0)
     return fail(TJK_EINVAL, "tjk_flash_fwd_sched: bad shape or counts");
   if (n_work == 0) return TJK_OK;
   if (!qkv || !out || !cu_seqlens || !work) return fail(TJK_EINVAL, "tjk_flash_fwd_sched: null pointer");
-  if (n_merges > 0 && (!merges || !partials)) return fail(TJK_EINVAL, "tjk_flash_fwd_sched: merges need partials");
+  if (n_slots > 0 && !partials) return fail(TJK_EINVAL, "tjk_flash_fwd_sched: split items need partials");
+  if ((int64_t)n_slots * 128 * 130 * 4 >= INT32_MAX) return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd_sched: too many slots");
   if (dtype != TJK_F16 && dtype != TJK_BF16)
     return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd_sched: 2-byte dtypes only (got %d)", dtype);
   if (head_dim > 128 || head_dim % 8)
@@ -913,16 +932,15 @@ extern "C" int tjk_flash_fwd_sched(const void* qkv, int64_t stride_s, int64_t st
   if (((int64_t)max_seqlen * stride_s + head_dim) * 2 >= INT32_MAX)
     return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd_sched: a sequence's K/V span exceeds 31-bit offsets");
   if (ld_out < (int64_t)heads * head_dim || ld_out % 4) return fail(TJK_EINVAL, "tjk_flash_fwd_sched: bad ld_out");
-  if (((uintptr_t)qkv & 15) || ((uintptr_t)out & 7) || ((uintptr_t)work & 15) || ((uintptr_t)merges & 15) ||
-      ((uintptr_t)partials & 15))
+  if (((uintptr_t)qkv & 15) || ((uintptr_t)out & 7) || ((uintptr_t)work & 15) || ((uintptr_t)partials & 15))
     return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd_sched: misaligned pointer");
   if (!(scale > 0.f)) return fail(TJK_EINVAL, "tjk_flash_fwd_sched: scale must be positive");
   const float scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
 #define TJK_SCHED(TT, HDP)                                                                                  \
   return launch_sched<TT, HDP>(qkv, stride_s, stride_c, stride_h, out, ld_out, batch, max_seqlen, heads, \
-                               head_dim, scale_log2, causal, cu_seqlens, work, n_work, merges, n_merges,  \
-                               partials, st)
+                               head_dim, scale_log2, causal, cu_seqlens, work, n_work, partials, n_slots, \
+                               st)
   if (dtype == TJK_F16) {
     if (head_dim <= 32) TJK_SCHED(f16, 32);
     if (head_dim <= 64) TJK_SCHED(f16, 64);

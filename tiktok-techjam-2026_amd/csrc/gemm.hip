@@ -87,12 +87,22 @@ struct EpiStage {
 // `parts` (stream-K finishers only) supplies parts.n fp32 partial tiles of
 // the same output tile, laid out like the accumulators; they are added in
 // order to acc + bias before the activation.
+// Cache-policy bits of buffer loads / stores on gfx950 (sc0 = 1, sc1 = 16):
+// sc1 makes an access device-coherent, sc0 sc1 on a store writes through.
+constexpr int kCpolSc1 = 16, kCpolSc0Sc1 = 17;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Access policy of the residual read-modify-write (TJK_EPI_BIAS_RESIDUAL):
+// plain, or write-through stores / device-coherent loads for a residual
+// tile that two workgroups update one after the other.
+enum { kResPlain = 0, kResWriteThrough = 1, kResCoherentLoad = 2 };
+
 struct NoParts {
   static constexpr int n = 0;
   __device__ f32x4 get(int, int) const { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 };
 
-template <typename T, int EPI, int FM, int FN, typename Parts = NoParts>
+template <typename T, int EPI, int FM, int FN, typename Parts = NoParts, int RPOL = kResPlain>
 __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* __restrict__ bias,
                                          void* __restrict__ Cv, int64_t ldc, int M, int N, int mw, int nw,
                                          int lane, char* __restrict__ stage, const Parts& parts = Parts()) {
@@ -167,11 +177,21 @@ __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* _
       if (m < M && n < N) {
         if constexpr (EPI == TJK_EPI_BIAS_RESIDUAL) {
           // fp32 pieces never straddle N (N % 4 == 0)
-          float4* r = reinterpret_cast<float4*>(static_cast<float*>(Cv) + (int64_t)m * ldc + n);
           const float4 a = __builtin_bit_cast(float4, piece);
-          float4 o = *r;
-          o.x += a.x; o.y += a.y; o.z += a.z; o.w += a.w;
-          *r = o;
+          if constexpr (RPOL == kResPlain) {
+            float4* r = reinterpret_cast<float4*>(static_cast<float*>(Cv) + (int64_t)m * ldc + n);
+            float4 o = *r;
+            o.x += a.x; o.y += a.y; o.z += a.z; o.w += a.w;
+            *r = o;
+          } else {  // the caller keeps M * ldc * 4 below 2^31
+            const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(Cv, (short)0, 0x7fffffff, 0x00020000);
+            const int off = (int)(((int64_t)m * ldc + n) * 4);
+            float4 o = __builtin_bit_cast(
+                float4, __builtin_amdgcn_raw_buffer_load_b128(rc, off, 0, RPOL == kResCoherentLoad ? kCpolSc1 : 0));
+            o.x += a.x; o.y += a.y; o.z += a.z; o.w += a.w;
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), rc, off, 0,
+                                                   RPOL == kResWriteThrough ? kCpolSc0Sc1 : 0);
+          }
         } else {
           T* c = static_cast<T*>(Cv) + (int64_t)m * ldc + n;
           if (E::SV == 4 || (a16 && n + E::SV <= N)) {
@@ -603,10 +623,6 @@ __global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
 // (8192^3: 1337 TFLOP/s vs 1300 for plan 8).
 
 constexpr int kMaxSkGrid = 2048;
-// Cache-policy bits of buffer loads / stores on gfx950 (sc0 = 1, sc1 = 16):
-// sc1 makes an access device-coherent, sc0 sc1 on a store writes through.
-constexpr int kCpolSc1 = 16, kCpolSc0Sc1 = 17;
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kSkSpinLimit = 1 << 22;
 
 struct SkParams {
@@ -616,10 +632,12 @@ struct SkParams {
   int nk;         // K tiles per output tile
 };
 
-// Workspace: int flags[kMaxSkGrid], int error, padding to 16 KB, then one
-// BM x BN fp32 partial per workgroup.
-constexpr size_t kSkHeader = 16384;
-static_assert((kMaxSkGrid + 1) * 4 <= (int)kSkHeader, "flag area");
+// Workspace: int flags[kMaxSkGrid], int error, the split-K flags
+// (kK2FlagOffset .. kSkHeader), then one BM x BN fp32 partial per workgroup.
+constexpr size_t kSkHeader = 32768;
+constexpr int kK2FlagOffset = 12288;
+constexpr int kMaxK2Tiles = (int)(kSkHeader - kK2FlagOffset) / 4;
+static_assert((kMaxSkGrid + 1) * 4 <= kK2FlagOffset, "flag area");
 
 __device__ __forceinline__ void raster_coords(int t, int tiles_m, int tiles_n, int& pid_m, int& pid_n) {
   const int group = t / (kGroupM * tiles_n);
@@ -760,9 +778,71 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_sk_kernel(
   }
 }
 
+// ------------------------------------------------- split-K residual GEMM
+//
+// For the residual projections (out-proj, FFN2: N = 1024) a tile size that
+// keeps the LDS traffic per MFMA low (192x128) gives only ~232 tiles for
+// 256 CUs, one 4-wave workgroup each, which leaves the MFMA pipes waiting on
+// LDS latency.  Here every tile is computed by two workgroups, one per half
+// of K, all resident at once (2 per CU): the first half adds its partial
+// and the bias into the fp32 residual with write-through stores and raises
+// the tile's flag; the second half waits for the flag (bounded polls), then
+// adds its partial reading the residual device-coherently, and clears the
+// flag.  out = (out + acc_lo + bias) + acc_hi, in that order every time, so
+// results are deterministic.  The second half's workgroups have the higher
+// ids, so they are dispatched after the ones they wait for.
+template <typename T, int BM, int BN, int WM, int WN, int BKB, int STAGES>
+__global__ __launch_bounds__(WM * WN * 64) void gemm_k2_residual_kernel(
+    const T* __restrict__ A, int64_t lda, const T* __restrict__ W, int64_t ldw,
+    const T* __restrict__ bias, float* __restrict__ C, int64_t ldc, int M, int N, int K,
+    int* __restrict__ flags) {
+  typedef DtlGeom<T, BM, BN, WM, WN, BKB, STAGES, 1> G;
+  constexpr int FM = G::FM, FN = G::FN;
+  constexpr int EPI = TJK_EPI_BIAS_RESIDUAL;
+  static_assert(G::NW * EpiStage<T, EPI, FN>::BYTES <= G::LDS, "epilogue staging exceeds LDS");
+  __shared__ __attribute__((aligned(1024))) char smem[G::LDS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int tiles = gridDim.x / 2;
+  const int hi_half = blockIdx.x >= tiles;
+  const int b = blockIdx.x - hi_half * tiles;
+  int pid_m, pid_n;
+  tile_coords(b, (M + BM - 1) / BM, (N + BN - 1) / BN, pid_m, pid_n);
+  const int m0 = pid_m * BM, n0 = pid_n * BN;
+  const int nk = K / G::BK, kmid = nk / 2;
+
+  f32x16 acc[FN][FM];
+  zero_acc<T, FM, FN>(acc);
+  dtl_accumulate<T, BM, BN, WM, WN, BKB, STAGES, 1>(smem, A, lda, W, ldw, M, N, m0, n0, hi_half ? kmid : 0,
+                                                    hi_half ? nk : kmid, acc);
+  char* const stage = smem + wave * EpiStage<T, EPI, FN>::BYTES;
+  if (!hi_half) {
+    epilogue<T, EPI, FM, FN, NoParts, kResWriteThrough>(acc, bias, C, ldc, M, N, m0 + wm * G::WTM,
+                                                        n0 + wn * G::WTN, lane, stage);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the tile is in memory
+    __syncthreads();
+    if (tid == 0) __hip_atomic_store(&flags[b], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    int spins = 0;
+    while (__hip_atomic_load(&flags[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
+      if (++spins > kSkSpinLimit) {
+        if (tid == 0) __hip_atomic_fetch_add(&flags[-1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    epilogue<T, EPI, FM, FN, NoParts, kResCoherentLoad>(acc, nullptr, C, ldc, M, N, m0 + wm * G::WTM,
+                                                        n0 + wn * G::WTN, lane, stage);
+    __syncthreads();
+    if (tid == 0) __hip_atomic_store(&flags[b], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // ------------------------------------------------------------------ plans
 
-enum { kStaged = 0, kDtl = 1, kSk = 2 };
+enum { kStaged = 0, kDtl = 1, kSk = 2, kK2 = 3 };
 
 struct GemmPlan {
   int kind, bm, bn, wm, wn, bkb, stages;
@@ -807,6 +887,9 @@ static const GemmPlan kPlans16[] = {
     {kSk, 192, 384, 2, 4, 128, 2, 1.00},      // 21 8 waves, wave tile 96x96
     {kSk, 192, 128, 2, 2, 128, 2, 1.00},      // 22 wave tile 96x64
     {kSk, 128, 128, 2, 2, 128, 2, 1.00},      // 23 wave tile 64x64
+    // 24, 25: split-K residual (TJK_EPI_BIAS_RESIDUAL only; workspace).
+    {kK2, 192, 128, 2, 2, 128, 2, 1.00},      // 24 wave tile 96x64, 2 WGs per tile
+    {kK2, 128, 128, 2, 2, 128, 2, 1.00},      // 25 wave tile 64x64, 2 WGs per tile
 };
 // fp32.
 static const GemmPlan kPlans32[] = {
@@ -848,7 +931,7 @@ static int auto_plan(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) 
   int best = 0;
   double best_cost = 1e300;
   for (int i = 0; i < count; ++i) {
-    if (p[i].kind == kSk) continue;
+    if (p[i].kind == kSk || p[i].kind == kK2) continue;
     if (p[i].kind == kDtl && !dtl_ok(p[i], K, lda, ldw, sizeof(T))) continue;
     const int64_t tiles = ((M + p[i].bm - 1) / p[i].bm) * ((N + p[i].bn - 1) / p[i].bn);
     const int64_t rounds = (tiles + 255) / 256;
@@ -948,6 +1031,30 @@ template <int BKB, int STAGES> struct SkLauncher {
   }
 };
 
+template <int BKB, int STAGES> struct K2Launcher {
+  template <typename T, int BM, int BN, int WM, int WN>
+  static size_t workspace_bytes() { return kSkHeader; }
+  template <typename T, int BM, int BN, int WM, int WN, int EPI>
+  static int go(const GemmArgs& g) {
+    if constexpr (EPI != TJK_EPI_BIAS_RESIDUAL) {
+      return fail(TJK_EUNSUPPORTED, "tjk_gemm_bias: split-K plans take only the residual epilogue");
+    } else {
+      if (!g.ws) return fail(TJK_EINVAL, "tjk_gemm_bias: split-K plan needs a workspace (tjk_gemm_bias_ws)");
+      if (g.ws_bytes < kSkHeader || ((uintptr_t)g.ws & 255))
+        return fail(TJK_EINVAL, "tjk_gemm_bias: split-K workspace needs %zu bytes, 256-byte aligned (got %zu)",
+                    kSkHeader, g.ws_bytes);
+      const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
+      if (tiles > kMaxK2Tiles - 1 || (int64_t)g.M * g.ldc * 4 >= INT32_MAX)
+        return fail(TJK_EUNSUPPORTED, "tjk_gemm_bias: shape too large for the split-K plan");
+      int* flags = reinterpret_cast<int*>(static_cast<char*>(g.ws) + kK2FlagOffset) + 1;  // [-1]: timeouts
+      hipLaunchKernelGGL((gemm_k2_residual_kernel<T, BM, BN, WM, WN, BKB, STAGES>), dim3(2 * tiles),
+                         dim3(WM * WN * 64), 0, g.s, (const T*)g.a, g.lda, (const T*)g.w, g.ldw, (const T*)g.bias,
+                         (float*)g.c, g.ldc, g.M, g.N, g.K, flags);
+      return TJK_OK;
+    }
+  }
+};
+
 template <typename L, typename T, int BM, int BN, int WM, int WN>
 static int launch_epi(int epi, const GemmArgs& g) {
   switch (epi) {
@@ -961,15 +1068,19 @@ typedef Launcher<kStaged> St;
 typedef DtlLauncher<128, 2> D2;
 typedef DtlLauncher<128, 2, 2> D2K2;
 typedef SkLauncher<128, 2> SK2;
+typedef K2Launcher<128, 2> K22;
 
-// Stream-K plans of the 2-byte table: (id, BM, BN, WM, WN).
-#define TJK_SK_PLANS(X)      \
+// Plans of the 2-byte table that need a workspace (stream-K, split-K):
+// (id, launcher, BM, BN, WM, WN).
+#define TJK_WS_PLANS(X)      \
   X(18, SK2, 256, 256, 2, 4) \
   X(19, SK2, 256, 256, 2, 2) \
   X(20, SK2, 192, 256, 2, 4) \
   X(21, SK2, 192, 384, 2, 4) \
   X(22, SK2, 192, 128, 2, 2) \
-  X(23, SK2, 128, 128, 2, 2)
+  X(23, SK2, 128, 128, 2, 2) \
+  X(24, K22, 192, 128, 2, 2) \
+  X(25, K22, 128, 128, 2, 2)
 
 template <typename T>
 static size_t sk_workspace_bytes(int plan) {
@@ -979,7 +1090,7 @@ static size_t sk_workspace_bytes(int plan) {
     switch (plan) {
 #define TJK_SK_WS(ID, L, BM, BN, WM, WN) \
   case ID: return L::template workspace_bytes<T, BM, BN, WM, WN>();
-      TJK_SK_PLANS(TJK_SK_WS)
+      TJK_WS_PLANS(TJK_SK_WS)
 #undef TJK_SK_WS
     }
     return 0;
@@ -1019,7 +1130,7 @@ static int run_gemm(int plan, int epi, const GemmArgs& g) {
       TJK_GEMM_CASE(15, D2, 96, 128, 1, 4)
       TJK_GEMM_CASE(16, D2K2, 192, 128, 2, 2)
       TJK_GEMM_CASE(17, D2K2, 128, 128, 2, 2)
-      TJK_SK_PLANS(TJK_GEMM_CASE)
+      TJK_WS_PLANS(TJK_GEMM_CASE)
     }
   }
 #undef TJK_GEMM_CASE

@@ -43,7 +43,7 @@ _SIGNATURES = {
                              _f32, _i32, _vp, _vp, _vp, _i32, _i32, _vp]),
     "tjk_flash_plan_count": (_i32, [_i32]),
     "tjk_flash_fwd_sched": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _f32, _i32,
-                                   _vp, _vp, _i32, _vp, _i32, _vp, _i32, _vp]),
+                                   _vp, _vp, _i32, _vp, _i32, _i32, _vp]),
     "tjk_flash_partial_bytes": (ctypes.c_size_t, [_i32, _i32]),
     "tjk_flash_sched_occupancy": (_i32, [_i32, _i32]),
     "tjk_ffn": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64,

@@ -210,9 +210,10 @@ def flash_attention_sched(qkv: torch.Tensor, out: torch.Tensor, cu_seqlens: torc
                           scale: Optional[float] = None) -> torch.Tensor:
     """Packed attention following a work list (``tjkernels.schedule``): the
     same math as ``flash_attention(..., cu_seqlens=...)``, with long query
-    blocks issued first and split over their key range (merged in a second
-    launch).  qkv: packed [T, 3, H, hd] (bf16 / fp16); out: [T, H*hd]."""
-    _require_gpu(qkv, out, cu_seqlens, schedule.work, schedule.merges, schedule.partials)
+    blocks issued first and split over their key range (the second half
+    merges the first's partial).  qkv: packed [T, 3, H, hd] (bf16 / fp16);
+    out: [T, H*hd].  Calls sharing one schedule must be stream-ordered."""
+    _require_gpu(qkv, out, cu_seqlens, schedule.work, schedule.partials)
     if qkv.dim() != 4 or qkv.shape[1] != 3 or qkv.stride(3) != 1:
         raise TjkError(f"packed qkv must be [T, 3, H, hd] with unit hd stride, got {tuple(qkv.shape)}")
     if cu_seqlens.dtype != torch.int32 or cu_seqlens.dim() != 1 or not cu_seqlens.is_contiguous():
@@ -226,8 +227,7 @@ def flash_attention_sched(qkv: torch.Tensor, out: torch.Tensor, cu_seqlens: torc
         qkv.data_ptr(), ss, sc, sh, out.data_ptr(), _rowmajor(out, "out"), cu_seqlens.numel() - 1,
         int(max_seqlen), h, hd, float(hd ** -0.5 if scale is None else scale), int(bool(causal)),
         cu_seqlens.data_ptr(), schedule.work.data_ptr(), schedule.work.shape[0],
-        schedule.merges.data_ptr(), schedule.merges.shape[0], schedule.partials.data_ptr(),
-        _code(qkv), _stream(qkv))
+        schedule.partials.data_ptr(), schedule.n_slots, _code(qkv), _stream(qkv))
     check(status, "tjk_flash_fwd_sched")
     return out
 

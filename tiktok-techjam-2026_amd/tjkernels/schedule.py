@@ -11,15 +11,17 @@ while most of the GPU idles at the end.  Here, from the host-known lengths:
   and hence the result, is a pure function of the lengths);
 * an item costing more than ``split_factor`` times the average work per
   resident workgroup (and at least ``min_split`` tiles) is split into two
-  halves over its key range; the halves write fp32 partials and a merge
-  launch combines them.
+  halves over its key range: the first (the larger, so it is issued first)
+  publishes an fp32 partial, the second merges it into its own result and
+  writes the output rows.
 
 Measured on MI355X at the packed C4 lengths (bf16, hd 64): grid order
-45.6 us, longest first 40.1 us, longest first with every item above the
-average split (192 splits) 51 us -- the kernel is throughput-bound (the
-softmax VALU work of a 64-key tile is about twice its MFMA time), so splits
-only add partial traffic and a launch.  ``split_factor`` = 2 keeps splitting
-for lists dominated by a few very long items.
+45.6 us, longest first 39.4 us; splitting every item above 1.0 / 1.2 / 1.5
+times the average (192 / 80 / 16 splits) 45.3 / 40.6 / 39.5 us.  The kernel
+is throughput-bound (the softmax VALU work of a 64-key tile is about twice
+its MFMA time) and each half pays its own Q load and pipeline fill, so the
+default ``split_factor`` = 2 only splits lists dominated by a few very long
+items.
 """
 
 from __future__ import annotations
@@ -35,16 +37,17 @@ BMQ, BNK = 128, 64
 @dataclass
 class AttentionSchedule:
     work: torch.Tensor      # int32 [n_work, 4]: (b*H + h, qb, t_lo | t_hi << 16, slot)
-    merges: torch.Tensor    # int32 [n_merges, 4]: (b*H + h, qb, slot_lo, slot_hi)
-    n_slots: int
-    partials: torch.Tensor  # fp32 scratch for the split halves
+    n_slots: int            # split items (partial slots)
+    partials: torch.Tensor  # fp32 partial slots + error word + flags (zero-filled)
     max_item: int           # largest item, in key tiles
     total: int              # key tiles over all items
 
 
 def build_items(lengths: Sequence[int], heads: int, causal: bool, slots: int, min_split: int = 6,
-                split_factor: float = 2.0) -> Tuple[List[Tuple[int, int, int, int, int, int]],
-                                                    List[Tuple[int, int, int, int]], int]:
+                split_factor: float = 2.0) -> Tuple[List[Tuple[int, int, int, int, int, int]], int]:
+    """[(cost, b*H + h, qb, t_lo, t_hi, slot)] in issue order, and the number
+    of partial slots.  slot -1: whole item; s >= 0: first half of split item
+    s; -2 - s: its second half."""
     items = []
     for b, n in enumerate(lengths):
         for qb in range((n + BMQ - 1) // BMQ):
@@ -54,18 +57,19 @@ def build_items(lengths: Sequence[int], heads: int, causal: bool, slots: int, mi
                 items.append((nkt, b * heads + h, qb))
     total = sum(c for c, _, _ in items)
     target = max(split_factor * total / max(slots, 1), float(min_split))
-    work, merges, n_slots = [], [], 0
+    work, n_slots = [], 0
     for nkt, bh, qb in items:
         if nkt > target:
-            mid = nkt // 2
+            mid = (nkt + 1) // 2
             work.append((mid, bh, qb, 0, mid, n_slots))
-            work.append((nkt - mid, bh, qb, mid, nkt, n_slots + 1))
-            merges.append((bh, qb, n_slots, n_slots + 1))
-            n_slots += 2
+            work.append((nkt - mid, bh, qb, mid, nkt, -2 - n_slots))
+            n_slots += 1
         else:
             work.append((nkt, bh, qb, 0, nkt, -1))
+    # the first half of a split item is at least as long and starts at key
+    # tile 0, so it sorts before its second half
     work.sort(key=lambda w: (-w[0], w[1], w[2], w[3]))
-    return work, merges, n_slots
+    return work, n_slots
 
 
 def build_schedule(lengths: Sequence[int], heads: int, head_dim: int, causal: bool,
@@ -78,12 +82,11 @@ def build_schedule(lengths: Sequence[int], heads: int, head_dim: int, causal: bo
         occ = lib.tjk_flash_sched_occupancy(head_dim, _lib.DTYPE_CODES[dtype])
         _lib.check(0 if occ > 0 else (occ or -1), "tjk_flash_sched_occupancy")
         slots = occ * torch.cuda.get_device_properties(device).multi_processor_count
-    work, merges, n_slots = build_items(lengths, heads, causal, slots, min_split, split_factor)
+    work, n_slots = build_items(lengths, heads, causal, slots, min_split, split_factor)
     w = torch.tensor([(bh, qb, lo | (hi << 16), slot) for _, bh, qb, lo, hi, slot in work] or [(0, 0, 0, -1)],
                      dtype=torch.int32)[:len(work)]
-    m = torch.tensor(merges or [(0, 0, 0, 0)], dtype=torch.int32)[:len(merges)]
-    nbytes = lib.tjk_flash_partial_bytes(head_dim, max(n_slots, 1))
-    return AttentionSchedule(work=w.contiguous().to(device), merges=m.contiguous().to(device), n_slots=n_slots,
-                             partials=torch.empty(nbytes // 4, dtype=torch.float32, device=device),
+    nbytes = lib.tjk_flash_partial_bytes(head_dim, n_slots) if n_slots else 16
+    return AttentionSchedule(work=w.contiguous().to(device), n_slots=n_slots,
+                             partials=torch.zeros((nbytes + 15) // 4, dtype=torch.float32, device=device),
                              max_item=max((c for c, *_ in work), default=0),
                              total=sum(c for c, *_ in work))
