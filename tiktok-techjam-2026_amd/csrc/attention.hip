@@ -478,7 +478,8 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
   const __amdgpu_buffer_rsrc_t rsk = __builtin_amdgcn_make_buffer_rsrc((void*)(qbase + sc), (short)0, span, 0x00020000);
   const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc((void*)(qbase + 2 * sc), (short)0, span, 0x00020000);
   uint4 rk[KPT], rv0[VPT], rv1[VPT];
-  auto load_kv = [&](int t) {  // tiles past the end read as zeros
+  auto load_kv_into = [&](int t, uint4 (&rk)[KPT], uint4 (&rv0)[VPT], uint4 (&rv1)[VPT]) {
+    // tiles past the end read as zeros
     const uint32_t tb = t < t_hi ? (uint32_t)t * BNK * row_bytes : kFaPastEnd;
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
@@ -499,7 +500,7 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
       rv1[i] = ok ? v1 : make_uint4(0, 0, 0, 0);
     }
   };
-  auto store_kv = [&](int st) {
+  auto store_kv_from = [&](int st, const uint4 (&rk)[KPT], const uint4 (&rv0)[VPT], const uint4 (&rv1)[VPT]) {
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int it = tid + i * 256, key = it / CH, c = it % CH;
@@ -514,6 +515,8 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
       }
     }
   };
+  auto load_kv = [&](int t) { load_kv_into(t, rk, rv0, rv1); };
+  auto store_kv = [&](int st) { store_kv_from(st, rk, rv0, rv1); };
 
   const int krow = swap_bits_2_3(l32);
   auto qk = [&](int st, f32x16 (&sa)[2]) {
@@ -613,10 +616,14 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
       }
   };
 
-  load_kv(t_lo);
-  store_kv(t_lo % NST);
-  load_kv(t_lo + 1);
-  store_kv((t_lo + 1) % NST);
+  {
+    // both first tiles in flight at once (one global latency, not two)
+    uint4 rk1[KPT], rv01[VPT], rv11[VPT];
+    load_kv(t_lo);
+    load_kv_into(t_lo + 1, rk1, rv01, rv11);
+    store_kv(t_lo % NST);
+    store_kv_from((t_lo + 1) % NST, rk1, rv01, rv11);
+  }
   __syncthreads();
 
   f32x16 scur[2];
