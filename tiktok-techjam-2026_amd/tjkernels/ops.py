@@ -27,7 +27,13 @@ def _code(t: torch.Tensor) -> int:
         raise TjkError(f"unsupported dtype {t.dtype}") from None
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t: torch.Tensor) -> int:
+    # the raw-handle query costs ~0.1 us against ~2 us for building a Stream
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index if t.device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
