@@ -102,10 +102,43 @@ struct NoParts {
   __device__ f32x4 get(int, int) const { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 };
 
-template <typename T, int EPI, int FM, int FN, typename Parts = NoParts, int RPOL = kResPlain>
+// The residual pieces (TJK_EPI_BIAS_RESIDUAL, plain policy) a wave's
+// epilogue will update, read into registers before the main loop.  A launch
+// whose tiles all run in one round otherwise starts every residual read at
+// the same moment, after the last MFMA; read early, they overlap the main
+// loop and the epilogue only writes.  Piece (j, it) is the one the
+// epilogue's store loop handles for 32-row block j, iteration it.
+struct NoPrefetch {
+  static constexpr bool on = false;
+  __device__ float4 get(int, int) const { return make_float4(0.f, 0.f, 0.f, 0.f); }
+};
+template <int FM, int FN>
+struct ResPrefetch {
+  static constexpr bool on = true;
+  static constexpr int WTN = FN * 32, LPR = WTN / 4, NPC = 32 * LPR, NIT = (NPC + 63) / 64;
+  float4 r[FM][NIT];
+  __device__ __forceinline__ void load(const float* __restrict__ C, int64_t ldc, int M, int N, int mw, int nw,
+                                       int lane) {
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        const int pc = lane + 64 * it;
+        const int m = mw + 32 * j + pc / LPR, n = nw + (pc % LPR) * 4;
+        r[j][it] = ((NPC % 64 == 0 || pc < NPC) && m < M && n < N)
+                       ? *reinterpret_cast<const float4*>(C + (int64_t)m * ldc + n)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+  }
+  __device__ __forceinline__ float4 get(int j, int it) const { return r[j][it]; }
+};
+
+template <typename T, int EPI, int FM, int FN, typename Parts = NoParts, int RPOL = kResPlain,
+          typename Pre = NoPrefetch>
 __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* __restrict__ bias,
                                          void* __restrict__ Cv, int64_t ldc, int M, int N, int mw, int nw,
-                                         int lane, char* __restrict__ stage, const Parts& parts = Parts()) {
+                                         int lane, char* __restrict__ stage, const Parts& parts = Parts(),
+                                         const Pre& pre = Pre()) {
   typedef EpiStage<T, EPI, FN> E;
   typedef typename E::S S;
   constexpr int LPR = E::WTN / E::SV;  // 16-byte pieces per staged row
@@ -180,7 +213,7 @@ __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* _
           const float4 a = __builtin_bit_cast(float4, piece);
           if constexpr (RPOL == kResPlain) {
             float4* r = reinterpret_cast<float4*>(static_cast<float*>(Cv) + (int64_t)m * ldc + n);
-            float4 o = *r;
+            float4 o = Pre::on ? pre.get(j, it) : *r;
             o.x += a.x; o.y += a.y; o.z += a.z; o.w += a.w;
             *r = o;
           } else {  // the caller keeps M * ldc * 4 below 2^31
@@ -338,6 +371,18 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
 // DMA of tile k+STAGES into tile k's slot and reads tile k+1's first
 // fragments while the last step's MFMAs run.  Every DMA has STAGES-1 tiles
 // of MFMA work to land, and no wave waits for LDS right after the barrier.
+// With a ring of three or more slots the DMA of tile k-1+STAGES (into the
+// slot tile k-1 freed at the previous barrier) is instead spread over the
+// MFMAs of tile k's steps before the last: the vector memory unit then gets
+// a few instructions per step rather than a burst after each barrier, and
+// every DMA still has at least one tile of MFMA work to land.  Measured on
+// MI355X (wall-clock probes of one launch, bias epilogue): 192x128 tiles in
+// a 4-slot ring (160 KB) run the C4 FFN2 main loop (5430x1024x4096) at 67%
+// of the clock-limited MFMA rate, against 62% for 3 slots with the spread
+// schedule, 55% for 3 slots issuing after the barrier and 52% for 2 slots.
+// Removing the W operand's LDS reads did not change the 2-slot loop's
+// speed; removing its DMA made it 25% faster: the loops are bound by the
+// DMA traffic per CU, not by LDS reads.
 // The DMA is issued on every iteration, past the end pointed outside the
 // buffer range (it moves nothing), which keeps the body one basic block;
 // scheduling directives interleave the MFMAs with the next step's ds_reads.
@@ -455,12 +500,16 @@ __device__ __forceinline__ void dtl_accumulate(
     }
   };
 
-  // Prologue: tiles 0 .. STAGES-1 in flight; tile 0 landed everywhere.
+  // Prologue: tiles 0 .. STAGES-1 in flight (STAGES-2 with the spread
+  // schedule, whose loop issues tile kt-1+STAGES during tile kt); tile 0
+  // landed everywhere.
+  constexpr bool SPREAD = STAGES >= 3;
+  constexpr int PRE = SPREAD ? STAGES - 1 : STAGES;
 #pragma unroll
-  for (int t = 0; t < STAGES; ++t)
+  for (int t = 0; t < PRE; ++t)
 #pragma unroll
     for (int q = 0; q < NDMA; ++q) dma(t, q);
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"((STAGES - 1) * NDMA) : "memory");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"((PRE - 1) * NDMA) : "memory");
   asm volatile("s_barrier" ::: "memory");
   constexpr int NMF = FN * FM, NDS = FN + FM;  // MFMAs and fragment reads per step
   constexpr int NSLOT = NMF > NDS ? NMF : NDS;
@@ -501,7 +550,7 @@ __device__ __forceinline__ void dtl_accumulate(
         // kt+STAGES.  Inline asm with a memory clobber keeps the compiler
         // from moving LDS accesses across either instruction.
         __builtin_amdgcn_sched_barrier(0);
-        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((STAGES - 2) * NDMA) : "memory");
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((STAGES - 2) * NDMA) : "memory");  // tile kt+1 landed
         asm volatile("s_barrier" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -510,7 +559,15 @@ __device__ __forceinline__ void dtl_accumulate(
         if (m < NMF) Mfma<T>::mma(acc[m / FM][m % FM], fw[b][m / FM], fa[b][m % FM]);
         if (m < FM) fa[b ^ 1][m] = frag_at(ra + m * 32 * BKB, rks);
         else if (m < NDS) fw[b ^ 1][m - FM] = frag_at(rw + (m - FM) * 32 * BKB, rks);
-        if (last) {
+        if constexpr (SPREAD) {
+          // DMA instructions of tile kt-1+STAGES over slots 0 .. (KS-1)*NSLOT-1
+          constexpr int TOT = (KS - 1) * NSLOT;
+          const int i = ks * NSLOT + m;
+          if (!last) {
+#pragma unroll
+            for (int q = i * NDMA / TOT; q < (i + 1) * NDMA / TOT; ++q) dma(kt - 1 + STAGES, q);
+          }
+        } else if (last) {
 #pragma unroll
           for (int q = m * NDMA / NSLOT; q < (m + 1) * NDMA / NSLOT; ++q) dma(kt + STAGES, q);
         }
@@ -551,6 +608,18 @@ __global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
   tile_coords(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, pid_m, pid_n);
   const int m0 = pid_m * BM, n0 = pid_n * BN;
 
+  // Residual reads issued ahead of the operand DMAs, where their registers
+  // fit beside the accumulators (plus ~144 for fragments and addresses)
+  // without lowering the occupancy the LDS ring allows.
+  constexpr int WAVES_PER_SIMD = (NW * KSPLIT / 4) * (160 * 1024 / G::LDS);
+  constexpr int PRE_REGS = FM * ResPrefetch<FM, FN>::NIT * 4;
+  constexpr bool PREFETCH = EPI == TJK_EPI_BIAS_RESIDUAL && KSPLIT == 1 &&
+                            FM * FN * 16 + PRE_REGS + 144 <= 512 / WAVES_PER_SIMD;
+  typedef typename std::conditional<PREFETCH, ResPrefetch<FM, FN>, NoPrefetch>::type Pre;
+  Pre pre;
+  if constexpr (PREFETCH)
+    pre.load(static_cast<const float*>(Cv), ldc, M, N, m0 + wm * G::WTM, n0 + wn * G::WTN, lane);
+
   f32x16 acc[FN][FM];
   zero_acc<T, FM, FN>(acc);
   dtl_accumulate<T, BM, BN, WM, WN, BKB, STAGES, KSPLIT>(smem, A, lda, W, ldw, M, N, m0, n0, 0, K / G::BK, acc);
@@ -584,8 +653,9 @@ __global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
           for (int r = 0; r < 16; ++r) acc[i][j][r] += ot[((i * FM + j) * 16 + r) * 64 + lane];
     }
   }
-  epilogue<T, EPI, FM, FN>(acc, bias, Cv, ldc, M, N, m0 + wm * G::WTM, n0 + wn * G::WTN, lane,
-                           smem + XCH + wave * EpiStage<T, EPI, FN>::BYTES);
+  epilogue<T, EPI, FM, FN, NoParts, kResPlain, Pre>(acc, bias, Cv, ldc, M, N, m0 + wm * G::WTM,
+                                                    n0 + wn * G::WTN, lane,
+                                                    smem + XCH + wave * EpiStage<T, EPI, FN>::BYTES, NoParts(), pre);
 }
 
 // ------------------------------------------------------------ stream-K GEMM
@@ -890,6 +960,12 @@ static const GemmPlan kPlans16[] = {
     // 24, 25: split-K residual (TJK_EPI_BIAS_RESIDUAL only; workspace).
     {kK2, 192, 128, 2, 2, 128, 2, 1.00},      // 24 wave tile 96x64, 2 WGs per tile
     {kK2, 128, 128, 2, 2, 128, 2, 1.00},      // 25 wave tile 64x64, 2 WGs per tile
+    // 26: a 4-slot ring (160 KB) with the spread DMA schedule, one workgroup
+    // per CU.  Other deep rings measured (C4/C5 projections, residual reads
+    // prefetched where registers allow) and dropped because a 2-slot plan
+    // was faster on every shape: 256x256 8 waves and 4 waves with 64-byte
+    // rows in 4 slots, 128x128 and 96x128 in 4 slots, 256x128 in 3 slots.
+    {kDtl, 192, 128, 2, 2, 128, 4, 0.85},     // 26 wave tile 96x64, 160 KB
 };
 // fp32.
 static const GemmPlan kPlans32[] = {
@@ -1067,6 +1143,7 @@ static int launch_epi(int epi, const GemmArgs& g) {
 typedef Launcher<kStaged> St;
 typedef DtlLauncher<128, 2> D2;
 typedef DtlLauncher<128, 2, 2> D2K2;
+typedef DtlLauncher<128, 4> D4;
 typedef SkLauncher<128, 2> SK2;
 typedef K2Launcher<128, 2> K22;
 
@@ -1131,6 +1208,7 @@ static int run_gemm(int plan, int epi, const GemmArgs& g) {
       TJK_GEMM_CASE(16, D2K2, 192, 128, 2, 2)
       TJK_GEMM_CASE(17, D2K2, 128, 128, 2, 2)
       TJK_WS_PLANS(TJK_GEMM_CASE)
+      TJK_GEMM_CASE(26, D4, 192, 128, 2, 2)
     }
   }
 #undef TJK_GEMM_CASE

@@ -28,8 +28,9 @@ import torch
 from . import _lib, ops, timing
 
 # Direct-to-LDS tile plans worth timing (2-byte types): 128x128, 256x256,
-# 64x64, 192x128, 192x256, 192x384, 96x128.  fp32 uses its own list.
-CANDIDATES_16 = (7, 8, 9, 12, 13, 14, 15)
+# 64x64, 192x128, 192x256, 192x384, 96x128 and 192x128 in a 4-slot ring.
+# fp32 uses its own list.
+CANDIDATES_16 = (7, 8, 9, 12, 13, 14, 15, 26)
 CANDIDATES_32 = (2, 3, 4)
 
 _choice: Dict[Tuple, int] = {}
