@@ -396,7 +396,7 @@ constexpr int kFaSpinLimit = 1 << 22;  // polls of a split item's flag before gi
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 template <typename T, int HDP, bool KEYMASK, bool FULLHD>
-__global__ __launch_bounds__(256) void flash_pipe_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ? 2 : 1, HDP <= 64 ? 2 : 1))) void flash_pipe_kernel(
     const T* __restrict__ qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh,
     T* __restrict__ out, int64_t ld_out, int B, int S, int H, int hd, float scale_log2,
     int causal, const int32_t* __restrict__ lengths, const uint8_t* __restrict__ key_mask,
@@ -552,7 +552,7 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
   float m_off = -INFINITY, l_run = 0.f;
 
   // softmax of one tile's scores (already masked) and O += V P
-  auto softmax_pv = [&](int st, f32x16 (&sa)[2], bool interleave) {
+  auto softmax_pv = [&](int st, f32x16 (&sa)[2]) {
     float mx = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -582,17 +582,6 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
     // two per instruction
 #pragma unroll
     for (int stp = 0; stp < 4; ++stp) l_run = Mfma<T>::sum8(pf[stp], l_run);
-    if (interleave) {
-      // Spread the next tile's S MFMAs (issued just before this call, same
-      // basic block) over the softmax VALU work so both pipes stay busy.
-      __builtin_amdgcn_sched_group_barrier(0x020, KPT + 2 * VPT, 0);  // global loads of tile t+2
-#pragma unroll
-      for (int i = 0; i < 2 * KC; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // K fragment
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // S MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 10, 0); // softmax VALU
-      }
-    }
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb) {
       const T* vp = &sV[st][(hb * 32 + l32) * LDV + 8 * hi];
@@ -616,6 +605,108 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
       }
   };
 
+  // ---- interior-tile pipeline (unmasked tiles).  The softmax of tile t is
+  // split around the row max: the max of S(t+1) is taken while the PV
+  // MFMAs of tile t run, and the exponentials of tile t while the S(t+1)
+  // MFMAs run, so every VALU-heavy stretch of the loop has MFMAs to hide
+  // behind (and the other wave of the SIMD finds the matrix pipe busy in
+  // the opposite phase).
+  typedef typename Mfma<T>::frag Frag;
+  // row max of a tile's scores in log2 units; both lanes of a query agree
+  auto rowmax = [&](const f32x16 (&sa)[2]) -> float {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sa[kb][r]);
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * scale_log2;
+  };
+  auto rescale = [&](float mx) {
+    if (__any(mx > m_off + kLazyRescale)) {
+      const float m_new = fmaxf(m_off, mx);
+      const float alpha = m_off == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_off - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[hb][r] *= alpha;
+      m_off = m_new;
+    }
+  };
+  // S(next) = K(st) Q^T, interleaved with P = 2^(S(cur) * scale - m_off)
+  // packed to the MFMA type (row sums from the rounded P)
+  auto qk_exp = [&](int st, f32x16 (&snext)[2], const f32x16 (&scur_)[2], Frag (&pf)[4]) {
+    Frag kf[KC][2];
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) kf[c][kb] = Mfma<T>::load(&sK[st][(kb * 32 + krow) * LDK + 8 * hi] + 16 * c);
+    // every fragment read issued together, one wait for all of them
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) asm volatile("" : "+v"(kf[c][kb]));
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) snext[kb][r] = 0.f;
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) Mfma<T>::mma(snext[kb], kf[c][kb], qf[c]);
+    const float nb = -m_off;
+    float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+    for (int stp = 0; stp < 4; ++stp) {
+      float p[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        p[e] = __builtin_amdgcn_exp2f(fmaf(scur_[stp >> 1][8 * (stp & 1) + e], scale_log2, nb));
+      pf[stp] = Mfma<T>::pack(p);
+      if (stp & 1) l1 = Mfma<T>::sum8(pf[stp], l1);
+      else l0 = Mfma<T>::sum8(pf[stp], l0);
+    }
+    l_run += l0 + l1;
+    // order: one MFMA per ~12 VALU (the exponentials of tile t)
+#pragma unroll
+    for (int i = 0; i < 2 * KC; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);
+    }
+  };
+  // O += V(st)^T P^T, interleaved with the row max of the next scores
+  auto pv_max = [&](int st, const Frag (&pf)[4], const f32x16 (&snext)[2]) -> float {
+    Frag vf[HB][4];
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+      const T* vp = &sV[st][(hb * 32 + l32) * LDV + 8 * hi];
+#pragma unroll
+      for (int stp = 0; stp < 4; ++stp) vf[hb][stp] = Mfma<T>::load(vp + 16 * stp);
+    }
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+      for (int stp = 0; stp < 4; ++stp) asm volatile("" : "+v"(vf[hb][stp]));
+#pragma unroll
+    for (int stp = 0; stp < 4; ++stp)
+#pragma unroll
+      for (int hb = 0; hb < HB; ++hb) Mfma<T>::mma(o[hb], vf[hb][stp], pf[stp]);
+    float mx = rowmax(snext);
+    asm volatile("" : "+v"(mx));  // keep the max here, under the PV MFMAs
+#pragma unroll
+    for (int i = 0; i < 4 * HB; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+    }
+    return mx;
+  };
+
+  // Ring invariant at the top of step t: LDS slots t and t+1 (mod NST) hold
+  // key tiles t and t+1, the staging registers hold tile t+2 (its loads in
+  // flight since the previous step), and scur holds S(t).  A step first
+  // stores tile t+2 into the slot tile t-1 freed, then loads tile t+3, so
+  // every global load has a whole step to land.
   {
     // both first tiles in flight at once (one global latency, not two)
     uint4 rk1[KPT], rv01[VPT], rv11[VPT];
@@ -625,6 +716,7 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
     store_kv_from((t_lo + 1) % NST, rk1, rv01, rv11);
   }
   __syncthreads();
+  load_kv(t_lo + 2);
 
   f32x16 scur[2];
   if (t_hi > t_lo) qk(t_lo % NST, scur);
@@ -634,39 +726,43 @@ __global__ __launch_bounds__(256) void flash_pipe_kernel(
   n_int = max(n_int, t_lo);
   int t = t_lo;
   f32x16 salt[2];
-  for (; t + 1 < n_int; t += 2) {  // two tiles per trip: scores ping-pong scur <-> salt
-    load_kv(t + 2);
-    qk((t + 1) % NST, salt);
-    softmax_pv(t % NST, scur, true);
-    store_kv((t + 2) % NST);
-    __syncthreads();
-    load_kv(t + 3);
-    qk((t + 2) % NST, scur);
-    softmax_pv((t + 1) % NST, salt, true);
-    store_kv((t + 3) % NST);
-    __syncthreads();
+  Frag pf[4];
+  if (t + 1 < n_int) {
+    float mx = rowmax(scur);
+    for (; t + 1 < n_int; t += 2) {  // two tiles per trip: scores ping-pong scur <-> salt
+      store_kv((t + 2) % NST);
+      load_kv(t + 3);
+      rescale(mx);
+      qk_exp((t + 1) % NST, salt, scur, pf);
+      mx = pv_max(t % NST, pf, salt);
+      __syncthreads();
+      store_kv((t + 3) % NST);
+      load_kv(t + 4);
+      rescale(mx);
+      qk_exp((t + 2) % NST, scur, salt, pf);
+      mx = pv_max((t + 1) % NST, pf, scur);
+      __syncthreads();
+    }
   }
   if (t < n_int) {
-    load_kv(t + 2);
-    qk((t + 1) % NST, salt);
-    softmax_pv(t % NST, scur, true);
     store_kv((t + 2) % NST);
+    load_kv(t + 3);
+    softmax_pv(t % NST, scur);
+    qk((t + 1) % NST, scur);
     __syncthreads();
-    scur[0] = salt[0];
-    scur[1] = salt[1];
     ++t;
   }
   for (; t < t_hi; ++t) {
-    load_kv(t + 2);
+    store_kv((t + 2) % NST);
+    load_kv(t + 3);
     f32x16 snext[2];
     const bool act_next = t + 1 < t_hi && (!causal || (t + 1) * BNK <= wq0 + 31);
     if (act_next) qk((t + 1) % NST, snext);
     const bool act = !causal || t * BNK <= wq0 + 31;
     if (act) {
       mask_tile(t, scur);
-      softmax_pv(t % NST, scur, false);
+      softmax_pv(t % NST, scur);
     }
-    store_kv((t + 2) % NST);
     __syncthreads();
     if (act_next) {
       scur[0] = snext[0];
