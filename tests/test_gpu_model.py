@@ -246,6 +246,15 @@ def test_packed_forward_matches_unpacked(device, causal):
             unpacked = eng._forward_impl(x.to(device), mask.to(device), MASK_GENERAL).cpu()
     finally:
         plans_mod.set_override(None)
+    # the same through the plan knob (TJ_NO_PACK / Plan.pack_prefix=False)
+    plans_mod.set_override(Plan(compute_dtype=torch.float32, cuda_graph=False, pack_prefix=False,
+                                label="unpacked"))
+    try:
+        with torch.inference_mode():
+            by_plan = _module(cfg, sd, torch.float32, device)(x.to(device), mask.to(device)).cpu()
+    finally:
+        plans_mod.set_override(None)
+    assert torch.equal(by_plan, unpacked)
     assert (packed[~mask] == 0).all() and (unpacked[~mask] == 0).all()
     diff = (packed[mask] - unpacked[mask]).abs().max().item()
     assert diff <= 1e-5, f"packed vs unpacked valid rows differ by {diff:.3e}"

@@ -125,6 +125,44 @@ def test_override_and_env_knobs(monkeypatch):
     monkeypatch.setenv("TJ_DEFERRED_RESIDUAL", "1")
     p = plans_mod.select_plan(4, 2048, 1024, 16, 4096, 4, True, torch.bfloat16, dev)
     assert not p.cuda_graph and not p.residual_epilogue
+    assert p.pack_prefix and p.attn_plan == -1
+    monkeypatch.setenv("TJ_NO_PACK", "1")
+    monkeypatch.setenv("TJ_ATTN_PLAN", "1")
+    p = plans_mod.select_plan(4, 2048, 1024, 16, 4096, 4, True, torch.bfloat16, dev)
+    assert not p.pack_prefix and p.attn_plan == 1
+    assert plans_mod.Plan.from_json(p.to_json()) == p
+
+
+def test_sweep_runs_cases_in_subprocesses_and_tabulates(tmp_path, monkeypatch):
+    """The sweep runs each workload through bench.py in its own process and
+    tabulates the JSON line; a crash or OOM in one case is recorded, not
+    raised (stand-in bench scripts, no GPU)."""
+    from tjkernels import sweep
+    ok = tmp_path / "ok.py"
+    ok.write_text("import json, os, sys\n"
+                  "w = sys.argv[sys.argv.index('--workload') + 1]\n"
+                  "v = 2.0 if os.environ.get('TJ_NO_GRAPH') == '1' else 1.0\n"
+                  "print('noise')\n"
+                  "print(json.dumps({'metric': 'm', 'value': v, 'p90_ms': v, 'tflops': 10.0, "
+                  "'pct_peak': 0.4, 'tflops_padded_equiv': 12.0, 'roofline': {'kernel': 'gemm_qkv', "
+                  "'achieved': 9.0, 'frac': 0.5}, 'accuracy': {'passed': True, 'max_abs': 1e-3}, "
+                  "'cpu_baseline': None, 'config': {'workload': w}}))\n")
+    oom = tmp_path / "oom.py"
+    oom.write_text("import sys\nprint('HIP out of memory', file=sys.stderr)\nsys.exit(1)\n")
+    monkeypatch.setattr(sweep, "BENCH", ok)
+    r = sweep.run_case("C2", 3, 1, False, {}, 60)
+    assert r["status"] == "PASS" and r["result"]["value"] == 1.0 and "--no-cpu-baseline" in r["cmd"]
+    monkeypatch.setattr(sweep, "BENCH", oom)
+    bad = sweep.run_case("C5", 3, 1, False, {}, 60)
+    assert bad["status"] == "OOM" and "result" not in bad
+    table = sweep.sweep_table([r, bad])
+    assert "| C2 | PASS | 1.0000" in table and "| C5 | OOM |" in table
+    monkeypatch.setattr(sweep, "BENCH", ok)
+    rc = sweep.main(["--workloads", "C2", "--ablation", "C2,C3", "--steps", "2", "--warmup", "0",
+                     "--out", str(tmp_path / "out"), "--tag", "t"])
+    assert rc == 0
+    md = list((tmp_path / "out").glob("t-*.md"))[0].read_text()
+    assert "| without hipGraph capture | 2.0000 (2.00x) | 2.0000 (2.00x) |" in md
 
 
 def test_mask_classification():

@@ -966,6 +966,11 @@ static const GemmPlan kPlans16[] = {
     // was faster on every shape: 256x256 8 waves and 4 waves with 64-byte
     // rows in 4 slots, 128x128 and 96x128 in 4 slots, 256x128 in 3 slots.
     {kDtl, 192, 128, 2, 2, 128, 4, 0.85},     // 26 wave tile 96x64, 160 KB
+    // 27, 28: small tiles in deep rings (8 and 6 slots) for launches of a few
+    // dozen workgroups with long K (C2's FFN2: 16 tiles, 32 K tiles each),
+    // where a 2-slot ring leaves each step waiting out the DMA latency.
+    {kDtl, 64, 64, 2, 2, 128, 8, 0.45},       // 27 wave tile 32x32, 128 KB
+    {kDtl, 128, 64, 2, 2, 128, 6, 0.50},      // 28 wave tile 64x32, 144 KB
 };
 // fp32.
 static const GemmPlan kPlans32[] = {
@@ -1144,6 +1149,8 @@ typedef Launcher<kStaged> St;
 typedef DtlLauncher<128, 2> D2;
 typedef DtlLauncher<128, 2, 2> D2K2;
 typedef DtlLauncher<128, 4> D4;
+typedef DtlLauncher<128, 6> D6;
+typedef DtlLauncher<128, 8> D8;
 typedef SkLauncher<128, 2> SK2;
 typedef K2Launcher<128, 2> K22;
 
@@ -1209,6 +1216,8 @@ static int run_gemm(int plan, int epi, const GemmArgs& g) {
       TJK_GEMM_CASE(17, D2K2, 128, 128, 2, 2)
       TJK_WS_PLANS(TJK_GEMM_CASE)
       TJK_GEMM_CASE(26, D4, 192, 128, 2, 2)
+      TJK_GEMM_CASE(27, D8, 64, 64, 2, 2)
+      TJK_GEMM_CASE(28, D6, 128, 64, 2, 2)
     }
   }
 #undef TJK_GEMM_CASE

@@ -406,6 +406,8 @@ class Engine:
                 mode, lens = MASK_PREFIX, host_lengths
         else:
             mode, lens = self._mask_info(mask)
+        if mode == MASK_PREFIX and not plan.pack_prefix:
+            mode, lens = MASK_GENERAL, None  # every row computed, per-key mask
         packing = self._packing(lens, x.shape[1]) if mode == MASK_PREFIX else None
         if plan.cuda_graph:
             return self._forward_graph(x, mask, mode, lens, packing)

@@ -15,7 +15,15 @@ Differences, all MI355X-specific:
   instead of deferring them to the next LayerNorm);
 * an fp32 model runs the IEEE fp32 plan by default, since only fp32 compute
   holds the 1e-4 per-element budget of fp32 plans;
-* tuned entries are keyed by shape *and* GPU architecture (``@gfx950``).
+* tuned entries are keyed by shape *and* GPU architecture (``@gfx950``);
+* ``pack_prefix``: prefix-masked batches run only their valid tokens (off:
+  every padded row is computed and zeroed at the end, the reference's way).
+
+Environment knobs (applied to the heuristic plan, so ablations set
+``TJ_IGNORE_PLANS=1`` as the reference's ablation does): ``TJ_NO_GRAPH``,
+``TJ_COMPUTE_DTYPE``, ``TJ_DEFERRED_RESIDUAL``, ``TJ_NO_PACK``,
+``TJ_ATTN_PLAN``; ``TJ_GEMM_TUNE=0`` (tjkernels.tiles) skips the measured
+tile choice.
 """
 
 from __future__ import annotations
@@ -51,6 +59,7 @@ class Plan:
     gemm_ffn1: int = -1
     gemm_ffn2: int = -1
     attn_plan: int = -1
+    pack_prefix: bool = True         # run only the valid tokens of prefix masks
     label: str = "default"
 
     def to_json(self) -> Dict[str, object]:
@@ -147,6 +156,11 @@ def select_plan(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int,
         plan = replace(plan, compute_dtype=_DTYPES[forced])
     if os.environ.get("TJ_DEFERRED_RESIDUAL") == "1":
         plan = replace(plan, residual_epilogue=False)
+    if os.environ.get("TJ_NO_PACK") == "1":
+        plan = replace(plan, pack_prefix=False)
+    attn_plan = os.environ.get("TJ_ATTN_PLAN")
+    if attn_plan is not None and attn_plan.lstrip("-").isdigit():
+        plan = replace(plan, attn_plan=int(attn_plan))
     return plan
 
 
