@@ -118,12 +118,14 @@ def test_override_and_env_knobs(monkeypatch):
     monkeypatch.setattr(plans_mod, "_cache", {})
     dev = torch.device("cuda", 0)
     base = plans_mod.select_plan(4, 2048, 1024, 16, 4096, 4, True, torch.bfloat16, dev)
-    assert base.cuda_graph and base.compute_dtype == torch.bfloat16 and base.residual_epilogue
+    assert not base.cuda_graph and base.compute_dtype == torch.bfloat16 and base.residual_epilogue
+    small = plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev)
+    assert small.cuda_graph  # launch-bound: replayed as a hipGraph
     big = plans_mod.select_plan(64, 4096, 1024, 16, 4096, 4, True, torch.bfloat16, dev)
     assert not big.cuda_graph  # x above 64 MiB: no whole-forward graph
     monkeypatch.setenv("TJ_NO_GRAPH", "1")
     monkeypatch.setenv("TJ_DEFERRED_RESIDUAL", "1")
-    p = plans_mod.select_plan(4, 2048, 1024, 16, 4096, 4, True, torch.bfloat16, dev)
+    p = plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev)
     assert not p.cuda_graph and not p.residual_epilogue
     assert p.pack_prefix and p.attn_plan == -1
     monkeypatch.setenv("TJ_NO_PACK", "1")

@@ -106,12 +106,17 @@ def default_plan(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int,
     if device.type != "cuda":
         raise RuntimeError("tjkernels runs on ROCm GPUs only; got device "
                            f"{device} (there is no CPU path)")
-    # Whole-forward graph costs one copy-in and one clone-out of the
-    # activation; worth it while that is small (the reference's 64 MiB rule,
-    # tjkernels/plans.py:109-110).
-    x_bytes = batch * seq * d_model * dtype.itemsize
+    # hipGraph replay pays only where launches dominate.  Measured on MI355X
+    # (same box, alternating runs): C2 (128 x 512 activations) 0.186 ms with
+    # the graph vs 0.222 ms eager, but C3 / C4 (3.1M / 8.4M activation
+    # elements) 2-3% faster with eager stream launches, the kernels being
+    # long enough to keep the queue ahead.  So the graph is used up to 2^20
+    # activation elements, and never above the reference's 64 MiB of x
+    # (tjkernels/plans.py:109-110).
+    elems = batch * seq * d_model
+    x_bytes = elems * dtype.itemsize
     return Plan(compute_dtype=dtype, residual_dtype=torch.float32,
-                cuda_graph=x_bytes <= 64 * 1024 * 1024, label="heuristic")
+                cuda_graph=elems <= (1 << 20) and x_bytes <= 64 * 1024 * 1024, label="heuristic")
 
 
 _cache: Optional[Dict[str, Plan]] = None
