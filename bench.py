@@ -242,12 +242,14 @@ def main() -> int:
         # The same forward with every padded row computed (per-key mask
         # attention, the reference's way), eager, for the packing gain.
         from tjkernels.engine import MASK_GENERAL
+        # (at most 20 forwards each; fewer when the run itself is short)
+        n_eager, w_eager = max(1, min(20, args.steps)), min(3, args.warmup)
         eager_unpacked = statistics.median(_time_steps(
-            lambda: engine._forward_impl(xd, md, MASK_GENERAL), 20, 3)[0])
+            lambda: engine._forward_impl(xd, md, MASK_GENERAL), n_eager, w_eager)[0])
         mode, lens = engine._mask_info(md)
         pk = engine._packing(lens, w.seq) if lens is not None else None
         eager_packed = statistics.median(_time_steps(
-            lambda: engine._forward_impl(xd, md, mode, pk), 20, 3)[0])
+            lambda: engine._forward_impl(xd, md, mode, pk), n_eager, w_eager)[0])
 
     from tjkernels import tiles
     flops = flops_per_forward(w)
@@ -260,8 +262,9 @@ def main() -> int:
     roofline = None
     if breakdown:
         dom = max((k for k in breakdown if breakdown[k]["flops"] > 0), key=lambda k: breakdown[k]["ms"])
-        with torch.inference_mode():
-            avg_ms = _kernel_avg_ms(calls[dom])
+        one_ms = breakdown[dom]["ms"] / breakdown[dom]["launches"]
+        with torch.inference_mode():  # about 0.2 s of replays, 3 to 50 launches
+            avg_ms = _kernel_avg_ms(calls[dom], reps=max(3, min(50, int(200.0 / max(one_ms, 1e-3)))))
         per_launch = breakdown[dom]["flops"] / breakdown[dom]["launches"]
         achieved = per_launch / (avg_ms * 1e-3) / 1e12
         roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 1), "peak": peak,
@@ -275,7 +278,10 @@ def main() -> int:
                 v["tflops"] = round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 1)
 
     cpu, acc = (None, None)
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and w.seq > 16384:
+        # the oracle materializes [H, S, S] scores: 640 GB at S = 100000
+        print(f"bench.py: no CPU baseline for S={w.seq} (the CPU oracle holds S x S scores)", file=sys.stderr)
+    elif not args.no_cpu_baseline:
         cpu, acc = _cpu_baseline(w, sd, x, mask, got)
 
     line = {

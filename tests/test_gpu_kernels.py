@@ -424,6 +424,50 @@ def test_flash_packed_layout_headline(device):
         assert (out.float() - out1.float()).abs().max().item() < 2e-2
 
 
+def _attn_rows_ref(q, k, v, rows, causal):
+    """fp64 attention of selected query rows of one (sequence, head): q, k, v
+    [S, hd] on the CPU; memory O(S) per row, so it scales to S = 100000."""
+    hd = q.shape[-1]
+    out = []
+    for i in rows:
+        n = i + 1 if causal else k.shape[0]
+        sc = (k[:n].double() @ q[i].double()) * hd ** -0.5
+        p = torch.softmax(sc, 0)
+        out.append(p @ v[:n].double())
+    return torch.stack(out)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_long_sequence_streams(device, causal):
+    """Long-sequence streaming (the reference matrix's case 14 length,
+    bench/shapes.py:67-69): S = 100000, padded [B,S,3,H,hd] and packed
+    (varlen) layouts, against fp64 on sampled query rows, each computed in
+    O(S) memory on the CPU.  The kernel holds O(tile) state per query block,
+    so nothing of size S x S exists anywhere."""
+    s, h, hd = 100000, 2, 64
+    g = _gen(14 + int(causal))
+    qkv = torch.randn(1, s, 3, h, hd, generator=g).to(torch.bfloat16)
+    rows = [0, 1, 63, 64, 4095, 33333, 65536, 99998, 99999]
+    out = torch.empty(s, h * hd, dtype=torch.bfloat16, device=device)
+    ops.flash_attention(qkv.to(device), out, causal=causal)
+    torch.cuda.synchronize()
+    got = out.cpu().view(s, h, hd)
+    for hh in range(h):
+        q, k, v = (qkv[0, :, i, hh] for i in range(3))
+        ref = _attn_rows_ref(q, k, v, rows, causal)
+        _close(got[rows, hh], ref, 1e-2, 1e-2)
+    # packed: the long sequence after a short one (rows offset by 37)
+    short = torch.randn(37, 3, h, hd, generator=g).to(torch.bfloat16)
+    packed = torch.cat([short, qkv[0]], 0)
+    cu = torch.tensor([0, 37, 37 + s], dtype=torch.int32, device=device)
+    out2 = torch.empty(37 + s, h * hd, dtype=torch.bfloat16, device=device)
+    ops.flash_attention(packed.to(device), out2, causal=causal, cu_seqlens=cu, max_seqlen=s)
+    torch.cuda.synchronize()
+    assert (out2[37:].float() - out.float()).abs().max().item() < 2e-2
+    if causal:  # the same kernel and key order per query: equal rows
+        assert torch.equal(out2[37:37 + 4096], out[:4096])
+
+
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("hd", [64, 128])
 @pytest.mark.parametrize("causal", [True, False])

@@ -16,7 +16,7 @@ import torch
 from oracle import model as oracle
 from tjkernels import Plan, TransformerConfig, UserOptimizedTransformer
 from tjkernels import plans as plans_mod
-from tjkernels.workloads import WORKLOADS, make_inputs, make_state_dict
+from tjkernels.workloads import WORKLOADS, Workload, make_inputs, make_state_dict
 
 pytestmark = pytest.mark.gpu
 
@@ -261,3 +261,30 @@ def test_packed_forward_matches_unpacked(device, causal):
     keep = lengths > 0
     ref = oracle.forward(sd, x[keep], mask[keep], cfg.num_heads, causal, torch.float32)
     _check(packed[keep], ref, mask[keep], torch.float32)
+
+
+def test_long_sequence_prefix_property(device):
+    """A 100000-token causal forward (case 14's length) runs in O(S) memory,
+    and its first P rows equal the forward of the first P tokens alone: under
+    causal attention no row sees a later token, and every other op is
+    row-wise.  The short forward is checked against the CPU oracle, so the
+    long one is pinned on those rows without an S x S reference."""
+    w = Workload("long", 2, 256, 4, 512, 1, 100000, torch.bfloat16, None, 0.02)
+    cfg = w.config
+    sd = make_state_dict(w, seed=5)
+    model = _module(cfg, sd, torch.bfloat16, device)
+    g = torch.Generator()
+    g.manual_seed(14)
+    x = torch.randn(1, 100000, 256, generator=g).to(torch.bfloat16)
+    p = 300
+    short_cfg = TransformerConfig(1, p, 256, 4, 512, 2, True)
+    short = _module(short_cfg, sd, torch.bfloat16, device)
+    with torch.inference_mode():
+        long_out = model(x.to(device)).cpu()
+        short_out = short(x[:, :p].contiguous().to(device)).cpu()
+    assert torch.isfinite(long_out).all()
+    d = (long_out[:, :p].float() - short_out.float()).abs().max().item()
+    assert d <= 2e-2, f"prefix rows differ from the short forward by {d:.3e}"
+    full = torch.ones(1, p, dtype=torch.bool)
+    ref = oracle.forward(sd, x[:, :p].float(), full, cfg.num_heads, True, torch.float32)
+    _check(short_out, ref, full, torch.bfloat16)

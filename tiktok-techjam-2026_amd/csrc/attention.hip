@@ -31,6 +31,8 @@
 // the math of tiles entirely above its own diagonal.  Workgroups are issued
 // longest-first (the last query blocks have the most key tiles).
 
+#include <algorithm>
+
 #include "tjk_common.h"
 
 namespace tjk {
@@ -401,7 +403,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
     T* __restrict__ out, int64_t ld_out, int B, int S, int H, int hd, float scale_log2,
     int causal, const int32_t* __restrict__ lengths, const uint8_t* __restrict__ key_mask,
     const int32_t* __restrict__ cu_seqlens, int nqb,
-    const int4* __restrict__ work, float* __restrict__ partials, int* __restrict__ flags) {
+    const int4* __restrict__ work, float* __restrict__ partials, int* __restrict__ flags, int grp) {
   static_assert(sizeof(T) == 2, "2-byte element types only");
   constexpr int BMQ = 128, BNK = 64, NST = 3, VEC = 8;
   constexpr int LDK = HDP + VEC, LDV = BNK + VEC;
@@ -428,8 +430,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
     t_hi = it.z >> 16;
     slot = it.w;
   } else {
-    const int rank = blockIdx.x / BH;
-    bh = blockIdx.x % BH;
+    // Longest query blocks first within groups of `grp` (b, h) pairs: a
+    // group's blocks run together, which bounds the K/V the blocks in
+    // flight stream (grp = B*H: one group, longest first over everything).
+    const int gi = blockIdx.x / (grp * nqb), r = blockIdx.x % (grp * nqb);
+    const int gsize = min(grp, BH - gi * grp);
+    const int rank = r / gsize;
+    bh = gi * grp + r % gsize;
     qb = causal ? nqb - 1 - rank : rank;
   }
   const int b = bh / H, h = bh % H;
@@ -864,7 +871,7 @@ static int launch_sched(const void* qkv, int64_t ss, int64_t sc, int64_t sh, voi
   hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, false, FULL>), dim3((unsigned)n_work), dim3(256), 0, st,      \
                      (const T*)qkv, (int64_t)0, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, \
                      (const int32_t*)nullptr, (const uint8_t*)nullptr, cu_seqlens, 0,                         \
-                     reinterpret_cast<const int4*>(work), partials, flags)
+                     reinterpret_cast<const int4*>(work), partials, flags, 1)
   if (hd == HDP) TJK_PIPE_SCHED(true); else TJK_PIPE_SCHED(false);
 #undef TJK_PIPE_SCHED
   return check_launch("tjk_flash_fwd_sched");
@@ -878,10 +885,17 @@ static int launch_pipe(const void* qkv, int64_t sb, int64_t ss, int64_t sc, int6
   const int nqb = (S + 127) / 128;
   const int64_t nblk = (int64_t)nqb * B * H;
   if (nblk > INT32_MAX) return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd: grid too large");
+  // (b, h) pairs per group: all of them while their K / V fit in about half
+  // the 256 MB Infinity Cache, else as many as fit (at least 8).  At the
+  // reference's case 14 (B = 32, H = 16, S = 100000) the 512 pairs stream
+  // 13 GB of K / V; grouped by 8 the blocks in flight share ~200 MB.
+  const int64_t kv_pair = (int64_t)S * hd * 2 * (int64_t)sizeof(T);
+  const int64_t fit = (int64_t)128 * 1024 * 1024 / (kv_pair > 0 ? kv_pair : 1);
+  const int grp = (int)std::max<int64_t>(std::min<int64_t>(B * H, std::max<int64_t>(fit, 8)), 1);
 #define TJK_PIPE(KM, FULL)                                                                                     \
   hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, KM, FULL>), dim3((unsigned)nblk), dim3(256), 0, st, (const T*)qkv, \
                      sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, lengths, key_mask,          \
-                     cu_seqlens, nqb, (const int4*)nullptr, (float*)nullptr, (int*)nullptr)
+                     cu_seqlens, nqb, (const int4*)nullptr, (float*)nullptr, (int*)nullptr, grp)
   if (key_mask != nullptr) {
     if (hd == HDP) TJK_PIPE(true, true); else TJK_PIPE(true, false);
   } else {
@@ -986,12 +1000,14 @@ extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s
   // head's K/V span must fit 31 bits); plans 1/2: one / two 32-query blocks
   // per wave without cross-tile pipelining (every dtype); plan 3: plan 1
   // with two key splits per query group (8 waves, merged through LDS).
-  // Measured on MI355X (bf16/fp16, hd 64/128): plan 1 is fastest at
-  // S >= 2048 (C4 padded 64 us vs 69 us for plan 0; C5 191 us vs 258 us),
-  // plan 0 below (C3 15 us; packed C4, lengths 1054-1710: 44.5 us vs
-  // 47.9 us); plans 2 and 3 were slower on every BASELINE shape.
+  // Measured on MI355X (bf16, causal, with plan 0's split softmax
+  // pipeline): at hd <= 64 plan 0 is fastest at every length (S = 2048:
+  // 59 vs 64 us; S = 100000: 841 vs 726 TFLOP/s); at hd 128 plan 1 up to
+  // S = 8192 (C5: 111 vs 123 us at 2048 x 4) and plan 0 from S = 32768
+  // (793 vs 765 TFLOP/s at 100000); plans 2 and 3 were slower on every
+  // BASELINE shape.
   const bool pipe_ok = dtype != TJK_F32 && ((int64_t)seq * stride_s + head_dim) * dtype_size(dtype) < INT32_MAX;
-  if (plan_id == -1) plan_id = (pipe_ok && seq < 2048) ? 0 : 1;
+  if (plan_id == -1) plan_id = (pipe_ok && (head_dim <= 64 || seq >= 16384)) ? 0 : 1;
   if (plan_id == 0 && !pipe_ok) plan_id = 1;
   const float scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);

@@ -70,6 +70,12 @@ WORKLOADS: Dict[str, Workload] = {
                    note="headline MFMA-utilisation config"),
     "C5": Workload("C5", 6, 2048, 16, 8192, 2, 4096, torch.bfloat16, None, 0.01,
                    note="large contraction, hd=128"),
+    # The reference matrix's case 14 (bench/shapes.py:67-69), which it never
+    # ran (README.md:167-180: 13 GB of input, an S x S score tensor in its
+    # reference).  Here attention streams K/V tiles in O(S) memory and the
+    # whole forward fits in ~65 GB of the 288 GB HBM.
+    "C14": Workload("C14", 2, 1024, 16, 1024, 32, 100000, torch.bfloat16, None, 0.02,
+                    note="reference case 14: S=100000 streaming"),
 }
 
 
