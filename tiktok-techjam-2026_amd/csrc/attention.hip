@@ -1005,9 +1005,12 @@ extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s
   // 59 vs 64 us; S = 100000: 841 vs 726 TFLOP/s); at hd 128 plan 1 up to
   // S = 8192 (C5: 111 vs 123 us at 2048 x 4) and plan 0 from S = 32768
   // (793 vs 765 TFLOP/s at 100000); plans 2 and 3 were slower on every
-  // BASELINE shape.
+  // BASELINE shape.  With a key mask plan 0 runs every tile through its
+  // masked (unpipelined) loop: plan 1 from S = 2048 (padded C4 with a
+  // per-key mask: 129 vs 168 us).
   const bool pipe_ok = dtype != TJK_F32 && ((int64_t)seq * stride_s + head_dim) * dtype_size(dtype) < INT32_MAX;
-  if (plan_id == -1) plan_id = (pipe_ok && (head_dim <= 64 || seq >= 16384)) ? 0 : 1;
+  if (plan_id == -1)
+    plan_id = (pipe_ok && (key_mask != nullptr ? seq < 2048 : (head_dim <= 64 || seq >= 16384))) ? 0 : 1;
   if (plan_id == 0 && !pipe_ok) plan_id = 1;
   const float scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
