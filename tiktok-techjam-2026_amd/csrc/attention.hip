@@ -49,8 +49,9 @@ template <> struct PairPack<bf16> {
     const uint32_t b[4] = {r1.x, r1.y, r1.z, r1.w};
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const uint32_t lo = (a[w] & 0xffffu) | (b[w] << 16);
-      const uint32_t hi = (a[w] >> 16) | (b[w] & 0xffff0000u);
+      // one v_perm_b32 per word: bytes 0-3 select from a, 4-7 from b
+      const uint32_t lo = __builtin_amdgcn_perm(b[w], a[w], 0x05040100u);  // {a.lo, b.lo}
+      const uint32_t hi = __builtin_amdgcn_perm(b[w], a[w], 0x07060302u);  // {a.hi, b.hi}
       *reinterpret_cast<uint32_t*>(dst + (2 * w) * ld) = lo;
       *reinterpret_cast<uint32_t*>(dst + (2 * w + 1) * ld) = hi;
     }
@@ -383,14 +384,15 @@ __global__ __launch_bounds__(256 * KS) void flash_fwd_kernel(
 // broken across tiles: the MFMAs of S for tile t+1 are issued before the
 // softmax of tile t, so the matrix cores work while the VALU does the
 // softmax.  That needs K of tile t+1 resident while V of tile t is still
-// read, so K/V tiles live in a 3-deep LDS ring; the global loads of tile
-// t+2 go out at the start of iteration t.  K/V are read through buffer
-// descriptors that end at this head's last key, so keys past S arrive as 0
-// without a bounds branch.  Tiles that need no masking (every key below the
-// workgroup's first query and inside the sequence) run a branch-free loop;
-// the diagonal / tail tiles run a second loop with masks and per-wave skips.
+// read, so K/V tiles live in a 4-deep LDS ring; the global loads of tile
+// t+3 go out at the start of iteration t.  K/V are read through per-tile
+// buffer descriptors that end at this head's last key, so keys past S
+// arrive as 0 without a bounds branch.  Tiles that need no masking (every
+// key below the workgroup's first query and inside the sequence) run a
+// loop unrolled over the ring, whose LDS slots are then compile-time
+// offsets; the diagonal / tail tiles run a second loop with masks and
+// per-wave skips.
 
-constexpr uint32_t kFaPastEnd = 0x7fff0000u;
 // Cache-policy bits of buffer loads / stores (sc0 = 1, sc1 = 16): sc1 makes
 // an access device-coherent, sc0 sc1 on a store writes through to memory.
 constexpr int kFaSc1 = 16, kFaSc0Sc1 = 17;
@@ -405,7 +407,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
     const int32_t* __restrict__ cu_seqlens, int nqb,
     const int4* __restrict__ work, float* __restrict__ partials, int* __restrict__ flags, int grp) {
   static_assert(sizeof(T) == 2, "2-byte element types only");
-  constexpr int BMQ = 128, BNK = 64, NST = 3, VEC = 8;
+  constexpr int BMQ = 128, BNK = 64, NST = 4, VEC = 8;
   constexpr int LDK = HDP + VEC, LDV = BNK + VEC;
   constexpr int KC = HDP / 16, HB = HDP / 32, CH = HDP / VEC;
   constexpr int KITEMS = BNK * CH, VITEMS = (BNK / 2) * CH;
@@ -479,19 +481,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
     }
   }
 
-  // K / V rows of this (b, h) through buffer descriptors ending at key Sb-1.
+  // K / V rows of this (b, h): the span from key 0 to the end of key Sb-1.
+  // Tile t is read through a descriptor starting at its first key (scalar
+  // work), so the per-lane offsets stay fixed across tiles; a tile past the
+  // item's range gets an empty descriptor and reads as zeros.
   const uint32_t row_bytes = (uint32_t)(ss * (int64_t)sizeof(T));
   const int span = (int)(((int64_t)(Sb - 1) * ss + hd) * (int64_t)sizeof(T));
-  const __amdgpu_buffer_rsrc_t rsk = __builtin_amdgcn_make_buffer_rsrc((void*)(qbase + sc), (short)0, span, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rsv = __builtin_amdgcn_make_buffer_rsrc((void*)(qbase + 2 * sc), (short)0, span, 0x00020000);
   uint4 rk[KPT], rv0[VPT], rv1[VPT];
-  auto load_kv_into = [&](int t, uint4 (&rk)[KPT], uint4 (&rv0)[VPT], uint4 (&rv1)[VPT]) {
-    // tiles past the end read as zeros
-    const uint32_t tb = t < t_hi ? (uint32_t)t * BNK * row_bytes : kFaPastEnd;
+  auto load_kv_into = [&](int t, uint4 (&rk)[KPT], uint4 (&rv0)[VPT], uint4 (&rv1)[VPT]) __attribute__((always_inline)) {
+    const int64_t t_elems = (int64_t)t * BNK * ss;
+    const int nrec = t < t_hi ? span - (int)(t_elems * (int64_t)sizeof(T)) : 0;
+    const __amdgpu_buffer_rsrc_t rsk =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(qbase + sc + t_elems), (short)0, nrec, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsv =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(qbase + 2 * sc + t_elems), (short)0, nrec, 0x00020000);
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int it = tid + i * 256, key = it / CH, c = it % CH;
-      const uint32_t off = tb + (uint32_t)key * row_bytes + (uint32_t)(c * 16);
+      const uint32_t off = (uint32_t)key * row_bytes + (uint32_t)(c * 16);
       uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsk, off, 0, 0));
       rk[i] = (FULLHD || c * VEC < hd) ? v : make_uint4(0, 0, 0, 0);
     }
@@ -499,7 +506,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
     for (int i = 0; i < VPT; ++i) {
       const int it = tid + i * 256;
       const int p = it % (BNK / 2), c = it / (BNK / 2);
-      const uint32_t off = tb + (uint32_t)(2 * p) * row_bytes + (uint32_t)(c * 16);
+      const uint32_t off = (uint32_t)(2 * p) * row_bytes + (uint32_t)(c * 16);
       uint4 v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsv, off, 0, 0));
       uint4 v1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsv, off + row_bytes, 0, 0));
       const bool ok = FULLHD || c * VEC < hd;
@@ -507,7 +514,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
       rv1[i] = ok ? v1 : make_uint4(0, 0, 0, 0);
     }
   };
-  auto store_kv_from = [&](int st, const uint4 (&rk)[KPT], const uint4 (&rv0)[VPT], const uint4 (&rv1)[VPT]) {
+  auto store_kv_from = [&](int st, uint4 (&rk)[KPT], uint4 (&rv0)[VPT], uint4 (&rv1)[VPT]) {
+    // the loads landed a step ago; pinning the registers here keeps the V
+    // transposition (v_perm) from being hoisted into the step that issued
+    // the loads, where it would wait for them
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      u32x4 a = __builtin_bit_cast(u32x4, rv0[i]), c = __builtin_bit_cast(u32x4, rv1[i]);
+      asm volatile("" : "+v"(a), "+v"(c));
+      rv0[i] = __builtin_bit_cast(uint4, a);
+      rv1[i] = __builtin_bit_cast(uint4, c);
+    }
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int it = tid + i * 256, key = it / CH, c = it % CH;
@@ -522,8 +539,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
       }
     }
   };
-  auto load_kv = [&](int t) { load_kv_into(t, rk, rv0, rv1); };
-  auto store_kv = [&](int st) { store_kv_from(st, rk, rv0, rv1); };
+  auto load_kv = [&](int t) __attribute__((always_inline)) { load_kv_into(t, rk, rv0, rv1); };
+  auto store_kv = [&](int st) __attribute__((always_inline)) { store_kv_from(st, rk, rv0, rv1); };
+  // ring slot of key tile tt (slot 0 holds the item's first tile)
+  auto slot_of = [&](int tt) { return (tt - t_lo) & (NST - 1); };
 
   const int krow = swap_bits_2_3(l32);
   auto qk = [&](int st, f32x16 (&sa)[2]) {
@@ -612,15 +631,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
       }
   };
 
-  // ---- interior-tile pipeline (unmasked tiles).  The softmax of tile t is
-  // split around the row max: the max of S(t+1) is taken while the PV
-  // MFMAs of tile t run, and the exponentials of tile t while the S(t+1)
-  // MFMAs run, so every VALU-heavy stretch of the loop has MFMAs to hide
-  // behind (and the other wave of the SIMD finds the matrix pipe busy in
-  // the opposite phase).
+  // ---- interior-tile pipeline (unmasked tiles).  The exponentials of tile
+  // t run while the MFMAs of S(t+1) run, so the VALU-heavy stretch of each
+  // step has MFMAs to hide behind (and the other wave of the SIMD finds the
+  // matrix pipe busy in the opposite phase, the PV product).  No row max is
+  // taken: P = 2^(S * scale - m_off) is formed with the running offset, and
+  // only when a lane's share of a query's tile sum exceeds kSumLimit (which
+  // bounds every P of the tile; a first tile, with m_off = -inf, gives inf)
+  // is the tile redone with m_off raised to the row max.  Every P the PV
+  // product sees is therefore <= kSumLimit.
   typedef typename Mfma<T>::frag Frag;
+  constexpr float kSumLimit = 4096.0f;
   // row max of a tile's scores in log2 units; both lanes of a query agree
-  auto rowmax = [&](const f32x16 (&sa)[2]) -> float {
+  auto rowmax = [&](const f32x16 (&sa)[2]) __attribute__((always_inline)) -> float {
     float mx = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -629,31 +652,48 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
     return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * scale_log2;
   };
-  auto rescale = [&](float mx) {
-    if (__any(mx > m_off + kLazyRescale)) {
-      const float m_new = fmaxf(m_off, mx);
-      const float alpha = m_off == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_off - m_new);
-      l_run *= alpha;
+  // P = 2^(S * scale - m_off) packed to the MFMA type; returns this lane's
+  // sum of the rounded P
+  auto exp_pack = [&](const f32x16 (&sc)[2], Frag (&pf)[4]) __attribute__((always_inline)) -> float {
+    const float nb = -m_off;
+    float l0 = 0.f, l1 = 0.f;
 #pragma unroll
-      for (int hb = 0; hb < HB; ++hb)
+    for (int stp = 0; stp < 4; ++stp) {
+      float p[8];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[hb][r] *= alpha;
-      m_off = m_new;
+      for (int e = 0; e < 8; ++e)
+        p[e] = __builtin_amdgcn_exp2f(fmaf(sc[stp >> 1][8 * (stp & 1) + e], scale_log2, nb));
+      pf[stp] = Mfma<T>::pack(p);
+      if (stp & 1) l1 = Mfma<T>::sum8(pf[stp], l1);
+      else l0 = Mfma<T>::sum8(pf[stp], l0);
     }
+    return l0 + l1;
   };
-  // S(next) = K(st) Q^T, interleaved with P = 2^(S(cur) * scale - m_off)
-  // packed to the MFMA type (row sums from the rounded P)
-  auto qk_exp = [&](int st, f32x16 (&snext)[2], const f32x16 (&scur_)[2], Frag (&pf)[4]) {
+  // S(next) = K(st) Q^T, interleaved with P of S(cur); returns the lane
+  // sum.  The V fragments of the PV product that follows (slot vst) are read
+  // here too, so their LDS latency hides behind the exponentials.
+  auto qk_exp = [&](int st, f32x16 (&snext)[2], const f32x16 (&scur_)[2], Frag (&pf)[4], int vst,
+                    Frag (&vf)[HB][4]) __attribute__((always_inline)) -> float {
     Frag kf[KC][2];
 #pragma unroll
     for (int c = 0; c < KC; ++c)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) kf[c][kb] = Mfma<T>::load(&sK[st][(kb * 32 + krow) * LDK + 8 * hi] + 16 * c);
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+      const T* vp = &sV[vst][(hb * 32 + l32) * LDV + 8 * hi];
+#pragma unroll
+      for (int stp = 0; stp < 4; ++stp) vf[hb][stp] = Mfma<T>::load(vp + 16 * stp);
+    }
     // every fragment read issued together, one wait for all of them
 #pragma unroll
     for (int c = 0; c < KC; ++c)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) asm volatile("" : "+v"(kf[c][kb]));
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+      for (int stp = 0; stp < 4; ++stp) asm volatile("" : "+v"(vf[hb][stp]));
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -662,113 +702,110 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
     for (int c = 0; c < KC; ++c)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) Mfma<T>::mma(snext[kb], kf[c][kb], qf[c]);
-    const float nb = -m_off;
-    float l0 = 0.f, l1 = 0.f;
-#pragma unroll
-    for (int stp = 0; stp < 4; ++stp) {
-      float p[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        p[e] = __builtin_amdgcn_exp2f(fmaf(scur_[stp >> 1][8 * (stp & 1) + e], scale_log2, nb));
-      pf[stp] = Mfma<T>::pack(p);
-      if (stp & 1) l1 = Mfma<T>::sum8(pf[stp], l1);
-      else l0 = Mfma<T>::sum8(pf[stp], l0);
-    }
-    l_run += l0 + l1;
+    const float lt = exp_pack(scur_, pf);
     // order: one MFMA per ~12 VALU (the exponentials of tile t)
 #pragma unroll
     for (int i = 0; i < 2 * KC; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);
     }
+    return lt;
   };
-  // O += V(st)^T P^T, interleaved with the row max of the next scores
-  auto pv_max = [&](int st, const Frag (&pf)[4], const f32x16 (&snext)[2]) -> float {
-    Frag vf[HB][4];
+  // accept P of tile `sc` (lane sum lt), or redo it from a raised offset
+  auto settle = [&](const f32x16 (&sc)[2], Frag (&pf)[4], float lt) __attribute__((always_inline)) {
+    if (__any(!(lt <= kSumLimit))) {
+      const float m_new = fmaxf(m_off, rowmax(sc));
+      const float alpha = m_off == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_off - m_new);
+      l_run *= alpha;
 #pragma unroll
-    for (int hb = 0; hb < HB; ++hb) {
-      const T* vp = &sV[st][(hb * 32 + l32) * LDV + 8 * hi];
+      for (int hb = 0; hb < HB; ++hb)
 #pragma unroll
-      for (int stp = 0; stp < 4; ++stp) vf[hb][stp] = Mfma<T>::load(vp + 16 * stp);
+        for (int r = 0; r < 16; ++r) o[hb][r] *= alpha;
+      m_off = m_new;
+      lt = exp_pack(sc, pf);
     }
-#pragma unroll
-    for (int hb = 0; hb < HB; ++hb)
-#pragma unroll
-      for (int stp = 0; stp < 4; ++stp) asm volatile("" : "+v"(vf[hb][stp]));
+    l_run += lt;
+  };
+  // O += V^T P^T from the fragments qk_exp read
+  auto pv = [&](const Frag (&vf)[HB][4], const Frag (&pf)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int stp = 0; stp < 4; ++stp)
 #pragma unroll
       for (int hb = 0; hb < HB; ++hb) Mfma<T>::mma(o[hb], vf[hb][stp], pf[stp]);
-    float mx = rowmax(snext);
-    asm volatile("" : "+v"(mx));  // keep the max here, under the PV MFMAs
-#pragma unroll
-    for (int i = 0; i < 4 * HB; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
-    }
-    return mx;
   };
 
-  // Ring invariant at the top of step t: LDS slots t and t+1 (mod NST) hold
-  // key tiles t and t+1, the staging registers hold tile t+2 (its loads in
-  // flight since the previous step), and scur holds S(t).  A step first
-  // stores tile t+2 into the slot tile t-1 freed, then loads tile t+3, so
-  // every global load has a whole step to land.
+  // Ring invariant at the top of step t: LDS slots of tiles t and t+1 hold
+  // them, the staging registers hold tile t+2 (its loads in flight since the
+  // previous step), and sc holds S(t).  A step first stores tile t+2 into
+  // the slot tile t-2 freed, then loads tile t+3, so every global load has
+  // a whole step to land; one barrier per step orders the slot reuse.
   {
     // both first tiles in flight at once (one global latency, not two)
     uint4 rk1[KPT], rv01[VPT], rv11[VPT];
     load_kv(t_lo);
     load_kv_into(t_lo + 1, rk1, rv01, rv11);
-    store_kv(t_lo % NST);
-    store_kv_from((t_lo + 1) % NST, rk1, rv01, rv11);
+    store_kv(0);
+    store_kv_from(1, rk1, rv01, rv11);
   }
   __syncthreads();
   load_kv(t_lo + 2);
 
   f32x16 scur[2];
-  if (t_hi > t_lo) qk(t_lo % NST, scur);
+  if (t_hi > t_lo) qk(0, scur);
   // Interior tiles: every key below the workgroup's first query and inside
   // the sequence, and a next tile exists in this item's range.
   int n_int = KEYMASK ? 0 : min(causal ? q0 / BNK : nkt, min(kend / BNK, t_hi - 1));
   n_int = max(n_int, t_lo);
   int t = t_lo;
+  // an unmasked first tile starts the offset at its row max, so the
+  // interior loop does not redo it
+  if (t < n_int) m_off = rowmax(scur);
   f32x16 salt[2];
   Frag pf[4];
-  if (t + 1 < n_int) {
-    float mx = rowmax(scur);
-    for (; t + 1 < n_int; t += 2) {  // two tiles per trip: scores ping-pong scur <-> salt
-      store_kv((t + 2) % NST);
-      load_kv(t + 3);
-      rescale(mx);
-      qk_exp((t + 1) % NST, salt, scur, pf);
-      mx = pv_max(t % NST, pf, salt);
-      __syncthreads();
-      store_kv((t + 3) % NST);
-      load_kv(t + 4);
-      rescale(mx);
-      qk_exp((t + 2) % NST, scur, salt, pf);
-      mx = pv_max((t + 1) % NST, pf, scur);
-      __syncthreads();
-    }
+  // one interior step; j is tile t's ring slot (a constant in the unrolled loop)
+  auto istep = [&](int tt, int j, const f32x16 (&sc)[2], f32x16 (&sn)[2]) __attribute__((always_inline)) {
+    store_kv((j + 2) & (NST - 1));
+    load_kv(tt + 3);
+    Frag vf[HB][4];
+    const float lt = qk_exp((j + 1) & (NST - 1), sn, sc, pf, j, vf);
+    settle(sc, pf, lt);
+    pv(vf, pf);
+    __syncthreads();
+  };
+  // four tiles per trip (one turn of the ring), scores ping-pong scur <-> salt
+  for (; t + 3 < n_int; t += 4) {
+    istep(t, 0, scur, salt);
+    istep(t + 1, 1, salt, scur);
+    istep(t + 2, 2, scur, salt);
+    istep(t + 3, 3, salt, scur);
   }
   if (t < n_int) {
-    store_kv((t + 2) % NST);
-    load_kv(t + 3);
-    softmax_pv(t % NST, scur);
-    qk((t + 1) % NST, scur);
-    __syncthreads();
+    istep(t, slot_of(t), scur, salt);
     ++t;
+    if (t < n_int) {
+      istep(t, slot_of(t), salt, scur);
+      ++t;
+      if (t < n_int) {
+        istep(t, slot_of(t), scur, salt);
+        ++t;
+        scur[0] = salt[0];
+        scur[1] = salt[1];
+      }
+    } else {
+      scur[0] = salt[0];
+      scur[1] = salt[1];
+    }
   }
   for (; t < t_hi; ++t) {
-    store_kv((t + 2) % NST);
+    store_kv(slot_of(t + 2));
     load_kv(t + 3);
     f32x16 snext[2];
     const bool act_next = t + 1 < t_hi && (!causal || (t + 1) * BNK <= wq0 + 31);
-    if (act_next) qk((t + 1) % NST, snext);
+    if (act_next) qk(slot_of(t + 1), snext);
     const bool act = !causal || t * BNK <= wq0 + 31;
     if (act) {
       mask_tile(t, scur);
-      softmax_pv(t % NST, scur);
+      softmax_pv(slot_of(t), scur);
     }
     __syncthreads();
     if (act_next) {
