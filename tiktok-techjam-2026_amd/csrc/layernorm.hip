@@ -40,7 +40,8 @@ int check_launch(const char* what) {
   return TJK_OK;
 }
 
-template <typename TRes, typename TDelta, typename TOut, int MAXCH>
+// FULL: n == 256 * MAXCH, every lane's chunks in range (no per-chunk guards).
+template <typename TRes, typename TDelta, typename TOut, int MAXCH, bool FULL>
 __global__ __launch_bounds__(256) void add_layernorm_kernel(
     const TRes* res, int64_t ld_res,  // may alias res_out (in-place update)
     const TDelta* __restrict__ delta, int64_t ld_delta,
@@ -50,49 +51,62 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(
     int64_t rows, int n, float eps, const int32_t* __restrict__ row_index,
     const uint8_t* __restrict__ row_mask) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
   const int nch = n >> 2;
-  const int64_t src = row_index != nullptr ? (int64_t)row_index[row] : row;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const bool live = row < rows;
+  const int64_t src = !live ? -1 : row_index != nullptr ? (int64_t)row_index[row] : row;
+
+  float4 x[MAXCH];
+  if (src >= 0) {
+    const TRes* rrow = res + src * ld_res;
+#pragma unroll
+    for (int j = 0; j < MAXCH; ++j) {
+      const int c = lane + 64 * j;
+      if (FULL || c < nch) {
+        x[j] = Quad<TRes>::to(reinterpret_cast<const typename Quad<TRes>::raw*>(rrow)[c]);
+      } else {
+        x[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    if (delta != nullptr) {
+      const TDelta* drow = delta + src * ld_delta;
+#pragma unroll
+      for (int j = 0; j < MAXCH; ++j) {
+        const int c = lane + 64 * j;
+        if (FULL || c < nch) {
+          float4 d = Quad<TDelta>::to(reinterpret_cast<const typename Quad<TDelta>::raw*>(drow)[c]);
+          x[j].x += d.x; x[j].y += d.y; x[j].z += d.z; x[j].w += d.w;
+        }
+      }
+    }
+  }
+  // gamma / beta staged once per workgroup (4 rows), by every thread before
+  // any wave leaves: read from L2 by each wave they were 8 KB per 1024-wide
+  // row, more than the row itself
+  __shared__ float4 s_gamma[64 * MAXCH], s_beta[64 * MAXCH];
+  for (int c = threadIdx.x; c < nch; c += 256) {
+    s_gamma[c] = reinterpret_cast<const float4*>(gamma)[c];
+    s_beta[c] = reinterpret_cast<const float4*>(beta)[c];
+  }
+  __syncthreads();
+  if (!live) return;
   if (src < 0) {  // scatter hole: an exact zero row, nothing read
     typename Quad<TOut>::raw* yrow = reinterpret_cast<typename Quad<TOut>::raw*>(out + row * ld_out);
 #pragma unroll
     for (int j = 0; j < MAXCH; ++j) {
       const int c = lane + 64 * j;
-      if (c < nch) yrow[c] = Quad<TOut>::from(make_float4(0.f, 0.f, 0.f, 0.f));
+      if (FULL || c < nch) yrow[c] = Quad<TOut>::from(make_float4(0.f, 0.f, 0.f, 0.f));
     }
     return;
   }
 
-  float4 x[MAXCH];
-  const TRes* rrow = res + src * ld_res;
   float s = 0.f;
-#pragma unroll
-  for (int j = 0; j < MAXCH; ++j) {
-    const int c = lane + 64 * j;
-    if (c < nch) {
-      x[j] = Quad<TRes>::to(reinterpret_cast<const typename Quad<TRes>::raw*>(rrow)[c]);
-    } else {
-      x[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-  }
-  if (delta != nullptr) {
-    const TDelta* drow = delta + src * ld_delta;
-#pragma unroll
-    for (int j = 0; j < MAXCH; ++j) {
-      const int c = lane + 64 * j;
-      if (c < nch) {
-        float4 d = Quad<TDelta>::to(reinterpret_cast<const typename Quad<TDelta>::raw*>(drow)[c]);
-        x[j].x += d.x; x[j].y += d.y; x[j].z += d.z; x[j].w += d.w;
-      }
-    }
-  }
   if (res_out != nullptr) {
     float4* orow = reinterpret_cast<float4*>(res_out + row * ld_res_out);
 #pragma unroll
     for (int j = 0; j < MAXCH; ++j) {
       const int c = lane + 64 * j;
-      if (c < nch) orow[c] = x[j];
+      if (FULL || c < nch) orow[c] = x[j];
     }
   }
 #pragma unroll
@@ -103,7 +117,7 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(
 #pragma unroll
   for (int j = 0; j < MAXCH; ++j) {
     const int c = lane + 64 * j;
-    if (c < nch) {
+    if (FULL || c < nch) {
       const float a = x[j].x - mean, b = x[j].y - mean, cc = x[j].z - mean, d = x[j].w - mean;
       q += (a * a + b * b) + (cc * cc + d * d);
     }
@@ -113,17 +127,15 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(
   const bool zero = row_mask != nullptr && row_mask[row] == 0;
 
   typename Quad<TOut>::raw* yrow = reinterpret_cast<typename Quad<TOut>::raw*>(out + row * ld_out);
-  const float4* g4 = reinterpret_cast<const float4*>(gamma);
-  const float4* b4 = reinterpret_cast<const float4*>(beta);
 #pragma unroll
   for (int j = 0; j < MAXCH; ++j) {
     const int c = lane + 64 * j;
-    if (c < nch) {
+    if (FULL || c < nch) {
       float4 y;
       if (zero) {
         y = make_float4(0.f, 0.f, 0.f, 0.f);
       } else {
-        const float4 g = g4[c], b = b4[c];
+        const float4 g = s_gamma[c], b = s_beta[c];
         y.x = (x[j].x - mean) * rstd * g.x + b.x;
         y.y = (x[j].y - mean) * rstd * g.y + b.y;
         y.z = (x[j].z - mean) * rstd * g.z + b.z;
@@ -141,12 +153,15 @@ static int launch_ln(const void* res, int64_t ld_res, const void* delta, int64_t
                      const int32_t* row_index, const uint8_t* row_mask, hipStream_t stream) {
   const int nch = n / 4;
   dim3 grid((unsigned)((rows + 3) / 4)), block(256);
-#define TJK_LN_CASE(MC)                                                                      \
-  if (nch <= 64 * MC) {                                                                      \
-    hipLaunchKernelGGL((add_layernorm_kernel<TRes, TDelta, TOut, MC>), grid, block, 0, stream, \
-                       (const TRes*)res, ld_res, (const TDelta*)delta, ld_delta, res_out,    \
-                       ld_res_out, (TOut*)out, ld_out, gamma, beta, rows, n, eps, row_index, row_mask); \
-    return check_launch("tjk_add_layernorm");                                                \
+#define TJK_LN_LAUNCH(MC, FULL)                                                                    \
+  hipLaunchKernelGGL((add_layernorm_kernel<TRes, TDelta, TOut, MC, FULL>), grid, block, 0, stream,     \
+                     (const TRes*)res, ld_res, (const TDelta*)delta, ld_delta, res_out, ld_res_out, \
+                     (TOut*)out, ld_out, gamma, beta, rows, n, eps, row_index, row_mask)
+#define TJK_LN_CASE(MC)                                   \
+  if (nch <= 64 * MC) {                                   \
+    if (nch == 64 * MC) TJK_LN_LAUNCH(MC, true);          \
+    else TJK_LN_LAUNCH(MC, false);                        \
+    return check_launch("tjk_add_layernorm");             \
   }
   TJK_LN_CASE(1)
   TJK_LN_CASE(2)
@@ -155,6 +170,7 @@ static int launch_ln(const void* res, int64_t ld_res, const void* delta, int64_t
   TJK_LN_CASE(16)
   TJK_LN_CASE(32)
 #undef TJK_LN_CASE
+#undef TJK_LN_LAUNCH
   return fail(TJK_EUNSUPPORTED, "tjk_add_layernorm: n=%d exceeds 8192", n);
 }
 
