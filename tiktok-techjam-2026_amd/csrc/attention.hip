@@ -584,7 +584,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sa[kb][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;  // both lanes of a query agree
+    {  // both lanes of a query agree (lane l and l^32 swap through v_permlane32_swap)
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * scale_log2;
+    }
     if (__any(mx > m_off + kLazyRescale)) {
       const float m_new = fmaxf(m_off, mx);
       const float alpha = m_off == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_off - m_new);
@@ -816,7 +819,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
 
   // normalise and store: register r of block hb is hd row hb*32 + 8*(r/4) + 4*hi + r%4
   const int q = wq0 + l32;
-  const float l = l_run + __shfl_xor(l_run, 32, 64);
+  const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+  const float l = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
   // Partial slot s: O^T rows [query][HDP] fp32, then m[BMQ], then l[BMQ].
   // The halves of a split item are different workgroups, possibly on
   // different XCDs: the partial is written through to memory (sc0 sc1) and
