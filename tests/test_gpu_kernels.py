@@ -404,6 +404,37 @@ def test_flash_closed_forms(device):
     assert torch.equal(out.view(b, s, -1)[:, :-1], out2.view(b, s, -1)[:, :-1])
 
 
+@pytest.mark.parametrize("pattern", ["rising", "falling", "huge"])
+def test_flash_offset_changes_across_tiles(device, pattern):
+    """Scores that climb across key tiles (the running offset must be raised
+    mid-sequence, repeatedly), that peak in the first tile and fall, or that
+    reach |S * scale| ~ 1e3 (exp2 far outside fp32 without an offset): every
+    plan against fp64, causal and not."""
+    b, s, h, hd = 2, 700, 2, 64
+    g = _gen({"rising": 11, "falling": 12, "huge": 13}[pattern])
+    qkv = torch.randn(b, s, 3, h, hd, generator=g) * 0.5
+    direction = torch.randn(h, hd, generator=g)
+    direction = direction / direction.norm(dim=-1, keepdim=True)
+    pos = torch.arange(s, dtype=torch.float32)[None, :, None, None]
+    if pattern == "rising":    # score grows ~ +0.25 per key: +175 over the sequence
+        qkv[:, :, 0] += 4.0 * direction
+        qkv[:, :, 1] += (pos / 16.0) * direction
+    elif pattern == "falling":  # largest scores in the first tile
+        qkv[:, :, 0] += 4.0 * direction
+        qkv[:, :, 1] += ((s - pos) / 16.0) * direction
+    else:                      # scores of order 1e3 with both signs
+        qkv[:, :, 0] *= 40.0
+    qkv = qkv.to(torch.bfloat16)
+    for causal in (True, False):
+        ref = _attn_ref(qkv, causal)
+        for plan in (0, 1, 3):
+            out = torch.full((b * s, h * hd), float("nan"), dtype=torch.bfloat16, device=device)
+            ops.flash_attention(qkv.to(device), out, causal=causal, plan=plan)
+            torch.cuda.synchronize()
+            assert torch.isfinite(out.float()).all(), (pattern, causal, plan)
+            _close(out, ref, 1e-2, 2e-2)
+
+
 def test_flash_packed_layout_headline(device):
     # C4 attention shape read in place from the packed QKV GEMM output
     b, s, h, hd = 4, 2048, 16, 64
