@@ -1041,17 +1041,17 @@ extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s
   // head's K/V span must fit 31 bits); plans 1/2: one / two 32-query blocks
   // per wave without cross-tile pipelining (every dtype); plan 3: plan 1
   // with two key splits per query group (8 waves, merged through LDS).
-  // Measured on MI355X (bf16, causal, with plan 0's split softmax
-  // pipeline): at hd <= 64 plan 0 is fastest at every length (S = 2048:
-  // 59 vs 64 us; S = 100000: 841 vs 726 TFLOP/s); at hd 128 plan 1 up to
-  // S = 8192 (C5: 111 vs 123 us at 2048 x 4) and plan 0 from S = 32768
-  // (793 vs 765 TFLOP/s at 100000); plans 2 and 3 were slower on every
-  // BASELINE shape.  With a key mask plan 0 runs every tile through its
-  // masked (unpipelined) loop: plan 1 from S = 2048 (padded C4 with a
-  // per-key mask: 129 vs 168 us).
+  // Measured on MI355X (bf16): at hd <= 64 plan 0 is fastest at every
+  // length (causal 4 x 2048: 54 vs 60 us; S = 32768: 944 vs 790 TFLOP/s);
+  // at hd 128 plan 1 up to S = 2048 (causal 4 x 2048: 112.5 vs 117.9 us)
+  // and plan 0 from S = 4096 (causal 2 x 4096: 192 vs 197 us, 2 x 8192:
+  // 671 vs 720 us); plans 2 and 3 were slower on every BASELINE shape.
+  // With a key mask plan 0 runs every tile through its masked
+  // (unpipelined) loop: plan 1 from S = 2048 (padded C4 with a per-key
+  // mask: 129 vs 168 us).
   const bool pipe_ok = dtype != TJK_F32 && ((int64_t)seq * stride_s + head_dim) * dtype_size(dtype) < INT32_MAX;
   if (plan_id == -1)
-    plan_id = (pipe_ok && (key_mask != nullptr ? seq < 2048 : (head_dim <= 64 || seq >= 16384))) ? 0 : 1;
+    plan_id = (pipe_ok && (key_mask != nullptr ? seq < 2048 : (head_dim <= 64 || seq >= 4096))) ? 0 : 1;
   if (plan_id == 0 && !pipe_ok) plan_id = 1;
   const float scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
