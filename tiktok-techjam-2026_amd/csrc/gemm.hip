@@ -971,6 +971,13 @@ static const GemmPlan kPlans16[] = {
     // where a 2-slot ring leaves each step waiting out the DMA latency.
     {kDtl, 64, 64, 2, 2, 128, 8, 0.45},       // 27 wave tile 32x32, 128 KB
     {kDtl, 128, 64, 2, 2, 128, 6, 0.50},      // 28 wave tile 64x32, 144 KB
+    // 29-31: the same small tiles with K split between 2 or 4 groups of 4
+    // waves inside the workgroup (partials added through LDS), which
+    // shortens the serial chain of K tiles a launch of a few dozen
+    // workgroups waits out.
+    {kDtl, 64, 64, 2, 2, 128, 2, 0.45, 4},    // 29 16 waves, 128 KB
+    {kDtl, 64, 64, 2, 2, 128, 4, 0.45, 2},    // 30 8 waves, 128 KB
+    {kDtl, 128, 64, 2, 2, 128, 3, 0.50, 2},   // 31 8 waves, 144 KB
 };
 // fp32.
 static const GemmPlan kPlans32[] = {
@@ -1148,6 +1155,9 @@ static int launch_epi(int epi, const GemmArgs& g) {
 typedef Launcher<kStaged> St;
 typedef DtlLauncher<128, 2> D2;
 typedef DtlLauncher<128, 2, 2> D2K2;
+typedef DtlLauncher<128, 2, 4> D2K4;
+typedef DtlLauncher<128, 4, 2> D4K2;
+typedef DtlLauncher<128, 3, 2> D3K2;
 typedef DtlLauncher<128, 4> D4;
 typedef DtlLauncher<128, 6> D6;
 typedef DtlLauncher<128, 8> D8;
@@ -1218,6 +1228,9 @@ static int run_gemm(int plan, int epi, const GemmArgs& g) {
       TJK_GEMM_CASE(26, D4, 192, 128, 2, 2)
       TJK_GEMM_CASE(27, D8, 64, 64, 2, 2)
       TJK_GEMM_CASE(28, D6, 128, 64, 2, 2)
+      TJK_GEMM_CASE(29, D2K4, 64, 64, 2, 2)
+      TJK_GEMM_CASE(30, D4K2, 64, 64, 2, 2)
+      TJK_GEMM_CASE(31, D3K2, 128, 64, 2, 2)
     }
   }
 #undef TJK_GEMM_CASE

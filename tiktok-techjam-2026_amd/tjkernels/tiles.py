@@ -28,9 +28,10 @@ import torch
 from . import _lib, ops, timing
 
 # Direct-to-LDS tile plans worth timing (2-byte types): 128x128, 256x256,
-# 64x64, 192x128, 192x256, 192x384, 96x128, 192x128 in a 4-slot ring, and
-# 64x64 / 128x64 in 8- / 6-slot rings.  fp32 uses its own list.
-CANDIDATES_16 = (7, 8, 9, 12, 13, 14, 15, 26, 27, 28)
+# 64x64, 192x128, 192x256, 192x384, 96x128, 192x128 in a 4-slot ring,
+# 64x64 / 128x64 in 8- / 6-slot rings, and 64x64 / 128x64 with K split
+# between 2 or 4 wave groups.  fp32 uses its own list.
+CANDIDATES_16 = (7, 8, 9, 12, 13, 14, 15, 26, 27, 28, 29, 30, 31)
 CANDIDATES_32 = (2, 3, 4)
 
 _choice: Dict[Tuple, int] = {}
