@@ -1048,10 +1048,12 @@ extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s
   // 671 vs 720 us); plans 2 and 3 were slower on every BASELINE shape.
   // With a key mask plan 0 runs every tile through its masked
   // (unpipelined) loop: plan 1 from S = 2048 (padded C4 with a per-key
-  // mask: 129 vs 168 us).
+  // mask: 129 vs 168 us).  A sequence of one 128-query block has only
+  // diagonal tiles and nothing to pipeline: plan 1 there too (C2's
+  // 1 x 128 x 8 heads fp16: 6.2 vs 6.8 us).
   const bool pipe_ok = dtype != TJK_F32 && ((int64_t)seq * stride_s + head_dim) * dtype_size(dtype) < INT32_MAX;
   if (plan_id == -1)
-    plan_id = (pipe_ok && (key_mask != nullptr ? seq < 2048 : (head_dim <= 64 || seq >= 4096))) ? 0 : 1;
+    plan_id = (pipe_ok && seq > 128 && (key_mask != nullptr ? seq < 2048 : (head_dim <= 64 || seq >= 4096))) ? 0 : 1;
   if (plan_id == 0 && !pipe_ok) plan_id = 1;
   const float scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
