@@ -807,7 +807,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
     if (act_next) qk(slot_of(t + 1), snext);
     const bool act = !causal || t * BNK <= wq0 + 31;
     if (act) {
-      mask_tile(t, scur);
+      // a tile below the wave's first query and inside the sequence (the
+      // first diagonal tile for the upper waves) needs no mask
+      if (KEYMASK || (causal && t * BNK + BNK - 1 > wq0) || t * BNK + BNK > kend) mask_tile(t, scur);
       softmax_pv(slot_of(t), scur);
     }
     __syncthreads();
