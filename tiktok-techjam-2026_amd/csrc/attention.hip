@@ -271,7 +271,10 @@ __global__ __launch_bounds__(256 * KS) void flash_fwd_kernel(
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[j][kb][r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        {  // lanes l and l^32 hold the two halves of a query's keys
+          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+          mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
         const float m_new = fmaxf(m_run[j], mx);
         const float m_use = m_new == -INFINITY ? 0.f : m_new * scale_log2;
         const float alpha = __builtin_amdgcn_exp2f(m_run[j] * scale_log2 - m_use);
@@ -358,7 +361,8 @@ __global__ __launch_bounds__(256 * KS) void flash_fwd_kernel(
 #pragma unroll
   for (int j = 0; j < NQ; ++j) {
     const int q = wq0 + j * 32 + l32;
-    const float l = l_run[j] + __shfl_xor(l_run[j], 32, 64);
+    const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run[j]), __float_as_uint(l_run[j]), false, false);
+    const float l = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
     const float inv = l > 0.f ? 1.0f / l : 0.f;
     if (q >= Sb) continue;
     T* orow = out + (row0 + q) * ld_out + (int64_t)h * hd;
