@@ -24,7 +24,10 @@
  *                         (kernel :34-125), and the SDPA masked fallback,
  *                         tjkernels/engine.py:184-203
  *   tjk_ffn            <- fused_ffn, tjkernels/kernels/__init__.py:80-89
- *                         (Triton kernel tjkernels/kernels/ffn.py:21-69)
+ *                         (Triton kernel tjkernels/kernels/ffn.py:21-69,
+ *                         shape gate ffn.py:103-110 -> tjk_ffn_supported)
+ *   tjk_flash_fwd_sched <- the grid of (query block, b*h) programs of
+ *                         tjkernels/kernels/attention.py:199-217
  */
 #ifndef TJK_H
 #define TJK_H
@@ -36,7 +39,7 @@
 extern "C" {
 #endif
 
-#define TJK_ABI_VERSION 3
+#define TJK_ABI_VERSION 4
 
 /* dtypes */
 #define TJK_F32 0
@@ -72,9 +75,13 @@ const char* tjk_last_error_string(void);
  * res_out must not alias res when row_index is given.
  * res_dtype, delta_dtype, out_dtype in {TJK_F32, TJK_F16, TJK_BF16};
  * delta may be NULL.  Requires n % 4 == 0, n <= 8192, 8-byte aligned rows.
+ * delta_splits > 1 (n <= 1024): delta is the sum of delta_splits slices
+ * delta_split_stride elements apart (the split partials of tjk_ffn), added
+ * in slice order -- x = res + (((d_0 + d_1) + d_2) + ...).
  */
 int tjk_add_layernorm(const void* res, int res_dtype, int64_t ld_res,
                       const void* delta, int delta_dtype, int64_t ld_delta,
+                      int delta_splits, int64_t delta_split_stride,
                       float* res_out, int64_t ld_res_out,
                       void* out, int out_dtype, int64_t ld_out,
                       const float* gamma, const float* beta,
@@ -95,28 +102,12 @@ int tjk_gemm_bias(const void* a, int64_t lda, const void* w, int64_t ldw,
                   int64_t m, int64_t n, int64_t k,
                   int dtype, int epilogue, int plan_id, void* stream);
 
-/*
- * tjk_gemm_bias with a caller-provided workspace, which the stream-K plans
- * need (tjk_gemm_bias returns TJK_EINVAL for them).  workspace_bytes >=
- * tjk_gemm_workspace_bytes(dtype, plan_id), 256-byte aligned, zero-filled
- * before its first use; every completed call leaves its flag area zero
- * again.  Calls sharing one workspace must not run concurrently (one
- * stream, or ordered streams).  Stream-K results are deterministic for a
- * given device (the K partition depends on the shape and the CU count).
- * Replaces the same torch.addmm call sites as tjk_gemm_bias.
- */
-int tjk_gemm_bias_ws(const void* a, int64_t lda, const void* w, int64_t ldw,
-                     const void* bias, void* c, int64_t ldc,
-                     int64_t m, int64_t n, int64_t k,
-                     int dtype, int epilogue, int plan_id,
-                     void* workspace, size_t workspace_bytes, void* stream);
-
-/* Workspace bytes plan_id needs on the current device (0: none). */
-size_t tjk_gemm_workspace_bytes(int dtype, int plan_id);
-
-/* Number of GEMM tile plans for `dtype`, and the tile of plan `id`. */
+/* Number of GEMM tile plans for `dtype`, and the tile of plan `id`:
+ * block_m x block_n outputs, `waves` waves, the K range split over
+ * k_groups wave groups whose sums are added at the end.  Plans with the same
+ * k_groups add up K in the same order: they give identical results. */
 int tjk_gemm_plan_count(int dtype);
-int tjk_gemm_plan_info(int dtype, int id, int* block_m, int* block_n, int* waves);
+int tjk_gemm_plan_info(int dtype, int id, int* block_m, int* block_n, int* waves, int* k_groups);
 
 /*
  * Flash-attention forward over a packed QKV buffer laid out [B, S, 3, H, hd]
@@ -162,36 +153,51 @@ int tjk_flash_plan_count(int dtype);
  *     and writes the output rows.  The first half must precede the second in
  *     the list (workgroups are dispatched in list order).
  * Every (query block, key tile) pair of every sequence must be covered
- * exactly once.  partials holds tjk_flash_partial_bytes(head_dim, n_slots)
- * bytes: the n_slots partials, an error word (timed-out waits) and one flag
- * per slot, zero-filled before the first call; every completed call leaves
- * the flags zero.  Calls sharing a partials buffer must not overlap.
- * max_seqlen bounds every sequence length.  Replaces the reference's grid of
- * (query block, b*h) programs, attention.py:199-217.
+ * exactly once.  partials holds partials_bytes >=
+ * tjk_flash_partial_bytes(head_dim, n_slots) bytes: the n_slots partials,
+ * an error word and one flag per slot, zero-filled before the first call
+ * (NULL is accepted with n_slots == 0, and then nothing is counted);
+ * every completed call leaves the flags zero.  The error word counts
+ * (never resets) items the kernel could not run as listed: a (b, h) outside
+ * the launch (dropped), a slot outside [0, n_slots) (rows written as NaN),
+ * and a second half whose wait for its first half timed out (rows written
+ * as NaN; the late first half then clears its flag).  Calls sharing a
+ * partials buffer must not overlap.  max_seqlen bounds every sequence
+ * length.
  */
 int tjk_flash_fwd_sched(const void* qkv, int64_t stride_s, int64_t stride_c, int64_t stride_h,
                         void* out, int64_t ld_out, int batch, int max_seqlen, int heads,
                         int head_dim, float scale, int causal, const int32_t* cu_seqlens,
-                        const int32_t* work, int n_work, float* partials, int n_slots,
-                        int dtype, void* stream);
+                        const int32_t* work, int n_work, float* partials, size_t partials_bytes,
+                        int n_slots, int dtype, void* stream);
 size_t tjk_flash_partial_bytes(int head_dim, int n_slots);
 /* Workgroups of the scheduled kernel resident per CU (> 0), or a negative /
  * hipError_t status. */
 int tjk_flash_sched_occupancy(int head_dim, int dtype);
 
 /*
- * Feed-forward block: out = gelu_erf(h W1^T + b1) W2^T + b2 with W1 [f, d],
- * W2 [d, f] (nn.Linear layout).  The [tokens, f] intermediate is rounded to
- * `dtype` (as the reference does) and lives in `workspace`
- * (tjk_ffn_workspace_bytes() bytes).  With epilogue TJK_EPI_BIAS_RESIDUAL
- * `out` is the fp32 residual and the result is added into it.
- * plan_ids = (plan of the first GEMM) | (plan of the second GEMM) << 8.
+ * Feed-forward block in one launch, the [rows, f] GELU intermediate kept in
+ * LDS.  For the f-slices s = 0 .. splits-1 (f / splits columns each):
+ *   P[s] = gelu_erf(A W1[s]^T + b1[s]) W2[:, s]^T  (+ b2 for s = 0)
+ * with W1 [f, d], W2 [d, f] (nn.Linear layout), the intermediate rounded to
+ * `dtype` as the reference rounds its hidden activation, and
+ *   A = a (`dtype`, a_dtype == dtype)                 if ln_gamma == NULL
+ *   A = LayerNorm(a) * ln_gamma + ln_beta             otherwise, a the fp32
+ *       residual (a_dtype == TJK_F32), biased variance, eps ln_eps; equal
+ *       to tjk_add_layernorm's output on the same rows.
+ * P[s] is stored as fp32 rows of `out` (leading dimension ld_out) at
+ * out + s * split_stride; tjk_add_layernorm(delta_splits = splits) then adds
+ * their sum to the residual.  With splits == 1 and accumulate != 0 the
+ * result is added into `out` (the fp32 residual) instead.
+ * Supported: f / splits == 128; d in {128, 256, 512} (fp32: 128, 256); see
+ * tjk_ffn_supported.  b1 / b2 may be NULL.
  */
-int tjk_ffn(const void* h, int64_t ldh, const void* w1, const void* b1,
-            const void* w2, const void* b2, void* out, int64_t ld_out,
-            void* workspace, int64_t tokens, int64_t d, int64_t f,
-            int dtype, int epilogue, int plan_ids, void* stream);
-size_t tjk_ffn_workspace_bytes(int64_t tokens, int64_t f, int dtype);
+int tjk_ffn(const void* a, int a_dtype, int64_t lda, const float* ln_gamma, const float* ln_beta,
+            float ln_eps, const void* w1, const void* b1, const void* w2, const void* b2, float* out,
+            int64_t ld_out, int64_t split_stride, int splits, int accumulate, int64_t rows, int64_t d,
+            int64_t f, int dtype, void* stream);
+/* 1 if tjk_ffn takes (d, f, splits, dtype), else 0. */
+int tjk_ffn_supported(int64_t d, int64_t f, int splits, int dtype);
 
 #ifdef __cplusplus
 }

@@ -115,9 +115,9 @@ def _gemm_case(device, m, n, k, dt, epi, plan, seed=0):
 
 # Plans of the staged kernel take any K % 8 == 0; direct-to-LDS plans need
 # K % 64 == 0 (bf16/fp16) and reject other K with TJK_EUNSUPPORTED.
-# Plans 26-28 use 4-, 8- and 6-slot rings with the spread DMA schedule;
-# 29-31 split K between 2 or 4 wave groups of one workgroup.
-STAGED16, DTL16, DTL16_K32 = range(0, 6), list(range(6, 18)) + [26, 27, 28, 29, 30, 31], ()
+# Plans 18-20 use 4-, 8- and 6-slot rings with the spread DMA schedule;
+# 16, 17 and 21-23 split K between 2 or 4 wave groups of one workgroup.
+STAGED16, DTL16, DTL16_K32 = range(0, 6), list(range(6, 24)), ()
 STAGED32, DTL32 = range(0, 2), range(2, 5)
 
 
@@ -137,105 +137,41 @@ def test_gemm_plans(device, plan, dt):
             _gemm_case(device, 64, 64, 40, dt, ops.EPI_BIAS, plan)
 
 
-@pytest.mark.parametrize("plan", [15, 26, 27, 28, 29, 30, 31])
+@pytest.mark.parametrize("plan", [15, 18, 19, 20, 21, 22, 23])
 @pytest.mark.parametrize("epi", [ops.EPI_BIAS_GELU, ops.EPI_BIAS_RESIDUAL])
 def test_gemm_deep_ring_and_prefetch_plans(device, plan, epi):
-    # Deep rings (26-28): K from one tile (fewer tiles than ring slots) to a
-    # long pipeline.  Plans 15 and 26 read the residual before the main loop.
-    # K-split plans (29-31): fewer K tiles than groups, and counts that do
+    # Deep rings (18-20): K from one tile (fewer tiles than ring slots) to a
+    # long pipeline.  Plans 15 and 18 read the residual before the main loop.
+    # K-split plans (21-23): fewer K tiles than groups, and counts that do
     # not divide evenly between the groups.
     for m, n, k in ((200, 256, 64), (300, 384, 192), (5430, 1024, 4096), (1000, 516, 1024), (128, 512, 2048)):
         _gemm_case(device, m, n, k, torch.bfloat16, epi, plan)
 
 
-# Stream-K plans: persistent grid, K-split partial tiles folded by the
-# tile's finisher in a fixed order.
-SK16 = range(18, 24)
-
-
-@pytest.mark.parametrize("plan", list(SK16))
-@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
-def test_gemm_stream_k_plans(device, plan, dt):
-    _gemm_case(device, 513, 1028, 1088, dt, ops.EPI_BIAS, plan)   # ragged M and N
-    _gemm_case(device, 64, 32, 64, dt, ops.EPI_BIAS, plan)        # one tile, one K tile
-    _gemm_case(device, 700, 256, 4096, dt, ops.EPI_BIAS, plan)    # few tiles, each split many ways
-    with pytest.raises(ops.TjkError, match="needs k"):
-        _gemm_case(device, 300, 200, 96, dt, ops.EPI_BIAS, plan)
-
-
-@pytest.mark.parametrize("plan", [18, 20, 22])
-@pytest.mark.parametrize("epi", [ops.EPI_BIAS_GELU, ops.EPI_BIAS_RESIDUAL])
-def test_gemm_stream_k_epilogues(device, plan, epi):
-    # the residual is added exactly once per element by the tile's finisher
-    _gemm_case(device, 5430, 1024, 1024, torch.bfloat16, epi, plan)
-    _gemm_case(device, 1000, 516, 2048, torch.bfloat16, epi, plan)
-
-
-@pytest.mark.parametrize("plan", [18, 22])
-def test_gemm_stream_k_with_data_parallel_rounds(device, plan):
-    # more than two full rounds of tiles: whole tiles first, stream-K after
-    _gemm_case(device, 5000, 7000, 128, torch.bfloat16, ops.EPI_BIAS, plan)
-
-
-def test_gemm_stream_k_deterministic_and_flags_cleared(device):
-    g = _gen(5)
-    a = torch.randn(5430, 4096, generator=g).bfloat16().to(device)
-    w = (torch.randn(1024, 4096, generator=g) / 64).bfloat16().to(device)
-    b = torch.randn(1024, generator=g).bfloat16().to(device)
-    r0 = torch.randn(5430, 1024, generator=g).to(device)
-    outs = []
-    for _ in range(3):
-        out = r0.clone()
-        ops.gemm(a, w, b, out, ops.EPI_BIAS_RESIDUAL, 18)
-        outs.append(out)
-    torch.cuda.synchronize()
-    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
-    header = ops.gemm_workspace(device)[:32768].view(torch.int32).cpu()
-    assert int(header.abs().sum()) == 0  # every flag cleared, no timed-out wait
-
-
-# Split-K residual plans: two workgroups per tile, one per half of K, the
-# second adding its half after the first (residual epilogue only).
-K2_16 = (24, 25)
-
-
-@pytest.mark.parametrize("plan", K2_16)
-def test_gemm_split_k_residual(device, plan):
-    for m, n, k in ((5430, 1024, 4096), (513, 1028, 1088), (64, 32, 64), (1000, 516, 128)):
-        _gemm_case(device, m, n, k, torch.bfloat16, ops.EPI_BIAS_RESIDUAL, plan)
-    _gemm_case(device, 700, 256, 2048, torch.float16, ops.EPI_BIAS_RESIDUAL, plan)
-    with pytest.raises(ops.TjkError, match="residual"):
-        _gemm_case(device, 256, 256, 256, torch.bfloat16, ops.EPI_BIAS, plan)
-
-
-def test_gemm_split_k_deterministic_and_flags_cleared(device):
-    g = _gen(6)
-    a = torch.randn(5430, 1024, generator=g).bfloat16().to(device)
-    w = (torch.randn(1024, 1024, generator=g) / 32).bfloat16().to(device)
-    b = torch.randn(1024, generator=g).bfloat16().to(device)
-    r0 = torch.randn(5430, 1024, generator=g).to(device)
-    outs = []
-    for plan in (24, 24, 24, 25, 25):
-        out = r0.clone()
-        ops.gemm(a, w, b, out, ops.EPI_BIAS_RESIDUAL, plan)
-        outs.append(out)
-    torch.cuda.synchronize()
-    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2]) and torch.equal(outs[3], outs[4])
-    header = ops.gemm_workspace(device)[:32768].view(torch.int32).cpu()
-    assert int(header.abs().sum()) == 0  # every flag cleared, no timed-out wait
-
-
-def test_gemm_stream_k_requires_workspace(device):
-    from tjkernels import _lib
-    lib = _lib.load()
-    a = torch.zeros(64, 64, dtype=torch.bfloat16, device=device)
-    out = torch.zeros(64, 64, dtype=torch.bfloat16, device=device)
-    st = lib.tjk_gemm_bias(a.data_ptr(), 64, a.data_ptr(), 64, None, out.data_ptr(), 64, 64, 64, 64,
-                           _lib.BF16, ops.EPI_BIAS, 18, None)
-    assert st < 0 and b"workspace" in lib.tjk_last_error_string()
-    small = torch.zeros(1024, dtype=torch.uint8, device=device)
-    with pytest.raises(ops.TjkError, match="workspace"):
-        ops.gemm(a, a, None, out, ops.EPI_BIAS, 18, workspace=small)
+@pytest.mark.parametrize("epi", [ops.EPI_BIAS, ops.EPI_BIAS_GELU, ops.EPI_BIAS_RESIDUAL])
+def test_gemm_k_order_classes_are_bitwise_identical(device, epi):
+    """Tiles of one K-summation class (tjkernels.tiles) produce the same bits,
+    so the run-time tile timing cannot change results; the two classes
+    differ only in the last bits."""
+    from tjkernels import tiles
+    g = _gen(11)
+    for m, n, k in ((5430, 1024, 4096), (128, 512, 2048), (700, 256, 1024)):
+        a = torch.randn(m, k, generator=g).bfloat16().to(device)
+        w = (torch.randn(n, k, generator=g) / math.sqrt(k)).bfloat16().to(device)
+        b = torch.randn(n, generator=g).bfloat16().to(device)
+        r0 = torch.randn(m, n, generator=g).to(device)
+        for cls, plans in tiles.CLASS_TILES_16.items():
+            outs = []
+            for plan in plans:
+                if epi == ops.EPI_BIAS_RESIDUAL:
+                    out = r0.clone()
+                else:
+                    out = torch.empty(m, n, dtype=torch.bfloat16, device=device)
+                ops.gemm(a, w, b, out, epi, plan)
+                outs.append(out)
+            torch.cuda.synchronize()
+            for plan, out in zip(plans[1:], outs[1:]):
+                assert torch.equal(out, outs[0]), f"class {cls}: plan {plan} differs from plan {plans[0]}"
 
 
 @pytest.mark.parametrize("plan", list(STAGED32) + list(DTL32))
@@ -582,3 +518,178 @@ def test_flash_scheduled(device, dt, hd, causal):
             ops.flash_attention_sched(qkv.to(device), again, cu_d, max(lengths), sched, causal=causal)
             torch.cuda.synchronize()
             assert torch.equal(again.cpu(), got), "split merge is not deterministic"
+
+
+def test_flash_scheduled_reports_items_it_cannot_run(device):
+    """Failure handling, forced from the host with lists validate_work would
+    reject (written straight to the device): an item for a (b, h) outside
+    the launch is dropped, an item with a slot outside [0, n_slots) writes
+    NaN rows, and a second half whose first half never runs waits out its
+    bounded poll, writes NaN rows and claims the flag -- each counted once
+    in the error word, every kernel exiting normally."""
+    from tjkernels import schedule as sched_mod
+    lengths, h, hd, dt = [128, 128], 2, 64, torch.bfloat16
+    t = sum(lengths)
+    qkv = torch.randn(t, 3, h, hd, generator=_gen(1)).to(dt).to(device)
+    cu = torch.tensor([0, 128, 256], dtype=torch.int32, device=device)
+    sched = sched_mod.build_schedule(lengths, h, hd, True, dt, device)
+    assert sched.n_slots == 0 and sched_mod.error_count(sched) == 0
+    work = sched.work.clone()
+    work[0, 0] = 99               # (b, h) outside the launch: dropped
+    work[1, 3] = 5                # slot 5 with no slots: NaN rows
+    bad = sched_mod.AttentionSchedule(work=work, n_slots=0, partials=sched.partials, max_item=sched.max_item,
+                                      total=sched.total, error_index=sched.error_index)
+    out = torch.zeros(t, h * hd, dtype=dt, device=device)
+    ops.flash_attention_sched(qkv, out, cu, 128, bad, causal=True)
+    torch.cuda.synchronize()
+    assert sched_mod.error_count(bad) == 2
+    bh1 = int(work[1, 0])
+    b1, h1 = bh1 // h, bh1 % h
+    rows = out[128 * b1:128 * (b1 + 1), h1 * hd:(h1 + 1) * hd]
+    assert torch.isnan(rows.float()).all()
+    # a lone second half (slot -2 of one slot): its wait times out
+    lone = sched_mod.build_schedule(lengths, h, hd, True, dt, device, slots=100000, min_split=1,
+                                    split_factor=1.0)
+    assert lone.n_slots > 0
+    w = lone.work.cpu()
+    second = int((w[:, 3] == -2).nonzero()[0])
+    only = w[second:second + 1].to(device)
+    solo = sched_mod.AttentionSchedule(work=only, n_slots=lone.n_slots, partials=lone.partials, max_item=1,
+                                       total=1, error_index=lone.error_index)
+    out.zero_()
+    ops.flash_attention_sched(qkv, out, cu, 128, solo, causal=True)
+    torch.cuda.synchronize()
+    assert sched_mod.error_count(solo) == 1
+    flag = lone.partials.view(torch.int32)[lone.error_index + 1].item()
+    assert flag == -1, "the timed-out second half claims the flag"
+    bh2 = int(w[second, 0])
+    b2, h2 = bh2 // h, bh2 % h
+    assert torch.isnan(out[128 * b2:128 * (b2 + 1), h2 * hd:(h2 + 1) * hd].float()).all()
+    # the late first half finds the claim and resets the flag for the next launch
+    first = int((w[:, 3] == 0).nonzero()[0])
+    late = sched_mod.AttentionSchedule(work=w[first:first + 1].to(device), n_slots=lone.n_slots,
+                                       partials=lone.partials, max_item=1, total=1, error_index=lone.error_index)
+    ops.flash_attention_sched(qkv, out, cu, 128, late, causal=True)
+    torch.cuda.synchronize()
+    assert lone.partials.view(torch.int32)[lone.error_index + 1].item() == 0
+
+
+# ------------------------------------------------------------ fused FFN
+
+def _ffn_reference(a_t, w1, b1, w2, b2, dtype):
+    """fp64 FFN with the kernel's roundings: A and the GELU intermediate in
+    the compute dtype (as the reference rounds its hidden activation)."""
+    hdn = a_t.double() @ w1.double().t() + b1.double()
+    hdn = (0.5 * hdn * (1 + torch.erf(hdn / math.sqrt(2)))).to(dtype).double()
+    return hdn @ w2.double().t() + b2.double()
+
+
+FFN_TOL = {torch.float32: (2e-5, 2e-5), torch.float16: (2e-3, 2e-3), torch.bfloat16: (1e-2, 1e-2)}
+
+
+@pytest.mark.parametrize("dt,d,f", [(torch.float16, 512, 2048), (torch.bfloat16, 512, 2048),
+                                     (torch.bfloat16, 256, 1024), (torch.float16, 128, 256),
+                                     (torch.float32, 128, 512), (torch.float32, 256, 384)])
+@pytest.mark.parametrize("rows", [1, 31, 96, 200])
+def test_ffn_fused_against_fp64(device, dt, d, f, rows):
+    """P = gelu_erf(A W1^T + b1) W2^T + b2 from h (no LayerNorm) and from
+    the fp32 residual (LayerNorm in the kernel), split over f / 128 slices
+    and summed, against fp64; rows past the input are never written."""
+    g = _gen(d * 3 + f + rows)
+    splits = f // 128
+    res = torch.randn(rows, d, generator=g) * 2 + 0.3
+    gamma, beta = torch.randn(d, generator=g), torch.randn(d, generator=g) * 0.1
+    w1 = (torch.randn(f, d, generator=g) / math.sqrt(d)).to(dt)
+    b1 = (torch.randn(f, generator=g) * 0.1).to(dt)
+    w2 = (torch.randn(d, f, generator=g) / math.sqrt(f)).to(dt)
+    b2 = (torch.randn(d, generator=g) * 0.1).to(dt)
+    dev = [t.to(device) for t in (res, gamma, beta, w1, b1, w2, b2)]
+    res_d, gamma_d, beta_d, w1_d, b1_d, w2_d, b2_d = dev
+    h = torch.empty(rows, d, dtype=dt, device=device)
+    ops.add_layernorm(res_d, None, gamma_d, beta_d, 1e-5, h)
+    rtol, atol = FFN_TOL[dt]
+    outs = []
+    for use_ln in (False, True):
+        parts = torch.full((splits, rows + 3, d), float("nan"), device=device)
+        ops.ffn(res_d if use_ln else h, w1_d, b1_d, w2_d, b2_d, parts[:, :rows], splits=splits,
+                ln=(gamma_d, beta_d, 1e-5) if use_ln else None)
+        torch.cuda.synchronize()
+        assert torch.isnan(parts[:, rows:]).all(), "rows past the input were written"
+        outs.append(parts[:, :rows].cpu())
+    # the in-kernel LayerNorm equals the add+LayerNorm kernel bit for bit
+    assert torch.equal(outs[0], outs[1])
+    ref = _ffn_reference(h.cpu(), w1, b1, w2, b2, dt)
+    _close(outs[0].double().sum(0), ref, rtol, atol)
+    # a single split adds straight into the residual
+    if ops.ffn_supported(d, 128, 1, dt):
+        r0 = torch.randn(rows, d, generator=g)
+        acc = r0.to(device)
+        ops.ffn(h, w1_d[:128], b1_d[:128], w2_d[:, :128].contiguous(), b2_d, acc, splits=1, accumulate=True)
+        torch.cuda.synchronize()
+        ref1 = _ffn_reference(h.cpu(), w1[:128], b1[:128], w2[:, :128], b2, dt) + r0.double()
+        _close(acc, ref1, rtol, atol)
+
+
+def test_ffn_fused_closed_forms(device):
+    """W1 = 0: the intermediate is gelu(b1), so P = gelu(b1) W2^T + b2 for
+    every row; W2 = 0: P = b2 (split 0) and 0 (other splits)."""
+    d, f, rows, dt = 512, 2048, 40, torch.float16
+    g = _gen(3)
+    h = torch.randn(rows, d, generator=g).to(dt).to(device)
+    b1 = torch.randn(f, generator=g).to(dt)
+    w2 = (torch.randn(d, f, generator=g) / 45).to(dt)
+    b2 = torch.randn(d, generator=g).to(dt)
+    parts = torch.empty(16, rows, d, device=device)
+    ops.ffn(h, torch.zeros(f, d, dtype=dt, device=device), b1.to(device), w2.to(device), b2.to(device), parts,
+            splits=16)
+    hdn = (0.5 * b1.double() * (1 + torch.erf(b1.double() / math.sqrt(2)))).to(dt).double()
+    want = (hdn @ w2.double().t() + b2.double()).expand(rows, d)
+    _close(parts.sum(0), want, 2e-3, 2e-3)
+    ops.ffn(h, torch.randn(f, d, dtype=dt, device=device), b1.to(device), torch.zeros(d, f, dtype=dt, device=device),
+            b2.to(device), parts, splits=16)
+    torch.cuda.synchronize()
+    assert torch.equal(parts[0].cpu(), b2.float().expand(rows, d))
+    assert (parts[1:] == 0).all()
+
+
+def test_ffn_rejects_unsupported_shapes(device):
+    h = torch.zeros(8, 1024, dtype=torch.bfloat16, device=device)
+    w1 = torch.zeros(4096, 1024, dtype=torch.bfloat16, device=device)
+    w2 = torch.zeros(1024, 4096, dtype=torch.bfloat16, device=device)
+    with pytest.raises(ops.TjkError, match="unsupported"):
+        ops.ffn(h, w1, None, w2, None, torch.zeros(32, 8, 1024, device=device), splits=32)
+
+
+@pytest.mark.parametrize("n,splits", [(128, 4), (512, 16), (512, 3), (1024, 8)])
+def test_add_layernorm_split_delta(device, n, splits):
+    """A [splits, rows, n] fp32 delta is summed slice by slice, in order,
+    then added to the residual: res_out equals that fp32 sum exactly, and
+    the normalised output matches fp64; gather and scatter rows read the
+    delta rows of their source row."""
+    rows = 45
+    g = _gen(n + splits)
+    res = torch.randn(rows, n, generator=g)
+    parts = torch.randn(splits, rows + 5, n, generator=g)[:, :rows]
+    gamma, beta = torch.randn(n, generator=g), torch.randn(n, generator=g)
+    acc = parts[0].clone()
+    for s_ in range(1, splits):
+        acc = acc + parts[s_]
+    want_res = res + acc
+    out = torch.empty(rows, n, dtype=torch.bfloat16, device=device)
+    res_d = res.to(device)
+    ops.add_layernorm(res_d, parts.to(device), gamma.to(device), beta.to(device), 1e-5, out, res_out=res_d)
+    torch.cuda.synchronize()
+    assert torch.equal(res_d.cpu(), want_res)
+    ref = oracle.layer_norm(want_res.double(), gamma.double(), beta.double(), 1e-5)
+    _close(out, ref, OUT_RTOL[torch.bfloat16], 4e-3)
+    # scatter: output row r reads source row idx[r] (and its delta rows)
+    idx = torch.tensor([3, -1, 0, 44, -1, 7], dtype=torch.int32)
+    out2 = torch.empty(idx.numel(), n, dtype=torch.float32, device=device)
+    ops.add_layernorm(res.to(device), parts.to(device), gamma.to(device), beta.to(device), 1e-5, out2,
+                      row_index=idx.to(device))
+    torch.cuda.synchronize()
+    for r, src in enumerate(idx.tolist()):
+        if src < 0:
+            assert (out2[r] == 0).all()
+        else:
+            _close(out2[r:r + 1], ref[src:src + 1], 2e-5, 1e-5)

@@ -77,9 +77,22 @@ def test_workload_parity(device, name):
     _run_workload(device, name, seeds=(1, 2))
 
 
-def test_c5_parity_first_sequence(device):
-    # sequences never interact, so the oracle checks the first one only
-    _run_workload(device, "C5", batch_subset=slice(0, 1))
+def test_c5_parity_both_sequences(device):
+    # the oracle costs seconds per C5 sequence; both are checked (the second
+    # starts at packed row 4096, so its offsets are exercised too)
+    _run_workload(device, "C5")
+
+
+@pytest.mark.parametrize("name", ["C1", "C2"])
+@pytest.mark.parametrize("ffn", ["gemm", "fused"])
+def test_ffn_kinds_hold_the_budget(device, name, ffn):
+    """Both FFN implementations -- two GEMM launches with the intermediate in
+    HBM, and the single launch with it in LDS and LayerNorm 2 inside -- hold
+    the workload's budget (C1: fp32 plan, 1e-4)."""
+    w = WORKLOADS[name]
+    cdt = torch.float32 if w.dtype == torch.float32 else w.dtype
+    _run_workload(device, name, seeds=(1, 3),
+                  plan=Plan(compute_dtype=cdt, ffn=ffn, cuda_graph=name == "C2", label=ffn))
 
 
 def test_c5_fp32_escalation_plan(device):
@@ -91,8 +104,8 @@ def test_c5_fp32_escalation_plan(device):
     x, mask, _ = make_inputs(w, seed=1)
     with torch.inference_mode():
         got = model(x.to(device), mask.to(device)).cpu()
-    ref = oracle.forward(sd, x[:1], mask[:1], w.heads, w.causal, torch.float32)
-    _check(got[:1], ref, mask[:1], torch.float32)
+    ref = oracle.forward(sd, x, mask, w.heads, w.causal, torch.float32)
+    _check(got, ref, mask, torch.float32)
 
 
 def test_c1_golden_fixture(device):
@@ -175,11 +188,12 @@ def test_general_mask_and_lengths_input(device):
     _check(got_l, oracle.forward(sd, x2, pmask, 4, True, torch.float32), pmask, torch.float32)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_graph_equals_eager(device, dtype):
+@pytest.mark.parametrize("dtype,ffn", [(torch.float32, "gemm"), (torch.bfloat16, "gemm"),
+                                       (torch.bfloat16, "fused"), (torch.float32, "fused")])
+def test_graph_equals_eager(device, dtype, ffn):
     """hipGraph replay == eager, bitwise, on fresh inputs, with eager work and
     synchronisations between replays (bench/test_correctness.py:94-125)."""
-    cfg = TransformerConfig(4, 64, 128, 4, 128, 2, True)
+    cfg = TransformerConfig(4, 64, 128, 4, 256, 2, True)
     torch.manual_seed(1)
     eager = _module(cfg, UserOptimizedTransformer(cfg).state_dict(), dtype, device)
     graphed = _module(cfg, eager.state_dict(), dtype, device)
@@ -193,13 +207,13 @@ def test_graph_equals_eager(device, dtype):
         m[:, 0] = True
         x = torch.randn(cfg.batch_size, cfg.seq_len, cfg.d_model, generator=g).masked_fill(~m[..., None], 0)
         cases.append((x.to(dtype), m))
-    plans_mod.set_override(Plan(compute_dtype=dtype, cuda_graph=False, label="eager"))
+    plans_mod.set_override(Plan(compute_dtype=dtype, cuda_graph=False, ffn=ffn, label="eager"))
     try:
         with torch.inference_mode():
             expected = [eager(x.to(device), m.to(device)).cpu() for x, m in cases]
     finally:
         plans_mod.set_override(None)
-    plans_mod.set_override(Plan(compute_dtype=dtype, cuda_graph=True, label="graphed"))
+    plans_mod.set_override(Plan(compute_dtype=dtype, cuda_graph=True, ffn=ffn, label="graphed"))
     try:
         with torch.inference_mode():
             for rep in range(2):
@@ -288,3 +302,45 @@ def test_long_sequence_prefix_property(device):
     full = torch.ones(1, p, dtype=torch.bool)
     ref = oracle.forward(sd, x[:, :p].float(), full, cfg.num_heads, True, torch.float32)
     _check(short_out, ref, full, torch.bfloat16)
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_mask_updated_in_place_between_forwards(device, graph):
+    """A mask buffer reused with new contents (written in place) is
+    re-classified: each forward equals the forward of a fresh mask tensor
+    with the same contents -- through the eager path and the hipGraph path
+    (whose key holds the prefix lengths) -- for prefix masks of new
+    lengths, a non-prefix mask and integer lengths updated in place."""
+    cfg = TransformerConfig(3, 64, 128, 4, 256, 2, True)
+    torch.manual_seed(4)
+    sd = {k: v.float() for k, v in UserOptimizedTransformer(cfg).state_dict().items()}
+    g = torch.Generator()
+    g.manual_seed(21)
+    x = torch.randn(3, 64, 128, generator=g).to(device)
+    plans_mod.set_override(Plan(compute_dtype=torch.float32, cuda_graph=graph, label="inplace"))
+    try:
+        reused = _module(cfg, sd, torch.float32, device)
+        fresh = _module(cfg, sd, torch.float32, device)
+        buf = torch.ones(3, 64, dtype=torch.bool, device=device)
+        lens_buf = torch.tensor([64, 64, 64], dtype=torch.int32, device=device)
+        contents = []
+        for lens in ([64, 10, 33], [5, 64, 20], [64, 64, 64], [40, 1, 64]):
+            contents.append(torch.arange(64)[None, :] < torch.tensor(lens)[:, None])
+        general = contents[0].clone()
+        general[0, 5] = False
+        contents.append(general)
+        with torch.inference_mode():
+            for want_mask in contents:
+                buf.copy_(want_mask.to(device))  # in place: same tensor, new contents
+                got = reused(x, buf)
+                ref = fresh(x, want_mask.to(device).clone())
+                torch.cuda.synchronize()
+                assert torch.equal(got.cpu(), ref.cpu())
+                assert (got.cpu()[~want_mask] == 0).all()
+            for lens in ([64, 10, 33], [5, 64, 20]):
+                lens_buf.copy_(torch.tensor(lens, dtype=torch.int32))
+                got = reused(x, lens_buf)
+                ref = fresh(x, (torch.arange(64)[None, :] < torch.tensor(lens)[:, None]).to(device))
+                assert torch.equal(got.cpu(), ref.cpu())
+    finally:
+        plans_mod.set_override(None)

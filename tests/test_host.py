@@ -36,9 +36,26 @@ def test_abi_rejects_bad_arguments_without_launching():
     assert b"null" in lib.tjk_last_error_string()
     assert lib.tjk_flash_fwd(None, 0, 0, 0, 0, None, 0, 1, 4, 1, 12, 0.5, 1, None, None,
                              None, _lib.BF16, -1, None) < 0
-    assert lib.tjk_add_layernorm(None, 0, 8, None, 0, 0, None, 0, None, 0, 8, None, None,
+    assert lib.tjk_add_layernorm(None, 0, 8, None, 0, 0, 1, 0, None, 0, None, 0, 8, None, None,
                                  2, 6, 1e-5, None, None, None) < 0
     assert b"null pointer" in lib.tjk_last_error_string()
+    # split deltas need a stride that keeps the slices apart
+    fake = 1 << 20  # never dereferenced: the call is rejected first
+    assert lib.tjk_add_layernorm(fake, 0, 8, fake, 0, 8, 4, 8, None, 0, fake, 0, 8, fake, fake,
+                                 2, 8, 1e-5, None, None, None) == _lib.EINVAL
+    # the single-launch FFN's shape gate (f / splits must be 128; d in {128, 256, 512})
+    assert lib.tjk_ffn_supported(512, 2048, 16, _lib.F16) == 1
+    assert lib.tjk_ffn_supported(128, 512, 4, _lib.F32) == 1
+    assert lib.tjk_ffn_supported(512, 2048, 8, _lib.F16) == 0
+    assert lib.tjk_ffn_supported(512, 2048, 16, _lib.F32) == 0
+    assert lib.tjk_ffn_supported(1024, 4096, 32, _lib.BF16) == 0
+    assert lib.tjk_ffn(fake, _lib.F16, 768, None, None, 0.0, fake, None, fake, None, fake, 768, 0, 24, 0,
+                       16, 768, 3072, _lib.F16, None) == _lib.EUNSUPPORTED
+    assert lib.tjk_ffn(fake, _lib.F16, 512, None, None, 0.0, fake, None, fake, None, fake, 512, 0, 16, 1,
+                       16, 512, 2048, _lib.F16, None) == _lib.EINVAL  # accumulate with 16 splits
+    # scheduled attention: split slots without enough partials bytes
+    assert lib.tjk_flash_fwd_sched(fake, 192, 64, 64, fake, 64, 1, 128, 1, 64, 0.125, 1, fake, fake, 2,
+                                   fake, 16, 1, _lib.BF16, None) == _lib.EINVAL
     # empty work is a successful no-op
     assert lib.tjk_gemm_bias(None, 8, None, 8, None, None, 8, 0, 4, 8, _lib.BF16, 0, -1, None) == 0
     assert lib.tjk_gemm_plan_count(_lib.BF16) >= 4
@@ -86,16 +103,20 @@ def test_plan_json_round_trip_and_table(tmp_path, monkeypatch):
     key = plans_mod.shape_key(4, 2048, 1024, 16, 4096, 4, True, torch.bfloat16, "gfx950")
     assert key == "b4_s2048_d1024_h16_f4096_l4_causal_bfloat16@gfx950"
     f = tmp_path / "plans.json"
-    monkeypatch.setattr(plans_mod, "_PLAN_FILE", f)
-    monkeypatch.setattr(plans_mod, "_cache", None)
+    monkeypatch.setattr(plans_mod, "TUNED", plans_mod.PlanTable(f))
     plans_mod.save_plans({key: p})
     plans_mod.save_plans({"other@gfx950": Plan(label="y")})
-    table = plans_mod._load_tuned()
+    table = plans_mod.TUNED.plans()
     assert table[key] == p and table["other@gfx950"].label == "y"
     # an unreadable table is ignored, never fatal
     f.write_text("{not json")
-    monkeypatch.setattr(plans_mod, "_cache", None)
-    assert plans_mod._load_tuned() == {}
+    monkeypatch.setattr(plans_mod, "TUNED", plans_mod.PlanTable(f))
+    assert plans_mod.TUNED.plans() == {}
+    # tables written before the FFN knob named the two-launch FFN "hip"
+    assert Plan.from_json({"ffn": "hip", "compute_dtype": "float16"}).ffn == "gemm"
+    # the committed table parses, and every entry validates
+    for plan in plans_mod.PlanTable(plans_mod.TUNED_PATH).plans().values():
+        plan.validate()
 
 
 def test_plan_validation_rejects_fallback_backends():
@@ -103,7 +124,10 @@ def test_plan_validation_rejects_fallback_backends():
         Plan(attn="sdpa").validate()
     with pytest.raises(ValueError, match="float32 residual"):
         Plan(residual_dtype=torch.float16).validate()
+    with pytest.raises(ValueError, match="ffn="):
+        Plan(ffn="torch").validate()
     Plan().validate()
+    Plan(ffn="fused").validate()
 
 
 def test_override_and_env_knobs(monkeypatch):
@@ -115,12 +139,16 @@ def test_override_and_env_knobs(monkeypatch):
     finally:
         plans_mod.set_override(None)
     monkeypatch.setattr(plans_mod, "device_arch", lambda d: "gfx950")
-    monkeypatch.setattr(plans_mod, "_cache", {})
+    monkeypatch.setattr(plans_mod, "TUNED", plans_mod.PlanTable(Path("/nonexistent/plans.json")))
     dev = torch.device("cuda", 0)
     base = plans_mod.select_plan(4, 2048, 1024, 16, 4096, 4, True, torch.bfloat16, dev)
     assert not base.cuda_graph and base.compute_dtype == torch.bfloat16 and base.residual_epilogue
+    assert base.ffn == "gemm"  # d = 1024: the two-launch FFN
     small = plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev)
     assert small.cuda_graph  # launch-bound: replayed as a hipGraph
+    assert small.ffn == "fused"  # C2: one FFN launch per layer
+    tiny = plans_mod.select_plan(2, 64, 128, 4, 512, 2, True, torch.float32, dev)
+    assert tiny.ffn == "fused" and tiny.compute_dtype == torch.float32  # C1
     big = plans_mod.select_plan(64, 4096, 1024, 16, 4096, 4, True, torch.bfloat16, dev)
     assert not big.cuda_graph  # x above 64 MiB: no whole-forward graph
     monkeypatch.setenv("TJ_NO_GRAPH", "1")
@@ -130,8 +158,10 @@ def test_override_and_env_knobs(monkeypatch):
     assert p.pack_prefix and p.attn_plan == -1
     monkeypatch.setenv("TJ_NO_PACK", "1")
     monkeypatch.setenv("TJ_ATTN_PLAN", "1")
+    monkeypatch.setenv("TJ_FFN", "gemm")
     p = plans_mod.select_plan(4, 2048, 1024, 16, 4096, 4, True, torch.bfloat16, dev)
     assert not p.pack_prefix and p.attn_plan == 1
+    assert plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev).ffn == "gemm"
     assert plans_mod.Plan.from_json(p.to_json()) == p
 
 
@@ -177,8 +207,6 @@ def test_mask_classification():
     general = prefix.clone()
     general[0, 1] = False
     assert eng._mask_mode(general) == MASK_GENERAL
-    # memoised on identity, with the prefix lengths read once
-    assert eng._mask_modes.get(prefix) == (MASK_PREFIX, (3, 6))
     assert eng._mask_info(prefix) == (MASK_PREFIX, (3, 6))
     # packing is exact without causal attention too (padded keys are excluded
     # by restricting each packed sequence to its own rows)
@@ -299,3 +327,93 @@ def test_attention_schedule_covers_every_tile_once():
             a, b = work[first[0]], work[second[0]]
             assert first[0] < second[0], "a second half is issued before its first half"
             assert (a[1], a[2]) == (b[1], b[2]) and a[3] == 0 and a[4] == b[3]
+
+
+def test_mask_memo_follows_in_place_updates(monkeypatch):
+    """The classification is remembered per tensor and recomputed after an
+    in-place update (the version counter moved), so a reused mask buffer
+    never packs with stale lengths; an unchanged mask is classified once."""
+    from tjkernels import engine as engine_mod
+    cfg = TransformerConfig(2, 6, 32, 4, 64, 1, True)
+    eng = Engine(UserOptimizedTransformer(cfg))
+    calls = []
+    real = engine_mod.classify_mask
+    monkeypatch.setattr(engine_mod, "classify_mask", lambda m: calls.append(1) or real(m))
+    mask = torch.arange(6)[None, :] < torch.tensor([[3], [6]])
+    _, info = eng._decode_mask(torch.zeros(2, 6, 32), mask)
+    assert (info.mode, info.lengths) == (MASK_PREFIX, (3, 6))
+    eng._decode_mask(torch.zeros(2, 6, 32), mask)
+    assert len(calls) == 1  # memoised
+    mask[0, 3] = True  # a longer prefix, written in place
+    _, info = eng._decode_mask(torch.zeros(2, 6, 32), mask)
+    assert (info.mode, info.lengths) == (MASK_PREFIX, (4, 6)) and len(calls) == 2
+    with torch.inference_mode():
+        mask[1, 0] = False  # in-place update under inference mode: still versioned
+    _, info = eng._decode_mask(torch.zeros(2, 6, 32), mask)
+    assert info.mode == MASK_GENERAL
+    mask.fill_(True)
+    _, info = eng._decode_mask(torch.zeros(2, 6, 32), mask)
+    assert info.mode == MASK_NONE
+    # integer prefix lengths take the same memo
+    lengths = torch.tensor([2, 6])
+    _, info = eng._decode_mask(torch.zeros(2, 6, 32), lengths)
+    assert (info.mode, info.lengths) == (MASK_PREFIX, (2, 6))
+    lengths[0] = 5
+    _, info = eng._decode_mask(torch.zeros(2, 6, 32), lengths)
+    assert (info.mode, info.lengths) == (MASK_PREFIX, (5, 6))
+    lengths[0] = 9  # clamped to S
+    _, info = eng._decode_mask(torch.zeros(2, 6, 32), lengths)
+    assert info.mode == MASK_NONE
+
+
+def test_work_list_validation_rejects_broken_lists():
+    """validate_work accepts the lists build_items makes and rejects each
+    kind of corruption the kernel would otherwise run: an item outside the
+    launch, a gap or an overlap in a query block's key tiles, a second half
+    issued before its first half, a slot out of range or reused."""
+    from tjkernels.schedule import build_items, validate_work
+    lengths, heads = [300, 70, 0, 260], 2
+    work, n_slots = build_items(lengths, heads, True, slots=32, min_split=2, split_factor=1.0)
+    assert n_slots > 0
+    good = [(bh, qb, lo, hi, slot) for _, bh, qb, lo, hi, slot in work]
+    validate_work(good, lengths, heads, True, n_slots)
+    first = next(i for i, w in enumerate(good) if w[4] >= 0)
+    second = next(i for i, w in enumerate(good) if w[4] == -2 - good[first][4])
+    whole = next(i for i, w in enumerate(good) if w[4] == -1)
+
+    def broken(edit):
+        w = [list(x) for x in good]
+        edit(w)
+        return [tuple(x) for x in w]
+
+    cases = {
+        "outside": broken(lambda w: w.__setitem__(whole, [len(lengths) * heads] + w[whole][1:])),
+        "gap": broken(lambda w: w[whole].__setitem__(3, w[whole][3] - 1) if w[whole][3] > 1 else
+                      w[whole].__setitem__(2, 1)),
+        "overlap": broken(lambda w: w[second].__setitem__(2, w[second][2] - 1)),
+        "order": broken(lambda w: w.insert(first, w.pop(second))),
+        "slot range": broken(lambda w: w[first].__setitem__(4, n_slots)),
+        "slot reuse": broken(lambda w: w.append(list(w[whole][:4]) + [w[first][4]])),
+        "missing": good[:whole] + good[whole + 1:],
+    }
+    for name, bad in cases.items():
+        with pytest.raises(ValueError):
+            validate_work(bad, lengths, heads, True, n_slots)
+
+
+def test_gemm_tile_classes_follow_the_library_table():
+    """Each timed candidate set holds plans of one K order only (the same
+    k_groups in the library's own table), and the class is a function of the
+    shape alone -- so the timed choice cannot change results."""
+    from tjkernels import ops, tiles
+    info = {pid: kg for pid, _, _, _, kg in ops.gemm_plans(torch.bfloat16)}
+    for cls, cands in tiles.CLASS_TILES_16.items():
+        assert {info[c] for c in cands} == {cls}
+    for (m, n, k) in [(128, 1536, 512), (128, 512, 2048), (2442, 768, 3072), (5430, 4096, 1024),
+                      (5430, 1024, 4096), (8192, 3072, 1024)]:
+        cls = tiles.k_class(m, n, k, torch.bfloat16)
+        assert cls == tiles.k_class(m, n, k, torch.bfloat16)
+        assert set(tiles.candidates(m, n, k, torch.bfloat16)) == set(tiles.CLASS_TILES_16[cls])
+    assert tiles.k_class(128, 512, 2048, torch.bfloat16) == 2   # C2 FFN2: launch-bound
+    assert tiles.k_class(5430, 4096, 1024, torch.bfloat16) == 1  # C4 FFN1
+    assert tiles.candidates(96, 512, 128, torch.float32) == tiles.CANDIDATES_32

@@ -400,7 +400,7 @@ __global__ __launch_bounds__(256 * KS) void flash_fwd_kernel(
 // Cache-policy bits of buffer loads / stores (sc0 = 1, sc1 = 16): sc1 makes
 // an access device-coherent, sc0 sc1 on a store writes through to memory.
 constexpr int kFaSc1 = 16, kFaSc0Sc1 = 17;
-constexpr int kFaSpinLimit = 1 << 22;  // polls of a split item's flag before giving up
+constexpr int kFaSpinLimit = 1 << 20;  // polls of a split item's flag before giving up (>= 0.1 s)
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 template <typename T, int HDP, bool KEYMASK, bool FULLHD>
@@ -409,7 +409,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
     T* __restrict__ out, int64_t ld_out, int B, int S, int H, int hd, float scale_log2,
     int causal, const int32_t* __restrict__ lengths, const uint8_t* __restrict__ key_mask,
     const int32_t* __restrict__ cu_seqlens, int nqb,
-    const int4* __restrict__ work, float* __restrict__ partials, int* __restrict__ flags, int grp) {
+    const int4* __restrict__ work, float* __restrict__ partials, int* __restrict__ flags, int n_slots,
+    int grp) {
   static_assert(sizeof(T) == 2, "2-byte element types only");
   constexpr int BMQ = 128, BNK = 64, NST = 4, VEC = 8;
   constexpr int LDK = HDP + VEC, LDV = BNK + VEC;
@@ -428,6 +429,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
   // publishes its partial in slot s; slot -2 - s: the second half, which
   // merges partial s into its own before the store.
   int bh, qb, t_lo = 0, t_hi = 1 << 30, slot = -1;
+  bool bad_slot = false;
   if (work != nullptr) {
     const int4 it = work[blockIdx.x];
     bh = it.x;
@@ -435,6 +437,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
     t_lo = it.z & 0xffff;
     t_hi = it.z >> 16;
     slot = it.w;
+    // An item outside the launch's (b, h) range cannot be placed: it is
+    // counted in the error word and dropped.  A slot outside [0, n_slots)
+    // (or its second-half image) has no partial to publish or merge: the
+    // item's rows are written as NaN and counted.
+    if (bh < 0 || bh >= BH || qb < 0 || t_lo > t_hi) {
+      if (flags != nullptr && threadIdx.x == 0)
+        __hip_atomic_fetch_add(&flags[-1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    if (slot != -1 && (slot >= n_slots || slot < -1 - n_slots)) {
+      bad_slot = true;
+      slot = -1;
+    }
   } else {
     // Longest query blocks first within groups of `grp` (b, h) pairs: a
     // group's blocks run together, which bounds the K/V the blocks in
@@ -831,7 +846,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
   // The halves of a split item are different workgroups, possibly on
   // different XCDs: the partial is written through to memory (sc0 sc1) and
   // read device-coherently (sc1), with a flag per slot in between.
-  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(partials, (short)0, 0x7fffffff, 0x00020000);
+  // The descriptor covers exactly the n_slots partial slots.
+  const __amdgpu_buffer_rsrc_t prs =
+      __builtin_amdgcn_make_buffer_rsrc(partials, (short)0, n_slots * (BMQ * (HDP + 2)) * 4, 0x00020000);
   auto pslot = [&](int sl) { return sl * (BMQ * (HDP + 2)) * 4; };  // byte offset
   const int prow = (wave * 32 + l32) * HDP * 4;
   if (slot >= 0) {
@@ -852,24 +869,50 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial is in memory
     __syncthreads();
-    if (tid == 0) __hip_atomic_store(&flags[slot], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) {
+      // 0 -> 1 publishes.  -1 means the second half stopped waiting (its rows
+      // are already NaN): the flag is reset for the next launch instead.
+      int expected = 0;
+      if (!__hip_atomic_compare_exchange_strong(&flags[slot], &expected, 1, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT))
+        __hip_atomic_store(&flags[slot], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     return;
   }
   float lm = l;
+  bool merged = true;
   if (slot <= -2) {
-    // Second half: wait for the first (bounded polls; a timeout is counted
-    // in the error word after the flags), then
+    // Second half: thread 0 waits for the first half's flag (bounded
+    // polls).  On a timeout it claims the flag (0 -> -1), counts the timeout
+    // in the error word and the item's rows are written as NaN; a first
+    // half that publishes later finds -1 and resets the flag, so nothing
+    // stale reaches the next launch.  Merged:
     //   O = O_hi a_hi + O_lo a_lo,  l = l_hi a_hi + l_lo a_lo,
     //   a_x = 2^(m_x - max(m_lo, m_hi)),  in this order every time.
-    const int ps = -2 - slot, pb = pslot(ps);
-    int spins = 0;
-    while (__hip_atomic_load(&flags[ps], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
-      if (++spins > kFaSpinLimit) {
-        if (tid == 0) __hip_atomic_fetch_add(&flags[-1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
+    const int ps = -2 - slot;
+    __shared__ int s_published;
+    if (tid == 0) {
+      int v = __hip_atomic_load(&flags[ps], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int spins = 0; v != 1 && spins < kFaSpinLimit; ++spins) {
+        __builtin_amdgcn_s_sleep(2);
+        v = __hip_atomic_load(&flags[ps], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-      __builtin_amdgcn_s_sleep(2);
+      if (v != 1) {
+        int expected = 0;
+        if (__hip_atomic_compare_exchange_strong(&flags[ps], &expected, -1, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT)) {
+          __hip_atomic_fetch_add(&flags[-1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          v = expected;  // published between the last poll and the claim
+        }
+      }
+      s_published = v == 1;
     }
+    __syncthreads();
+    merged = s_published != 0;
+  }
+  if (slot <= -2 && merged) {
+    const int ps = -2 - slot, pb = pslot(ps);
     const float m_lo = __builtin_bit_cast(
         float, __builtin_amdgcn_raw_buffer_load_b32(prs, pb + (BMQ * HDP + wave * 32 + l32) * 4, 0, kFaSc1));
     const float l_lo = __builtin_bit_cast(
@@ -888,7 +931,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
         for (int e = 0; e < 4; ++e) o[hb][4 * g + e] = fmaf(o[hb][4 * g + e], a_hi, v[e] * a_lo);
       }
   }
-  const float inv = lm > 0.f ? 1.0f / lm : 0.f;
+  float inv = lm > 0.f ? 1.0f / lm : 0.f;
+  if (!merged || bad_slot) {
+    if (bad_slot && flags != nullptr && tid == 0)
+      __hip_atomic_fetch_add(&flags[-1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    inv = __builtin_nanf("");
+  }
   if (q < Sb) {
     T* orow = out + (row0 + q) * ld_out + (int64_t)h * hd;
 #pragma unroll
@@ -903,7 +951,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
         }
       }
   }
-  if (slot <= -2) {
+  if (slot <= -2 && merged) {
     __syncthreads();  // every wave has read the partial
     if (tid == 0) __hip_atomic_store(&flags[-2 - slot], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -913,12 +961,13 @@ template <typename T, int HDP>
 static int launch_sched(const void* qkv, int64_t ss, int64_t sc, int64_t sh, void* out, int64_t ld_out,
                         int B, int S, int H, int hd, float scale_log2, int causal, const int32_t* cu_seqlens,
                         const int32_t* work, int n_work, float* partials, int n_slots, hipStream_t st) {
-  int* flags = n_slots > 0 ? reinterpret_cast<int*>(partials + (size_t)n_slots * 128 * (HDP + 2)) + 1 : nullptr;
+  // [n_slots partial slots][error word][n_slots flags]; flags[-1] is the error word
+  int* flags = partials != nullptr ? reinterpret_cast<int*>(partials + (size_t)n_slots * 128 * (HDP + 2)) + 1 : nullptr;
 #define TJK_PIPE_SCHED(FULL)                                                                                  \
   hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, false, FULL>), dim3((unsigned)n_work), dim3(256), 0, st,      \
                      (const T*)qkv, (int64_t)0, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, \
                      (const int32_t*)nullptr, (const uint8_t*)nullptr, cu_seqlens, 0,                         \
-                     reinterpret_cast<const int4*>(work), partials, flags, 1)
+                     reinterpret_cast<const int4*>(work), partials, flags, n_slots, 1)
   if (hd == HDP) TJK_PIPE_SCHED(true); else TJK_PIPE_SCHED(false);
 #undef TJK_PIPE_SCHED
   return check_launch("tjk_flash_fwd_sched");
@@ -942,7 +991,7 @@ static int launch_pipe(const void* qkv, int64_t sb, int64_t ss, int64_t sc, int6
 #define TJK_PIPE(KM, FULL)                                                                                     \
   hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, KM, FULL>), dim3((unsigned)nblk), dim3(256), 0, st, (const T*)qkv, \
                      sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, lengths, key_mask,          \
-                     cu_seqlens, nqb, (const int4*)nullptr, (float*)nullptr, (int*)nullptr, grp)
+                     cu_seqlens, nqb, (const int4*)nullptr, (float*)nullptr, (int*)nullptr, 0, grp)
   if (key_mask != nullptr) {
     if (hd == HDP) TJK_PIPE(true, true); else TJK_PIPE(true, false);
   } else {
@@ -1077,7 +1126,7 @@ extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s
 }
 
 extern "C" size_t tjk_flash_partial_bytes(int head_dim, int n_slots) {
-  if (head_dim <= 0 || n_slots <= 0) return 0;
+  if (head_dim <= 0 || n_slots < 0) return 0;
   const int hdp = head_dim <= 32 ? 32 : head_dim <= 64 ? 64 : 128;
   // partial slots, then the error word and one flag per slot
   return (size_t)n_slots * 128 * (hdp + 2) * sizeof(float) + (size_t)(n_slots + 1) * sizeof(int);
@@ -1086,13 +1135,15 @@ extern "C" size_t tjk_flash_partial_bytes(int head_dim, int n_slots) {
 extern "C" int tjk_flash_fwd_sched(const void* qkv, int64_t stride_s, int64_t stride_c, int64_t stride_h,
                                    void* out, int64_t ld_out, int batch, int max_seqlen, int heads,
                                    int head_dim, float scale, int causal, const int32_t* cu_seqlens,
-                                   const int32_t* work, int n_work, float* partials, int n_slots,
-                                   int dtype, void* stream) {
+                                   const int32_t* work, int n_work, float* partials, size_t partials_bytes,
+                                   int n_slots, int dtype, void* stream) {
   if (batch < 0 || max_seqlen < 0 || heads <= 0 || head_dim <= 0 || n_work < 0 || n_slots < 0)
     return fail(TJK_EINVAL, "tjk_flash_fwd_sched: bad shape or counts");
   if (n_work == 0) return TJK_OK;
   if (!qkv || !out || !cu_seqlens || !work) return fail(TJK_EINVAL, "tjk_flash_fwd_sched: null pointer");
-  if (n_slots > 0 && !partials) return fail(TJK_EINVAL, "tjk_flash_fwd_sched: split items need partials");
+  if ((n_slots > 0 || partials) && (!partials || partials_bytes < tjk_flash_partial_bytes(head_dim, n_slots)))
+    return fail(TJK_EINVAL, "tjk_flash_fwd_sched: %d split slots need %zu bytes of partials (got %zu)", n_slots,
+                tjk_flash_partial_bytes(head_dim, n_slots), partials_bytes);
   if ((int64_t)n_slots * 128 * 130 * 4 >= INT32_MAX) return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd_sched: too many slots");
   if (dtype != TJK_F16 && dtype != TJK_BF16)
     return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd_sched: 2-byte dtypes only (got %d)", dtype);

@@ -1,0 +1,429 @@
+// Device building blocks shared by the GEMM and fused-FFN kernels: the
+// erf GELU, the XCD-aware tile order, the LDS-staged epilogue and the
+// direct-to-LDS (buffer_load ... lds) MFMA main loop.
+#pragma once
+
+#include <type_traits>
+
+#include "tjk_common.h"
+
+namespace tjk {
+
+constexpr int kGroupM = 8;
+
+// GELU(v) = 0.5 v (1 + erf(v / sqrt 2)) with erf from Abramowitz & Stegun,
+// Handbook of Mathematical Functions, eq. 7.1.26 (|error| <= 1.5e-7): for
+// z >= 0, erf z = 1 - t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-z^2) with
+// t = 1 / (1 + p z), and erf(-z) = -erf(z).  Branch-free (one reciprocal, one
+// exp2) -- the library erff branches on |z| and measured ~35 VALU
+// instructions per value with divergent lanes, most of the FFN1 epilogue.
+__device__ __forceinline__ float gelu_erf(float v) {
+  const float z = fabsf(v) * 0.70710678118654752440f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
+  float poly = fmaf(1.061405429f, t, -1.453152027f);
+  poly = fmaf(poly, t, 1.421413741f);
+  poly = fmaf(poly, t, -0.284496736f);
+  poly = fmaf(poly, t, 0.254829592f);
+  poly *= t;
+  const float e = __builtin_amdgcn_exp2f(-(z * z) * 1.4426950408889634f);  // exp(-z^2)
+  const float erf_v = copysignf(fmaf(-poly, e, 1.0f), v);
+  const float hv = 0.5f * v;
+  return fmaf(hv, erf_v, hv);
+}
+
+// Bijection from hardware workgroup id to a tile order in which XCD x gets
+// the contiguous range of ids [start_x, start_x + count_x).
+__device__ __forceinline__ int xcd_remap(int bid, int nb) {
+  const int per = nb / 8, rem = nb % 8;
+  const int x = bid % 8, i = bid / 8;
+  return x < rem ? x * (per + 1) + i : rem * (per + 1) + (x - rem) * per + i;
+}
+
+
+// Internal epilogue mode beside the ABI's TJK_EPI_*: store the fp32 sum
+// (acc + bias) as is, no read-modify-write (the fused FFN's split partials).
+constexpr int kEpiStoreF32 = 3;
+
+// Epilogue shared by the GEMM and fused-FFN kernels.  The accumulators hold
+// C^T blocks: for block (i, j), lane (l32, hi) owns output row
+// m = mw + 32 j + l32 and, for g = 0..3, the four consecutive columns
+// n = nw + 32 i + 8 g + 4 hi.  Stored straight from that layout, every store
+// instruction would scatter 8-16 byte pieces over 32 rows (32 L2 requests
+// per instruction), which measured slower than the whole K=1024 main loop.
+// Instead each wave applies bias / GELU in registers, transposes one 32-row
+// block at a time through a private LDS region (row pitch padded by one
+// 16-byte piece) and writes whole row segments: 16 bytes per lane, WTN
+// contiguous elements per row.  The residual epilogue stages fp32 and does
+// its read-modify-write of the fp32 residual with the same row-contiguous
+// pieces; kEpiStoreF32 stages fp32 and stores it.
+template <typename T, int EPI, int FN>
+struct EpiStage {
+  static constexpr bool F32OUT = EPI == TJK_EPI_BIAS_RESIDUAL || EPI == kEpiStoreF32;
+  typedef typename std::conditional<F32OUT, float, T>::type S;  // staged type
+  static constexpr int WTN = FN * 32;
+  static constexpr int SV = 16 / (int)sizeof(S);  // elements per 16-byte piece
+  static constexpr int PITCH = WTN + SV;          // staged row pitch (elements)
+  static constexpr int BYTES = 32 * PITCH * (int)sizeof(S);  // LDS bytes per wave
+};
+
+// The residual pieces (TJK_EPI_BIAS_RESIDUAL) a wave's epilogue will
+// update, read into registers before the main loop.  A launch whose tiles
+// all run in one round otherwise starts every residual read at the same
+// moment, after the last MFMA; read early, they overlap the main loop and
+// the epilogue only writes.  Piece (j, it) is the one the epilogue's store
+// loop handles for 32-row block j, iteration it.
+struct NoPrefetch {
+  static constexpr bool on = false;
+  __device__ float4 get(int, int) const { return make_float4(0.f, 0.f, 0.f, 0.f); }
+};
+template <int FM, int FN>
+struct ResPrefetch {
+  static constexpr bool on = true;
+  static constexpr int WTN = FN * 32, LPR = WTN / 4, NPC = 32 * LPR, NIT = (NPC + 63) / 64;
+  float4 r[FM][NIT];
+  __device__ __forceinline__ void load(const float* __restrict__ C, int64_t ldc, int M, int N, int mw, int nw,
+                                       int lane) {
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        const int pc = lane + 64 * it;
+        const int m = mw + 32 * j + pc / LPR, n = nw + (pc % LPR) * 4;
+        r[j][it] = ((NPC % 64 == 0 || pc < NPC) && m < M && n < N)
+                       ? *reinterpret_cast<const float4*>(C + (int64_t)m * ldc + n)
+                       : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+  }
+  __device__ __forceinline__ float4 get(int j, int it) const { return r[j][it]; }
+};
+
+// Stores this wave's (32 FM) x (32 FN) block at rows mw.., columns nw.. of
+// C (rows >= M and columns >= N dropped).  `stage` is the wave's private
+// EpiStage<T, EPI, FN>::BYTES of LDS.
+template <typename T, int EPI, int FM, int FN, typename Pre = NoPrefetch>
+__device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* __restrict__ bias,
+                                         void* __restrict__ Cv, int64_t ldc, int M, int N, int mw, int nw,
+                                         int lane, char* __restrict__ stage, const Pre& pre = Pre()) {
+  typedef EpiStage<T, EPI, FN> E;
+  typedef typename E::S S;
+  constexpr int LPR = E::WTN / E::SV;  // 16-byte pieces per staged row
+  constexpr int NPC = 32 * LPR;        // pieces per 32-row block
+  constexpr int NIT = (NPC + 63) / 64; // read instructions per block
+  S* st = reinterpret_cast<S*>(stage);
+  const int l32 = lane & 31, hi = lane >> 5;
+  // 16-byte output pieces need a 16-byte aligned C and a leading dimension
+  // that keeps every row 16-byte aligned; otherwise pieces go out as halves.
+  const bool a16 = ((uintptr_t)Cv & 15) == 0 && (ldc % E::SV) == 0;
+
+  float4 bv[FN][4];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int n = nw + i * 32 + g * 8 + hi * 4;
+      bv[i][g] = (bias != nullptr && n < N)
+                     ? Quad<T>::to(*reinterpret_cast<const typename Quad<T>::raw*>(bias + n))
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+
+#pragma unroll
+  for (int j = 0; j < FM; ++j) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float4 v = make_float4(acc[i][j][4 * g + 0] + bv[i][g].x, acc[i][j][4 * g + 1] + bv[i][g].y,
+                               acc[i][j][4 * g + 2] + bv[i][g].z, acc[i][j][4 * g + 3] + bv[i][g].w);
+        if (EPI == TJK_EPI_BIAS_GELU) {
+          v.x = gelu_erf(v.x); v.y = gelu_erf(v.y); v.z = gelu_erf(v.z); v.w = gelu_erf(v.w);
+        }
+        S* dst = st + l32 * E::PITCH + i * 32 + g * 8 + hi * 4;
+        if constexpr (E::F32OUT)
+          *reinterpret_cast<float4*>(dst) = v;
+        else
+          *reinterpret_cast<typename Quad<T>::raw*>(dst) = Quad<T>::from(v);
+      }
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int pc = lane + 64 * it;  // piece index: row pc / LPR, piece pc % LPR
+      if (NPC % 64 != 0 && pc >= NPC) break;
+      const int rr = pc / LPR, cc = (pc % LPR) * E::SV;
+      const int m = mw + 32 * j + rr, n = nw + cc;
+      const uint4 piece = *reinterpret_cast<const uint4*>(st + rr * E::PITCH + cc);
+      if (m < M && n < N) {
+        if constexpr (EPI == TJK_EPI_BIAS_RESIDUAL) {
+          // fp32 pieces never straddle N (N % 4 == 0)
+          const float4 a = __builtin_bit_cast(float4, piece);
+          float4* r = reinterpret_cast<float4*>(static_cast<float*>(Cv) + (int64_t)m * ldc + n);
+          float4 o = Pre::on ? pre.get(j, it) : *r;
+          o.x += a.x; o.y += a.y; o.z += a.z; o.w += a.w;
+          *r = o;
+        } else if constexpr (EPI == kEpiStoreF32) {
+          *reinterpret_cast<uint4*>(static_cast<float*>(Cv) + (int64_t)m * ldc + n) = piece;
+        } else {
+          T* c = static_cast<T*>(Cv) + (int64_t)m * ldc + n;
+          if (E::SV == 4 || (a16 && n + E::SV <= N)) {
+            *reinterpret_cast<uint4*>(c) = piece;
+          } else {  // 2-byte types: halves of 4 elements (N % 4 == 0)
+            *reinterpret_cast<uint2*>(c) = make_uint2(piece.x, piece.y);
+            if (n + 4 < N) *reinterpret_cast<uint2*>(c + 4) = make_uint2(piece.z, piece.w);
+          }
+        }
+      }
+    }
+  }
+}
+
+// Tile coordinates of workgroup `bid`: XCD-contiguous ranges of a
+// GROUP_M-grouped raster over (tiles_m x tiles_n).
+__device__ __forceinline__ void tile_coords(int bid, int tiles_m, int tiles_n, int& pid_m, int& pid_n) {
+  const int t = xcd_remap(bid, tiles_m * tiles_n);
+  const int group = t / (kGroupM * tiles_n);
+  const int first_m = group * kGroupM;
+  const int gsize = min(tiles_m - first_m, kGroupM);
+  pid_m = first_m + (t % (kGroupM * tiles_n)) % gsize;
+  pid_n = (t % (kGroupM * tiles_n)) / gsize;
+}
+
+// ------------------------------------------------------- direct-to-LDS GEMM
+//
+// Same math and epilogue as gemm_kernel, with the operand tiles moved by
+// gfx950's LDS DMA (buffer_load_dwordx4 ... lds): each wave instruction
+// copies 64 x 16 B straight from global memory into 1 KB of LDS, so tiles
+// never pass through VGPRs.  Rows beyond M (or N) fall outside the buffer
+// descriptor's range and arrive as zeros, which removes every bounds branch
+// from the main loop.
+//
+// LDS holds STAGES tiles in a ring; a tile row is BKB bytes of K (64 or
+// 128) with no padding.  The 16-byte chunk c of row r is stored at chunk
+// c ^ swz(r), which spreads the ds_read_b128 fragment reads of 16
+// consecutive rows over all banks (for 32- and 64-bank LDS alike).
+//
+// Pipeline, one barrier per tile, placed before the tile's last 16-deep
+// step: by then every fragment of tile k is in registers, so after the
+// barrier (which also certifies that tile k+1 has landed) a wave issues the
+// DMA of tile k+STAGES into tile k's slot and reads tile k+1's first
+// fragments while the last step's MFMAs run.  Every DMA has STAGES-1 tiles
+// of MFMA work to land, and no wave waits for LDS right after the barrier.
+// With a ring of three or more slots the DMA of tile k-1+STAGES (into the
+// slot tile k-1 freed at the previous barrier) is instead spread over the
+// MFMAs of tile k's steps before the last: the vector memory unit then gets
+// a few instructions per step rather than a burst after each barrier, and
+// every DMA still has at least one tile of MFMA work to land.  Measured on
+// MI355X (wall-clock probes of one launch, bias epilogue): 192x128 tiles in
+// a 4-slot ring (160 KB) run the C4 FFN2 main loop (5430x1024x4096) at 67%
+// of the clock-limited MFMA rate, against 62% for 3 slots with the spread
+// schedule, 55% for 3 slots issuing after the barrier and 52% for 2 slots.
+// Removing the W operand's LDS reads did not change the 2-slot loop's
+// speed; removing its DMA made it 25% faster: the loops are bound by the
+// DMA traffic per CU, not by LDS reads.
+// The DMA is issued on every iteration, past the end pointed outside the
+// buffer range (it moves nothing), which keeps the body one basic block;
+// scheduling directives interleave the MFMAs with the next step's ds_reads.
+// Requires K % (BKB / sizeof(T)) == 0 and 16-byte aligned rows.
+
+template <int BKB> __device__ __forceinline__ int swz(int r);
+template <> __device__ __forceinline__ int swz<128>(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+template <> __device__ __forceinline__ int swz<64>(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Byte offset that lies beyond any buffer descriptor range used here.
+constexpr int kPastEnd = 0x7fff0000;
+
+// Tile geometry shared by the direct-to-LDS kernels.
+template <typename T, int BM, int BN, int WM, int WN, int BKB, int STAGES, int KSPLIT>
+struct DtlGeom {
+  static constexpr int NW = WM * WN;
+  static constexpr int BK = BKB / sizeof(T);          // K elements per tile
+  static constexpr int CPR = BKB / 16;                // 16-byte chunks per row
+  static constexpr int RPI = 64 / CPR;                // rows per DMA instruction
+  static constexpr int KS = BK / 16;                  // 16-deep MFMA steps per tile
+  static constexpr int CPS = sizeof(T) == 2 ? 2 : 4;  // chunks per 16-deep step
+  static constexpr int WTM = BM / WM, WTN = BN / WN;
+  static constexpr int FM = WTM / 32, FN = WTN / 32;
+  static constexpr int STAGE = (BM + BN) * BKB;       // bytes per LDS stage
+  static constexpr int DA = BM / (RPI * NW), DW = BN / (RPI * NW);
+  static constexpr int NDMA = DA + DW;                // DMA instructions per wave per tile
+  static constexpr int LDS = KSPLIT * STAGES * STAGE; // ring bytes
+  static_assert(DA * RPI * NW == BM && DW * RPI * NW == BN, "tile rows must split over the waves");
+  static_assert(STAGES >= 2 && (STAGES - 1) * NDMA <= 63, "vmcnt range");
+  static_assert(KS % 2 == 0, "fragment double buffer alternates per 16-deep step");
+};
+
+// acc += A[m0 : m0+BM, K tiles kt0..kt1) * W[n0 : n0+BN, same]^T for this
+// wave's sub-tile (K-split group kg takes K tiles kt0 + kg, kt0 + kg +
+// KSPLIT, ...).  On return every DMA has landed and the workgroup has met at
+// a barrier, so the LDS ring may be reused.  (smem is deliberately not
+// __restrict__: with it the compiler stops telling the LDS DMA writes and
+// the fragment reads of different ring slots apart and waits for every DMA
+// before each ds_read.)
+template <typename T, int BM, int BN, int WM, int WN, int BKB, int STAGES, int KSPLIT>
+__device__ __forceinline__ void dtl_accumulate(
+    char* smem, const T* __restrict__ A, int64_t lda, const T* __restrict__ W, int64_t ldw,
+    int M, int N, int m0, int n0, int kt0, int kt1,
+    f32x16 (&acc)[DtlGeom<T, BM, BN, WM, WN, BKB, STAGES, KSPLIT>::FN][DtlGeom<T, BM, BN, WM, WN, BKB, STAGES, KSPLIT>::FM]) {
+  typedef DtlGeom<T, BM, BN, WM, WN, BKB, STAGES, KSPLIT> G;
+  constexpr int NW = G::NW, KS = G::KS, CPR = G::CPR, RPI = G::RPI, CPS = G::CPS;
+  constexpr int WTM = G::WTM, WTN = G::WTN, FM = G::FM, FN = G::FN, STAGE = G::STAGE;
+  constexpr int DA = G::DA, NDMA = G::NDMA;
+  constexpr int DW = G::DW;
+
+  // K split inside the workgroup: KSPLIT groups of WM x WN waves, group kg
+  // streaming its K tiles through its own LDS ring.  The thread id passes an
+  // empty asm so that, inside a persistent kernel's tile loop, nothing
+  // derived from it is hoisted out of that loop (which keeps the per-lane
+  // DMA and fragment addresses of every call live at once).
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & 63, kg = (tid >> 6) / NW, wave = (tid >> 6) % NW;
+  const int wm = wave / WN, wn = wave % WN;
+  const int l32 = lane & 31, hi = lane >> 5;
+  char* const gsm = smem + kg * (STAGES * STAGE);
+
+  // Buffer descriptors over this tile's rows; reads past row M (N) return 0.
+  const int64_t a_rows = min((int64_t)BM, (int64_t)(M - m0));
+  const int64_t w_rows = min((int64_t)BN, (int64_t)(N - n0));
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(A + (int64_t)m0 * lda), (short)0, (int)(a_rows * lda * (int64_t)sizeof(T)), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(W + (int64_t)n0 * ldw), (short)0, (int)(w_rows * ldw * (int64_t)sizeof(T)), 0x00020000);
+
+  // DMA instruction i of this wave fills LDS rows (i*NW + wave)*RPI + 0..RPI-1;
+  // lane l lands at byte 16*l of that 1 KB: row +l/CPR, physical chunk l%CPR,
+  // so it fetches logical chunk (l%CPR) ^ swz(row).
+  uint32_t voff_a[DA], voff_w[DW];
+#pragma unroll
+  for (int i = 0; i < DA; ++i) {
+    const int r = (i * NW + wave) * RPI + lane / CPR;
+    voff_a[i] = (uint32_t)(r * lda * (int64_t)sizeof(T)) + (uint32_t)(((lane % CPR) ^ swz<BKB>(r)) << 4);
+  }
+#pragma unroll
+  for (int i = 0; i < DW; ++i) {
+    const int r = (i * NW + wave) * RPI + lane / CPR;
+    voff_w[i] = (uint32_t)(r * ldw * (int64_t)sizeof(T)) + (uint32_t)(((lane % CPR) ^ swz<BKB>(r)) << 4);
+  }
+  const int nit = (kt1 - kt0 + KSPLIT - 1) / KSPLIT;  // ring steps per group
+  // DMA instruction q (q < DA: A rows, else W rows) of this group's step it
+  // into its slot; past the segment it points outside the range and moves
+  // nothing.
+  auto dma = [&](int it, int q) {
+    char* sb = gsm + (it % STAGES) * STAGE;
+    const int kt = kt0 + it * KSPLIT + kg;
+    const uint32_t kb = kt < kt1 ? (uint32_t)(kt * BKB) : (uint32_t)kPastEnd;
+    if (q < DA)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_void*)(sb + (q * NW + wave) * 1024), 16,
+                                               (uint32_t)(voff_a[q] + kb), 0, 0, 0);
+    else
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_void*)(sb + BM * BKB + ((q - DA) * NW + wave) * 1024),
+                                               16, (uint32_t)(voff_w[q - DA] + kb), 0, 0, 0);
+  };
+
+  // Fragment reads: row (base + l32), logical chunk c at physical c ^ swz(l32).
+  const int sw = swz<BKB>(l32);
+  auto frag_at = [&](const char* rowbase, int ks) -> typename Mfma<T>::frag {
+    if constexpr (sizeof(T) == 2) {
+      return *reinterpret_cast<const typename Mfma<T>::frag*>(rowbase + (((CPS * ks + hi) ^ sw) << 4));
+    } else {
+      const float4 lo = *reinterpret_cast<const float4*>(rowbase + (((CPS * ks + 2 * hi) ^ sw) << 4));
+      const float4 up = *reinterpret_cast<const float4*>(rowbase + (((CPS * ks + 2 * hi + 1) ^ sw) << 4));
+      typename Mfma<T>::frag f;
+      f[0] = lo.x; f[1] = lo.y; f[2] = lo.z; f[3] = lo.w;
+      f[4] = up.x; f[5] = up.y; f[6] = up.z; f[7] = up.w;
+      return f;
+    }
+  };
+
+  // Prologue: tiles 0 .. STAGES-1 in flight (STAGES-2 with the spread
+  // schedule, whose loop issues tile kt-1+STAGES during tile kt); tile 0
+  // landed everywhere.
+  constexpr bool SPREAD = STAGES >= 3;
+  constexpr int PRE = SPREAD ? STAGES - 1 : STAGES;
+#pragma unroll
+  for (int t = 0; t < PRE; ++t)
+#pragma unroll
+    for (int q = 0; q < NDMA; ++q) dma(t, q);
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"((PRE - 1) * NDMA) : "memory");
+  asm volatile("s_barrier" ::: "memory");
+  constexpr int NMF = FN * FM, NDS = FN + FM;  // MFMAs and fragment reads per step
+  constexpr int NSLOT = NMF > NDS ? NMF : NDS;
+  typename Mfma<T>::frag fa[2][FM], fw[2][FN];
+  {
+    const char* sa = gsm + (wm * WTM + l32) * BKB;
+    const char* sw_ = gsm + BM * BKB + (wn * WTN + l32) * BKB;
+#pragma unroll
+    for (int j = 0; j < FM; ++j) fa[0][j] = frag_at(sa + j * 32 * BKB, 0);
+#pragma unroll
+    for (int i = 0; i < FN; ++i) fw[0][i] = frag_at(sw_ + i * 32 * BKB, 0);
+  }
+  // The loop body is emitted in source order (scheduling fences between the
+  // pieces): MFMA m of a step is followed by fragment read m of the next
+  // step (m < FM + FN), and after the barrier by DMA instructions, so the
+  // LDS reads and DMA issues hide under the MFMAs of the step before the
+  // one that needs them.
+  for (int kt = 0; kt < nit; ++kt) {
+    const char* st = gsm + (kt % STAGES) * STAGE;
+    const char* sa = st + (wm * WTM + l32) * BKB;
+    const char* sw_ = st + BM * BKB + (wn * WTN + l32) * BKB;
+    const char* nx = gsm + ((kt + 1) % STAGES) * STAGE;
+    const char* na = nx + (wm * WTM + l32) * BKB;
+    const char* nw = nx + BM * BKB + (wn * WTN + l32) * BKB;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int b = ks & 1;
+      const bool last = ks + 1 == KS;
+      // fragments of the next step: this tile's step ks+1, or after the
+      // barrier the next tile's step 0
+      const char* ra = last ? na : sa;
+      const char* rw = last ? nw : sw_;
+      const int rks = last ? 0 : ks + 1;
+      if (last) {
+        // Before the last step's MFMAs (its fragments are in registers): my
+        // reads of this slot are complete and my DMAs of step kt+1 have
+        // landed, then everyone's.  The slot is then free for step
+        // kt+STAGES.  Inline asm with a memory clobber keeps the compiler
+        // from moving LDS accesses across either instruction.
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((STAGES - 2) * NDMA) : "memory");  // tile kt+1 landed
+        asm volatile("s_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int m = 0; m < NSLOT; ++m) {
+        if (m < NMF) Mfma<T>::mma(acc[m / FM][m % FM], fw[b][m / FM], fa[b][m % FM]);
+        if (m < FM) fa[b ^ 1][m] = frag_at(ra + m * 32 * BKB, rks);
+        else if (m < NDS) fw[b ^ 1][m - FM] = frag_at(rw + (m - FM) * 32 * BKB, rks);
+        if constexpr (SPREAD) {
+          // DMA instructions of tile kt-1+STAGES over slots 0 .. (KS-1)*NSLOT-1
+          constexpr int TOT = (KS - 1) * NSLOT;
+          const int i = ks * NSLOT + m;
+          if (!last) {
+#pragma unroll
+            for (int q = i * NDMA / TOT; q < (i + 1) * NDMA / TOT; ++q) dma(kt - 1 + STAGES, q);
+          }
+        } else if (last) {
+#pragma unroll
+          for (int q = m * NDMA / NSLOT; q < (m + 1) * NDMA / NSLOT; ++q) dma(kt + STAGES, q);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+
+  // Reuse LDS once every DMA (including the ones issued past the last
+  // tile) has landed and every wave is done reading.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+}
+
+template <typename T, int FM, int FN>
+__device__ __forceinline__ void zero_acc(f32x16 (&acc)[FN][FM]) {
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+}
+
+}  // namespace tjk

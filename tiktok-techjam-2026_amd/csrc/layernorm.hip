@@ -44,7 +44,7 @@ int check_launch(const char* what) {
 template <typename TRes, typename TDelta, typename TOut, int MAXCH, bool FULL>
 __global__ __launch_bounds__(256) void add_layernorm_kernel(
     const TRes* res, int64_t ld_res,  // may alias res_out (in-place update)
-    const TDelta* __restrict__ delta, int64_t ld_delta,
+    const TDelta* __restrict__ delta, int64_t ld_delta, int n_delta, int64_t delta_stride,
     float* res_out, int64_t ld_res_out,
     TOut* __restrict__ out, int64_t ld_out,
     const float* __restrict__ gamma, const float* __restrict__ beta,
@@ -70,12 +70,49 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(
     }
     if (delta != nullptr) {
       const TDelta* drow = delta + src * ld_delta;
+      if (MAXCH > 4 || n_delta == 1) {
 #pragma unroll
-      for (int j = 0; j < MAXCH; ++j) {
-        const int c = lane + 64 * j;
-        if (FULL || c < nch) {
-          float4 d = Quad<TDelta>::to(reinterpret_cast<const typename Quad<TDelta>::raw*>(drow)[c]);
-          x[j].x += d.x; x[j].y += d.y; x[j].z += d.z; x[j].w += d.w;
+        for (int j = 0; j < MAXCH; ++j) {
+          const int c = lane + 64 * j;
+          if (FULL || c < nch) {
+            float4 d = Quad<TDelta>::to(reinterpret_cast<const typename Quad<TDelta>::raw*>(drow)[c]);
+            x[j].x += d.x; x[j].y += d.y; x[j].z += d.z; x[j].w += d.w;
+          }
+        }
+      } else if constexpr (MAXCH <= 4) {
+        // delta = d_0 + d_1 + ... + d_{n_delta-1}, summed in that order (the
+        // split partials of the fused FFN), then added to the residual.  The
+        // loads of UNR slices are issued together before their adds.
+        constexpr int UNR = 16 / MAXCH;
+        float4 dsum[MAXCH];
+        for (int p0 = 0; p0 < n_delta; p0 += UNR) {
+          float4 dv[UNR][MAXCH];
+#pragma unroll
+          for (int u = 0; u < UNR; ++u)
+#pragma unroll
+            for (int j = 0; j < MAXCH; ++j) {
+              const int c = lane + 64 * j;
+              dv[u][j] = (p0 + u < n_delta && (FULL || c < nch))
+                             ? Quad<TDelta>::to(reinterpret_cast<const typename Quad<TDelta>::raw*>(
+                                   drow + (int64_t)(p0 + u) * delta_stride)[c])
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+          for (int u = 0; u < UNR; ++u) {
+            if (p0 + u == 0) {
+#pragma unroll
+              for (int j = 0; j < MAXCH; ++j) dsum[j] = dv[0][j];
+            } else if (p0 + u < n_delta) {
+#pragma unroll
+              for (int j = 0; j < MAXCH; ++j) {
+                dsum[j].x += dv[u][j].x; dsum[j].y += dv[u][j].y; dsum[j].z += dv[u][j].z; dsum[j].w += dv[u][j].w;
+              }
+            }
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < MAXCH; ++j) {
+          x[j].x += dsum[j].x; x[j].y += dsum[j].y; x[j].z += dsum[j].z; x[j].w += dsum[j].w;
         }
       }
     }
@@ -147,15 +184,15 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(
 }
 
 template <typename TRes, typename TDelta, typename TOut>
-static int launch_ln(const void* res, int64_t ld_res, const void* delta, int64_t ld_delta,
-                     float* res_out, int64_t ld_res_out, void* out, int64_t ld_out,
+static int launch_ln(const void* res, int64_t ld_res, const void* delta, int64_t ld_delta, int n_delta,
+                     int64_t delta_stride, float* res_out, int64_t ld_res_out, void* out, int64_t ld_out,
                      const float* gamma, const float* beta, int64_t rows, int n, float eps,
                      const int32_t* row_index, const uint8_t* row_mask, hipStream_t stream) {
   const int nch = n / 4;
   dim3 grid((unsigned)((rows + 3) / 4)), block(256);
 #define TJK_LN_LAUNCH(MC, FULL)                                                                    \
   hipLaunchKernelGGL((add_layernorm_kernel<TRes, TDelta, TOut, MC, FULL>), grid, block, 0, stream,     \
-                     (const TRes*)res, ld_res, (const TDelta*)delta, ld_delta, res_out, ld_res_out, \
+                     (const TRes*)res, ld_res, (const TDelta*)delta, ld_delta, n_delta, delta_stride, res_out, ld_res_out, \
                      (TOut*)out, ld_out, gamma, beta, rows, n, eps, row_index, row_mask)
 #define TJK_LN_CASE(MC)                                   \
   if (nch <= 64 * MC) {                                   \
@@ -176,18 +213,18 @@ static int launch_ln(const void* res, int64_t ld_res, const void* delta, int64_t
 
 template <typename TRes, typename TDelta>
 static int dispatch_out(int out_dtype, const void* res, int64_t ld_res, const void* delta,
-                        int64_t ld_delta, float* res_out, int64_t ld_res_out, void* out,
+                        int64_t ld_delta, int n_delta, int64_t delta_stride, float* res_out, int64_t ld_res_out, void* out,
                         int64_t ld_out, const float* gamma, const float* beta, int64_t rows,
                         int n, float eps, const int32_t* row_index, const uint8_t* row_mask, hipStream_t stream) {
   switch (out_dtype) {
     case TJK_F32:
-      return launch_ln<TRes, TDelta, float>(res, ld_res, delta, ld_delta, res_out, ld_res_out, out, ld_out,
+      return launch_ln<TRes, TDelta, float>(res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ld_res_out, out, ld_out,
                                             gamma, beta, rows, n, eps, row_index, row_mask, stream);
     case TJK_F16:
-      return launch_ln<TRes, TDelta, f16>(res, ld_res, delta, ld_delta, res_out, ld_res_out, out, ld_out,
+      return launch_ln<TRes, TDelta, f16>(res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ld_res_out, out, ld_out,
                                           gamma, beta, rows, n, eps, row_index, row_mask, stream);
     case TJK_BF16:
-      return launch_ln<TRes, TDelta, bf16>(res, ld_res, delta, ld_delta, res_out, ld_res_out, out, ld_out,
+      return launch_ln<TRes, TDelta, bf16>(res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ld_res_out, out, ld_out,
                                            gamma, beta, rows, n, eps, row_index, row_mask, stream);
   }
   return fail(TJK_EINVAL, "tjk_add_layernorm: bad out dtype %d", out_dtype);
@@ -195,19 +232,19 @@ static int dispatch_out(int out_dtype, const void* res, int64_t ld_res, const vo
 
 template <typename TRes>
 static int dispatch_delta(int delta_dtype, int out_dtype, const void* res, int64_t ld_res,
-                          const void* delta, int64_t ld_delta, float* res_out, int64_t ld_res_out,
+                          const void* delta, int64_t ld_delta, int n_delta, int64_t delta_stride, float* res_out, int64_t ld_res_out,
                           void* out, int64_t ld_out, const float* gamma, const float* beta,
                           int64_t rows, int n, float eps, const int32_t* row_index,
                           const uint8_t* row_mask, hipStream_t stream) {
   switch (delta_dtype) {
     case TJK_F32:
-      return dispatch_out<TRes, float>(out_dtype, res, ld_res, delta, ld_delta, res_out, ld_res_out, out,
+      return dispatch_out<TRes, float>(out_dtype, res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ld_res_out, out,
                                        ld_out, gamma, beta, rows, n, eps, row_index, row_mask, stream);
     case TJK_F16:
-      return dispatch_out<TRes, f16>(out_dtype, res, ld_res, delta, ld_delta, res_out, ld_res_out, out,
+      return dispatch_out<TRes, f16>(out_dtype, res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ld_res_out, out,
                                      ld_out, gamma, beta, rows, n, eps, row_index, row_mask, stream);
     case TJK_BF16:
-      return dispatch_out<TRes, bf16>(out_dtype, res, ld_res, delta, ld_delta, res_out, ld_res_out, out,
+      return dispatch_out<TRes, bf16>(out_dtype, res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ld_res_out, out,
                                       ld_out, gamma, beta, rows, n, eps, row_index, row_mask, stream);
   }
   return fail(TJK_EINVAL, "tjk_add_layernorm: bad delta dtype %d", delta_dtype);
@@ -223,6 +260,7 @@ extern "C" const char* tjk_last_error_string(void) { return g_err; }
 
 extern "C" int tjk_add_layernorm(const void* res, int res_dtype, int64_t ld_res,
                                  const void* delta, int delta_dtype, int64_t ld_delta,
+                                 int delta_splits, int64_t delta_split_stride,
                                  float* res_out, int64_t ld_res_out,
                                  void* out, int out_dtype, int64_t ld_out,
                                  const float* gamma, const float* beta,
@@ -250,17 +288,24 @@ extern "C" int tjk_add_layernorm(const void* res, int res_dtype, int64_t ld_res,
   // in-place residual update would race with other rows' reads.
   if (row_index && res_out && (const void*)res_out == res)
     return fail(TJK_EINVAL, "tjk_add_layernorm: row_index with res_out aliasing res");
+  if (delta && (delta_splits < 1 || (delta_splits > 1 && (delta_split_stride < rows * ld_delta ||
+                                                          delta_split_stride % 4 != 0))))
+    return fail(TJK_EINVAL, "tjk_add_layernorm: delta_splits=%d needs a split stride >= rows x ld_delta, "
+                "multiple of 4", delta_splits);
+  if (delta && delta_splits > 1 && n > 1024)
+    return fail(TJK_EUNSUPPORTED, "tjk_add_layernorm: split deltas need n <= 1024");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int dd = delta ? delta_dtype : res_dtype;
+  const int nd = delta ? delta_splits : 0;
   switch (res_dtype) {
     case TJK_F32:
-      return dispatch_delta<float>(dd, out_dtype, res, ld_res, delta, ld_delta, res_out, ld_res_out, out,
+      return dispatch_delta<float>(dd, out_dtype, res, ld_res, delta, ld_delta, nd, delta_split_stride, res_out, ld_res_out, out,
                                    ld_out, gamma, beta, rows, (int)n, eps, row_index, row_mask, s);
     case TJK_F16:
-      return dispatch_delta<f16>(dd, out_dtype, res, ld_res, delta, ld_delta, res_out, ld_res_out, out,
+      return dispatch_delta<f16>(dd, out_dtype, res, ld_res, delta, ld_delta, nd, delta_split_stride, res_out, ld_res_out, out,
                                  ld_out, gamma, beta, rows, (int)n, eps, row_index, row_mask, s);
     case TJK_BF16:
-      return dispatch_delta<bf16>(dd, out_dtype, res, ld_res, delta, ld_delta, res_out, ld_res_out, out,
+      return dispatch_delta<bf16>(dd, out_dtype, res, ld_res, delta, ld_delta, nd, delta_split_stride, res_out, ld_res_out, out,
                                   ld_out, gamma, beta, rows, (int)n, eps, row_index, row_mask, s);
   }
   return fail(TJK_EINVAL, "tjk_add_layernorm: bad res dtype %d", res_dtype);

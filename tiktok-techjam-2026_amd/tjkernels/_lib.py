@@ -15,9 +15,10 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede the library load; see module docstring)
 
 LIB_PATH = Path(__file__).with_name("libtjk.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 F32, F16, BF16 = 0, 1, 2
+OK, EINVAL, EUNSUPPORTED = 0, -1, -2
 EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RESIDUAL = 0, 1, 2
 
 DTYPE_CODES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
@@ -29,26 +30,23 @@ _vp, _i64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_
 _SIGNATURES = {
     "tjk_abi_version": (_i32, []),
     "tjk_last_error_string": (ctypes.c_char_p, []),
-    "tjk_add_layernorm": (_i32, [_vp, _i32, _i64, _vp, _i32, _i64, _vp, _i64, _vp, _i32, _i64,
+    "tjk_add_layernorm": (_i32, [_vp, _i32, _i64, _vp, _i32, _i64, _i32, _i64, _vp, _i64, _vp, _i32, _i64,
                                  _vp, _vp, _i64, _i64, _f32, _vp, _vp, _vp]),
     "tjk_gemm_bias": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64,
                              _i32, _i32, _i32, _vp]),
-    "tjk_gemm_bias_ws": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64,
-                                _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp]),
-    "tjk_gemm_workspace_bytes": (ctypes.c_size_t, [_i32, _i32]),
     "tjk_gemm_plan_count": (_i32, [_i32]),
     "tjk_gemm_plan_info": (_i32, [_i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32),
-                                  ctypes.POINTER(_i32)]),
+                                  ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
     "tjk_flash_fwd": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _i64, _i32, _i32, _i32, _i32,
                              _f32, _i32, _vp, _vp, _vp, _i32, _i32, _vp]),
     "tjk_flash_plan_count": (_i32, [_i32]),
     "tjk_flash_fwd_sched": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _f32, _i32,
-                                   _vp, _vp, _i32, _vp, _i32, _i32, _vp]),
+                                   _vp, _vp, _i32, _vp, ctypes.c_size_t, _i32, _i32, _vp]),
     "tjk_flash_partial_bytes": (ctypes.c_size_t, [_i32, _i32]),
     "tjk_flash_sched_occupancy": (_i32, [_i32, _i32]),
-    "tjk_ffn": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64,
-                       _i32, _i32, _i32, _vp]),
-    "tjk_ffn_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i32]),
+    "tjk_ffn": (_i32, [_vp, _i32, _i64, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32,
+                       _i64, _i64, _i64, _i32, _vp]),
+    "tjk_ffn_supported": (_i32, [_i64, _i64, _i32, _i32]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

@@ -36,7 +36,7 @@ import torch
 
 from . import ops
 from .modules import UserOptimizedTransformer
-from .plans import Plan, default_plan, device_arch, save_plans, set_override, shape_key
+from .plans import Plan, default_plan, device_arch, fused_ffn_ok, save_plans, set_override, shape_key
 from .workloads import WORKLOADS, Workload, make_inputs, make_state_dict
 
 HELD_OUT_SEEDS = [777, 4242]
@@ -171,8 +171,10 @@ def tune_workload(w: Workload, trials: int = 2, margin: float = 0.85, iters: int
     # prefix-masked tokens M follows the input lengths.
 
     # coordinate descent over the plan-level knobs
-    for knob, values in (("attn_plan", [0, 1, 3]), ("residual_epilogue", [True, False]),
-                         ("cuda_graph", [True, False])):
+    knobs = [("attn_plan", [0, 1, 3]), ("residual_epilogue", [True, False]), ("cuda_graph", [True, False])]
+    if fused_ffn_ok(w.d_model, w.ffn_dim, cur["plan"].compute_dtype):
+        knobs.insert(0, ("ffn", ["gemm", "fused"]))
+    for knob, values in knobs:
         for v in values:
             if getattr(cur["plan"], knob) == v:
                 continue

@@ -1,42 +1,39 @@
-"""Execution engine: packs weights once, then runs the plan's HIP kernels.
+"""Execution engine of the hook: the reference's tjkernels/engine.py:58-324.
 
-Mirrors the reference engine (tjkernels/engine.py:58-324): a per-module
-``Engine`` cached on the module with ``object.__setattr__`` (so the
-``state_dict`` is untouched), weights packed once per (compute dtype,
-device), a mask classifier memoised on tensor identity, a per-shape plan
-cache, and an optional whole-forward hipGraph.
+An ``Engine`` lives on the module (set with ``object.__setattr__``, so the
+``state_dict`` keeps the baseline's keys) and owns packed copies of the
+module's parameters, never the parameters themselves.  A forward is a
+pre-LN causal encoder over an fp32 residual stream ``res``:
 
-The forward (reference :205-269) is a pre-LN causal encoder with an fp32
-residual stream ``res``:
+    res, h = x, LN1(x)                     layer 0: the first LayerNorm
+    per layer:
+        qkv  = h Wqkv^T + bqkv             one [3d, d] GEMM, rows q | k | v
+        ctx  = attention(qkv viewed as [B, S, 3, H, hd])
+        res += ctx Wo^T + bo               GEMM residual epilogue
+        FFN:  "gemm"  -- h = LN2(res); mid = gelu_erf(h W1^T + b1) (GEMM
+                         epilogue); res += mid W2^T + b2 (residual epilogue)
+              "fused" -- one launch: LN2, both GEMMs and GELU with the
+                         [T, f] intermediate in LDS; its f-slice partials
+                         are summed by the next LayerNorm
+        h = LN1 of the next layer (res [+ pending FFN partials])
+    out = LN_final(res [+ pending]), padded rows exact zeros
 
-    LN1(layer 0) reads x in the model dtype and writes res = fp32(x) and h
-    for each layer:
-        qkv  = h Wqkv^T + bqkv                    (one [3d, d] GEMM, packed q|k|v)
-        ctx  = flash_attention(qkv as [B,S,3,H,hd])
-        res += ctx Wo^T + bo                      (GEMM residual epilogue)
-        h    = LN2(res)
-        mid  = gelu_erf(h W1^T + b1)              (GEMM GELU epilogue)
-        res += mid W2^T + b2                      (GEMM residual epilogue)
-        h    = LN1 of the next layer (res)
-    out = LN_final(res), padded rows written as exact zeros
+``Plan.residual_epilogue=False`` writes the out-proj and FFN outputs in the
+compute dtype and lets the following LayerNorm add them, the reference's
+deferred-residual scheme (engine.py:232-264).
 
-With ``Plan.residual_epilogue=False`` the out-proj / FFN outputs are instead
-written in the compute dtype and added by the following LayerNorm, which is
-the reference's deferred-residual scheme (engine.py:232-264).
-
-Masks: NONE (no mask or all valid) needs nothing.  PREFIX (every sequence
-valid on a prefix of length len_b) packs the valid tokens: no valid row ever
-depends on a padded one -- under causal attention a valid query never sees
-a key at or beyond its sequence's length (engine.py:147-150), without it the
-padded keys are masked, and every other op is row-wise -- so the first
-LayerNorm gathers the sum(len_b) valid rows into consecutive rows, every
-GEMM and LayerNorm runs on those rows only, attention runs on the packed
-sequences (cu_seqlens), and the final LayerNorm scatters the rows back to
-[B, S] order with padded rows written as exact zeros.  The reference
-computes the padded rows and zeroes them at the end (engine.py:267-268);
-the valid rows come out the same either way.  GENERAL (any other mask)
-hands the mask to the attention kernel as a per-key mask, computes every
-row and zeroes the padded ones in the final LayerNorm.
+Masks (reference engine.py:131-158): NONE -- no mask or every token valid;
+PREFIX -- sequence b valid on its first len_b tokens; GENERAL -- anything
+else.  PREFIX forwards pack the valid tokens: no valid row depends on a
+padded one (under causal attention a valid query never sees a key at or past
+its sequence's length, engine.py:147-150; without it the padded keys are
+masked; every other op is row-wise), so the first LayerNorm gathers the
+sum(len_b) valid rows into consecutive rows, every GEMM and LayerNorm runs on
+those rows, attention runs on the packed sequences (cu_seqlens), and the
+final LayerNorm scatters them back with the padded rows written as exact
+zeros.  The reference computes the padded rows and zeroes them at the end
+(engine.py:267-268); the valid rows come out the same.  GENERAL hands the
+mask to attention as a per-key mask and zeroes padded rows at the end.
 """
 
 from __future__ import annotations
@@ -44,7 +41,7 @@ from __future__ import annotations
 import os
 from collections import OrderedDict
 from dataclasses import dataclass
-from typing import Dict, List, Optional, Tuple
+from typing import Dict, NamedTuple, Optional, Tuple
 
 import torch
 
@@ -53,33 +50,121 @@ from .graphs import GraphCache
 from .plans import Plan, select_plan
 
 try:
-    from torch.utils.weak import WeakTensorKeyDictionary as _WeakDict
-except Exception:  # pragma: no cover
-    _WeakDict = dict
+    from torch.utils.weak import WeakTensorKeyDictionary
+except ImportError:  # pragma: no cover - torch < 2.0
+    WeakTensorKeyDictionary = None
 
 MASK_NONE, MASK_PREFIX, MASK_GENERAL = 0, 1, 2
 
 
-@dataclass
-class LayerWeights:
-    """Packed weights of one block; every matrix keeps nn.Linear's [out, in]
-    layout, which is exactly the K-contiguous operand the GEMM wants."""
+# --------------------------------------------------------------- weights
 
-    ln1_w: torch.Tensor
-    ln1_b: torch.Tensor
-    ln1_eps: float
-    wqkv: torch.Tensor   # [3d, d]: rows q | k | v
-    bqkv: torch.Tensor   # [3d]
-    wo: torch.Tensor     # [d, d]
-    bo: torch.Tensor
-    ln2_w: torch.Tensor
-    ln2_b: torch.Tensor
-    ln2_eps: float
-    w1: torch.Tensor     # [f, d]
-    b1: torch.Tensor
-    w2: torch.Tensor     # [d, f]
-    b2: torch.Tensor
+class Norm(NamedTuple):
+    weight: torch.Tensor  # fp32 [d]
+    bias: torch.Tensor    # fp32 [d]
+    eps: float
 
+
+class Linear(NamedTuple):
+    weight: torch.Tensor  # compute dtype, nn.Linear [out, in]: the K-contiguous GEMM operand
+    bias: torch.Tensor    # compute dtype [out]
+
+
+class BlockWeights(NamedTuple):
+    norm1: Norm
+    qkv: Linear   # [3d, d]: q rows, then k, then v
+    out: Linear
+    norm2: Norm
+    fc1: Linear   # [f, d]
+    fc2: Linear   # [d, f]
+
+
+class ModelWeights(NamedTuple):
+    blocks: Tuple[BlockWeights, ...]
+    final: Norm
+    compute_dtype: torch.dtype
+
+
+def _norm(ln: torch.nn.LayerNorm) -> Norm:
+    return Norm(ln.weight.detach().float().contiguous(), ln.bias.detach().float().contiguous(), ln.eps)
+
+
+def _linear(*layers: torch.nn.Linear, dtype: torch.dtype) -> Linear:
+    weight = torch.cat([layer.weight.detach() for layer in layers], 0)
+    bias = torch.cat([layer.bias.detach() for layer in layers], 0)
+    return Linear(weight.to(dtype).contiguous(), bias.to(dtype).contiguous())
+
+
+def pack_weights(module: torch.nn.Module, dtype: torch.dtype) -> ModelWeights:
+    """Copies of the module's parameters in the layout the kernels take:
+    matrices in the compute dtype (nn.Linear layout kept, q/k/v stacked into
+    one [3d, d] operand), LayerNorm parameters in fp32."""
+    blocks = []
+    for blk in module.layers:
+        at = blk.attention
+        blocks.append(BlockWeights(
+            norm1=_norm(blk.norm1),
+            qkv=_linear(at.q_proj, at.k_proj, at.v_proj, dtype=dtype),
+            out=_linear(at.out_proj, dtype=dtype),
+            norm2=_norm(blk.norm2),
+            fc1=_linear(blk.ffn_in, dtype=dtype),
+            fc2=_linear(blk.ffn_out, dtype=dtype),
+        ))
+    return ModelWeights(tuple(blocks), _norm(module.final_norm), dtype)
+
+
+# ------------------------------------------------------------------ masks
+
+@dataclass(frozen=True)
+class MaskInfo:
+    mode: int
+    lengths: Optional[Tuple[int, ...]] = None  # PREFIX only
+
+
+def _version(t: torch.Tensor) -> Optional[int]:
+    # inference tensors keep no version counter (torch raises on access)
+    return None if t.is_inference() else t._version
+
+
+class TensorMemo:
+    """Host-side facts derived from a device tensor (one sync each),
+    remembered per tensor object and recomputed when the tensor's version
+    counter shows an in-place update since.  Tensors created under
+    ``torch.inference_mode`` have no version counter: for them the memo is
+    per object only, as the reference's (engine.py:139-141), so such a
+    tensor must not be updated in place between forwards."""
+
+    def __init__(self) -> None:
+        self._memo = WeakTensorKeyDictionary() if WeakTensorKeyDictionary is not None else {}
+
+    def get(self, t: torch.Tensor, derive):
+        version = _version(t)
+        hit = self._memo.get(t)
+        if hit is not None and hit[0] == version:
+            return hit[1]
+        value = derive(t)
+        self._memo[t] = (version, value)
+        return value
+
+
+def classify_mask(mask: torch.Tensor) -> MaskInfo:
+    """NONE / PREFIX (with the lengths) / GENERAL of a [B, S] bool mask."""
+    seq = mask.shape[-1]
+    counts = mask.sum(dim=-1)
+    as_prefix = torch.arange(seq, device=mask.device)[None, :] < counts[:, None]
+    if not bool(torch.equal(as_prefix, mask)):
+        return MaskInfo(MASK_GENERAL)
+    lengths = tuple(int(n) for n in counts.tolist())
+    return MaskInfo(MASK_NONE) if min(lengths) == seq else MaskInfo(MASK_PREFIX, lengths)
+
+
+def lengths_info(lengths: torch.Tensor, seq: int) -> MaskInfo:
+    """MaskInfo of integer prefix lengths [B] (clamped to [0, seq])."""
+    host = tuple(min(max(int(n), 0), seq) for n in lengths.tolist())
+    return MaskInfo(MASK_NONE) if min(host, default=seq) == seq else MaskInfo(MASK_PREFIX, host)
+
+
+# ---------------------------------------------------------------- packing
 
 @dataclass
 class Packing:
@@ -94,157 +179,123 @@ class Packing:
 
 
 def build_packing(lengths: Tuple[int, ...], seq: int, device: torch.device) -> Packing:
-    cu = [0]
+    starts = [0]
     for n in lengths:
-        cu.append(cu[-1] + n)
-    gather = torch.cat([torch.arange(b * seq, b * seq + n, dtype=torch.int32)
-                        for b, n in enumerate(lengths)]) if cu[-1] else torch.zeros(0, dtype=torch.int32)
+        starts.append(starts[-1] + n)
+    if starts[-1]:
+        gather = torch.cat([torch.arange(b * seq, b * seq + n, dtype=torch.int32) for b, n in enumerate(lengths)])
+    else:
+        gather = torch.zeros(0, dtype=torch.int32)
     scatter = torch.full((len(lengths) * seq,), -1, dtype=torch.int32)
-    scatter[gather.long()] = torch.arange(cu[-1], dtype=torch.int32)
-    return Packing(lengths=tuple(lengths), tokens=cu[-1], gather=gather.to(device),
-                   scatter=scatter.to(device), cu_seqlens=torch.tensor(cu, dtype=torch.int32, device=device))
+    scatter[gather.long()] = torch.arange(starts[-1], dtype=torch.int32)
+    return Packing(tuple(lengths), starts[-1], gather.to(device), scatter.to(device),
+                   torch.tensor(starts, dtype=torch.int32, device=device))
 
 
-@dataclass
-class _Fwd:
-    """Static context of one forward shape: workspace views of the processed
-    rows, tile plans, masks and the packing it runs on."""
+# ---------------------------------------------------------------- forward
 
-    batch: int
-    seq: int
-    mode: int
-    packing: Optional[Packing]
-    rows: int
-    gather: Optional[torch.Tensor] = None
-    scatter: Optional[torch.Tensor] = None
-    key_mask: Optional[torch.Tensor] = None
-    row_mask: Optional[torch.Tensor] = None
-    res: Optional[torch.Tensor] = None
-    h: Optional[torch.Tensor] = None
-    qkv: Optional[torch.Tensor] = None
-    ctx: Optional[torch.Tensor] = None
-    mid: Optional[torch.Tensor] = None
-    delta: Optional[torch.Tensor] = None
-    tp_qkv: int = -1
-    tp_out: int = -1
-    tp_ffn1: int = -1
-    tp_ffn2: int = -1
-    use_sched: bool = False
+class ModelShape(NamedTuple):
+    d_model: int
+    heads: int
+    head_dim: int
+    ffn_dim: int
+    layers: int
+    causal: bool
+
+
+class Tiles(NamedTuple):
+    qkv: int
+    out: int
+    fc1: int
+    fc2: int
 
 
 @dataclass
 class Workspace:
-    res: torch.Tensor    # [T, d] fp32
-    h: torch.Tensor      # [T, d] compute dtype
-    qkv: torch.Tensor    # [T, 3d]
-    ctx: torch.Tensor    # [T, d]
-    mid: torch.Tensor    # [T, f]
-    delta: Optional[torch.Tensor]  # [T, d] (deferred-residual plans only)
+    """Activation buffers of one (B, S, plan), sized for every row."""
+
+    res: torch.Tensor                # [T, d] fp32 residual stream
+    h: torch.Tensor                  # [T, d] LayerNorm output
+    qkv: torch.Tensor                # [T, 3d]
+    ctx: torch.Tensor                # [T, d] attention output
+    mid: Optional[torch.Tensor]      # [T, f] FFN intermediate (two-launch FFN)
+    delta: Optional[torch.Tensor]    # [T, d] deferred block output (deferred plans)
+    parts: Optional[torch.Tensor]    # [splits, T, d] fp32 FFN partials (fused FFN)
+
+
+@dataclass
+class Forward:
+    """Static context of one forward shape: views of the processed rows,
+    tile plans, the masks and packing it runs on."""
+
+    batch: int
+    seq: int
+    mode: int
+    rows: int
+    ws: Workspace
+    tiles: Tiles
+    packing: Optional[Packing] = None
+    key_mask: Optional[torch.Tensor] = None
+    use_sched: bool = False
+    splits: int = 1
+    pending: Optional[torch.Tensor] = None  # what the next LayerNorm adds to res
+
+    def view(self, name: str) -> Optional[torch.Tensor]:
+        t = getattr(self.ws, name)
+        if t is None:
+            return None
+        return t[:, :self.rows] if name == "parts" else t[:self.rows]
 
 
 class Engine:
     def __init__(self, module: torch.nn.Module) -> None:
         cfg = module.config
-        param = next(module.parameters())
-        self.device = param.device
-        self.dtype = param.dtype
-        self.d_model = cfg.d_model
-        self.num_heads = cfg.num_heads
-        self.head_dim = cfg.d_model // cfg.num_heads
-        self.ffn_dim = cfg.ffn_dim
-        self.num_layers = cfg.num_layers
-        self.causal = cfg.causal
+        first = next(module.parameters())
+        self.module = module
+        self.device, self.dtype = first.device, first.dtype
+        self.shape = ModelShape(cfg.d_model, cfg.num_heads, cfg.d_model // cfg.num_heads, cfg.ffn_dim,
+                                cfg.num_layers, cfg.causal)
         self.plan: Optional[Plan] = None
-        self._plan_cache: Dict[Tuple[int, int], Plan] = {}
-        self._built_for: Optional[Tuple] = None
-        self.layers: List[LayerWeights] = []
-        self.final_ln: Optional[Tuple[torch.Tensor, torch.Tensor, float]] = None
-        self._module = module
+        self.weights: Optional[ModelWeights] = None
+        self._plans: Dict[Tuple[int, int], Plan] = {}
+        self._masks = TensorMemo()
         self._graphs = GraphCache()
-        self._mask_modes = _WeakDict()
         self._workspaces: Dict[Tuple, Workspace] = {}
         self._packings: "OrderedDict[Tuple[int, Tuple[int, ...]], Packing]" = OrderedDict()
         self._static_masks: Dict[Tuple[int, int], torch.Tensor] = {}
-        self._fwds: Dict[Tuple, "_Fwd"] = {}
+        self._forwards: "OrderedDict[Tuple, Forward]" = OrderedDict()
+        self.check_waits = os.environ.get("TJ_CHECK_WAITS") == "1"
 
-    # ------------------------------------------------------------- weights
+    # compatibility names used by tools and tests
+    @property
+    def d_model(self) -> int:
+        return self.shape.d_model
 
-    @torch.no_grad()
-    def _build(self, plan: Plan) -> None:
-        key = (plan.compute_dtype, self.dtype, self.device)
-        if self._built_for == key:
+    @property
+    def num_heads(self) -> int:
+        return self.shape.heads
+
+    def _use_weights(self, plan: Plan) -> None:
+        if self.weights is not None and self.weights.compute_dtype == plan.compute_dtype:
             return
-        cdt = plan.compute_dtype
-        layers: List[LayerWeights] = []
-        for block in self._module.layers:
-            attn = block.attention
-            wqkv = torch.cat([attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight], 0)
-            bqkv = torch.cat([attn.q_proj.bias, attn.k_proj.bias, attn.v_proj.bias], 0)
-            layers.append(LayerWeights(
-                ln1_w=block.norm1.weight.float().contiguous(),
-                ln1_b=block.norm1.bias.float().contiguous(),
-                ln1_eps=block.norm1.eps,
-                wqkv=wqkv.to(cdt).contiguous(),
-                bqkv=bqkv.to(cdt).contiguous(),
-                wo=attn.out_proj.weight.to(cdt).contiguous(),
-                bo=attn.out_proj.bias.to(cdt).contiguous(),
-                ln2_w=block.norm2.weight.float().contiguous(),
-                ln2_b=block.norm2.bias.float().contiguous(),
-                ln2_eps=block.norm2.eps,
-                w1=block.ffn_in.weight.to(cdt).contiguous(),
-                b1=block.ffn_in.bias.to(cdt).contiguous(),
-                w2=block.ffn_out.weight.to(cdt).contiguous(),
-                b2=block.ffn_out.bias.to(cdt).contiguous(),
-            ))
-        self.layers = layers
-        fn = self._module.final_norm
-        self.final_ln = (fn.weight.float().contiguous(), fn.bias.float().contiguous(), fn.eps)
-        self._built_for = key
+        with torch.no_grad():
+            self.weights = pack_weights(self.module, plan.compute_dtype)
         self._graphs.clear()
-        self._fwds.clear()
+        self._forwards.clear()
         self._workspaces.clear()
 
-    def _workspace(self, batch: int, seq: int, plan: Plan) -> Workspace:
-        key = (batch, seq, plan.compute_dtype, plan.residual_epilogue)
-        ws = self._workspaces.get(key)
-        if ws is None:
-            t, d, f = batch * seq, self.d_model, self.ffn_dim
-            cdt, dev = plan.compute_dtype, self.device
-            ws = Workspace(
-                res=torch.empty((t, d), dtype=torch.float32, device=dev),
-                h=torch.empty((t, d), dtype=cdt, device=dev),
-                qkv=torch.empty((t, 3 * d), dtype=cdt, device=dev),
-                ctx=torch.empty((t, d), dtype=cdt, device=dev),
-                mid=torch.empty((t, f), dtype=cdt, device=dev),
-                delta=None if plan.residual_epilogue else torch.empty((t, d), dtype=cdt, device=dev),
-            )
-            self._workspaces[key] = ws
-        return ws
+    # -- masks and packing
 
-    # ---------------------------------------------------------------- mask
+    def _mask_info(self, mask: Optional[torch.Tensor]) -> Tuple[int, Optional[Tuple[int, ...]]]:
+        """(mode, prefix lengths) of a [B, S] bool mask, one host sync per
+        mask tensor and version."""
+        if mask is None:
+            return MASK_NONE, None
+        info = self._masks.get(mask, classify_mask)
+        return info.mode, info.lengths
 
     def _mask_mode(self, mask: Optional[torch.Tensor]) -> int:
         return self._mask_info(mask)[0]
-
-    def _mask_info(self, mask: Optional[torch.Tensor]) -> Tuple[int, Optional[Tuple[int, ...]]]:
-        """(NONE / PREFIX / GENERAL, prefix lengths for PREFIX) with one host
-        sync per distinct mask tensor, memoised on tensor identity as
-        tjkernels/engine.py:131-158 does."""
-        if mask is None:
-            return MASK_NONE, None
-        cached = self._mask_modes.get(mask)
-        if cached is not None:
-            return cached
-        lengths = mask.sum(dim=-1)
-        positions = torch.arange(mask.shape[-1], device=mask.device)
-        prefix = positions[None, :] < lengths[:, None]
-        if bool(torch.equal(prefix, mask)):
-            host = tuple(int(n) for n in lengths.tolist())
-            info = (MASK_NONE, None) if min(host) == mask.shape[-1] else (MASK_PREFIX, host)
-        else:
-            info = (MASK_GENERAL, None)
-        self._mask_modes[mask] = info
-        return info
 
     def _packing(self, lengths: Tuple[int, ...], seq: int) -> Packing:
         key = (seq, lengths)
@@ -252,102 +303,138 @@ class Engine:
         if pk is None:
             pk = build_packing(lengths, seq, self.device)
             self._packings[key] = pk
-            while len(self._packings) > 64:
+            if len(self._packings) > 64:
                 self._packings.popitem(last=False)
         else:
             self._packings.move_to_end(key)
         return pk
 
-    # ------------------------------------------------------------- compute
+    # -- per-shape preparation
+
+    def _workspace(self, batch: int, seq: int, plan: Plan, splits: int) -> Workspace:
+        fused = plan.ffn == "fused"
+        key = (batch, seq, plan.compute_dtype, plan.residual_epilogue, fused, splits)
+        ws = self._workspaces.get(key)
+        if ws is None:
+            t, d, f = batch * seq, self.shape.d_model, self.shape.ffn_dim
+            cdt, dev = plan.compute_dtype, self.device
+
+            def buf(*dims, dtype=cdt):
+                return torch.empty(dims, dtype=dtype, device=dev)
+
+            ws = Workspace(res=buf(t, d, dtype=torch.float32), h=buf(t, d), qkv=buf(t, 3 * d), ctx=buf(t, d),
+                           mid=None if fused else buf(t, f),
+                           delta=None if plan.residual_epilogue else buf(t, d),
+                           parts=buf(splits, t, d, dtype=torch.float32) if fused and splits > 1 else None)
+            self._workspaces[key] = ws
+        return ws
 
     def _prepare(self, batch: int, seq: int, mode: int, packing: Optional[Packing],
-                 mask: Optional[torch.Tensor]) -> "_Fwd":
-        """Everything a forward needs besides x and the output: workspace
-        views, tile plans, the attention schedule.  Launches nothing except
-        the one-time tile timing / schedule build of a new shape."""
-        plan = self.plan
-        assert plan is not None and self.final_ln is not None
-        ws = self._workspace(batch, seq, plan)
-        fw = _Fwd(batch=batch, seq=seq, mode=mode, packing=packing, rows=batch * seq)
-        if mode == MASK_PREFIX:
-            assert packing is not None
-            fw.rows, fw.gather, fw.scatter = packing.tokens, packing.gather, packing.scatter
-        elif mode == MASK_GENERAL:
-            fw.key_mask = mask
-            fw.row_mask = mask.reshape(-1)
-        rows = fw.rows
-        fw.res, fw.h, fw.qkv, fw.ctx, fw.mid = (ws.res[:rows], ws.h[:rows], ws.qkv[:rows],
-                                                ws.ctx[:rows], ws.mid[:rows])
-        fw.delta = None if ws.delta is None else ws.delta[:rows]
-        # Tile plans: forced by the Plan, else measured once per shape.
-        cdt, d, f = plan.compute_dtype, self.d_model, self.ffn_dim
+                 mask: Optional[torch.Tensor]) -> Forward:
+        """Everything a forward needs besides x and its output.  Launches
+        nothing except the one-time tile timing and schedule build of a new
+        shape."""
+        plan, shp = self.plan, self.shape
+        fused = plan.ffn == "fused"
+        splits = (plan.ffn_splits or max(shp.ffn_dim // 128, 1)) if fused else 1
+        rows = packing.tokens if mode == MASK_PREFIX else batch * seq
+        cdt, d, f = plan.compute_dtype, shp.d_model, shp.ffn_dim
         epi_res = ops.EPI_BIAS_RESIDUAL if plan.residual_epilogue else ops.EPI_BIAS
-        fw.tp_qkv = tiles.gemm_plan(rows, 3 * d, d, cdt, ops.EPI_BIAS, plan.gemm_qkv)
-        fw.tp_out = tiles.gemm_plan(rows, d, d, cdt, epi_res, plan.gemm_out)
-        fw.tp_ffn1 = tiles.gemm_plan(rows, f, d, cdt, ops.EPI_BIAS_GELU, plan.gemm_ffn1)
-        fw.tp_ffn2 = tiles.gemm_plan(rows, d, f, cdt, epi_res, plan.gemm_ffn2)
+        tp = Tiles(
+            qkv=tiles.gemm_plan(rows, 3 * d, d, cdt, ops.EPI_BIAS, plan.gemm_qkv),
+            out=tiles.gemm_plan(rows, d, d, cdt, epi_res, plan.gemm_out),
+            fc1=-1 if fused else tiles.gemm_plan(rows, f, d, cdt, ops.EPI_BIAS_GELU, plan.gemm_ffn1),
+            fc2=-1 if fused else tiles.gemm_plan(rows, d, f, cdt, epi_res, plan.gemm_ffn2))
+        fw = Forward(batch=batch, seq=seq, mode=mode, rows=rows, ws=self._workspace(batch, seq, plan, splits),
+                     tiles=tp, packing=packing if mode == MASK_PREFIX else None,
+                     key_mask=mask if mode == MASK_GENERAL else None, splits=splits)
+        if fused:
+            fw.pending = fw.view("parts")
+        elif not plan.residual_epilogue:
+            fw.pending = fw.view("delta")
         # Packed 2-byte attention below 2048 keys follows a longest-first work
-        # list (tjkernels.schedule; attn_plan -1 or 4).  Longer sequences run
-        # the plain plan-1 kernel, measured faster there; other plan ids
-        # force the plain kernel.
-        fw.use_sched = (mode == MASK_PREFIX and cdt != torch.float32 and rows > 0
-                        and (plan.attn_plan == 4 or (plan.attn_plan == -1 and max(packing.lengths) < 2048)))
-        if fw.use_sched and packing.attn is None:
-            packing.attn = sched_mod.build_schedule(packing.lengths, self.num_heads, self.head_dim,
-                                                    self.causal, cdt, self.device)
+        # list (attn_plan -1 or 4); longer sequences run the plain plan-0/1
+        # kernel, measured faster there; other plan ids force the plain kernel.
+        pk = fw.packing
+        fw.use_sched = (pk is not None and cdt != torch.float32 and rows > 0
+                        and (plan.attn_plan == 4 or (plan.attn_plan == -1 and max(pk.lengths) < 2048)))
+        if fw.use_sched and pk.attn is None:
+            pk.attn = sched_mod.build_schedule(pk.lengths, shp.heads, shp.head_dim, shp.causal, cdt, self.device)
         return fw
 
-    def _first(self, fw: "_Fwd", x: torch.Tensor) -> None:
-        """Layer-0 LN1: reads x (packing it under a prefix mask), writes the
-        fp32 residual and h."""
-        lw = self.layers[0]
-        ops.add_layernorm(x.reshape(fw.batch * fw.seq, self.d_model), None, lw.ln1_w, lw.ln1_b,
-                          lw.ln1_eps, fw.h, res_out=fw.res, row_index=fw.gather)
+    # -- the launches
 
-    def _body(self, fw: "_Fwd") -> None:
+    def _first(self, fw: Forward, x: torch.Tensor) -> None:
+        """Layer-0 LN1: reads x (gathering the valid rows of a prefix mask),
+        writes the fp32 residual and h."""
+        n1 = self.weights.blocks[0].norm1
+        gather = fw.packing.gather if fw.packing is not None else None
+        ops.add_layernorm(x.reshape(fw.batch * fw.seq, self.shape.d_model), None, n1.weight, n1.bias, n1.eps,
+                          fw.view("h"), res_out=fw.view("res"), row_index=gather)
+
+    def _attention(self, fw: Forward) -> None:
+        shp = self.shape
+        qkv, ctx, pk = fw.view("qkv"), fw.view("ctx"), fw.packing
+        if fw.use_sched:
+            ops.flash_attention_sched(qkv.view(fw.rows, 3, shp.heads, shp.head_dim), ctx, pk.cu_seqlens,
+                                      max(pk.lengths), pk.attn, causal=shp.causal)
+        elif pk is not None:
+            ops.flash_attention(qkv.view(fw.rows, 3, shp.heads, shp.head_dim), ctx, causal=shp.causal,
+                                plan=self.plan.attn_plan, cu_seqlens=pk.cu_seqlens, max_seqlen=max(pk.lengths))
+        else:
+            ops.flash_attention(qkv.view(fw.batch, fw.seq, 3, shp.heads, shp.head_dim), ctx, causal=shp.causal,
+                                key_mask=fw.key_mask, plan=self.plan.attn_plan)
+
+    def _ffn(self, fw: Forward, blk: BlockWeights) -> None:
+        plan = self.plan
+        res, h, n2 = fw.view("res"), fw.view("h"), blk.norm2
+        if plan.ffn == "fused":
+            parts = fw.view("parts")
+            if plan.residual_epilogue:
+                ln, a = (n2.weight, n2.bias, n2.eps), res  # LayerNorm 2 inside the kernel
+            else:
+                ops.add_layernorm(res, fw.view("delta"), n2.weight, n2.bias, n2.eps, h, res_out=res)
+                ln, a = None, h
+            if parts is None:
+                ops.ffn(a, blk.fc1.weight, blk.fc1.bias, blk.fc2.weight, blk.fc2.bias, res, ln=ln, accumulate=True)
+            else:
+                ops.ffn(a, blk.fc1.weight, blk.fc1.bias, blk.fc2.weight, blk.fc2.bias, parts, splits=fw.splits,
+                        ln=ln)
+            return
+        mid = fw.view("mid")
+        if plan.residual_epilogue:
+            ops.add_layernorm(res, None, n2.weight, n2.bias, n2.eps, h)
+            ops.gemm(h, blk.fc1.weight, blk.fc1.bias, mid, ops.EPI_BIAS_GELU, fw.tiles.fc1)
+            ops.gemm(mid, blk.fc2.weight, blk.fc2.bias, res, ops.EPI_BIAS_RESIDUAL, fw.tiles.fc2)
+        else:
+            delta = fw.view("delta")
+            ops.add_layernorm(res, delta, n2.weight, n2.bias, n2.eps, h, res_out=res)
+            ops.gemm(h, blk.fc1.weight, blk.fc1.bias, mid, ops.EPI_BIAS_GELU, fw.tiles.fc1)
+            ops.gemm(mid, blk.fc2.weight, blk.fc2.bias, delta, ops.EPI_BIAS, fw.tiles.fc2)
+
+    def _body(self, fw: Forward) -> None:
         """Every layer between the first LayerNorm and the final one: the
         part the hipGraph captures (fixed buffers only)."""
-        plan = self.plan
-        heads, hd, rows = self.num_heads, self.head_dim, fw.rows
-        res, h, qkv, ctx, mid, delta = fw.res, fw.h, fw.qkv, fw.ctx, fw.mid, fw.delta
-        fused = plan.residual_epilogue
-        pending = None
-        for i, lw in enumerate(self.layers):
+        res, h, ctx = fw.view("res"), fw.view("h"), fw.view("ctx")
+        for i, blk in enumerate(self.weights.blocks):
             if i > 0:
-                ops.add_layernorm(res, pending, lw.ln1_w, lw.ln1_b, lw.ln1_eps, h,
-                                  res_out=res if pending is not None else None)
-            ops.gemm(h, lw.wqkv, lw.bqkv, qkv, ops.EPI_BIAS, fw.tp_qkv)
-            if fw.use_sched:
-                pk = fw.packing
-                ops.flash_attention_sched(qkv.view(rows, 3, heads, hd), ctx, pk.cu_seqlens,
-                                          max(pk.lengths), pk.attn, causal=self.causal)
-            elif fw.mode == MASK_PREFIX:
-                pk = fw.packing
-                ops.flash_attention(qkv.view(rows, 3, heads, hd), ctx, causal=self.causal,
-                                    plan=plan.attn_plan, cu_seqlens=pk.cu_seqlens,
-                                    max_seqlen=max(pk.lengths))
+                n1 = blk.norm1
+                ops.add_layernorm(res, fw.pending, n1.weight, n1.bias, n1.eps, h,
+                                  res_out=res if fw.pending is not None else None)
+            ops.gemm(h, blk.qkv.weight, blk.qkv.bias, fw.view("qkv"), ops.EPI_BIAS, fw.tiles.qkv)
+            self._attention(fw)
+            if self.plan.residual_epilogue:
+                ops.gemm(ctx, blk.out.weight, blk.out.bias, res, ops.EPI_BIAS_RESIDUAL, fw.tiles.out)
             else:
-                ops.flash_attention(qkv.view(fw.batch, fw.seq, 3, heads, hd), ctx, causal=self.causal,
-                                    key_mask=fw.key_mask, plan=plan.attn_plan)
-            if fused:
-                ops.gemm(ctx, lw.wo, lw.bo, res, ops.EPI_BIAS_RESIDUAL, fw.tp_out)
-                ops.add_layernorm(res, None, lw.ln2_w, lw.ln2_b, lw.ln2_eps, h)
-            else:
-                ops.gemm(ctx, lw.wo, lw.bo, delta, ops.EPI_BIAS, fw.tp_out)
-                ops.add_layernorm(res, delta, lw.ln2_w, lw.ln2_b, lw.ln2_eps, h, res_out=res)
-            ops.gemm(h, lw.w1, lw.b1, mid, ops.EPI_BIAS_GELU, fw.tp_ffn1)
-            if fused:
-                ops.gemm(mid, lw.w2, lw.b2, res, ops.EPI_BIAS_RESIDUAL, fw.tp_ffn2)
-            else:
-                ops.gemm(mid, lw.w2, lw.b2, delta, ops.EPI_BIAS, fw.tp_ffn2)
-                pending = delta  # added by the next LayerNorm (deferred residual)
+                ops.gemm(ctx, blk.out.weight, blk.out.bias, fw.view("delta"), ops.EPI_BIAS, fw.tiles.out)
+            self._ffn(fw, blk)
 
-    def _final(self, fw: "_Fwd", out: torch.Tensor, row_mask: Optional[torch.Tensor]) -> None:
+    def _final(self, fw: Forward, out: torch.Tensor, row_mask: Optional[torch.Tensor]) -> None:
         """Final LayerNorm into the output, padded rows as exact zeros."""
-        fwt, fb, feps = self.final_ln
-        pending = None if self.plan.residual_epilogue else fw.delta
-        ops.add_layernorm(fw.res, pending, fwt, fb, feps, out.view(fw.batch * fw.seq, self.d_model),
-                          row_mask=row_mask, row_index=fw.scatter)
+        fin = self.weights.final
+        scatter = fw.packing.scatter if fw.packing is not None else None
+        ops.add_layernorm(fw.view("res"), fw.pending, fin.weight, fin.bias, fin.eps,
+                          out.view(fw.batch * fw.seq, self.shape.d_model), row_mask=row_mask, row_index=scatter)
 
     def _forward_impl(self, x: torch.Tensor, mask: Optional[torch.Tensor], mode: int,
                       packing: Optional[Packing] = None) -> torch.Tensor:
@@ -357,73 +444,79 @@ class Engine:
         out = torch.empty((batch, seq, d), dtype=self.dtype, device=x.device)
         self._first(fw, x)
         self._body(fw)
-        self._final(fw, out, fw.row_mask)
+        self._final(fw, out, mask.reshape(-1) if mode == MASK_GENERAL else None)
+        self._check(fw)
         return out
 
-    # ---------------------------------------------------------------- call
+    def _check(self, fw: Forward) -> None:
+        """With TJ_CHECK_WAITS=1: raise if the scheduled attention's error
+        word counted a timed-out wait or an invalid item (a host sync)."""
+        if self.check_waits and fw.use_sched:
+            n = sched_mod.error_count(fw.packing.attn)
+            if n:
+                raise RuntimeError(f"tjkernels: scheduled attention reported {n} failed items "
+                                   "(timed-out waits or invalid work items); the output holds NaN rows")
+
+    # -- the call
+
+    def _decode_mask(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> Tuple[Optional[torch.Tensor], MaskInfo]:
+        """The hook's second argument: None, a [B, S] bool-like mask, or
+        integer prefix lengths [B]."""
+        batch, seq = x.shape[:2]
+        if mask is None:
+            return None, MaskInfo(MASK_NONE)
+        if mask.dim() == 1 and not mask.dtype.is_floating_point and mask.dtype != torch.bool:
+            if mask.shape[0] != batch:
+                raise ValueError(f"lengths must be [B], got {tuple(mask.shape)}")
+            return None, self._masks.get(mask, lambda t: lengths_info(t, seq))
+        if tuple(mask.shape) != (batch, seq):
+            raise ValueError(f"valid_token_mask must be [B, S], got {tuple(mask.shape)}")
+        if mask.dtype != torch.bool:
+            mask = mask.to(torch.bool)
+        if not mask.is_contiguous():
+            mask = mask.contiguous()
+        return mask, self._masks.get(mask, classify_mask)
 
     def __call__(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None) -> torch.Tensor:
         if not x.is_cuda:
-            raise RuntimeError("tjkernels runs on ROCm GPUs only (input on "
-                               f"{x.device}); there is no CPU path")
-        if x.dim() != 3 or x.shape[-1] != self.d_model:
-            raise ValueError(f"expected x of shape [B, S, {self.d_model}], got {tuple(x.shape)}")
+            raise RuntimeError(f"tjkernels runs on ROCm GPUs only (input on {x.device}); there is no CPU path")
+        if x.dim() != 3 or x.shape[-1] != self.shape.d_model:
+            raise ValueError(f"expected x of shape [B, S, {self.shape.d_model}], got {tuple(x.shape)}")
         if x.dtype != self.dtype:
             raise ValueError(f"x dtype {x.dtype} != model dtype {self.dtype}")
         if not x.is_contiguous():
             x = x.contiguous()
-        host_lengths: Optional[Tuple[int, ...]] = None
-        if mask is not None and mask.dim() == 1 and not mask.dtype.is_floating_point \
-                and mask.dtype != torch.bool:
-            # forward(x, lengths): int prefix lengths [B]; read once on the host
-            # (the packed layout is sized from them) and turned into the
-            # equivalent prefix mask for the graph path's static inputs.
-            if mask.shape[0] != x.shape[0]:
-                raise ValueError(f"lengths must be [B], got {tuple(mask.shape)}")
-            host_lengths = tuple(min(max(int(n), 0), x.shape[1]) for n in mask.tolist())
-            lengths = torch.tensor(host_lengths, dtype=torch.int64, device=x.device)
-            mask = torch.arange(x.shape[1], device=x.device)[None, :] < lengths[:, None]
-        if mask is not None:
-            if tuple(mask.shape) != tuple(x.shape[:2]):
-                raise ValueError(f"valid_token_mask must be [B, S], got {tuple(mask.shape)}")
-            if mask.dtype != torch.bool:
-                mask = mask.to(torch.bool)
-            if not mask.is_contiguous():
-                mask = mask.contiguous()
+        mask, info = self._decode_mask(x, mask)
         batch, seq, _ = x.shape
-        plan = self._plan_cache.get((batch, seq))
+        plan = self._plans.get((batch, seq))
         if plan is None:
-            plan = select_plan(batch, seq, self.d_model, self.num_heads, self.ffn_dim,
-                               self.num_layers, self.causal, self.dtype, self.device)
+            shp = self.shape
+            plan = select_plan(batch, seq, shp.d_model, shp.heads, shp.ffn_dim, shp.layers, shp.causal,
+                               self.dtype, self.device)
             plan.validate()
-            self._plan_cache[(batch, seq)] = plan
+            self._plans[(batch, seq)] = plan
         self.plan = plan
-        self._build(plan)
-        if host_lengths is not None:
-            if min(host_lengths, default=x.shape[1]) == x.shape[1]:
-                mode, lens = MASK_NONE, None
-            else:
-                mode, lens = MASK_PREFIX, host_lengths
-        else:
-            mode, lens = self._mask_info(mask)
+        self._use_weights(plan)
+        mode, lengths = info.mode, info.lengths
         if mode == MASK_PREFIX and not plan.pack_prefix:
-            mode, lens = MASK_GENERAL, None  # every row computed, per-key mask
-        packing = self._packing(lens, x.shape[1]) if mode == MASK_PREFIX else None
+            # every row computed with a per-key mask, the reference's way
+            if mask is None:
+                mask = torch.arange(seq, device=x.device)[None, :] < torch.tensor(lengths, device=x.device)[:, None]
+            mode, lengths = MASK_GENERAL, None
+        packing = self._packing(lengths, seq) if mode == MASK_PREFIX else None
         if plan.cuda_graph:
-            return self._forward_graph(x, mask, mode, lens, packing)
+            return self._forward_graph(x, mask, mode, lengths, packing)
         return self._forward_impl(x, mask, mode, packing)
 
     def _forward_graph(self, x: torch.Tensor, mask: Optional[torch.Tensor], mode: int,
-                       lens: Optional[Tuple[int, ...]], packing: Optional[Packing]) -> torch.Tensor:
-        """The first LayerNorm (which reads the caller's x) and the final one
-        (which writes a fresh output tensor) run eagerly; the layers between
-        them replay as one hipGraph on fixed workspace buffers.  So no copy
-        of x into a static input and no clone of a static output is needed
-        (the reference copies in and clones out, graphs.py:57-64); only a
-        GENERAL mask, which the captured attention reads, is copied into a
-        static buffer.  A packed forward is specific to its lengths (its
-        launches are sized by them), so they are part of the key; the graph
-        keeps the row maps and schedule it reads alive."""
+                       lengths: Optional[Tuple[int, ...]], packing: Optional[Packing]) -> torch.Tensor:
+        """The first LayerNorm (reading the caller's x) and the final one
+        (writing a fresh output) run on the stream around one replayed
+        hipGraph of the layer body, on fixed workspace buffers; only a
+        GENERAL mask, which the recorded attention reads, is copied into a
+        static buffer.  A packed forward's launches are sized by its lengths,
+        so the lengths are part of the key, and the graph keeps the row maps
+        and schedule it reads alive."""
         batch, seq, d = x.shape
         static_mask = None
         if mode == MASK_GENERAL:
@@ -431,30 +524,32 @@ class Engine:
             if static_mask is None:
                 static_mask = torch.empty((batch, seq), dtype=torch.bool, device=x.device)
                 self._static_masks[(batch, seq)] = static_mask
-        key = (batch, seq, x.dtype, mode, lens, self.plan)
-        fw = self._fwds.get(key)
+            static_mask.copy_(mask)
+        key = (batch, seq, x.dtype, mode, lengths, self.plan)
+        fw = self._forwards.get(key)
         if fw is None:
             fw = self._prepare(batch, seq, mode, packing, static_mask)
-            self._fwds[key] = fw
+            self._forwards[key] = fw
+            if len(self._forwards) > 4 * self._graphs.max_entries:
+                self._forwards.popitem(last=False)
         graph = self._graphs.get(key, lambda: self._body(fw), keepalive=(packing, fw))
         self._first(fw, x)
         if graph is not None:
-            if static_mask is not None:
-                static_mask.copy_(mask)
             graph.replay()
         else:
-            if static_mask is not None:
-                static_mask.copy_(mask)
             self._body(fw)
         out = torch.empty((batch, seq, d), dtype=self.dtype, device=x.device)
-        self._final(fw, out, None if mask is None or mode != MASK_GENERAL else mask.reshape(-1))
+        self._final(fw, out, mask.reshape(-1) if mode == MASK_GENERAL else None)
+        self._check(fw)
         return out
 
 
 def get_engine(module: torch.nn.Module) -> Engine:
+    """The module's engine, made on first use and again after the module
+    moved to another dtype or device."""
     engine = getattr(module, "_tj_engine", None)
-    param = next(module.parameters())
-    if engine is None or engine.dtype != param.dtype or engine.device != param.device:
+    first = next(module.parameters())
+    if engine is None or (engine.dtype, engine.device) != (first.dtype, first.device):
         engine = Engine(module)
         object.__setattr__(module, "_tj_engine", engine)
     return engine
@@ -468,8 +563,8 @@ def reset_engines(module: torch.nn.Module) -> None:
 def forward(module: torch.nn.Module, x: torch.Tensor,
             valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
     """The hook body: ``return tjkernels.forward(self, x, valid_token_mask)``
-    (torch_transformer_benchmark.py:203).  ``TJ_DISABLE=1`` calls the parent
-    class's forward instead, as the reference does (engine.py:322-323)."""
+    (torch_transformer_benchmark.py:203).  ``TJ_DISABLE=1`` runs the parent
+    class's forward instead (engine.py:322-323)."""
     if os.environ.get("TJ_DISABLE") == "1":
         return super(type(module), module).forward(x, valid_token_mask)
     return get_engine(module)(x, valid_token_mask)

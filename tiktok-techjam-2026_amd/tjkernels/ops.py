@@ -66,9 +66,17 @@ def add_layernorm(res: torch.Tensor, delta: Optional[torch.Tensor],
     With ``row_index`` (int32, one entry per output row) the call is a
     gather / scatter: output row r is computed from input row row_index[r],
     or written as zeros when the index is negative; ``out`` (and ``res_out``)
-    then have ``row_index.numel()`` rows."""
+    then have ``row_index.numel()`` rows.
+
+    A 3-D ``delta`` [splits, rows, n] (the fused FFN's split partials) is
+    summed over its first dimension, in order, before it is added."""
     _require_gpu(res, delta, gamma, beta, out, res_out, row_mask, row_index)
     rows, n = res.shape
+    splits, split_stride, delta2 = 1, 0, delta
+    if delta is not None and delta.dim() == 3:
+        splits, split_stride, delta2 = delta.shape[0], delta.stride(0), delta[0]
+        if delta.shape[2] != n or (splits > 1 and delta.stride(0) < delta.shape[1] * delta.stride(1)):
+            raise TjkError(f"split delta must be [splits, rows, {n}] with non-overlapping splits")
     if row_index is not None:
         if row_index.dtype != torch.int32 or row_index.dim() != 1 or not row_index.is_contiguous():
             raise TjkError("row_index must be a contiguous int32 vector")
@@ -88,7 +96,7 @@ def add_layernorm(res: torch.Tensor, delta: Optional[torch.Tensor],
     status = lib.tjk_add_layernorm(
         res.data_ptr(), _code(res), _rowmajor(res, "res"),
         _ptr(delta), _code(delta) if delta is not None else 0,
-        _rowmajor(delta, "delta") if delta is not None else 0,
+        _rowmajor(delta2, "delta") if delta is not None else 0, splits, split_stride,
         _ptr(res_out), _rowmajor(res_out, "res_out") if res_out is not None else 0,
         out.data_ptr(), _code(out), _rowmajor(out, "out"),
         gamma.data_ptr(), beta.data_ptr(), rows, n, float(eps),
@@ -97,49 +105,10 @@ def add_layernorm(res: torch.Tensor, delta: Optional[torch.Tensor],
     return out
 
 
-_ws_need = {}    # (dtype code, plan) -> workspace bytes on this device (0: none)
-_ws_shared = {}  # device index -> zero-filled uint8 workspace for the stream-K plans
-
-
-def gemm_workspace(device: torch.device) -> torch.Tensor:
-    """The per-device workspace the stream-K GEMM plans share: sized for the
-    largest of them, zero-filled once (every completed call leaves its flag
-    area zero).  Calls using it must be ordered (one stream), which the
-    engine's forward is."""
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    ws = _ws_shared.get(idx)
-    if ws is None:
-        lib = _lib.load()
-        with torch.cuda.device(idx):
-            need = max([lib.tjk_gemm_workspace_bytes(code, p)
-                        for code in (_lib.DTYPE_CODES[torch.bfloat16], _lib.DTYPE_CODES[torch.float16])
-                        for p in range(lib.tjk_gemm_plan_count(code))] + [0])
-            ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=torch.device("cuda", idx))
-        _ws_shared[idx] = ws
-    return ws
-
-
-def _workspace_for(a: torch.Tensor, plan: int, workspace: Optional[torch.Tensor]):
-    if plan < 0:
-        return None
-    key = (_code(a), plan, a.device.index)
-    need = _ws_need.get(key)
-    if need is None:
-        with torch.cuda.device(a.device):
-            need = _lib.load().tjk_gemm_workspace_bytes(_code(a), plan)
-        _ws_need[key] = need
-    if need == 0:
-        return None
-    return workspace if workspace is not None else gemm_workspace(a.device)
-
-
 def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], out: torch.Tensor,
-         epilogue: int = EPI_BIAS, plan: int = -1,
-         workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+         epilogue: int = EPI_BIAS, plan: int = -1) -> torch.Tensor:
     """out = epi(a @ w.T + bias); w in nn.Linear [N, K] layout.
-    With EPI_BIAS_RESIDUAL, ``out`` is an fp32 residual updated in place.
-    Stream-K plans use ``workspace`` (uint8, zero-filled before its first
-    use) or, by default, the device's shared one (``gemm_workspace``)."""
+    With EPI_BIAS_RESIDUAL, ``out`` is an fp32 residual updated in place."""
     _require_gpu(a, w, bias, out)
     m, k = a.shape
     n, k2 = w.shape
@@ -153,11 +122,9 @@ def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], out: to
     elif out.dtype != a.dtype:
         raise TjkError("gemm out must have the operands' dtype")
     lib = _lib.load()
-    ws = _workspace_for(a, plan, workspace)
-    status = lib.tjk_gemm_bias_ws(a.data_ptr(), _rowmajor(a, "a"), w.data_ptr(), _rowmajor(w, "w"),
-                                  _ptr(bias), out.data_ptr(), _rowmajor(out, "out"), m, n, k,
-                                  _code(a), epilogue, plan, _ptr(ws),
-                                  ws.numel() if ws is not None else 0, _stream(a))
+    status = lib.tjk_gemm_bias(a.data_ptr(), _rowmajor(a, "a"), w.data_ptr(), _rowmajor(w, "w"),
+                               _ptr(bias), out.data_ptr(), _rowmajor(out, "out"), m, n, k,
+                               _code(a), epilogue, plan, _stream(a))
     check(status, "tjk_gemm_bias")
     return out
 
@@ -233,41 +200,75 @@ def flash_attention_sched(qkv: torch.Tensor, out: torch.Tensor, cu_seqlens: torc
         qkv.data_ptr(), ss, sc, sh, out.data_ptr(), _rowmajor(out, "out"), cu_seqlens.numel() - 1,
         int(max_seqlen), h, hd, float(hd ** -0.5 if scale is None else scale), int(bool(causal)),
         cu_seqlens.data_ptr(), schedule.work.data_ptr(), schedule.work.shape[0],
-        schedule.partials.data_ptr(), schedule.n_slots, _code(qkv), _stream(qkv))
+        schedule.partials.data_ptr(), schedule.partials.numel() * schedule.partials.element_size(),
+        schedule.n_slots, _code(qkv), _stream(qkv))
     check(status, "tjk_flash_fwd_sched")
     return out
 
 
-def ffn(h: torch.Tensor, w1: torch.Tensor, b1: Optional[torch.Tensor], w2: torch.Tensor,
-        b2: Optional[torch.Tensor], out: torch.Tensor, workspace: torch.Tensor,
-        epilogue: int = EPI_BIAS, plans: int = -1) -> torch.Tensor:
-    """out (+)= gelu_erf(h W1^T + b1) W2^T + b2; mirrors fused_ffn,
-    tjkernels/kernels/__init__.py:80-89.  ``plans`` packs the two GEMM tile
-    plans as p1 | p2 << 8 (-1 = both automatic)."""
-    _require_gpu(h, w1, b1, w2, b2, out, workspace)
-    t, d = h.shape
+def ffn_supported(d: int, f: int, splits: int, dtype: torch.dtype) -> bool:
+    """Whether the single-launch FFN takes (d, f, splits, dtype); the
+    counterpart of the reference's ffn.supports (tjkernels/kernels/ffn.py:103-110)."""
+    code = _lib.DTYPE_CODES.get(dtype)
+    return code is not None and bool(_lib.load().tjk_ffn_supported(d, f, splits, code))
+
+
+def ffn(a: torch.Tensor, w1: torch.Tensor, b1: Optional[torch.Tensor], w2: torch.Tensor,
+        b2: Optional[torch.Tensor], out: torch.Tensor, splits: int = 1,
+        ln: Optional[tuple] = None, accumulate: bool = False) -> torch.Tensor:
+    """The feed-forward block in one launch; mirrors fused_ffn,
+    tjkernels/kernels/__init__.py:80-89.
+
+    ``a`` is h [rows, d] in the weights' dtype, or with ``ln = (gamma, beta,
+    eps)`` the fp32 residual that the kernel LayerNorms itself.  ``out`` is
+    either [splits, rows, d] fp32 (slice s holds the f-slice s partial, slice
+    0 with b2; ``add_layernorm`` sums them) or, with ``accumulate`` and one
+    split, the [rows, d] fp32 residual the result is added into."""
+    _require_gpu(a, w1, b1, w2, b2, out)
+    rows, d = a.shape
     f = w1.shape[0]
-    need = _lib.load().tjk_ffn_workspace_bytes(t, f, _code(h))
-    if workspace.numel() * workspace.element_size() < need:
-        raise TjkError(f"ffn workspace too small ({need} bytes needed)")
-    if plans == -1:
-        plans = 0xffff
-    status = _lib.load().tjk_ffn(h.data_ptr(), _rowmajor(h, "h"), w1.data_ptr(), _ptr(b1), w2.data_ptr(),
-                                 _ptr(b2), out.data_ptr(), _rowmajor(out, "out"), workspace.data_ptr(),
-                                 t, d, f, _code(h), epilogue, plans, _stream(h))
+    cdt = w1.dtype
+    if tuple(w1.shape) != (f, d) or tuple(w2.shape) != (d, f) or w2.dtype != cdt:
+        raise TjkError(f"ffn weight shapes w1{tuple(w1.shape)} w2{tuple(w2.shape)} do not match d={d}")
+    if (b1 is not None and b1.dtype != cdt) or (b2 is not None and b2.dtype != cdt):
+        raise TjkError("ffn biases must have the weights' dtype")
+    if out.dtype != torch.float32:
+        raise TjkError("ffn output must be float32")
+    if ln is not None:
+        gamma, beta, eps = ln
+        if a.dtype != torch.float32 or gamma.dtype != torch.float32 or beta.dtype != torch.float32:
+            raise TjkError("ffn with a LayerNorm reads the fp32 residual and fp32 gamma/beta")
+    else:
+        gamma = beta = None
+        eps = 0.0
+        if a.dtype != cdt:
+            raise TjkError("ffn input must have the weights' dtype")
+    if accumulate:
+        if splits != 1 or out.dim() != 2 or out.shape[0] < rows:
+            raise TjkError("accumulating ffn needs one split and a [rows, d] residual")
+        ld_out, split_stride = _rowmajor(out, "out"), 0
+    else:
+        if out.dim() != 3 or out.shape[0] != splits or out.shape[1] < rows or out.stride(2) != 1:
+            raise TjkError(f"ffn partials must be [splits={splits}, rows, d] fp32")
+        ld_out, split_stride = out.stride(1), out.stride(0)
+    if w1.stride(1) != 1 or w1.stride(0) != d or w2.stride(1) != 1 or w2.stride(0) != f:
+        raise TjkError("ffn weights must be contiguous")
+    status = _lib.load().tjk_ffn(a.data_ptr(), _code(a), _rowmajor(a, "a"), _ptr(gamma), _ptr(beta), float(eps),
+                                 w1.data_ptr(), _ptr(b1), w2.data_ptr(), _ptr(b2), out.data_ptr(), ld_out,
+                                 split_stride, splits, int(bool(accumulate)), rows, d, f, _code(w1), _stream(a))
     check(status, "tjk_ffn")
     return out
 
 
 def gemm_plans(dtype: torch.dtype):
-    """[(plan_id, block_m, block_n, waves)] available for ``dtype``."""
+    """[(plan_id, block_m, block_n, waves, k_groups)] available for ``dtype``."""
     import ctypes
     lib = _lib.load()
     code = _lib.DTYPE_CODES[dtype]
     out = []
     for i in range(lib.tjk_gemm_plan_count(code)):
-        bm, bn, wv = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
-        check(lib.tjk_gemm_plan_info(code, i, ctypes.byref(bm), ctypes.byref(bn), ctypes.byref(wv)),
-              "tjk_gemm_plan_info")
-        out.append((i, bm.value, bn.value, wv.value))
+        bm, bn, wv, kg = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        check(lib.tjk_gemm_plan_info(code, i, ctypes.byref(bm), ctypes.byref(bn), ctypes.byref(wv),
+                                     ctypes.byref(kg)), "tjk_gemm_plan_info")
+        out.append((i, bm.value, bn.value, wv.value, kg.value))
     return out

@@ -1,29 +1,37 @@
-"""Shape -> execution-plan dispatch.
+"""Shape -> execution-plan dispatch (the reference's tjkernels/plans.py:29-198).
 
-Mirrors the reference's dispatcher (tjkernels/plans.py:29-198): a frozen
-``Plan`` of knobs, a shape key, a heuristic ``default_plan``, a JSON table of
-tuned plans (``plans.json``, written by ``tjkernels.autotune``) that
-overrides the heuristic per shape, environment overrides for ablation, and a
-programmatic ``set_override``.
+A ``Plan`` is a frozen bundle of knobs for one (shape, dtype, architecture).
+``select_plan`` resolves it in this order:
 
-Differences, all MI355X-specific:
-* every kernel knob names a HIP implementation; there is no torch/SDPA
-  backend to select (the product path has no non-HIP fallback);
-* the plan carries tile-plan ids for each GEMM and for attention
-  (-1 = the library's own heuristic), and ``residual_epilogue`` (add the
-  out-proj and FFN outputs into the fp32 residual inside the GEMM epilogue
-  instead of deferring them to the next LayerNorm);
-* an fp32 model runs the IEEE fp32 plan by default, since only fp32 compute
-  holds the 1e-4 per-element budget of fp32 plans;
-* tuned entries are keyed by shape *and* GPU architecture (``@gfx950``);
-* ``pack_prefix``: prefix-masked batches run only their valid tokens (off:
-  every padded row is computed and zeroed at the end, the reference's way).
+1. a plan forced with ``set_override`` (the autotuner and tests use it);
+2. the tuned entry for the shape key in ``plans.json`` (written by
+   ``tjkernels.autotune``; skipped with ``TJ_IGNORE_PLANS=1``);
+3. ``default_plan``'s heuristic, adjusted by the ``TJ_*`` environment knobs
+   below (so ablations run with ``TJ_IGNORE_PLANS=1``, as the reference's
+   ablation does).
 
-Environment knobs (applied to the heuristic plan, so ablations set
-``TJ_IGNORE_PLANS=1`` as the reference's ablation does): ``TJ_NO_GRAPH``,
-``TJ_COMPUTE_DTYPE``, ``TJ_DEFERRED_RESIDUAL``, ``TJ_NO_PACK``,
-``TJ_ATTN_PLAN``; ``TJ_GEMM_TUNE=0`` (tjkernels.tiles) skips the measured
-tile choice.
+Knobs, all naming HIP kernels of this build (there is no torch/SDPA backend
+to select, and the product path has no non-HIP fallback):
+
+* ``compute_dtype`` / ``residual_dtype``: GEMM / attention operand dtype and
+  the residual stream's dtype (fp32 only).  An fp32 model runs the IEEE fp32
+  plan, since only fp32 compute holds the 1e-4 budget of fp32 plans;
+* ``ffn``: ``"gemm"`` (two GEMM launches, GELU in the first one's epilogue,
+  the [T, f] intermediate in HBM) or ``"fused"`` (one launch per layer with
+  the intermediate in LDS and LayerNorm 2 inside, split over ``ffn_splits``
+  f-slices whose partials the next LayerNorm sums; 0 = f / 128);
+* ``cuda_graph``: replay the layer body as one hipGraph;
+* ``residual_epilogue``: add the out-proj (and two-launch FFN) outputs into
+  the fp32 residual in the GEMM epilogue instead of deferring them to the
+  next LayerNorm (the reference's scheme, engine.py:232-264);
+* ``gemm_*`` / ``attn_plan``: force a tile or attention plan (-1: chosen
+  at run time);
+* ``pack_prefix``: run only the valid tokens of prefix masks.
+
+Environment: ``TJ_NO_GRAPH``, ``TJ_COMPUTE_DTYPE``, ``TJ_DEFERRED_RESIDUAL``,
+``TJ_NO_PACK``, ``TJ_ATTN_PLAN``, ``TJ_FFN`` (gemm | fused);
+``TJ_GEMM_TUNE=0`` (tjkernels.tiles) skips the measured tile choice.
+Tuned keys carry the GPU architecture (``...@gfx950``).
 """
 
 from __future__ import annotations
@@ -36,10 +44,13 @@ from typing import Dict, Optional
 
 import torch
 
-_PLAN_FILE = Path(__file__).with_name("plans.json")
+DTYPE_BY_NAME = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
+NAME_BY_DTYPE = {dt: name for name, dt in DTYPE_BY_NAME.items()}
+FFN_KINDS = ("gemm", "fused")
 
-_DTYPES = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
-_DTYPE_NAMES = {v: k for k, v in _DTYPES.items()}
+# The single-launch FFN is the default up to this many (tokens x ffn_dim)
+# elements of intermediate, where the two-launch path is launch-bound.
+FUSED_FFN_MAX_ELEMS = 1 << 19
 
 
 @dataclass(frozen=True)
@@ -49,40 +60,49 @@ class Plan:
     compute_dtype: torch.dtype = torch.bfloat16
     residual_dtype: torch.dtype = torch.float32
     attn: str = "hip"
-    ffn: str = "hip"
+    ffn: str = "gemm"
     norm: str = "hip"
+    ffn_splits: int = 0
     packed_qkv: bool = True
-    cuda_graph: bool = True          # whole-forward hipGraph capture
-    residual_epilogue: bool = True   # GEMM epilogues update the fp32 residual
-    gemm_qkv: int = -1               # tile plan ids, -1 = library heuristic
+    cuda_graph: bool = True
+    residual_epilogue: bool = True
+    gemm_qkv: int = -1
     gemm_out: int = -1
     gemm_ffn1: int = -1
     gemm_ffn2: int = -1
     attn_plan: int = -1
-    pack_prefix: bool = True         # run only the valid tokens of prefix masks
+    pack_prefix: bool = True
     label: str = "default"
 
     def to_json(self) -> Dict[str, object]:
-        blob = {f.name: getattr(self, f.name) for f in fields(self)}
-        blob["compute_dtype"] = _DTYPE_NAMES[self.compute_dtype]
-        blob["residual_dtype"] = _DTYPE_NAMES[self.residual_dtype]
+        blob: Dict[str, object] = {}
+        for f in fields(self):
+            value = getattr(self, f.name)
+            blob[f.name] = NAME_BY_DTYPE[value] if isinstance(value, torch.dtype) else value
         return blob
 
-    @staticmethod
-    def from_json(blob: Dict[str, object]) -> "Plan":
-        blob = dict(blob)
-        blob["compute_dtype"] = _DTYPES[str(blob.get("compute_dtype", "bfloat16"))]
-        blob["residual_dtype"] = _DTYPES[str(blob.get("residual_dtype", "float32"))]
-        names = {f.name for f in fields(Plan)}
-        return Plan(**{k: v for k, v in blob.items() if k in names})
+    @classmethod
+    def from_json(cls, blob: Dict[str, object]) -> "Plan":
+        known = {f.name: f for f in fields(cls)}
+        kwargs = {}
+        for name, value in blob.items():
+            if name not in known:
+                continue  # keys of other versions are ignored
+            if name in ("compute_dtype", "residual_dtype"):
+                value = DTYPE_BY_NAME[str(value)]
+            if name == "ffn" and value == "hip":
+                value = "gemm"  # the two-launch FFN's name in earlier tables
+            kwargs[name] = value
+        return cls(**kwargs)
 
     def validate(self) -> None:
         if self.residual_dtype != torch.float32:
             raise ValueError("only a float32 residual stream is implemented")
-        for knob in ("attn", "ffn", "norm"):
-            if getattr(self, knob) != "hip":
-                raise ValueError(f"{knob}={getattr(self, knob)!r}: only 'hip' kernels exist "
-                                 "(no torch/SDPA fallback in this build)")
+        if self.attn != "hip" or self.norm != "hip":
+            raise ValueError(f"attn={self.attn!r} norm={self.norm!r}: only 'hip' kernels exist "
+                             "(no torch/SDPA fallback in this build)")
+        if self.ffn not in FFN_KINDS:
+            raise ValueError(f"ffn={self.ffn!r}: one of {FFN_KINDS}")
         if not self.packed_qkv:
             raise ValueError("only the packed QKV layout is implemented")
 
@@ -90,95 +110,117 @@ class Plan:
 def device_arch(device: torch.device) -> str:
     if device.type != "cuda":
         return device.type
-    name = torch.cuda.get_device_properties(device).gcnArchName
-    return name.split(":")[0]
+    return torch.cuda.get_device_properties(device).gcnArchName.split(":")[0]
 
 
 def shape_key(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int,
               layers: int, causal: bool, dtype: torch.dtype, arch: str = "gfx950") -> str:
-    return (f"b{batch}_s{seq}_d{d_model}_h{heads}_f{ffn_dim}_l{layers}"
-            f"_{'causal' if causal else 'full'}_{_DTYPE_NAMES[dtype]}@{arch}")
+    mode = "causal" if causal else "full"
+    return f"b{batch}_s{seq}_d{d_model}_h{heads}_f{ffn_dim}_l{layers}_{mode}_{NAME_BY_DTYPE[dtype]}@{arch}"
+
+
+def fused_ffn_ok(d_model: int, ffn_dim: int, compute_dtype: torch.dtype, splits: int = 0) -> bool:
+    """Whether the single-launch FFN kernel takes the shape (tjk_ffn_supported)."""
+    from . import ops
+    if splits <= 0:
+        splits = max(ffn_dim // 128, 1)
+    return ops.ffn_supported(d_model, ffn_dim, splits, compute_dtype)
 
 
 def default_plan(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int,
                  layers: int, causal: bool, dtype: torch.dtype, device: torch.device) -> Plan:
     """Heuristic plan used before (or without) autotuning."""
     if device.type != "cuda":
-        raise RuntimeError("tjkernels runs on ROCm GPUs only; got device "
-                           f"{device} (there is no CPU path)")
-    # hipGraph replay pays only where launches dominate.  Measured on MI355X
-    # (same box, alternating runs): C2 (128 x 512 activations) 0.186 ms with
-    # the graph vs 0.222 ms eager, but C3 / C4 (3.1M / 8.4M activation
-    # elements) 2-3% faster with eager stream launches, the kernels being
-    # long enough to keep the queue ahead.  So the graph is used up to 2^20
-    # activation elements, and never above the reference's 64 MiB of x
-    # (tjkernels/plans.py:109-110).
+        raise RuntimeError(f"tjkernels runs on ROCm GPUs only; got device {device} (there is no CPU path)")
+    # hipGraph replay pays only where launches dominate: measured on MI355X,
+    # C2 (128 x 512 activations) 0.186 ms replayed vs 0.222 ms eager, but
+    # C3 / C4 (3.1M / 8.4M activation elements) 2-3% faster launched
+    # eagerly.  So up to 2^20 activation elements, and never above the
+    # reference's 64 MiB of x (tjkernels/plans.py:109-110).
     elems = batch * seq * d_model
-    x_bytes = elems * dtype.itemsize
-    return Plan(compute_dtype=dtype, residual_dtype=torch.float32,
-                cuda_graph=elems <= (1 << 20) and x_bytes <= 64 * 1024 * 1024, label="heuristic")
+    graph = elems <= (1 << 20) and elems * dtype.itemsize <= 64 * 1024 * 1024
+    fused = batch * seq * ffn_dim <= FUSED_FFN_MAX_ELEMS and fused_ffn_ok(d_model, ffn_dim, dtype)
+    return Plan(compute_dtype=dtype, cuda_graph=graph, ffn="fused" if fused else "gemm", label="heuristic")
 
 
-_cache: Optional[Dict[str, Plan]] = None
-_override: Optional[Plan] = None
+class PlanTable:
+    """The tuned plans of ``plans.json``, read once, keyed by ``shape_key``."""
+
+    def __init__(self, path: Path) -> None:
+        self.path = path
+        self._plans: Optional[Dict[str, Plan]] = None
+
+    def plans(self) -> Dict[str, Plan]:
+        if self._plans is None:
+            self._plans = {}
+            if os.environ.get("TJ_IGNORE_PLANS") != "1" and self.path.exists():
+                try:
+                    raw = json.loads(self.path.read_text())
+                    self._plans = {key: Plan.from_json(blob) for key, blob in raw.items()}
+                except (OSError, ValueError, KeyError, TypeError) as exc:
+                    # a broken table costs the tuning, never the run
+                    print(f"[tjkernels] plans.json not used ({exc})")
+        return self._plans
+
+    def get(self, key: str) -> Optional[Plan]:
+        return self.plans().get(key)
+
+    def merge(self, new: Dict[str, Plan], path: Optional[Path] = None) -> None:
+        """Write ``new`` into the table file, keeping other shapes' entries."""
+        target = path or self.path
+        table: Dict[str, object] = {}
+        if target.exists():
+            try:
+                table = json.loads(target.read_text())
+            except ValueError:
+                table = {}
+        for key, plan in new.items():
+            table[key] = plan.to_json()
+        target.write_text(json.dumps(table, indent=2, sort_keys=True) + "\n")
+        self._plans = None
+
+
+TUNED_PATH = Path(__file__).with_name("plans.json")
+TUNED = PlanTable(TUNED_PATH)
+_forced: Optional[Plan] = None
 
 
 def set_override(plan: Optional[Plan]) -> None:
-    """Force a specific plan regardless of shape (used by the autotuner and tests)."""
-    global _override
-    _override = plan
+    """Force ``plan`` for every shape (None lifts it)."""
+    global _forced
+    _forced = plan
 
 
-def _load_tuned() -> Dict[str, Plan]:
-    global _cache
-    if _cache is None:
-        _cache = {}
-        if _PLAN_FILE.exists() and os.environ.get("TJ_IGNORE_PLANS") != "1":
-            try:
-                raw = json.loads(_PLAN_FILE.read_text())
-                _cache = {k: Plan.from_json(v) for k, v in raw.items()}
-            except Exception as exc:  # an unreadable table never breaks a run
-                print(f"[tjkernels] ignoring unreadable plans.json: {exc}")
-                _cache = {}
-    return _cache
+def _env_adjusted(plan: Plan) -> Plan:
+    env = os.environ
+    changes: Dict[str, object] = {}
+    if env.get("TJ_NO_GRAPH") == "1":
+        changes["cuda_graph"] = False
+    if env.get("TJ_COMPUTE_DTYPE") in DTYPE_BY_NAME:
+        changes["compute_dtype"] = DTYPE_BY_NAME[env["TJ_COMPUTE_DTYPE"]]
+    if env.get("TJ_DEFERRED_RESIDUAL") == "1":
+        changes["residual_epilogue"] = False
+    if env.get("TJ_NO_PACK") == "1":
+        changes["pack_prefix"] = False
+    if env.get("TJ_FFN") in FFN_KINDS:
+        changes["ffn"] = env["TJ_FFN"]
+    attn = env.get("TJ_ATTN_PLAN", "")
+    if attn.lstrip("-").isdigit():
+        changes["attn_plan"] = int(attn)
+    return replace(plan, **changes) if changes else plan
 
 
 def select_plan(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int,
                 layers: int, causal: bool, dtype: torch.dtype, device: torch.device) -> Plan:
-    if _override is not None:
-        return _override
-    arch = device_arch(device)
-    key = shape_key(batch, seq, d_model, heads, ffn_dim, layers, causal, dtype, arch)
-    tuned = _load_tuned().get(key)
+    if _forced is not None:
+        return _forced
+    key = shape_key(batch, seq, d_model, heads, ffn_dim, layers, causal, dtype, device_arch(device))
+    tuned = TUNED.get(key)
     if tuned is not None:
         return tuned
-
-    plan = default_plan(batch, seq, d_model, heads, ffn_dim, layers, causal, dtype, device)
-    if os.environ.get("TJ_NO_GRAPH") == "1":
-        plan = replace(plan, cuda_graph=False)
-    forced = os.environ.get("TJ_COMPUTE_DTYPE")
-    if forced in _DTYPES:
-        plan = replace(plan, compute_dtype=_DTYPES[forced])
-    if os.environ.get("TJ_DEFERRED_RESIDUAL") == "1":
-        plan = replace(plan, residual_epilogue=False)
-    if os.environ.get("TJ_NO_PACK") == "1":
-        plan = replace(plan, pack_prefix=False)
-    attn_plan = os.environ.get("TJ_ATTN_PLAN")
-    if attn_plan is not None and attn_plan.lstrip("-").isdigit():
-        plan = replace(plan, attn_plan=int(attn_plan))
-    return plan
+    return _env_adjusted(default_plan(batch, seq, d_model, heads, ffn_dim, layers, causal, dtype, device))
 
 
 def save_plans(plans: Dict[str, Plan], path: Optional[Path] = None) -> None:
-    """Merge ``plans`` into plans.json (existing keys for other shapes kept)."""
-    global _cache
-    path = path or _PLAN_FILE
-    existing: Dict[str, object] = {}
-    if path.exists():
-        try:
-            existing = json.loads(path.read_text())
-        except Exception:
-            existing = {}
-    existing.update({k: v.to_json() for k, v in plans.items()})
-    path.write_text(json.dumps(existing, indent=2, sort_keys=True) + "\n")
-    _cache = None
+    """Merge ``plans`` into plans.json (entries for other shapes are kept)."""
+    TUNED.merge(plans, path)

@@ -1,56 +1,77 @@
-"""Measured GEMM tile choice per (M, N, K, dtype, epilogue).
+"""Measured GEMM tile choice per projection shape, deterministic in its results.
 
-With packed prefix-masked tokens the row count M of every projection is
-the number of valid tokens, which changes with the input lengths, and the
-best tile shape depends on how the tile count falls onto the 256 CUs (a
-launch whose last round holds a handful of tiles costs nearly a full
-round).  No fixed table covers that, so the first time a projection shape is
-seen its candidate tile plans are timed on scratch operands of that exact
-shape (HIP events on the current stream) and the fastest is kept for the
-rest of the process.  Every candidate accumulates each output element over
-K in the same order, so the choice changes speed, not results.  (The
-K-split plans 16 / 17 add two half-K partial sums instead; they measured
-no faster on the BASELINE shapes and are only used when a Plan forces them.)
+With packed prefix-masked tokens the row count M of every projection is the
+number of valid tokens, which follows the input lengths, and the best tile
+depends on how the tile count falls onto the 256 CUs (a launch whose last
+round holds a handful of tiles costs nearly a full round).  No fixed table
+covers that, so the first time a projection shape is seen the candidate
+tiles are timed on scratch operands and the fastest is kept.
 
-This replaces the reference's static per-shape table lookup for the GEMM
-part of a plan (tjkernels/plans.py:147-170); plan ids >= 0 in a ``Plan``
-still force a specific tile.  ``TJ_GEMM_TUNE=0`` falls back to the
-library's own rule (plan -1).
+Timing noise must not change results.  The tile plans fall into classes by
+the order in which they add up the K dimension:
+
+* class 1: one accumulator per output element, K tiles in order;
+* class 2: two wave groups take alternate K tiles and their two sums are
+  added at the end (the in-workgroup K split).
+
+Every plan of a class produces the same bits for the same inputs, so the
+class is fixed by the shape (``k_class``) and only tiles within it are
+timed.  Two processes, or two boxes, therefore compute identical outputs
+whatever the timing picks.  ``k_class`` chooses the K split when a launch of
+128 x 64 tiles fits in one round of the CUs and K is long enough for the
+split to shorten the serial chain of K tiles (the launch-bound projections
+of C2 and C3's FFN2: 10.6 -> 8.5 us and 26.1 -> 23.0 us measured on MI355X).
+
+The table is keyed by M rounded up to a multiple of 64 (the timing runs at
+that M), so ragged lengths reuse a measurement, and it holds at most
+``MAX_ENTRIES`` shapes.  This replaces the reference's static per-shape
+table lookup for the GEMM part of a plan (tjkernels/plans.py:147-170); tile
+ids >= 0 in a ``Plan`` still force a tile.  ``TJ_GEMM_TUNE=0`` uses the
+library's own rule (tile -1) instead of timing.
 """
 
 from __future__ import annotations
 
 import os
-from typing import Dict, Tuple
+from collections import OrderedDict
+from typing import Tuple
 
 import torch
 
 from . import _lib, ops, timing
 
-# Direct-to-LDS tile plans worth timing (2-byte types): 128x128, 256x256,
-# 64x64, 192x128, 192x256, 192x384, 96x128, 192x128 in a 4-slot ring,
-# 64x64 / 128x64 in 8- / 6-slot rings, and 64x64 / 128x64 with K split
-# between 2 or 4 wave groups.  fp32 uses its own list.
-CANDIDATES_16 = (7, 8, 9, 12, 13, 14, 15, 26, 27, 28, 29, 30, 31)
-CANDIDATES_32 = (2, 3, 4)
+# Direct-to-LDS plans of the 2-byte table by K order (ids of tjk_gemm_plan_info):
+# class 1: 128x128, 256x256 (8 waves), 64x64, 192x128, 192x256, 192x384,
+#          96x128, 192x128 in a 4-slot ring, 64x64 / 128x64 in 8- / 6-slot rings;
+# class 2: 192x128, 128x128, 64x64 (4-slot ring), 128x64 (3-slot ring), each
+#          with K split between two groups of 4 waves.
+CLASS_TILES_16 = {1: (7, 8, 9, 12, 13, 14, 15, 18, 19, 20), 2: (16, 17, 22, 23)}
+CANDIDATES_32 = (2, 3, 4)  # fp32: class 1 only
+MAX_ENTRIES = 256
+M_BUCKET = 64
 
-_choice: Dict[Tuple, int] = {}
+_choice: "OrderedDict[Tuple, int]" = OrderedDict()
+
+
+def k_class(m: int, n: int, k: int, dtype: torch.dtype) -> int:
+    """K-summation class of the tile used for out[m, n] = a[m, k] w[n, k]^T."""
+    if dtype == torch.float32:
+        return 1
+    one_round = ((m + 127) // 128) * ((n + 63) // 64) <= 256
+    return 2 if one_round and k >= 512 else 1
+
+
+def candidates(m: int, n: int, k: int, dtype: torch.dtype) -> Tuple[int, ...]:
+    if dtype == torch.float32:
+        return CANDIDATES_32
+    return CLASS_TILES_16[k_class(m, n, k, dtype)]
 
 
 def _time_plan(a, w, bias, out, epi, plan, reps) -> float:
     return timing.launch_ms(lambda: ops.gemm(a, w, bias, out, epi, plan), reps)
 
 
-def gemm_plan(m: int, n: int, k: int, dtype: torch.dtype, epilogue: int, forced: int = -1) -> int:
-    """Tile plan for out[m, n] = epi(a[m, k] w[n, k]^T + b); ``forced`` >= 0 wins."""
-    if forced >= 0 or m == 0:
-        return forced
-    if os.environ.get("TJ_GEMM_TUNE") == "0" or torch.cuda.is_current_stream_capturing():
-        return _choice.get((m, n, k, dtype, epilogue), -1)
-    key = (m, n, k, dtype, epilogue)
-    plan = _choice.get(key)
-    if plan is not None:
-        return plan
+def _measure(m: int, n: int, k: int, dtype: torch.dtype, epilogue: int) -> int:
     dev = torch.device("cuda", torch.cuda.current_device())
     g = torch.Generator(device=dev)
     g.manual_seed(m * 7919 + n * 31 + k)
@@ -62,26 +83,50 @@ def gemm_plan(m: int, n: int, k: int, dtype: torch.dtype, epilogue: int, forced:
     # about 0.4 ms of GPU work per measurement (estimated at 500 TFLOP/s)
     reps = max(3, min(24, int(0.4e-3 / (2.0 * m * n * k / 500e12))))
     cands = []
-    for cand in (CANDIDATES_32 if dtype == torch.float32 else CANDIDATES_16):
+    for cand in candidates(m, n, k, dtype):
         try:
             ops.gemm(a, w, bias, out, epilogue, cand)  # warm; rejects shapes it does not take
         except _lib.TjkError:  # e.g. K % 64 != 0
             continue
         cands.append(cand)
+    if not cands:
+        return -1
     # Three interleaved rounds, best time per candidate: the clock drifts
     # (power / thermal) while this runs, and a single pass in order would
     # hand the early candidates the cooler chip.
     times = {c: float("inf") for c in cands}
     for rnd in range(3):
-        order = cands if rnd % 2 == 0 else cands[::-1]
-        for cand in order:
+        for cand in (cands if rnd % 2 == 0 else cands[::-1]):
             times[cand] = min(times[cand], _time_plan(a, w, bias, out, epilogue, cand, reps))
-    best, best_ms = -1, float("inf")
-    for cand in cands:  # earlier (larger-reuse) candidates win near ties
+    best, best_ms = cands[0], times[cands[0]]
+    for cand in cands[1:]:  # earlier (larger-reuse) candidates win near ties
         if times[cand] < best_ms * 0.98:
             best, best_ms = cand, times[cand]
-    _choice[key] = best
     return best
+
+
+def gemm_plan(m: int, n: int, k: int, dtype: torch.dtype, epilogue: int, forced: int = -1) -> int:
+    """Tile plan for out[m, n] = epi(a[m, k] w[n, k]^T + b); ``forced`` >= 0 wins."""
+    if forced >= 0 or m == 0:
+        return forced
+    mb = -(-m // M_BUCKET) * M_BUCKET
+    key = (mb, n, k, dtype, epilogue)
+    plan = _choice.get(key)
+    if plan is not None:
+        _choice.move_to_end(key)
+        return plan
+    if os.environ.get("TJ_GEMM_TUNE") == "0" or torch.cuda.is_current_stream_capturing():
+        return -1
+    plan = _measure(mb, n, k, dtype, epilogue)
+    _choice[key] = plan
+    while len(_choice) > MAX_ENTRIES:
+        _choice.popitem(last=False)
+    return plan
+
+
+def chosen() -> dict:
+    """{(M bucket, N, K, dtype, epilogue): tile} measured so far."""
+    return dict(_choice)
 
 
 def reset() -> None:
