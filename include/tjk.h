@@ -75,9 +75,11 @@ const char* tjk_last_error_string(void);
  * res_out must not alias res when row_index is given.
  * res_dtype, delta_dtype, out_dtype in {TJK_F32, TJK_F16, TJK_BF16};
  * delta may be NULL.  Requires n % 4 == 0, n <= 8192, 8-byte aligned rows.
- * delta_splits > 1 (n <= 1024): delta is the sum of delta_splits slices
- * delta_split_stride elements apart (the split partials of tjk_ffn), added
- * in slice order -- x = res + (((d_0 + d_1) + d_2) + ...).
+ * delta_splits > 1 (fp32 delta, n <= 1024): delta is the sum of
+ * delta_splits slices delta_split_stride elements apart (the split partials
+ * of tjk_ffn), in a fixed order: the slices form four consecutive groups of
+ * q = ceil(delta_splits / 4), each summed in slice order (S_g), and
+ * x = res + (((S_0 + S_1) + S_2) + S_3) (empty groups skipped).
  */
 int tjk_add_layernorm(const void* res, int res_dtype, int64_t ld_res,
                       const void* delta, int delta_dtype, int64_t ld_delta,

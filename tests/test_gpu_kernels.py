@@ -591,12 +591,13 @@ FFN_TOL = {torch.float32: (2e-5, 2e-5), torch.float16: (2e-3, 2e-3), torch.bfloa
                                      (torch.bfloat16, 256, 1024), (torch.float16, 128, 256),
                                      (torch.float32, 128, 512), (torch.float32, 256, 384)])
 @pytest.mark.parametrize("rows", [1, 31, 96, 200])
-def test_ffn_fused_against_fp64(device, dt, d, f, rows):
+@pytest.mark.parametrize("slice_cols", [64, 128])
+def test_ffn_fused_against_fp64(device, dt, d, f, rows, slice_cols):
     """P = gelu_erf(A W1^T + b1) W2^T + b2 from h (no LayerNorm) and from
     the fp32 residual (LayerNorm in the kernel), split over f / 128 slices
     and summed, against fp64; rows past the input are never written."""
     g = _gen(d * 3 + f + rows)
-    splits = f // 128
+    splits = f // slice_cols
     res = torch.randn(rows, d, generator=g) * 2 + 0.3
     gamma, beta = torch.randn(d, generator=g), torch.randn(d, generator=g) * 0.1
     w1 = (torch.randn(f, d, generator=g) / math.sqrt(d)).to(dt)
@@ -621,12 +622,13 @@ def test_ffn_fused_against_fp64(device, dt, d, f, rows):
     ref = _ffn_reference(h.cpu(), w1, b1, w2, b2, dt)
     _close(outs[0].double().sum(0), ref, rtol, atol)
     # a single split adds straight into the residual
-    if ops.ffn_supported(d, 128, 1, dt):
+    c = slice_cols
+    if ops.ffn_supported(d, c, 1, dt):
         r0 = torch.randn(rows, d, generator=g)
         acc = r0.to(device)
-        ops.ffn(h, w1_d[:128], b1_d[:128], w2_d[:, :128].contiguous(), b2_d, acc, splits=1, accumulate=True)
+        ops.ffn(h, w1_d[:c], b1_d[:c], w2_d[:, :c].contiguous(), b2_d, acc, splits=1, accumulate=True)
         torch.cuda.synchronize()
-        ref1 = _ffn_reference(h.cpu(), w1[:128], b1[:128], w2[:, :128], b2, dt) + r0.double()
+        ref1 = _ffn_reference(h.cpu(), w1[:c], b1[:c], w2[:, :c], b2, dt) + r0.double()
         _close(acc, ref1, rtol, atol)
 
 
@@ -660,20 +662,28 @@ def test_ffn_rejects_unsupported_shapes(device):
         ops.ffn(h, w1, None, w2, None, torch.zeros(32, 8, 1024, device=device), splits=32)
 
 
-@pytest.mark.parametrize("n,splits", [(128, 4), (512, 16), (512, 3), (1024, 8)])
+@pytest.mark.parametrize("n,splits", [(128, 4), (512, 16), (512, 3), (1024, 8), (512, 32), (96, 2)])
 def test_add_layernorm_split_delta(device, n, splits):
-    """A [splits, rows, n] fp32 delta is summed slice by slice, in order,
-    then added to the residual: res_out equals that fp32 sum exactly, and
-    the normalised output matches fp64; gather and scatter rows read the
-    delta rows of their source row."""
+    """A [splits, rows, n] fp32 delta is summed in the documented fixed
+    order -- four consecutive groups of ceil(splits / 4) slices, each in
+    slice order, then the group sums in group order -- and added to the
+    residual: res_out equals that fp32 sum exactly, and the normalised
+    output matches fp64; scatter rows read the delta rows of their source."""
     rows = 45
     g = _gen(n + splits)
     res = torch.randn(rows, n, generator=g)
     parts = torch.randn(splits, rows + 5, n, generator=g)[:, :rows]
     gamma, beta = torch.randn(n, generator=g), torch.randn(n, generator=g)
-    acc = parts[0].clone()
-    for s_ in range(1, splits):
-        acc = acc + parts[s_]
+    q = (splits + 3) // 4
+    acc = None
+    for grp in range(4):
+        sl = list(range(grp * q, min(grp * q + q, splits)))
+        if not sl:
+            continue
+        part = parts[sl[0]].clone()
+        for s_ in sl[1:]:
+            part = part + parts[s_]
+        acc = part if acc is None else acc + part
     want_res = res + acc
     out = torch.empty(rows, n, dtype=torch.bfloat16, device=device)
     res_d = res.to(device)

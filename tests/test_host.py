@@ -46,6 +46,7 @@ def test_abi_rejects_bad_arguments_without_launching():
     # the single-launch FFN's shape gate (f / splits must be 128; d in {128, 256, 512})
     assert lib.tjk_ffn_supported(512, 2048, 16, _lib.F16) == 1
     assert lib.tjk_ffn_supported(128, 512, 4, _lib.F32) == 1
+    assert lib.tjk_ffn_supported(512, 2048, 32, _lib.BF16) == 1  # 64-column slices
     assert lib.tjk_ffn_supported(512, 2048, 8, _lib.F16) == 0
     assert lib.tjk_ffn_supported(512, 2048, 16, _lib.F32) == 0
     assert lib.tjk_ffn_supported(1024, 4096, 32, _lib.BF16) == 0

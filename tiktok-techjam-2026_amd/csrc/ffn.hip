@@ -17,34 +17,43 @@
 //      stream through an LDS DMA ring while A stays resident; the result is
 //      rounded to the compute dtype (as the reference rounds its hidden
 //      activation) into LDS: the [rows, f] intermediate never leaves the CU;
-//   3. P[s] = mid W2[:, s]^T -- a 32 x d tile, W2's column slice streaming
-//      through the same ring, mid resident as the A operand;
+//   3. P[s] = mid W2[:, s]^T -- a 32 x d tile with mid resident as the A
+//      operand and W2's column slice in LDS;
 //   4. P[s] is stored as fp32 (split 0 adds b2), or with a single split it
 //      can be added straight into the fp32 residual.
 //
-// The splits' partials are summed in split order by the next add+LayerNorm
-// (tjk_add_layernorm's delta_splits), which is where the reference adds its
-// deferred FFN output (tjkernels/engine.py:232-264): no cross-workgroup
-// reduction, no waiting, and the sum order is fixed, so results are
-// deterministic.  The split spreads a launch-bound shape (C2: 128 tokens,
-// f = 2048) over 64 workgroups instead of 4.
+// The kernel is latency-bound at the shapes it serves (C2: 128 tokens), so
+// the weight copies start first: when W2's slice fits in LDS beside W1's
+// ring (64-column slices) all of it is in flight from the start, else its
+// first tiles load during the GELU; W1's first tiles load while the
+// LayerNorm runs.
+//
+// The splits' partials are summed by the next add+LayerNorm
+// (tjk_add_layernorm's delta_splits, in a fixed order), which is where the
+// reference adds its deferred FFN output (tjkernels/engine.py:232-264): no
+// cross-workgroup reduction, no waiting, deterministic results.
 
 #include "gemm_tiles.h"
 
 namespace tjk {
 
 constexpr int kFfnRows = 32;  // rows per workgroup
-constexpr int kFfnWaves = 4;  // each wave owns a quarter of the tile's columns
+constexpr int kFfnWaves = 4;
 
 // Physical 16-byte chunk of logical chunk c in row r of a resident operand
-// (rows of >= 16 chunks): an XOR over 16-chunk groups, so the fragment reads
-// of 16 consecutive rows at one logical chunk hit 16 different 16-byte bank
-// groups.
-__device__ __forceinline__ int res_chunk(int c, int r) { return c ^ (r & 15); }
+// whose rows hold NCH chunks: an XOR over groups of min(NCH, 16) chunks, so
+// the fragment reads of consecutive rows at one logical chunk hit different
+// 16-byte bank groups.
+template <int NCH>
+__device__ __forceinline__ int res_chunk(int c, int r) {
+  static_assert(NCH >= 8 && (NCH % 8) == 0, "resident rows need a multiple of 8 chunks");
+  return c ^ (r & ((NCH >= 16 ? 16 : 8) - 1));
+}
 
-// Geometry of one phase: W tiles of BN rows x BKB bytes of K in a ring of
-// STAGES slots, the A operand resident.
-template <typename T, int BN, int BKB, int STAGES>
+// Geometry of one phase: W tiles of BN rows x BKB bytes of K in STAGES LDS
+// slots, the A operand resident.  WN waves own BN / WN columns each (the
+// others only help with the copies).
+template <typename T, int BN, int BKB, int STAGES, int WN>
 struct FfnPhase {
   static constexpr int NW = kFfnWaves;
   static constexpr int BK = BKB / (int)sizeof(T);     // K elements per tile
@@ -52,54 +61,77 @@ struct FfnPhase {
   static constexpr int RPI = 64 / CPR;                // ring rows per DMA instruction
   static constexpr int KS = BK / 16;                  // 16-deep MFMA steps per tile
   static constexpr int CPS = sizeof(T) == 2 ? 2 : 4;  // chunks per 16-deep step
-  static constexpr int WTN = BN / NW, FN = WTN / 32;  // wave columns, 32-column blocks
+  static constexpr int WTN = BN / WN, FN = WTN / 32;  // wave columns, 32-column blocks
   static constexpr int STAGE = BN * BKB;
   static constexpr int NDMA = BN / (RPI * NW);        // DMA instructions per wave per tile
   static constexpr int LDS = STAGES * STAGE;
   static_assert(NDMA * RPI * NW == BN, "W tile rows must split over the waves");
-  static_assert(FN >= 1 && FN * 32 == WTN, "wave columns must be whole 32-column blocks");
+  static_assert(WN >= 1 && WN <= NW && FN >= 1 && FN * 32 * WN == BN, "whole 32-column blocks per wave");
   static_assert(STAGES >= 2 && (STAGES - 1) * NDMA <= 63, "vmcnt range");
   static_assert(KS % 2 == 0, "fragment double buffer alternates per 16-deep step");
 };
 
-// acc += A[0:32, K] * W[0:BN, K]^T for this wave's columns, where A is
-// resident in LDS (row pitch a_pitch bytes, chunks placed by res_chunk) and
-// W (rows w_rows valid, leading dimension ldw elements, nk K tiles) streams
-// through the ring.  The same pipeline as the GEMM's dtl_accumulate: one
-// barrier per K tile, placed before the tile's last 16-deep step; after it
-// the next tile's first fragments are read and its DMAs issued under the
-// last step's MFMAs (spread over the earlier steps with three or more
-// slots).  On return every DMA has landed and the workgroup has met at a
-// barrier, so the ring may be reused.
-template <typename T, int BN, int BKB, int STAGES>
-__device__ __forceinline__ void resident_a_accumulate(
-    char* ring, const char* sa, int a_pitch, const T* __restrict__ W, int64_t ldw, int w_rows, int nk,
-    f32x16 (&acc)[FfnPhase<T, BN, BKB, STAGES>::FN][1]) {
-  typedef FfnPhase<T, BN, BKB, STAGES> G;
-  constexpr int NW = G::NW, KS = G::KS, CPR = G::CPR, RPI = G::RPI, CPS = G::CPS;
-  constexpr int WTN = G::WTN, FN = G::FN, STAGE = G::STAGE, NDMA = G::NDMA;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int l32 = lane & 31, hi = lane >> 5;
+// The W operand of one phase streaming through LDS slots while the A
+// operand (32 rows, row pitch APITCH bytes, chunks placed by res_chunk)
+// stays resident:  acc += A[0:32, K] * W[0:BN, K]^T for this wave's
+// columns.  W has w_rows valid rows (leading dimension ldw elements) and nk
+// K tiles.  prologue() issues the first tiles' DMAs; they depend on nothing
+// in LDS, so a caller issues them before preparing A.  accumulate() is the
+// GEMM's dtl_accumulate pipeline: one barrier per K tile, placed before the
+// tile's last 16-deep step; after it the next tile's first fragments are
+// read and its DMAs issued under the last step's MFMAs (spread over the
+// earlier steps with three or more slots).  On return every DMA has landed
+// and the workgroup has met at a barrier, so the slots may be reused.
+// DMAs of streams issued after this one's prologue must not be outstanding
+// when accumulate() starts (each stream's waits count only its own).
+template <typename T, int BN, int BKB, int STAGES, int WN, int APITCH>
+struct WStream {
+  typedef FfnPhase<T, BN, BKB, STAGES, WN> G;
+  static constexpr int NW = G::NW, KS = G::KS, CPR = G::CPR, RPI = G::RPI, CPS = G::CPS;
+  static constexpr int WTN = G::WTN, FN = G::FN, STAGE = G::STAGE, NDMA = G::NDMA;
+  static constexpr int ACH = APITCH / 16;  // chunks per resident A row
+  static constexpr bool SPREAD = STAGES >= 3;
+  static constexpr int PRE = SPREAD ? STAGES - 1 : STAGES;  // tiles in flight before the loop
 
-  // W rows past w_rows and K past the slice read as zero: the descriptor
-  // ends at the last valid byte of the slice.
-  const int64_t span = ((int64_t)(w_rows - 1) * ldw + (int64_t)nk * G::BK) * (int64_t)sizeof(T);
-  const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, (int)span, 0x00020000);
+  char* ring;
+  int nk, lane, wave, l32, hi;
+  __amdgpu_buffer_rsrc_t rsw;
   uint32_t voff[NDMA];
+
+  __device__ __forceinline__ WStream(char* ring_, const T* __restrict__ W, int64_t ldw, int w_rows, int nk_)
+      : ring(ring_), nk(nk_) {
+    const int tid = threadIdx.x;
+    lane = tid & 63;
+    wave = tid >> 6;
+    l32 = lane & 31;
+    hi = lane >> 5;
+    // W rows past w_rows and K past the slice read as zero: the descriptor
+    // ends at the last valid byte of the slice.
+    const int64_t span = ((int64_t)(w_rows - 1) * ldw + (int64_t)nk * G::BK) * (int64_t)sizeof(T);
+    rsw = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, (int)span, 0x00020000);
 #pragma unroll
-  for (int i = 0; i < NDMA; ++i) {
-    const int r = (i * NW + wave) * RPI + lane / CPR;
-    voff[i] = (uint32_t)(r * ldw * (int64_t)sizeof(T)) + (uint32_t)(((lane % CPR) ^ swz<BKB>(r)) << 4);
+    for (int i = 0; i < NDMA; ++i) {
+      const int r = (i * NW + wave) * RPI + lane / CPR;
+      voff[i] = (uint32_t)(r * ldw * (int64_t)sizeof(T)) + (uint32_t)(((lane % CPR) ^ swz<BKB>(r)) << 4);
+    }
   }
-  auto dma = [&](int kt, int q) {
+
+  __device__ __forceinline__ void dma(int kt, int q) {
     char* sb = ring + (kt % STAGES) * STAGE;
     const uint32_t kb = kt < nk ? (uint32_t)(kt * BKB) : (uint32_t)kPastEnd;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_void*)(sb + (q * NW + wave) * 1024), 16,
                                              (uint32_t)(voff[q] + kb), 0, 0, 0);
-  };
-  // W fragment: ring row `row`, logical chunk c (swizzled by swz<BKB>)
-  auto wfrag = [&](const char* slot, int row, int ks) -> typename Mfma<T>::frag {
+  }
+
+  __device__ __forceinline__ void prologue() {
+#pragma unroll
+    for (int t = 0; t < PRE; ++t)
+#pragma unroll
+      for (int q = 0; q < NDMA; ++q) dma(t, q);
+  }
+
+  // W fragment: slot row `row`, step ks (chunks swizzled by swz<BKB>)
+  __device__ __forceinline__ typename Mfma<T>::frag wfrag(const char* slot, int row, int ks) const {
     const char* rb = slot + row * BKB;
     const int sw = swz<BKB>(row);
     if constexpr (sizeof(T) == 2) {
@@ -112,97 +144,111 @@ __device__ __forceinline__ void resident_a_accumulate(
       f[4] = up.x; f[5] = up.y; f[6] = up.z; f[7] = up.w;
       return f;
     }
-  };
+  }
+
   // A fragment: resident row l32, K tile kt, step ks
-  const char* arow = sa + l32 * a_pitch;
-  auto afrag = [&](int kt, int ks) -> typename Mfma<T>::frag {
+  __device__ __forceinline__ typename Mfma<T>::frag afrag(const char* arow, int kt, int ks) const {
     const int c = kt * CPR + CPS * ks;
     if constexpr (sizeof(T) == 2) {
-      return *reinterpret_cast<const typename Mfma<T>::frag*>(arow + (res_chunk(c + hi, l32) << 4));
+      return *reinterpret_cast<const typename Mfma<T>::frag*>(arow + (res_chunk<ACH>(c + hi, l32) << 4));
     } else {
-      const float4 lo = *reinterpret_cast<const float4*>(arow + (res_chunk(c + 2 * hi, l32) << 4));
-      const float4 up = *reinterpret_cast<const float4*>(arow + (res_chunk(c + 2 * hi + 1, l32) << 4));
+      const float4 lo = *reinterpret_cast<const float4*>(arow + (res_chunk<ACH>(c + 2 * hi, l32) << 4));
+      const float4 up = *reinterpret_cast<const float4*>(arow + (res_chunk<ACH>(c + 2 * hi + 1, l32) << 4));
       typename Mfma<T>::frag f;
       f[0] = lo.x; f[1] = lo.y; f[2] = lo.z; f[3] = lo.w;
       f[4] = up.x; f[5] = up.y; f[6] = up.z; f[7] = up.w;
       return f;
     }
-  };
+  }
 
-  constexpr bool SPREAD = STAGES >= 3;
-  constexpr int PRE = SPREAD ? STAGES - 1 : STAGES;
+  // Requires prologue() before, and A complete in LDS and published by a
+  // workgroup barrier.
+  __device__ __forceinline__ void accumulate(const char* sa, f32x16 (&acc)[FN][1]) {
+    const char* arow = sa + l32 * APITCH;
+    const bool active = wave < WN;  // wave-uniform
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"((PRE - 1) * NDMA) : "memory");
+    asm volatile("s_barrier" ::: "memory");
+    constexpr int NMF = FN, NDS = FN + 1;  // MFMAs and fragment reads per step
+    constexpr int NSLOT = NMF > NDS ? NMF : NDS;
+    typename Mfma<T>::frag fa[2], fw[2][FN];
+    if (active) {
+      fa[0] = afrag(arow, 0, 0);
 #pragma unroll
-  for (int t = 0; t < PRE; ++t)
+      for (int i = 0; i < FN; ++i) fw[0][i] = wfrag(ring, wave * WTN + 32 * i + l32, 0);
+    }
+    for (int kt = 0; kt < nk; ++kt) {
+      const char* st = ring + (kt % STAGES) * STAGE;
+      const char* nx = ring + ((kt + 1) % STAGES) * STAGE;
 #pragma unroll
-    for (int q = 0; q < NDMA; ++q) dma(t, q);
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"((PRE - 1) * NDMA) : "memory");
-  asm volatile("s_barrier" ::: "memory");
-  constexpr int NMF = FN, NDS = FN + 1;  // MFMAs and fragment reads per step
-  constexpr int NSLOT = NMF > NDS ? NMF : NDS;
-  typename Mfma<T>::frag fa[2], fw[2][FN];
-  fa[0] = afrag(0, 0);
-#pragma unroll
-  for (int i = 0; i < FN; ++i) fw[0][i] = wfrag(ring, wave * WTN + 32 * i + l32, 0);
-  for (int kt = 0; kt < nk; ++kt) {
-    const char* st = ring + (kt % STAGES) * STAGE;
-    const char* nx = ring + ((kt + 1) % STAGES) * STAGE;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int b = ks & 1;
-      const bool last = ks + 1 == KS;
-      const char* rw = last ? nx : st;
-      const int rks = last ? 0 : ks + 1;
-      const int rkt = last ? min(kt + 1, nk - 1) : kt;  // (the last tile re-reads itself: unused)
-      if (last) {
-        __builtin_amdgcn_sched_barrier(0);
-        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((STAGES - 2) * NDMA) : "memory");
-        asm volatile("s_barrier" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-      for (int m = 0; m < NSLOT; ++m) {
-        if (m < NMF) Mfma<T>::mma(acc[m][0], fw[b][m], fa[b]);
-        if (m == 0) fa[b ^ 1] = afrag(rkt, rks);
-        else if (m < NDS) fw[b ^ 1][m - 1] = wfrag(rw, wave * WTN + 32 * (m - 1) + l32, rks);
-        if constexpr (SPREAD) {
-          constexpr int TOT = (KS - 1) * NSLOT;
-          const int i = ks * NSLOT + m;
-          if (!last) {
-#pragma unroll
-            for (int q = i * NDMA / TOT; q < (i + 1) * NDMA / TOT; ++q) dma(kt - 1 + STAGES, q);
-          }
-        } else if (last) {
-#pragma unroll
-          for (int q = m * NDMA / NSLOT; q < (m + 1) * NDMA / NSLOT; ++q) dma(kt + STAGES, q);
+      for (int ks = 0; ks < KS; ++ks) {
+        const int b = ks & 1;
+        const bool last = ks + 1 == KS;
+        const char* rw = last ? nx : st;
+        const int rks = last ? 0 : ks + 1;
+        const int rkt = last ? min(kt + 1, nk - 1) : kt;  // (the last tile re-reads itself: unused)
+        if (last) {
+          __builtin_amdgcn_sched_barrier(0);
+          asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((STAGES - 2) * NDMA) : "memory");
+          asm volatile("s_barrier" ::: "memory");
+          __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int m = 0; m < NSLOT; ++m) {
+          if (active) {
+            if (m < NMF) Mfma<T>::mma(acc[m][0], fw[b][m], fa[b]);
+            if (m == 0) fa[b ^ 1] = afrag(arow, rkt, rks);
+            else if (m < NDS) fw[b ^ 1][m - 1] = wfrag(rw, wave * WTN + 32 * (m - 1) + l32, rks);
+          }
+          if constexpr (SPREAD) {
+            constexpr int TOT = (KS - 1) * NSLOT;
+            const int i = ks * NSLOT + m;
+            if (!last) {
+#pragma unroll
+              for (int q = i * NDMA / TOT; q < (i + 1) * NDMA / TOT; ++q) dma(kt - 1 + STAGES, q);
+            }
+          } else if (last) {
+#pragma unroll
+            for (int q = m * NDMA / NSLOT; q < (m + 1) * NDMA / NSLOT; ++q) dma(kt + STAGES, q);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-}
+};
 
-// LDS plan of one instantiation: [A rows][mid][ring], the ring shared by
-// both phases (and by the epilogue staging after phase 2).
+template <int A, int B> struct Max { static constexpr int v = A > B ? A : B; };
+template <int A, int B> struct Min { static constexpr int v = A < B ? A : B; };
+
+// LDS plan of one (dtype, d, slice) instantiation.  Regions, in order:
+//   W1 ring (ST1 slots of FC rows x 128 B),
+//   W2 slots (SEP: the whole slice, two tiles; else the W1 ring is reused
+//   for W2 after phase 1), A rows, mid rows.  The epilogue staging of phase
+//   3 overlays the weight regions.
 template <typename T, int D, int FC>
 struct FfnLayout {
-  static constexpr int ES = sizeof(T);
+  static constexpr int ES = sizeof(T), KB = 1024;
   static constexpr int A_PITCH = D * ES, MID_PITCH = FC * ES;
   static constexpr int A_BYTES = kFfnRows * A_PITCH, MID_BYTES = kFfnRows * MID_PITCH;
-  static constexpr int BUDGET = 160 * 1024 - A_BYTES - MID_BYTES;
-  // phase 2's W2 tile is D rows: 128-byte rows when two slots fit, else 64
-  static constexpr int BKB2 = (2 * D * 128 <= BUDGET || ES == 4) ? 128 : 64;
-  static constexpr int ST2 = (BUDGET / (D * BKB2)) < 4 ? (BUDGET / (D * BKB2)) : 4;
-  static constexpr int ST1 = (BUDGET / (FC * 128)) < 4 ? (BUDGET / (FC * 128)) : 4;
-  typedef FfnPhase<T, FC, 128, ST1> P1;
-  typedef FfnPhase<T, D, BKB2, ST2> P2;
+  static constexpr int WN1 = Min<FC / 32, kFfnWaves>::v;  // waves computing phase 1
+  static constexpr int ST1 = 4;
+  typedef FfnPhase<T, FC, 128, ST1, WN1> P1;
+  // W2 slice in two K tiles when it fits beside everything else
+  static constexpr int BKB_SEP = FC * ES / 2;
+  static constexpr bool SEP = (BKB_SEP == 64 || BKB_SEP == 128) &&
+                              P1::LDS + 2 * D * BKB_SEP + A_BYTES + MID_BYTES <= 160 * KB;
+  static constexpr int BUDGET_SHARED = 160 * KB - A_BYTES - MID_BYTES;
+  static constexpr int BKB2 = SEP ? BKB_SEP : ((2 * D * 128 <= BUDGET_SHARED || ES == 4) ? 128 : 64);
+  static constexpr int ST2 = SEP ? 2 : Min<BUDGET_SHARED / (D * BKB2), 4>::v;
+  typedef FfnPhase<T, D, BKB2, ST2, kFfnWaves> P2;
+  static constexpr int W2_OFF = SEP ? P1::LDS : 0;
+  static constexpr int WEIGHTS = SEP ? P1::LDS + P2::LDS : Max<P1::LDS, P2::LDS>::v;
   static constexpr int STAGE_EPI = kFfnWaves * EpiStage<T, kEpiStoreF32, P2::FN>::BYTES;
-  static constexpr int RING = P1::LDS > P2::LDS ? (P1::LDS > STAGE_EPI ? P1::LDS : STAGE_EPI)
-                                                 : (P2::LDS > STAGE_EPI ? P2::LDS : STAGE_EPI);
-  static constexpr int TOTAL = A_BYTES + MID_BYTES + RING;
-  static_assert(A_PITCH >= 256 && MID_PITCH >= 256, "resident rows need >= 16 chunks");
-  static_assert(TOTAL <= 160 * 1024, "fused FFN exceeds LDS");
+  static constexpr int RING = Max<WEIGHTS, STAGE_EPI>::v;
+  static constexpr int TOTAL = RING + A_BYTES + MID_BYTES;
+  static_assert(TOTAL <= 160 * KB, "fused FFN exceeds LDS");
 };
 
 template <typename T, int D, int FC, bool LNA>
@@ -215,78 +261,134 @@ __global__ __launch_bounds__(256) void ffn_fused_kernel(
   typedef typename Lay::P1 P1;
   typedef typename Lay::P2 P2;
   constexpr int VEC = 16 / (int)sizeof(T);
+  constexpr int ACH = Lay::A_PITCH / 16, MCH = Lay::MID_PITCH / 16;
   __shared__ __attribute__((aligned(1024))) char smem[Lay::TOTAL];
   char* ring = smem;
   char* sa = smem + Lay::RING;
   char* smid = sa + Lay::A_BYTES;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l32 = lane & 31, hi = lane >> 5;
+  const int hi = lane >> 5, l32 = lane & 31;
   // XCD-contiguous logical order, split-major: the row blocks of one f-slice
   // (which read the same W1 / W2 slices) run on one XCD and share its L2.
   const int t = xcd_remap(blockIdx.x, nrb * splits);
   const int s = t / nrb, m0 = (t % nrb) * kFfnRows, fc0 = s * FC;
 
+  // this wave's b1 columns, read before any DMA so that no later wait for
+  // them has to drain the weight copies
+  float4 b1v[P1::FN][4];
+#pragma unroll
+  for (int i = 0; i < P1::FN; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int n = min(wave, Lay::WN1 - 1) * P1::WTN + 32 * i + 8 * g + 4 * hi;
+      b1v[i][g] = b1 ? Quad<T>::to(*reinterpret_cast<const typename Quad<T>::raw*>(b1 + fc0 + n))
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+
+  WStream<T, FC, 128, Lay::ST1, Lay::WN1, Lay::A_PITCH> w1s(ring, W1 + (int64_t)fc0 * D, D, FC, D / P1::BK);
+  WStream<T, D, Lay::BKB2, Lay::ST2, kFfnWaves, Lay::MID_PITCH> w2s(ring + Lay::W2_OFF, W2 + fc0, f, D,
+                                                                    FC / P2::BK);
+  // The streams' waits count their own copies only: W2's (when it has its
+  // own slots) are issued first, so they are older than all of W1's.
+  auto start_copies = [&]() {
+    if constexpr (Lay::SEP) w2s.prologue();
+    w1s.prologue();
+  };
+
   // ---- 1. A rows into LDS (compute dtype)
   if constexpr (LNA) {
-    // one row per wave at a time; lane l owns the 4-element chunks l, l+64, ...
-    constexpr int NCH = D / 4, MAXCH = (NCH + 63) / 64;
+    // rows wave, wave + 4, ...: every row's loads issued at once, then the
+    // LayerNorm of each; lane l owns the 4-element chunks l, l+64, ...
+    constexpr int NCH = D / 4, MAXCH = (NCH + 63) / 64, RPW = kFfnRows / kFfnWaves;
     const float* res = static_cast<const float*>(Av);
-    for (int r = wave; r < kFfnRows; r += kFfnWaves) {
-      const int m = m0 + r;
-      char* row = sa + r * Lay::A_PITCH;
-      if (m >= M) {
-        for (int c = lane; c < Lay::A_PITCH / 16; c += 64) *reinterpret_cast<uint4*>(row + (c << 4)) = make_uint4(0, 0, 0, 0);
-        continue;
-      }
-      float4 x[MAXCH];
+    float4 x[RPW][MAXCH], gm[MAXCH], bt[MAXCH];
+#pragma unroll
+    for (int j = 0; j < MAXCH; ++j) {
+      const int c = lane + 64 * j;
+      const bool in = NCH % 64 == 0 || c < NCH;
+      gm[j] = in ? reinterpret_cast<const float4*>(gamma)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+      bt[j] = in ? reinterpret_cast<const float4*>(beta)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      const int m = m0 + wave + kFfnWaves * i;
 #pragma unroll
       for (int j = 0; j < MAXCH; ++j) {
         const int c = lane + 64 * j;
-        x[j] = (NCH % 64 == 0 || c < NCH) ? reinterpret_cast<const float4*>(res + (int64_t)m * lda)[c]
-                                          : make_float4(0.f, 0.f, 0.f, 0.f);
+        x[i][j] = (m < M && (NCH % 64 == 0 || c < NCH)) ? reinterpret_cast<const float4*>(res + (int64_t)m * lda)[c]
+                                                        : make_float4(0.f, 0.f, 0.f, 0.f);
       }
-      // the add+LayerNorm kernel's arithmetic, operation for operation
+    }
+    start_copies();
+    // the add+LayerNorm kernel's arithmetic, operation for operation, with
+    // the eight rows' wave reductions interleaved
+    const float inv_n = 1.0f / (float)D;
+    float mean[RPW], rstd[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
       float sm = 0.f;
 #pragma unroll
-      for (int j = 0; j < MAXCH; ++j) sm += (x[j].x + x[j].y) + (x[j].z + x[j].w);
-      const float inv_n = 1.0f / (float)D;
-      const float mean = wave_sum(sm) * inv_n;
+      for (int j = 0; j < MAXCH; ++j) sm += (x[i][j].x + x[i][j].y) + (x[i][j].z + x[i][j].w);
+      mean[i] = sm;
+    }
+    wave_sum_n<RPW>(mean);
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      mean[i] *= inv_n;
       float q = 0.f;
 #pragma unroll
       for (int j = 0; j < MAXCH; ++j) {
         const int c = lane + 64 * j;
         if (NCH % 64 == 0 || c < NCH) {
-          const float a = x[j].x - mean, b = x[j].y - mean, cc = x[j].z - mean, d = x[j].w - mean;
+          const float a = x[i][j].x - mean[i], b = x[i][j].y - mean[i], cc = x[i][j].z - mean[i],
+                      d = x[i][j].w - mean[i];
           q += (a * a + b * b) + (cc * cc + d * d);
         }
       }
-      const float var = wave_sum(q) * inv_n;
-      const float rstd = 1.0f / sqrtf(var + eps);
+      rstd[i] = q;
+    }
+    wave_sum_n<RPW>(rstd);
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) rstd[i] = 1.0f / sqrtf(rstd[i] * inv_n + eps);
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      const int r = wave + kFfnWaves * i, m = m0 + r;
+      char* row = sa + r * Lay::A_PITCH;
 #pragma unroll
       for (int j = 0; j < MAXCH; ++j) {
         const int c = lane + 64 * j;
         if (NCH % 64 == 0 || c < NCH) {
-          const float4 g = reinterpret_cast<const float4*>(gamma)[c];
-          const float4 bb = reinterpret_cast<const float4*>(beta)[c];
           float4 y;
-          y.x = (x[j].x - mean) * rstd * g.x + bb.x;
-          y.y = (x[j].y - mean) * rstd * g.y + bb.y;
-          y.z = (x[j].z - mean) * rstd * g.z + bb.z;
-          y.w = (x[j].w - mean) * rstd * g.w + bb.w;
+          if (m < M) {
+            y.x = (x[i][j].x - mean[i]) * rstd[i] * gm[j].x + bt[j].x;
+            y.y = (x[i][j].y - mean[i]) * rstd[i] * gm[j].y + bt[j].y;
+            y.z = (x[i][j].z - mean[i]) * rstd[i] * gm[j].z + bt[j].z;
+            y.w = (x[i][j].w - mean[i]) * rstd[i] * gm[j].w + bt[j].w;
+          } else {
+            y = make_float4(0.f, 0.f, 0.f, 0.f);  // rows past the input: zeros
+          }
           // elements 4c .. 4c+3: chunk 4c / VEC, byte (4c % VEC) * size
           const int ch = (4 * c) / VEC, off = ((4 * c) % VEC) * (int)sizeof(T);
-          *reinterpret_cast<typename Quad<T>::raw*>(row + (res_chunk(ch, r) << 4) + off) = Quad<T>::from(y);
+          *reinterpret_cast<typename Quad<T>::raw*>(row + (res_chunk<ACH>(ch, r) << 4) + off) = Quad<T>::from(y);
         }
       }
     }
   } else {
     const T* A = static_cast<const T*>(Av);
-    constexpr int CPRA = Lay::A_PITCH / 16;  // 16-byte chunks per row
-    for (int i = tid; i < kFfnRows * CPRA; i += 256) {
-      const int r = i / CPRA, c = i % CPRA, m = m0 + r;
-      const uint4 v = m < M ? *reinterpret_cast<const uint4*>(A + (int64_t)m * lda + c * VEC) : make_uint4(0, 0, 0, 0);
-      *reinterpret_cast<uint4*>(sa + r * Lay::A_PITCH + (res_chunk(c, r) << 4)) = v;
+    constexpr int PER = kFfnRows * ACH / 256;
+    static_assert(PER * 256 == kFfnRows * ACH, "A rows must split over the threads");
+    uint4 v[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int i = tid + 256 * k, r = i / ACH, c = i % ACH, m = m0 + r;
+      v[k] = m < M ? *reinterpret_cast<const uint4*>(A + (int64_t)m * lda + c * VEC) : make_uint4(0, 0, 0, 0);
+    }
+    start_copies();
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int i = tid + 256 * k, r = i / ACH, c = i % ACH;
+      *reinterpret_cast<uint4*>(sa + r * Lay::A_PITCH + (res_chunk<ACH>(c, r) << 4)) = v[k];
     }
   }
   __syncthreads();
@@ -295,28 +397,29 @@ __global__ __launch_bounds__(256) void ffn_fused_kernel(
   {
     f32x16 acc[P1::FN][1];
     zero_acc<T, 1, P1::FN>(acc);
-    resident_a_accumulate<T, FC, 128, Lay::ST1>(ring, sa, Lay::A_PITCH, W1 + (int64_t)fc0 * D, D, FC,
-                                                D / P1::BK, acc);
+    w1s.accumulate(sa, acc);
+    if constexpr (!Lay::SEP) w2s.prologue();  // the ring is free: W2's first tiles load under the GELU
+    if (wave < Lay::WN1) {
 #pragma unroll
-    for (int i = 0; i < P1::FN; ++i)
+      for (int i = 0; i < P1::FN; ++i)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int n = wave * P1::WTN + 32 * i + 8 * g + 4 * hi;  // column within the slice
-        const float4 bv = b1 ? Quad<T>::to(*reinterpret_cast<const typename Quad<T>::raw*>(b1 + fc0 + n))
-                             : make_float4(0.f, 0.f, 0.f, 0.f);
-        float4 v = make_float4(gelu_erf(acc[i][0][4 * g + 0] + bv.x), gelu_erf(acc[i][0][4 * g + 1] + bv.y),
-                               gelu_erf(acc[i][0][4 * g + 2] + bv.z), gelu_erf(acc[i][0][4 * g + 3] + bv.w));
-        const int ch = n / VEC, off = (n % VEC) * (int)sizeof(T);
-        *reinterpret_cast<typename Quad<T>::raw*>(smid + l32 * Lay::MID_PITCH + (res_chunk(ch, l32) << 4) + off) =
-            Quad<T>::from(v);
-      }
+        for (int g = 0; g < 4; ++g) {
+          const int n = wave * P1::WTN + 32 * i + 8 * g + 4 * hi;  // column within the slice
+          const float4 bv = b1v[i][g];
+          float4 v = make_float4(gelu_erf(acc[i][0][4 * g + 0] + bv.x), gelu_erf(acc[i][0][4 * g + 1] + bv.y),
+                                 gelu_erf(acc[i][0][4 * g + 2] + bv.z), gelu_erf(acc[i][0][4 * g + 3] + bv.w));
+          const int ch = n / VEC, off = (n % VEC) * (int)sizeof(T);
+          *reinterpret_cast<typename Quad<T>::raw*>(smid + l32 * Lay::MID_PITCH + (res_chunk<MCH>(ch, l32) << 4) +
+                                                    off) = Quad<T>::from(v);
+        }
+    }
   }
   __syncthreads();
 
   // ---- 3. P = mid W2[:, fc0 : fc0+FC]^T
   f32x16 acc[P2::FN][1];
   zero_acc<T, 1, P2::FN>(acc);
-  resident_a_accumulate<T, D, Lay::BKB2, Lay::ST2>(ring, smid, Lay::MID_PITCH, W2 + fc0, f, D, FC / P2::BK, acc);
+  w2s.accumulate(smid, acc);
 
   // ---- 4. store the fp32 partial (split 0 adds b2), or add into the residual
   char* stage = ring + wave * EpiStage<T, kEpiStoreF32, P2::FN>::BYTES;
@@ -328,7 +431,8 @@ __global__ __launch_bounds__(256) void ffn_fused_kernel(
   }
 }
 
-// Instantiated (d, f-slice) pairs: d in {128, 256, 512}, slice 128.
+// Instantiated: d in {128, 256, 512} (fp32: 128, 256), f-slices of 64 or
+// 128 columns.
 template <typename T, int D, int FC>
 static int launch_ffn_d(const void* a, int64_t lda, const float* gamma, const float* beta, float eps,
                         const void* w1, const void* b1, const void* w2, const void* b2, float* out, int64_t ldo,
@@ -346,32 +450,41 @@ static int launch_ffn_d(const void* a, int64_t lda, const float* gamma, const fl
   return check_launch("tjk_ffn");
 }
 
-constexpr int kFfnSlice = 128;
-
 static bool ffn_shape_ok(int64_t d, int64_t f, int64_t splits, int dtype) {
   if (dtype != TJK_F32 && dtype != TJK_F16 && dtype != TJK_BF16) return false;
-  if (splits < 1 || f % splits != 0 || f / splits != kFfnSlice) return false;
+  if (splits < 1 || f % splits != 0 || (f / splits != 64 && f / splits != 128)) return false;
   if (dtype == TJK_F32) return d == 128 || d == 256;
   return d == 128 || d == 256 || d == 512;
+}
+
+template <typename T, int FC>
+static int launch_ffn_fc(int64_t d, const void* a, int64_t lda, const float* gamma, const float* beta, float eps,
+                         const void* w1, const void* b1, const void* w2, const void* b2, float* out, int64_t ldo,
+                         int64_t split_stride, int accumulate, int M, int f, int splits, hipStream_t s) {
+  switch (d) {
+    case 128:
+      return launch_ffn_d<T, 128, FC>(a, lda, gamma, beta, eps, w1, b1, w2, b2, out, ldo, split_stride, accumulate,
+                                      M, f, splits, s);
+    case 256:
+      return launch_ffn_d<T, 256, FC>(a, lda, gamma, beta, eps, w1, b1, w2, b2, out, ldo, split_stride, accumulate,
+                                      M, f, splits, s);
+    default:
+      if constexpr (sizeof(T) == 2)
+        return launch_ffn_d<T, 512, FC>(a, lda, gamma, beta, eps, w1, b1, w2, b2, out, ldo, split_stride,
+                                        accumulate, M, f, splits, s);
+      return fail(TJK_EUNSUPPORTED, "tjk_ffn: d=%lld not supported for fp32", (long long)d);
+  }
 }
 
 template <typename T>
 static int launch_ffn(int64_t d, const void* a, int64_t lda, const float* gamma, const float* beta, float eps,
                       const void* w1, const void* b1, const void* w2, const void* b2, float* out, int64_t ldo,
                       int64_t split_stride, int accumulate, int M, int f, int splits, hipStream_t s) {
-  switch (d) {
-    case 128:
-      return launch_ffn_d<T, 128, kFfnSlice>(a, lda, gamma, beta, eps, w1, b1, w2, b2, out, ldo, split_stride,
-                                             accumulate, M, f, splits, s);
-    case 256:
-      return launch_ffn_d<T, 256, kFfnSlice>(a, lda, gamma, beta, eps, w1, b1, w2, b2, out, ldo, split_stride,
-                                             accumulate, M, f, splits, s);
-    default:
-      if constexpr (sizeof(T) == 2)
-        return launch_ffn_d<T, 512, kFfnSlice>(a, lda, gamma, beta, eps, w1, b1, w2, b2, out, ldo, split_stride,
-                                               accumulate, M, f, splits, s);
-      return fail(TJK_EUNSUPPORTED, "tjk_ffn: d=%lld not supported for fp32", (long long)d);
-  }
+  if (f / splits == 64)
+    return launch_ffn_fc<T, 64>(d, a, lda, gamma, beta, eps, w1, b1, w2, b2, out, ldo, split_stride, accumulate, M,
+                                f, splits, s);
+  return launch_ffn_fc<T, 128>(d, a, lda, gamma, beta, eps, w1, b1, w2, b2, out, ldo, split_stride, accumulate, M,
+                               f, splits, s);
 }
 
 }  // namespace tjk
@@ -389,8 +502,8 @@ extern "C" int tjk_ffn(const void* a, int a_dtype, int64_t lda, const float* ln_
   if (rows < 0 || d <= 0 || f <= 0) return fail(TJK_EINVAL, "tjk_ffn: bad shape rows=%lld d=%lld f=%lld",
                                                 (long long)rows, (long long)d, (long long)f);
   if (!ffn_shape_ok(d, f, splits, dtype))
-    return fail(TJK_EUNSUPPORTED, "tjk_ffn: unsupported d=%lld f=%lld splits=%d dtype=%d (f / splits must be %d; "
-                "d in {128, 256, 512}, fp32 d <= 256)", (long long)d, (long long)f, splits, dtype, kFfnSlice);
+    return fail(TJK_EUNSUPPORTED, "tjk_ffn: unsupported d=%lld f=%lld splits=%d dtype=%d (f / splits must be 64 or "
+                "128; d in {128, 256, 512}, fp32 d <= 256)", (long long)d, (long long)f, splits, dtype);
   if (rows == 0) return TJK_OK;
   if (rows > INT32_MAX / 2 || f > INT32_MAX || d * f * dtype_size(dtype) >= kPastEnd)
     return fail(TJK_EUNSUPPORTED, "tjk_ffn: shape exceeds the 32-bit buffer range");

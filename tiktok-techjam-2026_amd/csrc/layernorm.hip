@@ -20,6 +20,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <type_traits>
+
 #include "tjk_common.h"
 
 namespace tjk {
@@ -44,7 +46,7 @@ int check_launch(const char* what) {
 template <typename TRes, typename TDelta, typename TOut, int MAXCH, bool FULL>
 __global__ __launch_bounds__(256) void add_layernorm_kernel(
     const TRes* res, int64_t ld_res,  // may alias res_out (in-place update)
-    const TDelta* __restrict__ delta, int64_t ld_delta, int n_delta, int64_t delta_stride,
+    const TDelta* __restrict__ delta, int64_t ld_delta,
     float* res_out, int64_t ld_res_out,
     TOut* __restrict__ out, int64_t ld_out,
     const float* __restrict__ gamma, const float* __restrict__ beta,
@@ -70,49 +72,12 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(
     }
     if (delta != nullptr) {
       const TDelta* drow = delta + src * ld_delta;
-      if (MAXCH > 4 || n_delta == 1) {
 #pragma unroll
-        for (int j = 0; j < MAXCH; ++j) {
-          const int c = lane + 64 * j;
-          if (FULL || c < nch) {
-            float4 d = Quad<TDelta>::to(reinterpret_cast<const typename Quad<TDelta>::raw*>(drow)[c]);
-            x[j].x += d.x; x[j].y += d.y; x[j].z += d.z; x[j].w += d.w;
-          }
-        }
-      } else if constexpr (MAXCH <= 4) {
-        // delta = d_0 + d_1 + ... + d_{n_delta-1}, summed in that order (the
-        // split partials of the fused FFN), then added to the residual.  The
-        // loads of UNR slices are issued together before their adds.
-        constexpr int UNR = 16 / MAXCH;
-        float4 dsum[MAXCH];
-        for (int p0 = 0; p0 < n_delta; p0 += UNR) {
-          float4 dv[UNR][MAXCH];
-#pragma unroll
-          for (int u = 0; u < UNR; ++u)
-#pragma unroll
-            for (int j = 0; j < MAXCH; ++j) {
-              const int c = lane + 64 * j;
-              dv[u][j] = (p0 + u < n_delta && (FULL || c < nch))
-                             ? Quad<TDelta>::to(reinterpret_cast<const typename Quad<TDelta>::raw*>(
-                                   drow + (int64_t)(p0 + u) * delta_stride)[c])
-                             : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-#pragma unroll
-          for (int u = 0; u < UNR; ++u) {
-            if (p0 + u == 0) {
-#pragma unroll
-              for (int j = 0; j < MAXCH; ++j) dsum[j] = dv[0][j];
-            } else if (p0 + u < n_delta) {
-#pragma unroll
-              for (int j = 0; j < MAXCH; ++j) {
-                dsum[j].x += dv[u][j].x; dsum[j].y += dv[u][j].y; dsum[j].z += dv[u][j].z; dsum[j].w += dv[u][j].w;
-              }
-            }
-          }
-        }
-#pragma unroll
-        for (int j = 0; j < MAXCH; ++j) {
-          x[j].x += dsum[j].x; x[j].y += dsum[j].y; x[j].z += dsum[j].z; x[j].w += dsum[j].w;
+      for (int j = 0; j < MAXCH; ++j) {
+        const int c = lane + 64 * j;
+        if (FULL || c < nch) {
+          float4 d = Quad<TDelta>::to(reinterpret_cast<const typename Quad<TDelta>::raw*>(drow)[c]);
+          x[j].x += d.x; x[j].y += d.y; x[j].z += d.z; x[j].w += d.w;
         }
       }
     }
@@ -183,16 +148,168 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(
   }
 }
 
+// Split deltas (the fused FFN's fp32 f-slice partials): one row per
+// workgroup.  Wave w sums the consecutive slices [w q, (w + 1) q), q =
+// ceil(n_delta / 4), in order, with all of its loads issued together; wave
+// 0 then adds the four sums in wave order, x = res + (((S_0 + S_1) + S_2) +
+// S_3) (waves without slices skipped), and normalises the row with the row
+// kernel's arithmetic.  Spreading one row's slices over four waves keeps a
+// launch of a few hundred rows from waiting out n_delta / 4 load latencies.
+template <typename TRes, typename TOut, int MAXCH>
+__global__ __launch_bounds__(256) void add_layernorm_parts_kernel(
+    const TRes* res, int64_t ld_res,  // may alias res_out (in-place update)
+    const float* __restrict__ parts, int64_t ld_parts, int n_parts, int64_t part_stride,
+    float* res_out, int64_t ld_res_out, TOut* __restrict__ out, int64_t ld_out,
+    const float* __restrict__ gamma, const float* __restrict__ beta, int n, float eps,
+    const int32_t* __restrict__ row_index, const uint8_t* __restrict__ row_mask) {
+  constexpr int PER = 32 / MAXCH;  // slices per load batch of one wave
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nch = n >> 2;
+  const int64_t row = blockIdx.x;
+  const int64_t src = row_index != nullptr ? (int64_t)row_index[row] : row;
+  __shared__ float4 s_sum[3][MAXCH][64];
+  if (src < 0) {  // scatter hole: an exact zero row
+    if (wave == 0) {
+      typename Quad<TOut>::raw* yrow = reinterpret_cast<typename Quad<TOut>::raw*>(out + row * ld_out);
+#pragma unroll
+      for (int j = 0; j < MAXCH; ++j)
+        if (lane + 64 * j < nch) yrow[lane + 64 * j] = Quad<TOut>::from(make_float4(0.f, 0.f, 0.f, 0.f));
+    }
+    return;
+  }
+  const int q = (n_parts + 3) / 4, p_lo = min(wave * q, n_parts), p_hi = min(p_lo + q, n_parts);
+  float4 x[MAXCH];
+  if (wave == 0) {
+    const TRes* rrow = res + src * ld_res;
+#pragma unroll
+    for (int j = 0; j < MAXCH; ++j) {
+      const int c = lane + 64 * j;
+      x[j] = c < nch ? Quad<TRes>::to(reinterpret_cast<const typename Quad<TRes>::raw*>(rrow)[c])
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  float4 acc[MAXCH];
+  const float* prow = parts + src * ld_parts;
+  for (int p0 = p_lo; p0 < p_hi; p0 += PER) {
+    float4 v[PER][MAXCH];
+#pragma unroll
+    for (int u = 0; u < PER; ++u)
+#pragma unroll
+      for (int j = 0; j < MAXCH; ++j) {
+        const int c = lane + 64 * j;
+        v[u][j] = (p0 + u < p_hi && c < nch)
+                      ? reinterpret_cast<const float4*>(prow + (int64_t)(p0 + u) * part_stride)[c]
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      if (p0 + u == p_lo) {
+#pragma unroll
+        for (int j = 0; j < MAXCH; ++j) acc[j] = v[u][j];
+      } else if (p0 + u < p_hi) {
+#pragma unroll
+        for (int j = 0; j < MAXCH; ++j) {
+          acc[j].x += v[u][j].x; acc[j].y += v[u][j].y; acc[j].z += v[u][j].z; acc[j].w += v[u][j].w;
+        }
+      }
+    }
+  }
+  if (wave > 0 && p_lo < p_hi) {
+#pragma unroll
+    for (int j = 0; j < MAXCH; ++j) s_sum[wave - 1][j][lane] = acc[j];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 1; w < 4; ++w) {
+    if (w * q < n_parts) {
+#pragma unroll
+      for (int j = 0; j < MAXCH; ++j) {
+        const float4 o = s_sum[w - 1][j][lane];
+        acc[j].x += o.x; acc[j].y += o.y; acc[j].z += o.z; acc[j].w += o.w;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < MAXCH; ++j) {
+    x[j].x += acc[j].x; x[j].y += acc[j].y; x[j].z += acc[j].z; x[j].w += acc[j].w;
+  }
+  if (res_out != nullptr) {
+    float4* orow = reinterpret_cast<float4*>(res_out + row * ld_res_out);
+#pragma unroll
+    for (int j = 0; j < MAXCH; ++j)
+      if (lane + 64 * j < nch) orow[lane + 64 * j] = x[j];
+  }
+  float sm = 0.f;
+#pragma unroll
+  for (int j = 0; j < MAXCH; ++j) sm += (x[j].x + x[j].y) + (x[j].z + x[j].w);
+  const float inv_n = 1.0f / (float)n;
+  const float mean = wave_sum(sm) * inv_n;
+  float qq = 0.f;
+#pragma unroll
+  for (int j = 0; j < MAXCH; ++j) {
+    if (lane + 64 * j < nch) {
+      const float a = x[j].x - mean, b = x[j].y - mean, cc = x[j].z - mean, d = x[j].w - mean;
+      qq += (a * a + b * b) + (cc * cc + d * d);
+    }
+  }
+  const float var = wave_sum(qq) * inv_n;
+  const float rstd = 1.0f / sqrtf(var + eps);
+  const bool zero = row_mask != nullptr && row_mask[row] == 0;
+  typename Quad<TOut>::raw* yrow = reinterpret_cast<typename Quad<TOut>::raw*>(out + row * ld_out);
+#pragma unroll
+  for (int j = 0; j < MAXCH; ++j) {
+    const int c = lane + 64 * j;
+    if (c < nch) {
+      float4 y;
+      if (zero) {
+        y = make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        const float4 g = reinterpret_cast<const float4*>(gamma)[c], b = reinterpret_cast<const float4*>(beta)[c];
+        y.x = (x[j].x - mean) * rstd * g.x + b.x;
+        y.y = (x[j].y - mean) * rstd * g.y + b.y;
+        y.z = (x[j].z - mean) * rstd * g.z + b.z;
+        y.w = (x[j].w - mean) * rstd * g.w + b.w;
+      }
+      yrow[c] = Quad<TOut>::from(y);
+    }
+  }
+}
+
+template <typename TRes, typename TOut>
+static int launch_ln_parts(const void* res, int64_t ld_res, const float* parts, int64_t ld_parts, int n_parts,
+                           int64_t part_stride, float* res_out, int64_t ld_res_out, void* out, int64_t ld_out,
+                           const float* gamma, const float* beta, int64_t rows, int n, float eps,
+                           const int32_t* row_index, const uint8_t* row_mask, hipStream_t stream) {
+  const int nch = n / 4;
+  const dim3 grid((unsigned)rows), block(256);
+#define TJK_LNP(MC)                                                                                           \
+  hipLaunchKernelGGL((add_layernorm_parts_kernel<TRes, TOut, MC>), grid, block, 0, stream, (const TRes*)res,   \
+                     ld_res, parts, ld_parts, n_parts, part_stride, res_out, ld_res_out, (TOut*)out, ld_out, gamma, \
+                     beta, n, eps, row_index, row_mask)
+  if (nch <= 64) TJK_LNP(1);
+  else if (nch <= 128) TJK_LNP(2);
+  else TJK_LNP(4);
+#undef TJK_LNP
+  return check_launch("tjk_add_layernorm");
+}
+
 template <typename TRes, typename TDelta, typename TOut>
 static int launch_ln(const void* res, int64_t ld_res, const void* delta, int64_t ld_delta, int n_delta,
                      int64_t delta_stride, float* res_out, int64_t ld_res_out, void* out, int64_t ld_out,
                      const float* gamma, const float* beta, int64_t rows, int n, float eps,
                      const int32_t* row_index, const uint8_t* row_mask, hipStream_t stream) {
+  if constexpr (std::is_same<TDelta, float>::value) {
+    if (n_delta > 1)
+      return launch_ln_parts<TRes, TOut>(res, ld_res, (const float*)delta, ld_delta, n_delta, delta_stride, res_out,
+                                         ld_res_out, out, ld_out, gamma, beta, rows, n, eps, row_index, row_mask,
+                                         stream);
+  }
   const int nch = n / 4;
   dim3 grid((unsigned)((rows + 3) / 4)), block(256);
 #define TJK_LN_LAUNCH(MC, FULL)                                                                    \
   hipLaunchKernelGGL((add_layernorm_kernel<TRes, TDelta, TOut, MC, FULL>), grid, block, 0, stream,     \
-                     (const TRes*)res, ld_res, (const TDelta*)delta, ld_delta, n_delta, delta_stride, res_out, ld_res_out, \
+                     (const TRes*)res, ld_res, (const TDelta*)delta, ld_delta, res_out, ld_res_out, \
                      (TOut*)out, ld_out, gamma, beta, rows, n, eps, row_index, row_mask)
 #define TJK_LN_CASE(MC)                                   \
   if (nch <= 64 * MC) {                                   \
@@ -292,8 +409,8 @@ extern "C" int tjk_add_layernorm(const void* res, int res_dtype, int64_t ld_res,
                                                           delta_split_stride % 4 != 0))))
     return fail(TJK_EINVAL, "tjk_add_layernorm: delta_splits=%d needs a split stride >= rows x ld_delta, "
                 "multiple of 4", delta_splits);
-  if (delta && delta_splits > 1 && n > 1024)
-    return fail(TJK_EUNSUPPORTED, "tjk_add_layernorm: split deltas need n <= 1024");
+  if (delta && delta_splits > 1 && (n > 1024 || delta_dtype != TJK_F32))
+    return fail(TJK_EUNSUPPORTED, "tjk_add_layernorm: split deltas are fp32 rows of n <= 1024");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const int dd = delta ? delta_dtype : res_dtype;
   const int nd = delta ? delta_splits : 0;

@@ -199,4 +199,32 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+// wave_sum of N independent values at once: each value goes through
+// exactly wave_sum's operations (same results, bit for bit), with the N
+// DPP chains interleaved so their latencies overlap.
+template <int N>
+__device__ __forceinline__ void wave_sum_n(float (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    v[i] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v[i]), 0xB1, 0xF, 0xF, true));
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    v[i] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v[i]), 0x4E, 0xF, 0xF, true));
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    v[i] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v[i]), 0x141, 0xF, 0xF, true));
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    v[i] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v[i]), 0x140, 0xF, 0xF, true));
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int iv = __builtin_bit_cast(int, v[i]);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48));
+    v[i] = (r0 + r1) + (r2 + r3);
+  }
+}
+
 }  // namespace tjk

@@ -131,7 +131,7 @@ class _Evaluator:
                     usage = max(usage, budget_usage(ref, got, self.atol, self.rtol))
                 xb, mb = self.bench_input
                 ms = _time_ms(lambda: model(xb, mb), self.iters)
-        except ops.TjkError as exc:
+        except (ops.TjkError, ValueError) as exc:
             return {"plan": plan, "admissible": False, "error": str(exc)[:160]}
         finally:
             set_override(None)
@@ -159,7 +159,11 @@ def tune_workload(w: Workload, trials: int = 2, margin: float = 0.85, iters: int
     cur = ev.evaluate(base)
     show("heuristic", cur)
     if not admissible(cur) and base.compute_dtype != torch.float32:
-        esc = ev.evaluate(replace(base, compute_dtype=torch.float32, label="autotuned-fp32"))
+        # fp32 compute (IEEE fp32 MFMA, the reference's escalation with TF32
+        # off, bench/autotune.py:203-217); the single-launch FFN only where
+        # it has an fp32 kernel for the shape
+        ffn = "fused" if base.ffn == "fused" and fused_ffn_ok(w.d_model, w.ffn_dim, torch.float32) else "gemm"
+        esc = ev.evaluate(replace(base, compute_dtype=torch.float32, ffn=ffn, label="autotuned-fp32"))
         show("escalate-fp32", esc)
         if admissible(esc):
             cur = esc
@@ -194,6 +198,7 @@ def main(argv: Optional[List[str]] = None) -> int:
     ap.add_argument("--margin", type=float, default=0.85)
     ap.add_argument("--iters", type=int, default=30)
     ap.add_argument("--dry-run", action="store_true")
+    ap.add_argument("--out", default=None, help="plans file to merge into (default: the package's plans.json)")
     args = ap.parse_args(argv)
     tuned: Dict[str, Plan] = {}
     for name in args.workloads.split(","):
@@ -207,8 +212,9 @@ def main(argv: Optional[List[str]] = None) -> int:
         tuned[key] = plan
         print(f"    -> {res['latency_ms']:.3f} ms budget={res['usage']:.0%} {plan.to_json()}", flush=True)
     if tuned and not args.dry_run:
-        save_plans(tuned)
-        print(f"wrote {len(tuned)} plan(s) to plans.json", flush=True)
+        from pathlib import Path
+        save_plans(tuned, Path(args.out) if args.out else None)
+        print(f"wrote {len(tuned)} plan(s) to {args.out or 'plans.json'}", flush=True)
     return 0
 
 

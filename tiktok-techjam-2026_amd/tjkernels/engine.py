@@ -47,7 +47,7 @@ import torch
 
 from . import ops, schedule as sched_mod, tiles
 from .graphs import GraphCache
-from .plans import Plan, select_plan
+from .plans import Plan, fused_ffn_ok, select_plan
 
 try:
     from torch.utils.weak import WeakTensorKeyDictionary
@@ -194,6 +194,18 @@ def build_packing(lengths: Tuple[int, ...], seq: int, device: torch.device) -> P
 
 # ---------------------------------------------------------------- forward
 
+def ffn_slices(rows: int, ffn_dim: int) -> int:
+    """f-slices of the single-launch FFN: 128 columns each, or 64 when 128
+    would leave fewer than 32 workgroups of 32 rows (measured on MI355X: C2,
+    128 rows and f = 2048, 16 slices 0.160 ms vs 32 slices 0.168 ms per
+    forward; C1's fp32 FFN, 96 rows and f = 512, 9.7 us with 8 slices vs
+    11.3 us with 4)."""
+    blocks = -(-rows // 32)
+    if ffn_dim % 128 == 0 and blocks * (ffn_dim // 128) >= 32:
+        return ffn_dim // 128
+    return max(ffn_dim // 64, 1)
+
+
 class ModelShape(NamedTuple):
     d_model: int
     heads: int
@@ -336,8 +348,8 @@ class Engine:
         shape."""
         plan, shp = self.plan, self.shape
         fused = plan.ffn == "fused"
-        splits = (plan.ffn_splits or max(shp.ffn_dim // 128, 1)) if fused else 1
         rows = packing.tokens if mode == MASK_PREFIX else batch * seq
+        splits = (plan.ffn_splits or ffn_slices(rows, shp.ffn_dim)) if fused else 1
         cdt, d, f = plan.compute_dtype, shp.d_model, shp.ffn_dim
         epi_res = ops.EPI_BIAS_RESIDUAL if plan.residual_epilogue else ops.EPI_BIAS
         tp = Tiles(
@@ -494,6 +506,10 @@ class Engine:
             plan = select_plan(batch, seq, shp.d_model, shp.heads, shp.ffn_dim, shp.layers, shp.causal,
                                self.dtype, self.device)
             plan.validate()
+            if plan.ffn == "fused" and not fused_ffn_ok(shp.d_model, shp.ffn_dim, plan.compute_dtype,
+                                                        plan.ffn_splits):
+                raise ValueError(f"plan {plan.label!r}: the single-launch FFN has no kernel for d={shp.d_model}, "
+                                 f"f={shp.ffn_dim}, {plan.compute_dtype} (see tjk_ffn_supported)")
             self._plans[(batch, seq)] = plan
         self.plan = plan
         self._use_weights(plan)

@@ -29,7 +29,7 @@ to select, and the product path has no non-HIP fallback):
 * ``pack_prefix``: run only the valid tokens of prefix masks.
 
 Environment: ``TJ_NO_GRAPH``, ``TJ_COMPUTE_DTYPE``, ``TJ_DEFERRED_RESIDUAL``,
-``TJ_NO_PACK``, ``TJ_ATTN_PLAN``, ``TJ_FFN`` (gemm | fused);
+``TJ_NO_PACK``, ``TJ_ATTN_PLAN``, ``TJ_FFN`` (gemm | fused), ``TJ_FFN_SPLITS``;
 ``TJ_GEMM_TUNE=0`` (tjkernels.tiles) skips the measured tile choice.
 Tuned keys carry the GPU architecture (``...@gfx950``).
 """
@@ -120,11 +120,12 @@ def shape_key(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int,
 
 
 def fused_ffn_ok(d_model: int, ffn_dim: int, compute_dtype: torch.dtype, splits: int = 0) -> bool:
-    """Whether the single-launch FFN kernel takes the shape (tjk_ffn_supported)."""
+    """Whether the single-launch FFN kernel takes the shape (tjk_ffn_supported):
+    ``splits`` slices, or with 0 both slice widths the engine may pick."""
     from . import ops
-    if splits <= 0:
-        splits = max(ffn_dim // 128, 1)
-    return ops.ffn_supported(d_model, ffn_dim, splits, compute_dtype)
+    if splits > 0:
+        return ops.ffn_supported(d_model, ffn_dim, splits, compute_dtype)
+    return all(ops.ffn_supported(d_model, ffn_dim, max(ffn_dim // w, 1), compute_dtype) for w in (64, 128))
 
 
 def default_plan(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int,
@@ -204,6 +205,9 @@ def _env_adjusted(plan: Plan) -> Plan:
         changes["pack_prefix"] = False
     if env.get("TJ_FFN") in FFN_KINDS:
         changes["ffn"] = env["TJ_FFN"]
+    splits = env.get("TJ_FFN_SPLITS", "")
+    if splits.isdigit():
+        changes["ffn_splits"] = int(splits)
     attn = env.get("TJ_ATTN_PLAN", "")
     if attn.lstrip("-").isdigit():
         changes["attn_plan"] = int(attn)

@@ -7,10 +7,10 @@ TRACE.csv is ``*_kernel_trace.csv`` of ``rocprofv3 --kernel-trace``; FETCH /
 WRITE are ``*_counter_collection.csv`` of two ``rocprofv3 --pmc FETCH_SIZE``
 / ``--pmc WRITE_SIZE`` runs.  Kernels are labelled by their position in the
 forward: the forward's launch sequence is fixed (first LayerNorm, then per
-layer QKV GEMM, attention, out-proj GEMM, LayerNorm, FFN1 GEMM, FFN2 GEMM,
-LayerNorm, and the final LayerNorm), so every complete sequence that starts
-with the first LayerNorm (the one reading the model-dtype input) is split
-into labelled launches.  Sequences are grouped by the first LayerNorm's grid
+layer QKV GEMM, attention, out-proj GEMM, and either LayerNorm + FFN1 GEMM +
+FFN2 GEMM or the single-launch FFN, LayerNorm, and the final LayerNorm), so
+every complete sequence that starts with the first LayerNorm (the one
+reading the model-dtype input) is split into labelled launches.  Sequences are grouped by the first LayerNorm's grid
 (the packed forward has fewer rows than the all-rows one) and each group is
 reported separately.  HBM bytes per launch are FETCH_SIZE and WRITE_SIZE
 (KiB per dispatch) scaled by what the same counters read for the bench's
@@ -25,7 +25,8 @@ import collections
 import csv
 from typing import Dict, List, Optional, Tuple
 
-GEMM, FLASH, LN, COPY = "gemm_dtl_kernel", "flash_", "add_layernorm_kernel", "__amd_rocclr_copyBuffer"
+GEMM, FLASH, LN, FFN = "gemm_dtl_kernel", "flash_", "add_layernorm_kernel", "ffn_fused_kernel"
+COPY = "__amd_rocclr_copyBuffer"
 
 
 def _is_first_ln(name: str) -> bool:
@@ -34,15 +35,20 @@ def _is_first_ln(name: str) -> bool:
     return LN in name and ("add_layernorm_kernelIDF16b" in name or "add_layernorm_kernelIDF16_" in name)
 
 
-def _labels(layers: int) -> List[str]:
+def _labels(layers: int, fused: bool = False) -> List[str]:
     seq = ["ln_first"]
     for i in range(layers):
         if i:
             seq.append("add_layernorm")
-        seq += ["gemm_qkv", "flash_attention", "gemm_out_residual", "add_layernorm",
-                "gemm_ffn1_gelu", "gemm_ffn2_residual"]
+        seq += ["gemm_qkv", "flash_attention", "gemm_out_residual"]
+        seq += ["ffn_fused"] if fused else ["add_layernorm", "gemm_ffn1_gelu", "gemm_ffn2_residual"]
     seq.append("ln_final")
     return seq
+
+
+def _kind_ok(label: str, name: str) -> bool:
+    return ((GEMM in name) == label.startswith("gemm") and (FLASH in name) == (label == "flash_attention")
+            and (FFN in name) == (label == "ffn_fused"))
 
 
 def _grid(r: dict) -> int:
@@ -54,26 +60,27 @@ def _wg(r: dict) -> int:
 
 
 def _tjk(name: str) -> bool:
-    return GEMM in name or FLASH in name or LN in name
+    return GEMM in name or FLASH in name or LN in name or FFN in name
 
 
 def _forwards(rows: List[dict], layers: int) -> Dict[int, List[List[Tuple[str, dict]]]]:
     """{first-LN grid: [forward as [(label, row)]]} from dispatch-ordered rows."""
-    labels = _labels(layers)
     tjk = [r for r in rows if _tjk(r["Kernel_Name"])]
     out: Dict[int, List[List[Tuple[str, dict]]]] = collections.defaultdict(list)
     i = 0
     while i < len(tjk):
-        if _is_first_ln(tjk[i]["Kernel_Name"]) and i + len(labels) <= len(tjk):
-            seq = tjk[i:i + len(labels)]
-            ok = all((GEMM in r["Kernel_Name"]) == lab.startswith("gemm")
-                     and (FLASH in r["Kernel_Name"]) == (lab == "flash_attention")
-                     for lab, r in zip(labels, seq))
-            if ok and not any(_is_first_ln(r["Kernel_Name"]) for r in seq[1:]):
-                out[_grid(seq[0])].append(list(zip(labels, seq)))
-                i += len(labels)
-                continue
-        i += 1
+        matched = False
+        if _is_first_ln(tjk[i]["Kernel_Name"]):
+            for labels in (_labels(layers), _labels(layers, fused=True)):
+                seq = tjk[i:i + len(labels)]
+                if (len(seq) == len(labels) and all(_kind_ok(lab, r["Kernel_Name"]) for lab, r in zip(labels, seq))
+                        and not any(_is_first_ln(r["Kernel_Name"]) for r in seq[1:])):
+                    out[_grid(seq[0])].append(list(zip(labels, seq)))
+                    i += len(labels)
+                    matched = True
+                    break
+        if not matched:
+            i += 1
     return out
 
 
@@ -106,7 +113,7 @@ def summarize(trace: str, layers: int = 4, fetch: Optional[str] = None,
         lines.append(f"forward group: first LayerNorm grid {grid} threads, {len(fwds)} forwards, "
                      f"kernel time per forward {sorted(totals)[len(totals) // 2]:.1f} us (median)")
         lines.append(f"{'label':<20} {'launches/fwd':>12} {'avg us':>9} {'us/fwd':>9} {'WGs':>6}  kernel")
-        for lab in dict.fromkeys(_labels(layers)):
+        for lab in dict.fromkeys(lab for lab, _ in fwds[-1]):
             v = per[lab]
             n = len(v) // len(fwds)
             lines.append(f"{lab:<20} {n:>12} {sum(v) / len(v):>9.2f} {sum(v) / len(fwds):>9.1f} "
@@ -131,10 +138,11 @@ def summarize(trace: str, layers: int = 4, fetch: Optional[str] = None,
                     acc[lab].append(float(r["Counter_Value"]) * 1024.0 * factor)
             scaled[tag] = {lab: sum(v) / len(v) for lab, v in acc.items()}
         lines.append(f"{'label':<20} {'fetch MB':>9} {'write MB':>9} {'total MB':>9}")
-        for lab in dict.fromkeys(_labels(layers)):
+        seen = list(dict.fromkeys(_labels(layers) + _labels(layers, fused=True)))
+        for lab in [x for x in seen if x in scaled["fetch"] or x in scaled["write"]]:
             fb, wb = scaled["fetch"].get(lab, 0.0), scaled["write"].get(lab, 0.0)
             lines.append(f"{lab:<20} {fb / 1e6:>9.1f} {wb / 1e6:>9.1f} {(fb + wb) / 1e6:>9.1f}")
-        for lab in dict.fromkeys(_labels(layers)):
+        for lab in [x for x in seen if x in scaled["fetch"] or x in scaled["write"]]:
             fb, wb = scaled["fetch"].get(lab, 0.0), scaled["write"].get(lab, 0.0)
             lines.append(f"traffic_bytes_per_launch[{lab}] {fb + wb:.0f}")
     return "\n".join(lines)

@@ -20,7 +20,12 @@ Ablation variants (each against the full stack on the same workloads):
   * library tile rule, no measured tiles TJ_GEMM_TUNE=0
   * padded rows computed (no packing)    TJ_NO_PACK=1
   * plain attention kernel (plan 1)      TJ_ATTN_PLAN=1
+  * two-launch FFN (no single-launch)    TJ_FFN=gemm
   * fp32 compute (accuracy escalation)   TJ_COMPUTE_DTYPE=float32
+
+The report opens with the system it ran on (GPU, its architecture and CU
+count, ROCm / torch versions, host CPU and the cores the CPU baseline may
+use), as the reference's report header does (bench/make_report.py:34-95).
 """
 
 from __future__ import annotations
@@ -44,8 +49,49 @@ LEAVE_ONE = [
     ("library tile rule", {"TJ_GEMM_TUNE": "0"}),
     ("padded rows computed", {"TJ_NO_PACK": "1"}),
     ("plain attention kernel", {"TJ_ATTN_PLAN": "1"}),
+    ("two-launch FFN", {"TJ_FFN": "gemm"}),
     ("fp32 compute", {"TJ_COMPUTE_DTYPE": "float32"}),
 ]
+
+
+_SYSTEM_PROBE = r"""
+import json, os, platform, torch
+info = {"torch": torch.__version__, "hip": getattr(torch.version, "hip", None),
+        "host_cores": len(os.sched_getaffinity(0)), "host": platform.node()}
+try:
+    with open("/proc/cpuinfo") as f:
+        info["cpu"] = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), None)
+    with open("/proc/meminfo") as f:
+        info["host_mem_gib"] = round(int(f.readline().split()[1]) / 2**20, 1)
+except OSError:
+    pass
+if torch.cuda.is_available():
+    p = torch.cuda.get_device_properties(0)
+    info.update(gpu=p.name, arch=p.gcnArchName, cus=p.multi_processor_count,
+                vram_gib=round(p.total_memory / 2**30, 1), gpus_visible=torch.cuda.device_count())
+print(json.dumps(info))
+"""
+
+
+def system_info(timeout: float = 120.0) -> Dict[str, object]:
+    """GPU and host facts, read in a child process (the caller never touches
+    the GPU itself)."""
+    try:
+        proc = subprocess.run([sys.executable, "-c", _SYSTEM_PROBE], capture_output=True, text=True,
+                              timeout=timeout, cwd=str(REPO))
+        line = [ln for ln in proc.stdout.splitlines() if ln.startswith("{")]
+        return json.loads(line[-1]) if line else {"error": proc.stderr.strip()[-200:]}
+    except (subprocess.TimeoutExpired, ValueError) as exc:
+        return {"error": str(exc)[:200]}
+
+
+def system_header(info: Dict[str, object]) -> str:
+    if "error" in info:
+        return f"System: unknown ({info['error']})\n"
+    gpu = (f"{info.get('gpu', 'no GPU')} ({info.get('arch', '?')}, {info.get('cus', '?')} CUs, "
+           f"{info.get('vram_gib', '?')} GiB)")
+    return (f"System: {gpu}; ROCm/HIP {info.get('hip')}, torch {info.get('torch')}; host "
+            f"{info.get('cpu', '?')}, {info.get('host_cores', '?')} cores usable, {info.get('host_mem_gib', '?')} GiB\n")
 
 
 def run_case(workload: str, steps: int, warmup: int, cpu: bool, env: Dict[str, str],
@@ -143,6 +189,7 @@ def main(argv: Optional[List[str]] = None) -> int:
     out = Path(args.out)
     out.mkdir(parents=True, exist_ok=True)
 
+    info = system_info()
     records = []
     for w in [s for s in args.workloads.split(",") if s]:
         print(f"--- {w}", flush=True)
@@ -152,7 +199,7 @@ def main(argv: Optional[List[str]] = None) -> int:
         if "error_tail" in r:
             print("    " + str(r["error_tail"]).replace("\n", "\n    "), flush=True)
         records.append(r)
-    text = f"## Sweep ({args.tag})\n\n" + sweep_table(records) + "\n"
+    text = f"## Sweep ({args.tag})\n\n" + system_header(info) + "\n" + sweep_table(records) + "\n"
 
     abl_rows: List[Dict[str, object]] = []
     abl = [s for s in args.ablation.split(",") if s]
@@ -170,7 +217,7 @@ def main(argv: Optional[List[str]] = None) -> int:
         text += ablation_table(abl_rows, abl) + "\n"
 
     stamp = time.strftime("%Y%m%d-%H%M%S")
-    (out / f"{args.tag}-{stamp}.json").write_text(json.dumps({"tag": args.tag, "records": records,
+    (out / f"{args.tag}-{stamp}.json").write_text(json.dumps({"tag": args.tag, "system": info, "records": records,
                                                               "ablation": abl_rows}, indent=2))
     (out / f"{args.tag}-{stamp}.md").write_text(text)
     print("\n" + text, flush=True)
