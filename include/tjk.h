@@ -173,6 +173,25 @@ int tjk_flash_fwd_sched(const void* qkv, int64_t stride_s, int64_t stride_c, int
                         const int32_t* work, int n_work, float* partials, size_t partials_bytes,
                         int n_slots, int dtype, void* stream);
 size_t tjk_flash_partial_bytes(int head_dim, int n_slots);
+
+/*
+ * tjk_flash_fwd_sched without the partials argument: the workspace (split
+ * partials, error word, flags) is a static device array of
+ * tjk_flash_sched_static_bytes() bytes (4 MiB) that every device the
+ * library runs on holds until the process ends; the entry point allocates
+ * nothing.  No counterpart in the reference: it is for callers that cannot
+ * allocate (code under stream capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  n_slots must keep tjk_flash_partial_bytes(head_dim,
+ * n_slots) within the array (TJK_EUNSUPPORTED otherwise, nothing launched).
+ * Each call first clears the error word and flags with a fill kernel on
+ * `stream`; calls on one device share the array, so calls that overlap
+ * (unordered streams) race.  The current device must be the stream's.
+ */
+int tjk_flash_fwd_sched_static(const void* qkv, int64_t stride_s, int64_t stride_c, int64_t stride_h,
+                               void* out, int64_t ld_out, int batch, int max_seqlen, int heads,
+                               int head_dim, float scale, int causal, const int32_t* cu_seqlens,
+                               const int32_t* work, int n_work, int n_slots, int dtype, void* stream);
+size_t tjk_flash_sched_static_bytes(void);
 /* Workgroups of the scheduled kernel resident per CU (> 0), or a negative /
  * hipError_t status. */
 int tjk_flash_sched_occupancy(int head_dim, int dtype);

@@ -32,6 +32,7 @@
 // longest-first (the last query blocks have the most key tiles).
 
 #include <algorithm>
+#include <mutex>
 
 #include "tjk_common.h"
 
@@ -957,12 +958,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
   }
 }
 
+__global__ __launch_bounds__(256) void clear_words_kernel(int* p, int n) {
+  for (int i = threadIdx.x; i < n; i += 256) p[i] = 0;
+}
+
 template <typename T, int HDP>
 static int launch_sched(const void* qkv, int64_t ss, int64_t sc, int64_t sh, void* out, int64_t ld_out,
                         int B, int S, int H, int hd, float scale_log2, int causal, const int32_t* cu_seqlens,
-                        const int32_t* work, int n_work, float* partials, int n_slots, hipStream_t st) {
+                        const int32_t* work, int n_work, float* partials, int n_slots, bool clear, hipStream_t st) {
   // [n_slots partial slots][error word][n_slots flags]; flags[-1] is the error word
   int* flags = partials != nullptr ? reinterpret_cast<int*>(partials + (size_t)n_slots * 128 * (HDP + 2)) + 1 : nullptr;
+  if (clear && flags != nullptr) {
+    // a fill kernel, not hipMemsetAsync: the call may be recorded into a graph
+    hipLaunchKernelGGL(clear_words_kernel, dim3(1), dim3(256), 0, st, flags - 1, n_slots + 1);
+  }
 #define TJK_PIPE_SCHED(FULL)                                                                                  \
   hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, false, FULL>), dim3((unsigned)n_work), dim3(256), 0, st,      \
                      (const T*)qkv, (int64_t)0, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, \
@@ -1132,37 +1141,35 @@ extern "C" size_t tjk_flash_partial_bytes(int head_dim, int n_slots) {
   return (size_t)n_slots * 128 * (hdp + 2) * sizeof(float) + (size_t)(n_slots + 1) * sizeof(int);
 }
 
-extern "C" int tjk_flash_fwd_sched(const void* qkv, int64_t stride_s, int64_t stride_c, int64_t stride_h,
-                                   void* out, int64_t ld_out, int batch, int max_seqlen, int heads,
-                                   int head_dim, float scale, int causal, const int32_t* cu_seqlens,
-                                   const int32_t* work, int n_work, float* partials, size_t partials_bytes,
-                                   int n_slots, int dtype, void* stream) {
+static int flash_sched_entry(const char* who, const void* qkv, int64_t stride_s, int64_t stride_c,
+                             int64_t stride_h, void* out, int64_t ld_out, int batch, int max_seqlen, int heads,
+                             int head_dim, float scale, int causal, const int32_t* cu_seqlens, const int32_t* work,
+                             int n_work, float* partials, size_t partials_bytes, int n_slots, int dtype,
+                             bool clear, hipStream_t st) {
   if (batch < 0 || max_seqlen < 0 || heads <= 0 || head_dim <= 0 || n_work < 0 || n_slots < 0)
-    return fail(TJK_EINVAL, "tjk_flash_fwd_sched: bad shape or counts");
+    return fail(TJK_EINVAL, "%s: bad shape or counts", who);
   if (n_work == 0) return TJK_OK;
-  if (!qkv || !out || !cu_seqlens || !work) return fail(TJK_EINVAL, "tjk_flash_fwd_sched: null pointer");
+  if (!qkv || !out || !cu_seqlens || !work) return fail(TJK_EINVAL, "%s: null pointer", who);
   if ((n_slots > 0 || partials) && (!partials || partials_bytes < tjk_flash_partial_bytes(head_dim, n_slots)))
-    return fail(TJK_EINVAL, "tjk_flash_fwd_sched: %d split slots need %zu bytes of partials (got %zu)", n_slots,
+    return fail(TJK_EINVAL, "%s: %d split slots need %zu bytes of partials (got %zu)", who, n_slots,
                 tjk_flash_partial_bytes(head_dim, n_slots), partials_bytes);
-  if ((int64_t)n_slots * 128 * 130 * 4 >= INT32_MAX) return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd_sched: too many slots");
-  if (dtype != TJK_F16 && dtype != TJK_BF16)
-    return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd_sched: 2-byte dtypes only (got %d)", dtype);
+  if ((int64_t)n_slots * 128 * 130 * 4 >= INT32_MAX) return fail(TJK_EUNSUPPORTED, "%s: too many slots", who);
+  if (dtype != TJK_F16 && dtype != TJK_BF16) return fail(TJK_EUNSUPPORTED, "%s: 2-byte dtypes only (got %d)", who, dtype);
   if (head_dim > 128 || head_dim % 8)
-    return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd_sched: head_dim=%d must be a multiple of 8 and <= 128", head_dim);
+    return fail(TJK_EUNSUPPORTED, "%s: head_dim=%d must be a multiple of 8 and <= 128", who, head_dim);
   if (stride_s % 8 || stride_c % 8 || stride_h % 8)
-    return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd_sched: strides must be multiples of 8 elements");
+    return fail(TJK_EUNSUPPORTED, "%s: strides must be multiples of 8 elements", who);
   if (((int64_t)max_seqlen * stride_s + head_dim) * 2 >= INT32_MAX)
-    return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd_sched: a sequence's K/V span exceeds 31-bit offsets");
-  if (ld_out < (int64_t)heads * head_dim || ld_out % 4) return fail(TJK_EINVAL, "tjk_flash_fwd_sched: bad ld_out");
+    return fail(TJK_EUNSUPPORTED, "%s: a sequence's K/V span exceeds 31-bit offsets", who);
+  if (ld_out < (int64_t)heads * head_dim || ld_out % 4) return fail(TJK_EINVAL, "%s: bad ld_out", who);
   if (((uintptr_t)qkv & 15) || ((uintptr_t)out & 7) || ((uintptr_t)work & 15) || ((uintptr_t)partials & 15))
-    return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd_sched: misaligned pointer");
-  if (!(scale > 0.f)) return fail(TJK_EINVAL, "tjk_flash_fwd_sched: scale must be positive");
+    return fail(TJK_EUNSUPPORTED, "%s: misaligned pointer", who);
+  if (!(scale > 0.f)) return fail(TJK_EINVAL, "%s: scale must be positive", who);
   const float scale_log2 = scale * 1.4426950408889634f;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
 #define TJK_SCHED(TT, HDP)                                                                                  \
   return launch_sched<TT, HDP>(qkv, stride_s, stride_c, stride_h, out, ld_out, batch, max_seqlen, heads, \
                                head_dim, scale_log2, causal, cu_seqlens, work, n_work, partials, n_slots, \
-                               st)
+                               clear, st)
   if (dtype == TJK_F16) {
     if (head_dim <= 32) TJK_SCHED(f16, 32);
     if (head_dim <= 64) TJK_SCHED(f16, 64);
@@ -1172,6 +1179,70 @@ extern "C" int tjk_flash_fwd_sched(const void* qkv, int64_t stride_s, int64_t st
   if (head_dim <= 64) TJK_SCHED(bf16, 64);
   TJK_SCHED(bf16, 128);
 #undef TJK_SCHED
+}
+
+extern "C" int tjk_flash_fwd_sched(const void* qkv, int64_t stride_s, int64_t stride_c, int64_t stride_h,
+                                   void* out, int64_t ld_out, int batch, int max_seqlen, int heads,
+                                   int head_dim, float scale, int causal, const int32_t* cu_seqlens,
+                                   const int32_t* work, int n_work, float* partials, size_t partials_bytes,
+                                   int n_slots, int dtype, void* stream) {
+  return flash_sched_entry("tjk_flash_fwd_sched", qkv, stride_s, stride_c, stride_h, out, ld_out, batch, max_seqlen,
+                           heads, head_dim, scale, causal, cu_seqlens, work, n_work, partials, partials_bytes,
+                           n_slots, dtype, false, reinterpret_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------- allocation-free variant
+//
+// The scheduled kernel's workspace (split partials, error word, flags) in a
+// file-scope device array instead of a caller's buffer, for callers that
+// cannot allocate.  Each device holds its own copy for the life of the
+// process; its address is looked up once per device with
+// hipGetSymbolAddress (the array's name is only a host-side stand-in) and
+// that pointer is what the kernels get.  Every call clears the error word
+// and the flags with a fill kernel first (graph-capture safe); calls that
+// overlap on one device share the array and race.
+constexpr size_t kSchedScratchBytes = size_t(4) << 20;
+static __device__ __attribute__((aligned(256))) unsigned char scratch[kSchedScratchBytes];
+
+static std::mutex g_scratch_mu;
+static float* g_scratch[64];
+
+static int scratch_on_current_device(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(hip_status(e), "tjk_flash_fwd_sched_static: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= 64) return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd_sched_static: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(e != hipSuccess ? hip_status(e) : TJK_EUNSUPPORTED,
+                  "tjk_flash_fwd_sched_static: hipGetSymbolAddress: %s", hipGetErrorString(e));
+    g_scratch[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch[dev];
+  return TJK_OK;
+}
+
+extern "C" size_t tjk_flash_sched_static_bytes(void) { return kSchedScratchBytes; }
+
+extern "C" int tjk_flash_fwd_sched_static(const void* qkv, int64_t stride_s, int64_t stride_c, int64_t stride_h,
+                                          void* out, int64_t ld_out, int batch, int max_seqlen, int heads,
+                                          int head_dim, float scale, int causal, const int32_t* cu_seqlens,
+                                          const int32_t* work, int n_work, int n_slots, int dtype, void* stream) {
+  if (head_dim <= 0 || n_slots < 0) return fail(TJK_EINVAL, "tjk_flash_fwd_sched_static: bad shape or counts");
+  const size_t need = tjk_flash_partial_bytes(head_dim, n_slots);
+  if (need > kSchedScratchBytes)
+    return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd_sched_static: %d split slots need %zu bytes, above the %zu-byte "
+                "static workspace", n_slots, need, kSchedScratchBytes);
+  if (n_work <= 0) return n_work < 0 ? fail(TJK_EINVAL, "tjk_flash_fwd_sched_static: bad shape or counts") : TJK_OK;
+  float* ws = nullptr;
+  const int rc = scratch_on_current_device(&ws);
+  if (rc != TJK_OK) return rc;
+  return flash_sched_entry("tjk_flash_fwd_sched_static", qkv, stride_s, stride_c, stride_h, out, ld_out, batch,
+                           max_seqlen, heads, head_dim, scale, causal, cu_seqlens, work, n_work, ws,
+                           kSchedScratchBytes, n_slots, dtype, true, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int tjk_flash_sched_occupancy(int head_dim, int dtype) {

@@ -43,6 +43,9 @@ _SIGNATURES = {
     "tjk_flash_fwd_sched": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _f32, _i32,
                                    _vp, _vp, _i32, _vp, ctypes.c_size_t, _i32, _i32, _vp]),
     "tjk_flash_partial_bytes": (ctypes.c_size_t, [_i32, _i32]),
+    "tjk_flash_fwd_sched_static": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _f32, _i32,
+                                          _vp, _vp, _i32, _i32, _i32, _vp]),
+    "tjk_flash_sched_static_bytes": (ctypes.c_size_t, []),
     "tjk_flash_sched_occupancy": (_i32, [_i32, _i32]),
     "tjk_ffn": (_i32, [_vp, _i32, _i64, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32,
                        _i64, _i64, _i64, _i32, _vp]),
