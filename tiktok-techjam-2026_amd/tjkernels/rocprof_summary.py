@@ -1,6 +1,7 @@
 """Per-kernel-class summary of a rocprofv3 run of ``bench.py``.
 
     python -m tjkernels.rocprof_summary TRACE.csv [--fetch FETCH.csv --write WRITE.csv]
+                                        [--pmc PMC.csv ...] [--cus 256]
                                         [--layers 4] [--copy-calib-bytes 268435456]
 
 TRACE.csv is ``*_kernel_trace.csv`` of ``rocprofv3 --kernel-trace``; FETCH /
@@ -15,7 +16,18 @@ reading the model-dtype input) is split into labelled launches.  Sequences are g
 reported separately.  HBM bytes per launch are FETCH_SIZE and WRITE_SIZE
 (KiB per dispatch) scaled by what the same counters read for the bench's
 plain 256 MiB copy (``__amd_rocclr_copyBuffer`` of 268435456 bytes read and
-written).
+written).  ``--pmc`` takes ``*_counter_collection.csv`` files of runs with
+several counters each and tabulates the mean per dispatch of every counter
+per label, with the derived figures:
+
+* MFMA busy % = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / XCDs x CUs x 4
+  SIMDs): GRBM_GUI_ACTIVE is summed over the XCDs, SQ_VALU_MFMA_BUSY_CYCLES
+  over the SIMDs (32 per v_mfma_f32_32x32x16 -- the C4 QKV GEMM's count is
+  exactly 32 x its SQ_INSTS_MFMA, which is M N K / (32 32 16));
+* LDS bank-conflict share = SQ_LDS_BANK_CONFLICT / SQ_ACTIVE_INST_LDS;
+* VALU instructions per MFMA instruction = SQ_INSTS_VALU / SQ_INSTS_MFMA
+  (SQ_INSTS_VALU counts the MFMAs too; they are subtracted);
+* transcendental share = SQ_INSTS_VALU_TRANS_F32 / (SQ_INSTS_VALU - SQ_INSTS_MFMA).
 """
 
 from __future__ import annotations
@@ -95,6 +107,60 @@ def _counter(path: str) -> Tuple[List[dict], Optional[float]]:
     return rows, (max(copies) if copies else None)
 
 
+def _pmc_by_label(paths: List[str], layers: int) -> Dict[str, Dict[str, float]]:
+    """{label: {counter: mean per dispatch}} over the first forward group of
+    each multi-counter counter-collection file."""
+    out: Dict[str, Dict[str, float]] = collections.defaultdict(dict)
+    for path in paths:
+        rows = list(csv.DictReader(open(path)))
+        by_dispatch: Dict[int, Dict[str, float]] = collections.defaultdict(dict)
+        meta: Dict[int, dict] = {}
+        for r in rows:
+            d = int(r["Dispatch_Id"])
+            by_dispatch[d][r["Counter_Name"]] = by_dispatch[d].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+            meta[d] = r
+        disp = [dict(meta[d], _counters=by_dispatch[d]) for d in sorted(meta)]
+        groups = _forwards(disp, layers)
+        if not groups:
+            continue
+        acc: Dict[str, Dict[str, List[float]]] = collections.defaultdict(lambda: collections.defaultdict(list))
+        for f in groups[min(groups)]:
+            for lab, r in f:
+                for name, v in r["_counters"].items():
+                    acc[lab][name].append(v)
+        for lab, counters in acc.items():
+            for name, vals in counters.items():
+                out[lab][name] = sum(vals) / len(vals)
+    return out
+
+
+def pmc_table(paths: List[str], layers: int = 4, cus: int = 256, xcds: int = 8) -> str:
+    data = _pmc_by_label(paths, layers)
+    if not data:
+        return "no complete forward found in the counter files"
+    names = sorted({n for c in data.values() for n in c})
+    lines = ["Counters per dispatch (mean over the forward's launches of each label):",
+             f"{'label':<20} " + " ".join(f"{n:>26}" for n in names)]
+    for lab, c in data.items():
+        lines.append(f"{lab:<20} " + " ".join(f"{c.get(n, float('nan')):>26.4g}" for n in names))
+    lines.append("")
+    lines.append(f"{'label':<20} {'MFMA busy %':>12} {'VALU/MFMA':>10} {'trans share':>12} {'LDS conflict':>13}")
+    for lab, c in data.items():
+        busy = c.get("SQ_VALU_MFMA_BUSY_CYCLES")
+        gui = c.get("GRBM_GUI_ACTIVE")
+        mf = c.get("SQ_INSTS_MFMA")
+        va = c.get("SQ_INSTS_VALU")
+        tr = c.get("SQ_INSTS_VALU_TRANS_F32")
+        util = 100.0 * busy / (gui / xcds * cus * 4) if busy is not None and gui else None
+        conf, lds = c.get("SQ_LDS_BANK_CONFLICT"), c.get("SQ_ACTIVE_INST_LDS")
+        cshare = conf / lds if conf is not None and lds else None
+        ratio = (va - mf) / mf if va is not None and mf else None
+        trans = tr / (va - mf) if tr is not None and va is not None and mf is not None and va > mf else None
+        fmt = lambda v, spec: "n/a" if v is None else format(v, spec)
+        lines.append(f"{lab:<20} {fmt(util, '12.1f')} {fmt(ratio, '10.2f')} {fmt(trans, '12.3f')} {fmt(cshare, '13.3f')}")
+    return "\n".join(lines)
+
+
 def summarize(trace: str, layers: int = 4, fetch: Optional[str] = None,
               write: Optional[str] = None, calib_bytes: float = 268435456.0) -> str:
     rows = list(csv.DictReader(open(trace)))
@@ -155,8 +221,14 @@ def main() -> int:
     ap.add_argument("--write")
     ap.add_argument("--layers", type=int, default=4)
     ap.add_argument("--copy-calib-bytes", type=float, default=268435456.0)
+    ap.add_argument("--pmc", nargs="*", default=[])
+    ap.add_argument("--cus", type=int, default=256)
+    ap.add_argument("--xcds", type=int, default=8)
     args = ap.parse_args()
     print(summarize(args.trace, args.layers, args.fetch, args.write, args.copy_calib_bytes))
+    if args.pmc:
+        print()
+        print(pmc_table(args.pmc, args.layers, args.cus, args.xcds))
     return 0
 
 
