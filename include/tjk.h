@@ -127,6 +127,10 @@ int tjk_gemm_plan_info(int dtype, int id, int* block_m, int* block_n, int* waves
  *              with key_mask.
  * A query row with no admissible key is written as 0.
  * head_dim in [1, 128], head_dim % 8 == 0 (16-byte aligned rows).
+ * plan_id: -1 chooses; 0 software-pipelined (2-byte types); 1 / 2 one / two
+ * 32-query blocks per wave; 3 plan 1 with two key splits; 4 whole sequences
+ * of at most 128 tokens, one wave per 32 queries (seq > 128 returns
+ * TJK_EUNSUPPORTED).  Every plan computes the same function.
  */
 int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s,
                   int64_t stride_c, int64_t stride_h,

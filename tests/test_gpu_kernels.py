@@ -295,7 +295,7 @@ def test_flash_shapes(device, dt, hd, seq, causal):
     g = _gen(hd * 1000 + seq)
     qkv = torch.randn(b, seq, 3, h, hd, generator=g).to(dt)
     ref = _attn_ref(qkv, causal)
-    for plan in (0, 1, 2, 3):
+    for plan in (0, 1, 2, 3) + ((4,) if seq <= 128 else ()):
         out = torch.full((b * seq, h * hd), float("nan"), dtype=dt, device=device)
         ops.flash_attention(qkv.to(device), out, causal=causal, plan=plan)
         torch.cuda.synchronize()
@@ -325,6 +325,67 @@ def test_flash_key_mask_and_lengths(device, dt):
         ops.flash_attention(qkv.to(device), out, causal=False, lengths=lengths.to(device), plan=plan)
         torch.cuda.synchronize()
         _close(out, ref, 1e-5 if dt == torch.float32 else 1e-2, 1e-5 if dt == torch.float32 else 1e-2)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("hd", [8, 32, 64, 128])
+def test_flash_short_sequences(device, dt, hd):
+    """Plan 4 (a whole sequence of <= 128 tokens per one-wave workgroup of
+    32 queries) against fp64: lengths around the 32-key blocks, causal and
+    not, a per-key mask, prefix lengths, packed sequences (no row outside a
+    sequence written), agreement with plan 1, and sequences over 128 tokens
+    refused."""
+    g = _gen(400 + hd)
+    tol = 1e-5 if dt == torch.float32 else 1e-2
+    h = 3
+    for seq in (1, 31, 32, 33, 96, 128):
+        qkv = torch.randn(2, seq, 3, h, hd, generator=g).to(dt)
+        for causal in (True, False):
+            ref = _attn_ref(qkv, causal)
+            out = torch.full((2 * seq, h * hd), float("nan"), dtype=dt, device=device)
+            ops.flash_attention(qkv.to(device), out, causal=causal, plan=4)
+            out1 = torch.empty_like(out)
+            ops.flash_attention(qkv.to(device), out1, causal=causal, plan=1)
+            torch.cuda.synchronize()
+            _close(out, ref, tol, tol)
+            assert (out.float() - out1.float()).abs().max().item() <= 2 * tol + 1e-6, (seq, causal)
+    # per-key mask and prefix lengths
+    seq = 128
+    qkv = torch.randn(3, seq, 3, h, hd, generator=g).to(dt)
+    key_mask = torch.rand(3, seq, generator=g) > 0.4
+    key_mask[:, 0] = True
+    for causal in (True, False):
+        out = torch.empty(3 * seq, h * hd, dtype=dt, device=device)
+        ops.flash_attention(qkv.to(device), out, causal=causal, key_mask=key_mask.to(device), plan=4)
+        torch.cuda.synchronize()
+        _close(out, _attn_ref(qkv, causal, key_mask), tol, tol)
+    lengths = torch.tensor([128, 1, 77], dtype=torch.int32)
+    pm = torch.arange(seq)[None, :] < lengths[:, None].long()
+    out = torch.empty(3 * seq, h * hd, dtype=dt, device=device)
+    ops.flash_attention(qkv.to(device), out, causal=False, lengths=lengths.to(device), plan=4)
+    torch.cuda.synchronize()
+    _close(out, _attn_ref(qkv, False, pm), tol, tol)
+    # packed sequences, including an empty one
+    lens = [128, 0, 1, 77, 33]
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    t = cu[-1]
+    packed = torch.randn(t, 3, h, hd, generator=g).to(dt)
+    cu_d = torch.tensor(cu, dtype=torch.int32, device=device)
+    for causal in (True, False):
+        out = torch.full((t + 5, h * hd), 7.0, dtype=dt, device=device)
+        ops.flash_attention(packed.to(device), out, causal=causal, plan=4, cu_seqlens=cu_d, max_seqlen=128)
+        torch.cuda.synchronize()
+        got = out.cpu()
+        for b, n in enumerate(lens):
+            if n:
+                _close(got[cu[b]:cu[b + 1]], _attn_ref(packed[cu[b]:cu[b + 1]].unsqueeze(0), causal), tol, tol)
+        assert (got[t:] == 7.0).all(), "rows past the packed tokens were written"
+    # the automatic plan takes plan 4 up to 128 tokens and refuses it above
+    qkv = torch.randn(1, 129, 3, h, hd, generator=g).to(dt)
+    with pytest.raises(ops.TjkError):
+        ops.flash_attention(qkv.to(device), torch.empty(129, h * hd, dtype=dt, device=device), plan=4)
 
 
 def test_flash_closed_forms(device):

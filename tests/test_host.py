@@ -60,7 +60,10 @@ def test_abi_rejects_bad_arguments_without_launching():
     # empty work is a successful no-op
     assert lib.tjk_gemm_bias(None, 8, None, 8, None, None, 8, 0, 4, 8, _lib.BF16, 0, -1, None) == 0
     assert lib.tjk_gemm_plan_count(_lib.BF16) >= 4
-    assert lib.tjk_flash_plan_count(_lib.F32) == 4
+    assert lib.tjk_flash_plan_count(_lib.F32) == 5
+    # plan 4 takes sequences of at most 128 tokens (checked before any launch)
+    assert lib.tjk_flash_fwd(fake, 0, 3 * 64, 64, 64, fake, 64, 1, 129, 1, 64, 0.125, 1, None, None,
+                             None, _lib.BF16, 4, None) == _lib.EUNSUPPORTED
 
 
 def test_state_dict_keys_match_reference_layout():

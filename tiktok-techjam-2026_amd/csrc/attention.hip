@@ -381,6 +381,180 @@ __global__ __launch_bounds__(256 * KS) void flash_fwd_kernel(
   }
 }
 
+// ------------------------------------------------ short sequences (plan 4)
+//
+// Every key of a sequence of at most 128 tokens fits one workgroup: a
+// one-wave workgroup takes 32 queries of one (b, h), stages the K rows it
+// needs and their V rows (transposed) into LDS in one round of loads, and
+// computes S^T = K Q^T over all of its keys at once, an exact softmax (one
+// row max, no running rescale) and O^T = V^T P^T.  The grid is
+// B * H * ceil(S / 32) workgroups -- four times plan 1's at S = 128 -- and
+// each workgroup waits for memory once before its math; plan 1 at C2's
+// 1 x 128 x 8 heads spends ~2 us loading and ~2.6 us in two masked
+// key-tile iterations on 8 workgroups.
+template <typename T, int HDP, bool KEYMASK>
+__global__ __launch_bounds__(64) void flash_short_kernel(
+    const T* __restrict__ qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh,
+    T* __restrict__ out, int64_t ld_out, int B, int S, int H, int hd, float scale_log2,
+    int causal, const int32_t* __restrict__ lengths, const uint8_t* __restrict__ key_mask,
+    const int32_t* __restrict__ cu_seqlens, int nqb) {
+  constexpr int MAXK = 128;                // keys per sequence
+  constexpr int NKB = MAXK / 32;           // 32-key blocks
+  constexpr int VEC = 16 / sizeof(T);      // elements per 16-byte chunk
+  constexpr int LDK = HDP + VEC;           // K row pitch (elements)
+  constexpr int LDV = MAXK + VEC;          // V^T row pitch (elements)
+  constexpr int KC = HDP / 16, HB = HDP / 32, CH = HDP / VEC;
+  constexpr int KPL = MAXK * CH / 64;      // K chunks per lane
+  constexpr int VPL = (MAXK / 2) * CH / 64;  // (key pair, chunk) items per lane
+  typedef typename Mfma<T>::frag Frag;
+
+  __shared__ __attribute__((aligned(16))) T sK[MAXK * LDK];
+  __shared__ __attribute__((aligned(16))) T sV[HDP * LDV];
+
+  const int BH = B * H;
+  const int rank = blockIdx.x / BH, bh = blockIdx.x % BH;
+  const int qb = causal ? nqb - 1 - rank : rank;  // causal: most keys first
+  const int b = bh / H, h = bh % H;
+  const int lane = threadIdx.x, l32 = lane & 31, hi = lane >> 5;
+
+  int Sb = S;
+  int64_t row0 = (int64_t)b * S, boff = (int64_t)b * sb;
+  if (cu_seqlens != nullptr) {
+    row0 = cu_seqlens[b];
+    Sb = cu_seqlens[b + 1] - cu_seqlens[b];
+    boff = row0 * ss;
+  }
+  const T* qbase = qkv + boff + (int64_t)h * sh;
+  const T* kbase = qbase + sc;
+  const T* vbase = qbase + 2 * sc;
+  int kv_len = Sb;
+  if (lengths != nullptr) kv_len = min(kv_len, max(lengths[b], 0));
+  const int q0 = qb * 32;
+  if (q0 >= Sb) return;
+  int kend = causal ? min(q0 + 32, Sb) : Sb;
+  kend = min(kend, kv_len);  // keys >= kend are never admissible (and never read)
+  const int nkb = (kend + 31) / 32;
+
+  // Q fragments (B operand of S^T): lane holds Q[q][16c + 8*hi + 0..7]
+  const int q = q0 + l32;
+  Frag qf[KC];
+#pragma unroll
+  for (int c = 0; c < KC; ++c) {
+    const int col = 16 * c + 8 * hi;
+    if (q < Sb && col < hd) {
+      qf[c] = Mfma<T>::load(qbase + (int64_t)q * ss + col);
+    } else {
+      float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      qf[c] = Mfma<T>::pack(z);
+    }
+  }
+  // K rows and V rows (two keys per item) of keys < kend, zeros past it:
+  // every LDS word the math reads is written.
+  uint4 rk[KPL], rv0[VPL], rv1[VPL];
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) {
+    const int it = lane + i * 64, key = it / CH, col = (it % CH) * VEC;
+    rk[i] = (key < kend && col < hd) ? *reinterpret_cast<const uint4*>(kbase + (int64_t)key * ss + col)
+                                     : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int it = lane + i * 64, p = it % (MAXK / 2), col = (it / (MAXK / 2)) * VEC;
+    const bool ok = col < hd;
+    rv0[i] = (ok && 2 * p < kend) ? *reinterpret_cast<const uint4*>(vbase + (int64_t)(2 * p) * ss + col)
+                                  : make_uint4(0, 0, 0, 0);
+    rv1[i] = (ok && 2 * p + 1 < kend) ? *reinterpret_cast<const uint4*>(vbase + (int64_t)(2 * p + 1) * ss + col)
+                                      : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) {
+    const int it = lane + i * 64, key = it / CH, c = it % CH;
+    *reinterpret_cast<uint4*>(&sK[key * LDK + c * VEC]) = rk[i];
+  }
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int it = lane + i * 64, p = it % (MAXK / 2), c = it / (MAXK / 2);
+    PairPack<T>::write(&sV[(c * VEC) * LDV + 2 * p], LDV, rv0[i], rv1[i]);
+  }
+  __syncthreads();
+
+  // S^T = K Q^T per 32-key block: register r of block kb is key
+  // kb*32 + 16*(r/8) + 8*hi + r%8 (K rows read with bits 2 and 3 swapped)
+  const int krow = swap_bits_2_3(l32);
+  f32x16 s[NKB];
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
+    if (kb < nkb) {
+      const T* kp = &sK[(kb * 32 + krow) * LDK + 8 * hi];
+#pragma unroll
+      for (int c = 0; c < KC; ++c) Mfma<T>::mma(s[kb], Mfma<T>::load(kp + 16 * c), qf[c]);
+    }
+  }
+  // masks and the row max (lanes l and l^32 hold the two halves of a query's keys)
+  const int lim = causal ? min(q + 1, kend) : kend;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = kb * 32 + 16 * (r >> 3) + 8 * hi + (r & 7);
+      bool keep = key < lim;
+      if constexpr (KEYMASK) keep = keep && key_mask[(int64_t)b * S + key] != 0;
+      s[kb][r] = keep ? s[kb][r] : -INFINITY;
+      mx = fmaxf(mx, s[kb][r]);
+    }
+  {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+  }
+  const float m_use = mx == -INFINITY ? 0.f : mx * scale_log2;
+  // P = 2^(S scale - max), its fp32 row sum, and O^T = V^T P^T in 16-key steps
+  f32x16 o[HB];
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[hb][r] = 0.f;
+  float ls = 0.f;
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    if (kb < nkb) {
+      float p[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        p[r] = __builtin_amdgcn_exp2f(fmaf(s[kb][r], scale_log2, -m_use));
+        ls += p[r];
+      }
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const Frag pf = Mfma<T>::pack(&p[8 * st]);
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb)
+          Mfma<T>::mma(o[hb], Mfma<T>::load(&sV[(hb * 32 + l32) * LDV + 8 * hi] + 16 * (2 * kb + st)), pf);
+      }
+    }
+  }
+
+  // normalise and store: register r of block hb is hd row hb*32 + 8*(r/4) + 4*hi + r%4
+  const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ls), __float_as_uint(ls), false, false);
+  const float l = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  if (q >= Sb) return;
+  T* orow = out + (row0 + q) * ld_out + (int64_t)h * hd;
+#pragma unroll
+  for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int col = hb * 32 + 8 * g + 4 * hi;
+      if (col < hd) {
+        const float4 v = make_float4(o[hb][4 * g] * inv, o[hb][4 * g + 1] * inv, o[hb][4 * g + 2] * inv,
+                                     o[hb][4 * g + 3] * inv);
+        *reinterpret_cast<typename Quad<T>::raw*>(orow + col) = Quad<T>::from(v);
+      }
+    }
+}
+
 // ------------------------------------------------ software-pipelined variant
 //
 // Same math and output as flash_fwd_kernel (one 32-query block per wave),
@@ -1032,6 +1206,25 @@ static int launch_flash(const void* qkv, int64_t sb, int64_t ss, int64_t sc, int
 }
 
 template <typename T, int HDP>
+static int launch_short(const void* qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh, void* out,
+                        int64_t ld_out, int B, int S, int H, int hd, float scale_log2, int causal,
+                        const int32_t* lengths, const uint8_t* key_mask, const int32_t* cu_seqlens,
+                        hipStream_t st) {
+  const int nqb = (S + 31) / 32;
+  const int64_t nblk = (int64_t)nqb * B * H;
+  if (nblk > INT32_MAX) return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd: grid too large");
+  if (key_mask != nullptr)
+    hipLaunchKernelGGL((flash_short_kernel<T, HDP, true>), dim3((unsigned)nblk), dim3(64), 0, st, (const T*)qkv,
+                       sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, lengths, key_mask,
+                       cu_seqlens, nqb);
+  else
+    hipLaunchKernelGGL((flash_short_kernel<T, HDP, false>), dim3((unsigned)nblk), dim3(64), 0, st, (const T*)qkv,
+                       sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, lengths, key_mask,
+                       cu_seqlens, nqb);
+  return check_launch("tjk_flash_fwd");
+}
+
+template <typename T, int HDP>
 static int flash_plan(int plan, const void* qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh, void* out,
                       int64_t ld_out, int B, int S, int H, int hd, float scale_log2, int causal,
                       const int32_t* lengths, const uint8_t* key_mask, const int32_t* cu_seqlens,
@@ -1040,6 +1233,13 @@ static int flash_plan(int plan, const void* qkv, int64_t sb, int64_t ss, int64_t
     if (plan == 0)
       return launch_pipe<T, HDP>(qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
                                  key_mask, cu_seqlens, st);
+  }
+  // plan 4: sequences of at most 128 tokens (checked by the entry point);
+  // fp32 at hd 128 would not fit its K / V^T tiles and runs plan 1
+  if constexpr (sizeof(T) == 2 || HDP <= 64) {
+    if (plan == 4)
+      return launch_short<T, HDP>(qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
+                                  key_mask, cu_seqlens, st);
   }
   if (plan == 2)
     return launch_flash<T, HDP, 2, 1>(qkv, sb, ss, sc, sh, out, ld_out, B, S, H, hd, scale_log2, causal, lengths,
@@ -1075,7 +1275,7 @@ using namespace tjk;
 extern "C" int tjk_flash_plan_count(int dtype) {
   if (dtype != TJK_F32 && dtype != TJK_F16 && dtype != TJK_BF16)
     return fail(TJK_EINVAL, "tjk_flash_plan_count: bad dtype %d", dtype);
-  return 4;
+  return 5;
 }
 
 extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s,
@@ -1091,7 +1291,9 @@ extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s
   if (dtype != TJK_F32 && dtype != TJK_F16 && dtype != TJK_BF16) return fail(TJK_EINVAL, "tjk_flash_fwd: bad dtype %d", dtype);
   if (head_dim > 128 || head_dim % 8)
     return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd: head_dim=%d must be a multiple of 8 and <= 128", head_dim);
-  if (plan_id < -1 || plan_id > 3) return fail(TJK_EINVAL, "tjk_flash_fwd: plan %d out of range", plan_id);
+  if (plan_id < -1 || plan_id > 4) return fail(TJK_EINVAL, "tjk_flash_fwd: plan %d out of range", plan_id);
+  if (plan_id == 4 && seq > 128)
+    return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd: plan 4 takes sequences of at most 128 tokens, got %d", seq);
   if (cu_seqlens && key_mask)
     return fail(TJK_EINVAL, "tjk_flash_fwd: cu_seqlens (packed sequences) and key_mask are exclusive");
   const int vec = 16 / dtype_size(dtype);
@@ -1114,10 +1316,16 @@ extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s
   // (unpipelined) loop: plan 1 from S = 2048 (padded C4 with a per-key
   // mask: 129 vs 168 us).  A sequence of one 128-query block has only
   // diagonal tiles and nothing to pipeline: plan 1 there too (C2's
-  // 1 x 128 x 8 heads fp16: 6.2 vs 6.8 us).
+  // 1 x 128 x 8 heads fp16: 6.2 vs 6.8 us).  Plan 4 (whole sequence in one
+  // one-wave workgroup per 32 queries) takes every sequence of at most 128
+  // tokens.
   const bool pipe_ok = dtype != TJK_F32 && ((int64_t)seq * stride_s + head_dim) * dtype_size(dtype) < INT32_MAX;
-  if (plan_id == -1)
-    plan_id = (pipe_ok && seq > 128 && (key_mask != nullptr ? seq < 2048 : (head_dim <= 64 || seq >= 4096))) ? 0 : 1;
+  if (plan_id == -1) {
+    if (seq <= 128)
+      plan_id = 4;
+    else
+      plan_id = (pipe_ok && (key_mask != nullptr ? seq < 2048 : (head_dim <= 64 || seq >= 4096))) ? 0 : 1;
+  }
   if (plan_id == 0 && !pipe_ok) plan_id = 1;
   const float scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);

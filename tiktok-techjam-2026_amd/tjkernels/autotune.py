@@ -175,7 +175,8 @@ def tune_workload(w: Workload, trials: int = 2, margin: float = 0.85, iters: int
     # prefix-masked tokens M follows the input lengths.
 
     # coordinate descent over the plan-level knobs
-    knobs = [("attn_plan", [0, 1, 3]), ("residual_epilogue", [True, False]), ("cuda_graph", [True, False])]
+    attn_plans = [0, 1, 3] + ([4] if w.seq <= 128 else [])
+    knobs = [("attn_plan", attn_plans), ("residual_epilogue", [True, False]), ("cuda_graph", [True, False])]
     if fused_ffn_ok(w.d_model, w.ffn_dim, cur["plan"].compute_dtype):
         knobs.insert(0, ("ffn", ["gemm", "fused"]))
     for knob, values in knobs:

@@ -47,7 +47,7 @@ import torch
 
 from . import ops, schedule as sched_mod, tiles
 from .graphs import GraphCache
-from .plans import Plan, fused_ffn_ok, select_plan
+from .plans import ATTN_SCHEDULED, Plan, fused_ffn_ok, select_plan
 
 try:
     from torch.utils.weak import WeakTensorKeyDictionary
@@ -364,12 +364,15 @@ class Engine:
             fw.pending = fw.view("parts")
         elif not plan.residual_epilogue:
             fw.pending = fw.view("delta")
-        # Packed 2-byte attention below 2048 keys follows a longest-first work
-        # list (attn_plan -1 or 4); longer sequences run the plain plan-0/1
-        # kernel, measured faster there; other plan ids force the plain kernel.
+        # Packed 2-byte attention of 129 to 2047 keys follows a longest-first
+        # work list (attn_plan -1, or ATTN_SCHEDULED to force it); longer
+        # sequences run the plain plan-0/1 kernel, measured faster there, and
+        # sequences of at most 128 keys the short-sequence plan 4; other plan
+        # ids force the plain kernel.
         pk = fw.packing
         fw.use_sched = (pk is not None and cdt != torch.float32 and rows > 0
-                        and (plan.attn_plan == 4 or (plan.attn_plan == -1 and max(pk.lengths) < 2048)))
+                        and (plan.attn_plan == ATTN_SCHEDULED
+                             or (plan.attn_plan == -1 and 128 < max(pk.lengths) < 2048)))
         if fw.use_sched and pk.attn is None:
             pk.attn = sched_mod.build_schedule(pk.lengths, shp.heads, shp.head_dim, shp.causal, cdt, self.device)
         return fw

@@ -25,7 +25,8 @@ to select, and the product path has no non-HIP fallback):
   the fp32 residual in the GEMM epilogue instead of deferring them to the
   next LayerNorm (the reference's scheme, engine.py:232-264);
 * ``gemm_*`` / ``attn_plan``: force a tile or attention plan (-1: chosen
-  at run time);
+  at run time; attention 0-4 are the library's plans of tjk_flash_fwd,
+  ``ATTN_SCHEDULED`` (5) the work-list kernel for packed sequences);
 * ``pack_prefix``: run only the valid tokens of prefix masks.
 
 Environment: ``TJ_NO_GRAPH``, ``TJ_COMPUTE_DTYPE``, ``TJ_DEFERRED_RESIDUAL``,
@@ -47,6 +48,9 @@ import torch
 DTYPE_BY_NAME = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}
 NAME_BY_DTYPE = {dt: name for name, dt in DTYPE_BY_NAME.items()}
 FFN_KINDS = ("gemm", "fused")
+# attn_plan id beyond the library's tjk_flash_fwd plans (0-4): the scheduled
+# work-list kernel for packed sequences (tjk_flash_fwd_sched)
+ATTN_SCHEDULED = 5
 
 # The single-launch FFN is the default up to this many (tokens x ffn_dim)
 # elements of intermediate, where the two-launch path is launch-bound.
