@@ -344,3 +344,45 @@ def test_mask_updated_in_place_between_forwards(device, graph):
                 assert torch.equal(got.cpu(), ref.cpu())
     finally:
         plans_mod.set_override(None)
+
+
+_TWO_PROCESS_SCRIPT = r"""
+import hashlib, json, sys
+import torch
+from tjkernels import UserOptimizedTransformer, tiles
+from tjkernels.workloads import WORKLOADS, make_inputs, make_state_dict
+w = WORKLOADS["C4"]
+m = UserOptimizedTransformer(w.config)
+m.load_state_dict(make_state_dict(w, seed=0), strict=True)
+m = m.to(device="cuda", dtype=w.dtype).eval()
+x, mask, _ = make_inputs(w, seed=1)
+with torch.inference_mode():
+    out = m(x.to(w.dtype).cuda(), mask.cuda())
+torch.cuda.synchronize()
+raw = out.contiguous().view(torch.int16).cpu().numpy().tobytes()
+print(json.dumps({"sha": hashlib.sha256(raw).hexdigest(),
+                  "tiles": sorted(str(k) + ":" + str(v) for k, v in tiles.chosen().items())}))
+"""
+
+
+def test_two_processes_bitwise_identical(device, tmp_path):
+    """Two fresh processes run the packed C4 forward, one choosing GEMM tiles
+    by timing and one with the library's own tile rule (TJ_GEMM_TUNE=0):
+    whatever tiles they run, every tile of a shape's K-summation class adds
+    K in the same order, so the outputs are bitwise identical."""
+    import json
+    import os
+    import subprocess
+    import sys
+    script = tmp_path / "c4_forward.py"
+    script.write_text(_TWO_PROCESS_SCRIPT)
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    pkg = os.path.join(root, "tiktok-techjam-2026_amd")
+    res = []
+    for extra in ({}, {"TJ_GEMM_TUNE": "0"}):
+        env = dict(os.environ, PYTHONPATH=os.pathsep.join([pkg, root, os.environ.get("PYTHONPATH", "")]), **extra)
+        r = subprocess.run([sys.executable, str(script)], env=env, capture_output=True, text=True, timeout=300)
+        assert r.returncode == 0, r.stderr[-3000:]
+        res.append(json.loads(r.stdout.strip().splitlines()[-1]))
+    assert res[0]["tiles"] != res[1]["tiles"], "the two runs should have used different tile choices"
+    assert res[0]["sha"] == res[1]["sha"], "outputs differ between processes"
