@@ -80,8 +80,10 @@ def _measure(m: int, n: int, k: int, dtype: torch.dtype, epilogue: int) -> int:
     bias = torch.zeros(n, device=dev, dtype=dtype)
     out = torch.empty(m, n, device=dev,
                       dtype=torch.float32 if epilogue == ops.EPI_BIAS_RESIDUAL else dtype)
-    # about 0.4 ms of GPU work per measurement (estimated at 500 TFLOP/s)
-    reps = max(3, min(24, int(0.4e-3 / (2.0 * m * n * k / 500e12))))
+    # about 1.5 ms of GPU work per measurement (estimated at 500 TFLOP/s):
+    # with 0.4 ms and three rounds the packed C4 FFN1 / FFN2 picks moved
+    # between tiles 2-5% apart from one process to the next
+    reps = max(3, min(64, int(1.5e-3 / (2.0 * m * n * k / 500e12))))
     cands = []
     for cand in candidates(m, n, k, dtype):
         try:
@@ -91,11 +93,11 @@ def _measure(m: int, n: int, k: int, dtype: torch.dtype, epilogue: int) -> int:
         cands.append(cand)
     if not cands:
         return -1
-    # Three interleaved rounds, best time per candidate: the clock drifts
+    # Five interleaved rounds, best time per candidate: the clock drifts
     # (power / thermal) while this runs, and a single pass in order would
     # hand the early candidates the cooler chip.
     times = {c: float("inf") for c in cands}
-    for rnd in range(3):
+    for rnd in range(5):
         for cand in (cands if rnd % 2 == 0 else cands[::-1]):
             times[cand] = min(times[cand], _time_plan(a, w, bias, out, epilogue, cand, reps))
     best, best_ms = cands[0], times[cands[0]]
