@@ -155,6 +155,11 @@ def test_override_and_env_knobs(monkeypatch):
     assert tiny.ffn == "fused" and tiny.compute_dtype == torch.float32  # C1
     big = plans_mod.select_plan(64, 4096, 1024, 16, 4096, 4, True, torch.bfloat16, dev)
     assert not big.cuda_graph  # x above 64 MiB: no whole-forward graph
+    # fp32 compute at C2's d = 512 has no single-launch FFN kernel: two launches
+    monkeypatch.setenv("TJ_COMPUTE_DTYPE", "float32")
+    p32 = plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev)
+    assert p32.compute_dtype == torch.float32 and p32.ffn == "gemm"
+    monkeypatch.delenv("TJ_COMPUTE_DTYPE")
     monkeypatch.setenv("TJ_NO_GRAPH", "1")
     monkeypatch.setenv("TJ_DEFERRED_RESIDUAL", "1")
     p = plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev)

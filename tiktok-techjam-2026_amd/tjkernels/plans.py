@@ -196,7 +196,7 @@ def set_override(plan: Optional[Plan]) -> None:
     _forced = plan
 
 
-def _env_adjusted(plan: Plan) -> Plan:
+def _env_adjusted(plan: Plan, d_model: int, ffn_dim: int) -> Plan:
     env = os.environ
     changes: Dict[str, object] = {}
     if env.get("TJ_NO_GRAPH") == "1":
@@ -215,7 +215,13 @@ def _env_adjusted(plan: Plan) -> Plan:
     attn = env.get("TJ_ATTN_PLAN", "")
     if attn.lstrip("-").isdigit():
         changes["attn_plan"] = int(attn)
-    return replace(plan, **changes) if changes else plan
+    out = replace(plan, **changes) if changes else plan
+    # a compute dtype the single-launch FFN has no kernel for (fp32 at
+    # d = 512) falls back to the two-launch FFN unless TJ_FFN forces it
+    if (out.ffn == "fused" and "ffn" not in changes
+            and not fused_ffn_ok(d_model, ffn_dim, out.compute_dtype, out.ffn_splits)):
+        out = replace(out, ffn="gemm")
+    return out
 
 
 def select_plan(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int,
@@ -226,7 +232,8 @@ def select_plan(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int,
     tuned = TUNED.get(key)
     if tuned is not None:
         return tuned
-    return _env_adjusted(default_plan(batch, seq, d_model, heads, ffn_dim, layers, causal, dtype, device))
+    return _env_adjusted(default_plan(batch, seq, d_model, heads, ffn_dim, layers, causal, dtype, device),
+                         d_model, ffn_dim)
 
 
 def save_plans(plans: Dict[str, Plan], path: Optional[Path] = None) -> None:
