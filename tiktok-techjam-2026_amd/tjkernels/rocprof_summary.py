@@ -37,7 +37,9 @@ import collections
 import csv
 from typing import Dict, List, Optional, Tuple
 
-GEMM, FLASH, LN, FFN = "gemm_dtl_kernel", "flash_", "add_layernorm_kernel", "ffn_fused_kernel"
+# add_layernorm_kernel and add_layernorm_parts_kernel (the split-delta sum
+# after the single-launch FFN) both count as LayerNorm launches
+GEMM, FLASH, LN, FFN = "gemm_dtl_kernel", "flash_", "add_layernorm", "ffn_fused_kernel"
 COPY = "__amd_rocclr_copyBuffer"
 
 
