@@ -188,11 +188,14 @@ def test_general_mask_and_lengths_input(device):
     _check(got_l, oracle.forward(sd, x2, pmask, 4, True, torch.float32), pmask, torch.float32)
 
 
-@pytest.mark.parametrize("dtype,ffn", [(torch.float32, "gemm"), (torch.bfloat16, "gemm"),
-                                       (torch.bfloat16, "fused"), (torch.float32, "fused")])
-def test_graph_equals_eager(device, dtype, ffn):
+@pytest.mark.parametrize("dtype,ffn,whole", [(torch.float32, "gemm", False), (torch.bfloat16, "gemm", False),
+                                             (torch.bfloat16, "fused", False), (torch.float32, "fused", False),
+                                             (torch.bfloat16, "fused", True), (torch.float32, "gemm", True)])
+def test_graph_equals_eager(device, dtype, ffn, whole):
     """hipGraph replay == eager, bitwise, on fresh inputs, with eager work and
-    synchronisations between replays (bench/test_correctness.py:94-125)."""
+    synchronisations between replays (bench/test_correctness.py:94-125);
+    ``whole``: the whole forward captured (static input copied in, output
+    cloned), so every output must also be a fresh tensor."""
     cfg = TransformerConfig(4, 64, 128, 4, 256, 2, True)
     torch.manual_seed(1)
     eager = _module(cfg, UserOptimizedTransformer(cfg).state_dict(), dtype, device)
@@ -213,15 +216,20 @@ def test_graph_equals_eager(device, dtype, ffn):
             expected = [eager(x.to(device), m.to(device)).cpu() for x, m in cases]
     finally:
         plans_mod.set_override(None)
-    plans_mod.set_override(Plan(compute_dtype=dtype, cuda_graph=True, ffn=ffn, label="graphed"))
+    plans_mod.set_override(Plan(compute_dtype=dtype, cuda_graph=True, whole_graph=whole, ffn=ffn, label="graphed"))
     try:
         with torch.inference_mode():
             for rep in range(2):
+                outs = []
                 for (x, m), want in zip(cases, expected):
                     got = graphed(x.to(device), m.to(device))
                     torch.cuda.synchronize()
                     assert torch.equal(got.cpu(), want)
                     _ = (got * 2).sum().item()  # eager work between replays
+                    outs.append(got)
+                # earlier outputs are not overwritten by later replays
+                for got, want in zip(outs, expected):
+                    assert torch.equal(got.cpu(), want)
         assert len(graphed._tj_engine._graphs) >= 1
     finally:
         plans_mod.set_override(None)

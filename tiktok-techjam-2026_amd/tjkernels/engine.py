@@ -276,6 +276,8 @@ class Engine:
         self._packings: "OrderedDict[Tuple[int, Tuple[int, ...]], Packing]" = OrderedDict()
         self._static_masks: Dict[Tuple[int, int], torch.Tensor] = {}
         self._forwards: "OrderedDict[Tuple, Forward]" = OrderedDict()
+        # static input / output of whole-forward graphs, per graph key
+        self._graph_io: "OrderedDict[Tuple, Tuple[torch.Tensor, torch.Tensor]]" = OrderedDict()
         self.check_waits = os.environ.get("TJ_CHECK_WAITS") == "1"
 
     # compatibility names used by tools and tests
@@ -533,9 +535,11 @@ class Engine:
         (writing a fresh output) run on the stream around one replayed
         hipGraph of the layer body, on fixed workspace buffers; only a
         GENERAL mask, which the recorded attention reads, is copied into a
-        static buffer.  A packed forward's launches are sized by its lengths,
-        so the lengths are part of the key, and the graph keeps the row maps
-        and schedule it reads alive."""
+        static buffer.  With ``plan.whole_graph`` both LayerNorms are in the
+        graph too: x is copied into a static input and the static output is
+        cloned, one graph launch per forward.  A packed forward's launches
+        are sized by its lengths, so the lengths are part of the key, and the
+        graph keeps the row maps and schedule it reads alive."""
         batch, seq, d = x.shape
         static_mask = None
         if mode == MASK_GENERAL:
@@ -551,6 +555,31 @@ class Engine:
             self._forwards[key] = fw
             if len(self._forwards) > 4 * self._graphs.max_entries:
                 self._forwards.popitem(last=False)
+        row_mask = static_mask.reshape(-1) if mode == MASK_GENERAL else None
+        if self.plan.whole_graph:
+            # the buffers a graph was captured on live and die with it: a key
+            # the graph cache no longer holds gets new buffers and a new capture
+            io = self._graph_io.get(key)
+            if io is None or key not in self._graphs:
+                io = (torch.empty_like(x), torch.empty((batch, seq, d), dtype=self.dtype, device=x.device))
+                self._graph_io[key] = io
+                while len(self._graph_io) > self._graphs.max_entries:
+                    self._graph_io.popitem(last=False)
+            x_in, y_out = io
+
+            def whole() -> None:
+                self._first(fw, x_in)
+                self._body(fw)
+                self._final(fw, y_out, row_mask)
+
+            x_in.copy_(x)
+            graph = self._graphs.get(key, whole, keepalive=(packing, fw, io))
+            if graph is not None:
+                graph.replay()
+            else:
+                whole()
+            self._check(fw)
+            return y_out.clone()
         graph = self._graphs.get(key, lambda: self._body(fw), keepalive=(packing, fw))
         self._first(fw, x)
         if graph is not None:
@@ -558,7 +587,7 @@ class Engine:
         else:
             self._body(fw)
         out = torch.empty((batch, seq, d), dtype=self.dtype, device=x.device)
-        self._final(fw, out, mask.reshape(-1) if mode == MASK_GENERAL else None)
+        self._final(fw, out, row_mask)
         self._check(fw)
         return out
 

@@ -83,6 +83,9 @@ class GraphCache:
             self._entries.popitem(last=False)
         return entry
 
+    def __contains__(self, key: Hashable) -> bool:
+        return key in self._entries
+
     def clear(self) -> None:
         self._entries.clear()
 

@@ -21,6 +21,11 @@ to select, and the product path has no non-HIP fallback):
   the intermediate in LDS and LayerNorm 2 inside, split over ``ffn_splits``
   f-slices whose partials the next LayerNorm sums; 0 = f / 128);
 * ``cuda_graph``: replay the layer body as one hipGraph;
+* ``whole_graph`` (with ``cuda_graph``): capture the first and final
+  LayerNorm too, reading x from a static input buffer and writing a static
+  output that is cloned -- the reference's copy-in / clone-out
+  (graphs.py:57-64): one graph launch and two copies per forward instead of
+  two eager LayerNorm launches around the replayed body;
 * ``residual_epilogue``: add the out-proj (and two-launch FFN) outputs into
   the fp32 residual in the GEMM epilogue instead of deferring them to the
   next LayerNorm (the reference's scheme, engine.py:232-264);
@@ -29,7 +34,7 @@ to select, and the product path has no non-HIP fallback):
   ``ATTN_SCHEDULED`` (5) the work-list kernel for packed sequences);
 * ``pack_prefix``: run only the valid tokens of prefix masks.
 
-Environment: ``TJ_NO_GRAPH``, ``TJ_COMPUTE_DTYPE``, ``TJ_DEFERRED_RESIDUAL``,
+Environment: ``TJ_NO_GRAPH``, ``TJ_WHOLE_GRAPH`` (0 / 1), ``TJ_COMPUTE_DTYPE``, ``TJ_DEFERRED_RESIDUAL``,
 ``TJ_NO_PACK``, ``TJ_ATTN_PLAN``, ``TJ_FFN`` (gemm | fused), ``TJ_FFN_SPLITS``;
 ``TJ_GEMM_TUNE=0`` (tjkernels.tiles) skips the measured tile choice.
 Tuned keys carry the GPU architecture (``...@gfx950``).
@@ -69,6 +74,7 @@ class Plan:
     ffn_splits: int = 0
     packed_qkv: bool = True
     cuda_graph: bool = True
+    whole_graph: bool = False
     residual_epilogue: bool = True
     gemm_qkv: int = -1
     gemm_out: int = -1
@@ -201,6 +207,8 @@ def _env_adjusted(plan: Plan, d_model: int, ffn_dim: int) -> Plan:
     changes: Dict[str, object] = {}
     if env.get("TJ_NO_GRAPH") == "1":
         changes["cuda_graph"] = False
+    if env.get("TJ_WHOLE_GRAPH") in ("0", "1"):
+        changes["whole_graph"] = env["TJ_WHOLE_GRAPH"] == "1"
     if env.get("TJ_COMPUTE_DTYPE") in DTYPE_BY_NAME:
         changes["compute_dtype"] = DTYPE_BY_NAME[env["TJ_COMPUTE_DTYPE"]]
     if env.get("TJ_DEFERRED_RESIDUAL") == "1":
