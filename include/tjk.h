@@ -28,6 +28,10 @@
  *                         shape gate ffn.py:103-110 -> tjk_ffn_supported)
  *   tjk_flash_fwd_sched <- the grid of (query block, b*h) programs of
  *                         tjkernels/kernels/attention.py:199-217
+ *   tjk_attn_block     <- the QKV addmm, flash_attention and out-proj addmm
+ *                         (tjkernels/engine.py:245-247) fused for sequences
+ *                         of at most 128 tokens, the tiny-shape fusion of
+ *                         README.md:193-196
  */
 #ifndef TJK_H
 #define TJK_H
@@ -39,7 +43,7 @@
 extern "C" {
 #endif
 
-#define TJK_ABI_VERSION 4
+#define TJK_ABI_VERSION 5
 
 /* dtypes */
 #define TJK_F32 0
@@ -223,6 +227,32 @@ int tjk_ffn(const void* a, int a_dtype, int64_t lda, const float* ln_gamma, cons
             int64_t f, int dtype, void* stream);
 /* 1 if tjk_ffn takes (d, f, splits, dtype), else 0. */
 int tjk_ffn_supported(int64_t d, int64_t f, int splits, int dtype);
+
+/*
+ * Attention block of one layer in one launch, for sequences of at most 128
+ * tokens: per head h (head_dim 64),
+ *   [Q | K | V] = x W_qkv[h rows]^T + b_qkv[h]     rounded to `dtype`
+ *   ctx_h       = softmax(Q K^T * scale (+ causal mask)) V   rounded to `dtype`
+ *   P[h]        = ctx_h W_out[:, 64h : 64h+64]^T (+ b_out for h = 0)   fp32
+ * x [rows, d] (leading dimension ld_x), W_qkv [3d, d] and W_out [d, d]
+ * contiguous in nn.Linear layout, b_qkv [3d] / b_out [d] (may be NULL).
+ * P[h] is stored as fp32 rows of `parts` (leading dimension ld_parts) at
+ * parts + h * part_stride; tjk_add_layernorm(delta_splits = heads) then adds
+ * their sum -- the out-projection output -- to the residual.  ctx_out (may
+ * be NULL; leading dimension ld_ctx) also receives the context [rows, d].
+ * Sequences: `batch` of `seq` tokens each (rows b*seq ..), or with
+ * cu_seqlens (int32 [batch+1]) packed back to back, every length <= seq.
+ * The same Q / K / V give the same context bits as tjk_flash_fwd plan 4.
+ * Supported: see tjk_attn_block_supported (bf16 / fp16, head_dim 64,
+ * d_model = 64 heads in {128, 256, 384, 512}, seq <= 128).
+ */
+int tjk_attn_block(const void* x, int64_t ld_x, const void* w_qkv, const void* b_qkv,
+                   const void* w_out, const void* b_out, float* parts, int64_t ld_parts,
+                   int64_t part_stride, void* ctx_out, int64_t ld_ctx, const int32_t* cu_seqlens,
+                   int batch, int seq, int heads, int head_dim, float scale, int causal, int dtype,
+                   void* stream);
+/* 1 if tjk_attn_block takes the shape, else 0. */
+int tjk_attn_block_supported(int64_t d_model, int heads, int head_dim, int64_t max_seqlen, int dtype);
 
 #ifdef __cplusplus
 }

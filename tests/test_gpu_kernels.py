@@ -764,3 +764,114 @@ def test_add_layernorm_split_delta(device, n, splits):
             assert (out2[r] == 0).all()
         else:
             _close(out2[r:r + 1], ref[src:src + 1], 2e-5, 1e-5)
+
+
+# ------------------------------------------------------------ attention block
+
+def _block_case(g, lengths, d, dt):
+    rows = sum(lengths)
+    x = torch.randn(rows, d, generator=g).to(dt)
+    wqkv = (torch.randn(3 * d, d, generator=g) / math.sqrt(d)).to(dt)
+    bqkv = (torch.randn(3 * d, generator=g) * 0.1).to(dt)
+    wout = (torch.randn(d, d, generator=g) / math.sqrt(d)).to(dt)
+    bout = (torch.randn(d, generator=g) * 0.1).to(dt)
+    return x, wqkv, bqkv, wout, bout
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("d,lengths,causal,packed", [
+    (512, [128], True, False),              # C2's shape
+    (256, [100, 100], True, False),         # uniform batch, partial last query block
+    (384, [1, 37, 128, 64, 0, 96], True, True),  # packed ragged lengths, one empty
+    (128, [77, 128, 5], False, True),       # non-causal packed
+    (512, [96, 96, 96], False, False),
+    (256, [1], True, False),
+])
+def test_attn_block_against_unfused_and_fp64(device, dt, d, lengths, causal, packed):
+    """tjk_attn_block == the unfused launches: its context equals the QKV
+    GEMM (plan 9, which sums K in the same order) followed by attention plan
+    4, bit for bit; the per-head partials sum to ctx W_out^T + b_out (fp64 of
+    the kernel's own context, fp32 accumulation tolerance); the context
+    matches fp64 attention of that Q/K/V; rows past the input are never
+    written."""
+    heads = d // 64
+    g = _gen(d + 7 * len(lengths) + int(causal))
+    x, wqkv, bqkv, wout, bout = _block_case(g, lengths, d, dt)
+    rows = x.shape[0]
+    xd, wqkv_d, bqkv_d, wout_d, bout_d = (t.to(device) for t in (x, wqkv, bqkv, wout, bout))
+    parts = torch.full((heads, rows + 3, d), float("nan"), device=device)
+    ctx = torch.full((rows + 3, d), float("nan"), dtype=dt, device=device)
+    cu = torch.tensor([0] + list(torch.tensor(lengths).cumsum(0)), dtype=torch.int32)
+    kw = dict(cu_seqlens=cu.to(device), max_seqlen=max(lengths)) if packed else \
+        dict(batch=len(lengths), seq=lengths[0])
+    ops.attn_block(xd, wqkv_d, bqkv_d, wout_d, bout_d, parts[:, :rows], heads, causal=causal,
+                   ctx_out=ctx[:rows], **kw)
+    # the unfused launches on the same inputs
+    qkv = torch.empty(rows, 3 * d, dtype=dt, device=device)
+    ops.gemm(xd, wqkv_d, bqkv_d, qkv, ops.EPI_BIAS, plan=9)
+    ref_ctx = torch.empty(rows, d, dtype=dt, device=device)
+    if packed:
+        ops.flash_attention(qkv.view(rows, 3, heads, 64), ref_ctx, causal=causal, plan=4,
+                            cu_seqlens=cu.to(device), max_seqlen=max(lengths))
+    else:
+        ops.flash_attention(qkv.view(len(lengths), lengths[0], 3, heads, 64), ref_ctx, causal=causal, plan=4)
+    torch.cuda.synchronize()
+    got_ctx = ctx[:rows].cpu()
+    assert torch.isnan(ctx[rows:].float()).all() and torch.isnan(parts[:, rows:]).all(), \
+        "rows past the input were written"
+    assert torch.equal(got_ctx, ref_ctx.cpu()), "context differs from QKV GEMM + attention plan 4"
+    # out-projection partials: their sum is ctx W_out^T + b_out
+    want = got_ctx.double() @ wout.double().t() + bout.double()
+    _close(parts[:, :rows].double().sum(0), want, 1e-5, 1e-5)
+    # the context against fp64 attention of the GEMM's Q / K / V
+    qkv_c = qkv.cpu()
+    start = 0
+    for n in lengths:
+        if n:
+            seq_qkv = qkv_c[start:start + n].view(1, n, 3, heads, 64)
+            _close(got_ctx[start:start + n], _attn_ref(seq_qkv, causal), 1e-2, 1e-2)
+        start += n
+
+
+def test_attn_block_closed_forms(device):
+    """W_qkv = 0: Q = bq, K = bk, V = bv for every row, so every query's
+    context is bv (softmax weights sum to 1), and the partials sum to
+    bv_heads W_out^T + b_out on every row; W_out = 0: only head 0 carries
+    b_out."""
+    d, heads, n, dt = 256, 4, 70, torch.bfloat16
+    g = _gen(11)
+    x = torch.randn(n, d, generator=g).to(dt)
+    bqkv = torch.randn(3 * d, generator=g).to(dt)
+    wout = (torch.randn(d, d, generator=g) / 16).to(dt)
+    bout = torch.randn(d, generator=g).to(dt)
+    parts = torch.empty(heads, n, d, device=device)
+    ctx = torch.empty(n, d, dtype=dt, device=device)
+    ops.attn_block(x.to(device), torch.zeros(3 * d, d, dtype=dt, device=device), bqkv.to(device),
+                   wout.to(device), bout.to(device), parts, heads, causal=True, batch=1, seq=n, ctx_out=ctx)
+    torch.cuda.synchronize()
+    bv = bqkv[2 * d:].float()
+    _close(ctx, bv.double().expand(n, d), 8e-3, 1e-3)
+    want = (bv.to(dt).double() @ wout.double().t() + bout.double()).expand(n, d)
+    _close(parts.sum(0), want, 1e-2, 1e-2)
+    ops.attn_block(x.to(device), torch.randn(3 * d, d, dtype=dt, device=device) / 16, bqkv.to(device),
+                   torch.zeros(d, d, dtype=dt, device=device), bout.to(device), parts, heads, causal=True,
+                   batch=1, seq=n)
+    torch.cuda.synchronize()
+    assert torch.equal(parts[0].cpu(), bout.float().expand(n, d))
+    assert (parts[1:] == 0).all()
+
+
+def test_attn_block_rejects_unsupported_shapes(device):
+    d = 512
+    x = torch.zeros(200, d, dtype=torch.bfloat16, device=device)
+    w = torch.zeros(3 * d, d, dtype=torch.bfloat16, device=device)
+    wo = torch.zeros(d, d, dtype=torch.bfloat16, device=device)
+    parts = torch.zeros(8, 200, d, device=device)
+    with pytest.raises(ops.TjkError, match="unsupported|at most 128"):
+        ops.attn_block(x, w, None, wo, None, parts, 8, batch=1, seq=200)   # sequence longer than 128
+    with pytest.raises(ops.TjkError, match="unsupported|head_dim"):
+        ops.attn_block(x[:, :d], w, None, wo, None, torch.zeros(16, 200, d, device=device), 16,
+                       batch=2, seq=100)   # head_dim 32
+    assert not ops.attn_block_supported(1024, 16, 64, 128, torch.bfloat16)
+    assert not ops.attn_block_supported(512, 8, 64, 128, torch.float32)
+    assert ops.attn_block_supported(512, 8, 64, 128, torch.float16)

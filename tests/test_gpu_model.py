@@ -235,6 +235,97 @@ def test_graph_equals_eager(device, dtype, ffn, whole):
         plans_mod.set_override(None)
 
 
+BLOCK_CASES = [
+    dict(id="c2-graph", workload="C2"),
+    dict(id="ragged-causal", cfg=(6, 128, 256, 4, 512, 2, True), dtype=torch.bfloat16, padding=0.7),
+    dict(id="ragged-noncausal-graph", cfg=(5, 100, 384, 6, 768, 2, False), dtype=torch.float16, padding=0.5,
+         graph=True, ffn="gemm"),
+    dict(id="deferred-two-launch-ffn", cfg=(3, 64, 512, 8, 1024, 2, True), dtype=torch.bfloat16, padding=0.0,
+         residual_epilogue=False, ffn="gemm"),
+]
+
+
+@pytest.mark.parametrize("case", BLOCK_CASES, ids=[c["id"] for c in BLOCK_CASES])
+def test_attention_block_plan(device, case, monkeypatch):
+    """Plan.attn_block: the QKV GEMM, attention and out-projection of each
+    layer in one launch, the per-head partials summed into the residual by
+    LayerNorm 2, holds the budget against the oracle -- at C2, on packed
+    ragged sequences (causal and not, eager and graphed), and with the
+    deferred residual and the two-launch FFN.  A non-prefix mask, which the
+    block kernel does not take, runs the three launches on the same plan."""
+    from tjkernels import ops as ops_mod
+    calls = []
+    real = ops_mod.attn_block
+    monkeypatch.setattr(ops_mod, "attn_block", lambda *a, **k: calls.append(1) or real(*a, **k))
+    if "workload" in case:
+        w = WORKLOADS[case["workload"]]
+        _run_workload(device, case["workload"], seeds=(1, 2),
+                      plan=Plan(compute_dtype=w.dtype, ffn="fused", cuda_graph=True, attn_block=True,
+                                label="block"))
+        assert calls, "the attention block was not used"
+        return
+    cfg = TransformerConfig(*case["cfg"])
+    dtype = case["dtype"]
+    torch.manual_seed(3)
+    sd = {k: v.to(dtype).float() for k, v in UserOptimizedTransformer(cfg).state_dict().items()}
+    model = _module(cfg, sd, dtype, device)
+    plan = Plan(compute_dtype=dtype, attn_block=True, cuda_graph=case.get("graph", False),
+                residual_epilogue=case.get("residual_epilogue", True), ffn=case.get("ffn", "fused"),
+                label="block")
+    plans_mod.set_override(plan)
+    try:
+        for seed in (1, 2):
+            x, mask = _inputs(cfg, dtype, seed=seed, padding=case["padding"])
+            with torch.inference_mode():
+                got = model(x.to(device), mask.to(device)).cpu()
+            ref = oracle.forward(sd, x.float(), mask, cfg.num_heads, cfg.causal, torch.float32)
+            _check(got, ref, mask, dtype)
+        assert calls, "the attention block was not used"
+        n_block = len(calls)
+        # a non-prefix mask: per-key masked attention, three launches per layer
+        g = torch.Generator()
+        g.manual_seed(5)
+        m = torch.rand(cfg.batch_size, cfg.seq_len, generator=g) > 0.4
+        m[:, 0] = True
+        x = torch.randn(cfg.batch_size, cfg.seq_len, cfg.d_model, generator=g).masked_fill(~m[..., None], 0)
+        x = x.to(dtype)
+        with torch.inference_mode():
+            got = model(x.to(device), m.to(device)).cpu()
+        _check(got, oracle.forward(sd, x.float(), m, cfg.num_heads, cfg.causal, torch.float32), m, dtype)
+        assert len(calls) == n_block, "the attention block ran on a general mask"
+    finally:
+        plans_mod.set_override(None)
+
+
+def test_attention_block_graph_equals_eager(device):
+    """With the attention block, hipGraph replay == eager bit for bit on
+    fresh prefix-masked inputs, replayed twice with eager work between."""
+    cfg = TransformerConfig(3, 96, 256, 4, 512, 2, True)
+    dtype = torch.bfloat16
+    torch.manual_seed(6)
+    eager = _module(cfg, UserOptimizedTransformer(cfg).state_dict(), dtype, device)
+    graphed = _module(cfg, eager.state_dict(), dtype, device)
+    cases = [_inputs(cfg, dtype, seed=80 + i, padding=0.5 * (i % 2)) for i in range(3)]
+    plans_mod.set_override(Plan(compute_dtype=dtype, attn_block=True, cuda_graph=False, ffn="fused", label="e"))
+    try:
+        with torch.inference_mode():
+            expected = [eager(x.to(device), m.to(device)).cpu() for x, m in cases]
+    finally:
+        plans_mod.set_override(None)
+    plans_mod.set_override(Plan(compute_dtype=dtype, attn_block=True, cuda_graph=True, ffn="fused", label="g"))
+    try:
+        with torch.inference_mode():
+            for _ in range(2):
+                for (x, m), want in zip(cases, expected):
+                    got = graphed(x.to(device), m.to(device))
+                    torch.cuda.synchronize()
+                    assert torch.equal(got.cpu(), want)
+                    _ = (got * 2).sum().item()
+        assert len(graphed._tj_engine._graphs) >= 1
+    finally:
+        plans_mod.set_override(None)
+
+
 def test_deferred_residual_plan_matches(device):
     """The reference's deferred-residual scheme (residual_epilogue=False)
     stays inside the budget too."""

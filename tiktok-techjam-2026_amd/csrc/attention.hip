@@ -34,13 +34,9 @@
 #include <algorithm>
 #include <mutex>
 
-#include "tjk_common.h"
+#include "attn_short.h"
 
 namespace tjk {
-
-__device__ __forceinline__ int swap_bits_2_3(int x) {
-  return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1);
-}
 
 template <typename T> struct PairPack;
 template <> struct PairPack<bf16> {
@@ -399,7 +395,6 @@ __global__ __launch_bounds__(64) void flash_short_kernel(
     int causal, const int32_t* __restrict__ lengths, const uint8_t* __restrict__ key_mask,
     const int32_t* __restrict__ cu_seqlens, int nqb) {
   constexpr int MAXK = 128;                // keys per sequence
-  constexpr int NKB = MAXK / 32;           // 32-key blocks
   constexpr int VEC = 16 / sizeof(T);      // elements per 16-byte chunk
   constexpr int LDK = HDP + VEC;           // K row pitch (elements)
   constexpr int LDV = MAXK + VEC;          // V^T row pitch (elements)
@@ -435,36 +430,48 @@ __global__ __launch_bounds__(64) void flash_short_kernel(
   kend = min(kend, kv_len);  // keys >= kend are never admissible (and never read)
   const int nkb = (kend + 31) / 32;
 
+  // Every load below is unconditional, at an index clamped into the
+  // sequence (row 0 exists: q0 < Sb), and its value replaced by zeros where
+  // it lies outside: a load under a per-lane condition is waited for on its
+  // own, one memory round trip per load.
   // Q fragments (B operand of S^T): lane holds Q[q][16c + 8*hi + 0..7]
   const int q = q0 + l32;
+  const T* qrow = qbase + (int64_t)min(q, Sb - 1) * ss;
   Frag qf[KC];
 #pragma unroll
+  for (int c = 0; c < KC; ++c) qf[c] = Mfma<T>::load(qrow + min(16 * c + 8 * hi, hd - 8));
+#pragma unroll
   for (int c = 0; c < KC; ++c) {
-    const int col = 16 * c + 8 * hi;
-    if (q < Sb && col < hd) {
-      qf[c] = Mfma<T>::load(qbase + (int64_t)q * ss + col);
-    } else {
+    if (!(q < Sb && 16 * c + 8 * hi < hd)) {
       float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
       qf[c] = Mfma<T>::pack(z);
     }
   }
   // K rows and V rows (two keys per item) of keys < kend, zeros past it:
   // every LDS word the math reads is written.
+  const int klast = max(kend - 1, 0);
   uint4 rk[KPL], rv0[VPL], rv1[VPL];
 #pragma unroll
   for (int i = 0; i < KPL; ++i) {
     const int it = lane + i * 64, key = it / CH, col = (it % CH) * VEC;
-    rk[i] = (key < kend && col < hd) ? *reinterpret_cast<const uint4*>(kbase + (int64_t)key * ss + col)
-                                     : make_uint4(0, 0, 0, 0);
+    rk[i] = *reinterpret_cast<const uint4*>(kbase + (int64_t)min(key, klast) * ss + min(col, hd - VEC));
+  }
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int it = lane + i * 64, p = it % (MAXK / 2), col = min((it / (MAXK / 2)) * VEC, hd - VEC);
+    rv0[i] = *reinterpret_cast<const uint4*>(vbase + (int64_t)min(2 * p, klast) * ss + col);
+    rv1[i] = *reinterpret_cast<const uint4*>(vbase + (int64_t)min(2 * p + 1, klast) * ss + col);
+  }
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) {
+    const int it = lane + i * 64, key = it / CH, col = (it % CH) * VEC;
+    if (!(key < kend && col < hd)) rk[i] = make_uint4(0, 0, 0, 0);
   }
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int it = lane + i * 64, p = it % (MAXK / 2), col = (it / (MAXK / 2)) * VEC;
-    const bool ok = col < hd;
-    rv0[i] = (ok && 2 * p < kend) ? *reinterpret_cast<const uint4*>(vbase + (int64_t)(2 * p) * ss + col)
-                                  : make_uint4(0, 0, 0, 0);
-    rv1[i] = (ok && 2 * p + 1 < kend) ? *reinterpret_cast<const uint4*>(vbase + (int64_t)(2 * p + 1) * ss + col)
-                                      : make_uint4(0, 0, 0, 0);
+    if (!(col < hd && 2 * p < kend)) rv0[i] = make_uint4(0, 0, 0, 0);
+    if (!(col < hd && 2 * p + 1 < kend)) rv1[i] = make_uint4(0, 0, 0, 0);
   }
 #pragma unroll
   for (int i = 0; i < KPL; ++i) {
@@ -478,68 +485,12 @@ __global__ __launch_bounds__(64) void flash_short_kernel(
   }
   __syncthreads();
 
-  // S^T = K Q^T per 32-key block: register r of block kb is key
-  // kb*32 + 16*(r/8) + 8*hi + r%8 (K rows read with bits 2 and 3 swapped)
-  const int krow = swap_bits_2_3(l32);
-  f32x16 s[NKB];
-#pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
-    if (kb < nkb) {
-      const T* kp = &sK[(kb * 32 + krow) * LDK + 8 * hi];
-#pragma unroll
-      for (int c = 0; c < KC; ++c) Mfma<T>::mma(s[kb], Mfma<T>::load(kp + 16 * c), qf[c]);
-    }
-  }
-  // masks and the row max (lanes l and l^32 hold the two halves of a query's keys)
+  // exact softmax over the resident keys (math shared with tjk_attn_block)
   const int lim = causal ? min(q + 1, kend) : kend;
-  float mx = -INFINITY;
-#pragma unroll
-  for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = kb * 32 + 16 * (r >> 3) + 8 * hi + (r & 7);
-      bool keep = key < lim;
-      if constexpr (KEYMASK) keep = keep && key_mask[(int64_t)b * S + key] != 0;
-      s[kb][r] = keep ? s[kb][r] : -INFINITY;
-      mx = fmaxf(mx, s[kb][r]);
-    }
-  {
-    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-    mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-  }
-  const float m_use = mx == -INFINITY ? 0.f : mx * scale_log2;
-  // P = 2^(S scale - max), its fp32 row sum, and O^T = V^T P^T in 16-key steps
   f32x16 o[HB];
-#pragma unroll
-  for (int hb = 0; hb < HB; ++hb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[hb][r] = 0.f;
-  float ls = 0.f;
-#pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) {
-    if (kb < nkb) {
-      float p[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        p[r] = __builtin_amdgcn_exp2f(fmaf(s[kb][r], scale_log2, -m_use));
-        ls += p[r];
-      }
-#pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        const Frag pf = Mfma<T>::pack(&p[8 * st]);
-#pragma unroll
-        for (int hb = 0; hb < HB; ++hb)
-          Mfma<T>::mma(o[hb], Mfma<T>::load(&sV[(hb * 32 + l32) * LDV + 8 * hi] + 16 * (2 * kb + st)), pf);
-      }
-    }
-  }
-
-  // normalise and store: register r of block hb is hd row hb*32 + 8*(r/4) + 4*hi + r%4
-  const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ls), __float_as_uint(ls), false, false);
-  const float l = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
-  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  const float inv = short_attention<T, HDP, MAXK>(
+      sK, sV, qf, nkb, lim, scale_log2,
+      [&](int key) { return !KEYMASK || key_mask[(int64_t)b * S + key] != 0; }, o);
   if (q >= Sb) return;
   T* orow = out + (row0 + q) * ld_out + (int64_t)h * hd;
 #pragma unroll

@@ -274,16 +274,19 @@ __global__ __launch_bounds__(256) void ffn_fused_kernel(
   const int t = xcd_remap(blockIdx.x, nrb * splits);
   const int s = t / nrb, m0 = (t % nrb) * kFfnRows, fc0 = s * FC;
 
-  // this wave's b1 columns, read before any DMA so that no later wait for
-  // them has to drain the weight copies
-  float4 b1v[P1::FN][4];
+  // this wave's b1 columns, raw, read before any DMA so that no later wait
+  // for them has to drain the weight copies.  The loads are unconditional
+  // (without b1 they read W1 and the values are dropped): a load under a
+  // condition is waited for on its own, one memory round trip per load.
+  typedef typename Quad<T>::raw Raw;
+  const T* b1p = b1 != nullptr ? b1 + fc0 : W1;
+  Raw b1r[P1::FN][4];
 #pragma unroll
   for (int i = 0; i < P1::FN; ++i)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int n = min(wave, Lay::WN1 - 1) * P1::WTN + 32 * i + 8 * g + 4 * hi;
-      b1v[i][g] = b1 ? Quad<T>::to(*reinterpret_cast<const typename Quad<T>::raw*>(b1 + fc0 + n))
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
+      b1r[i][g] = *reinterpret_cast<const Raw*>(b1p + n);
     }
 
   WStream<T, FC, 128, Lay::ST1, Lay::WN1, Lay::A_PITCH> w1s(ring, W1 + (int64_t)fc0 * D, D, FC, D / P1::BK);
@@ -405,7 +408,7 @@ __global__ __launch_bounds__(256) void ffn_fused_kernel(
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int n = wave * P1::WTN + 32 * i + 8 * g + 4 * hi;  // column within the slice
-          const float4 bv = b1v[i][g];
+          const float4 bv = b1 != nullptr ? Quad<T>::to(b1r[i][g]) : make_float4(0.f, 0.f, 0.f, 0.f);
           float4 v = make_float4(gelu_erf(acc[i][0][4 * g + 0] + bv.x), gelu_erf(acc[i][0][4 * g + 1] + bv.y),
                                  gelu_erf(acc[i][0][4 * g + 2] + bv.z), gelu_erf(acc[i][0][4 * g + 3] + bv.w));
           const int ch = n / VEC, off = (n % VEC) * (int)sizeof(T);

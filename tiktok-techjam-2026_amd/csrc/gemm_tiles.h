@@ -115,15 +115,30 @@ __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* _
   // that keeps every row 16-byte aligned; otherwise pieces go out as halves.
   const bool a16 = ((uintptr_t)Cv & 15) == 0 && (ldc % E::SV) == 0;
 
+  // Bias of this wave's columns.  All loads go out before any is used --
+  // one memory round trip; a load under a per-lane condition would be
+  // waited for on its own, one round trip per load -- with columns past N
+  // clamped into range and zeroed afterwards (N % 4 == 0, N >= 4).
+  typedef typename Quad<T>::raw Raw;
+  Raw braw[FN][4];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) braw[i][g] = Raw{};
+  if (bias != nullptr) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        braw[i][g] = *reinterpret_cast<const Raw*>(bias + min(nw + i * 32 + g * 8 + hi * 4, N - 4));
+  }
   float4 bv[FN][4];
 #pragma unroll
   for (int i = 0; i < FN; ++i)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int n = nw + i * 32 + g * 8 + hi * 4;
-      bv[i][g] = (bias != nullptr && n < N)
-                     ? Quad<T>::to(*reinterpret_cast<const typename Quad<T>::raw*>(bias + n))
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
+      bv[i][g] = n < N ? Quad<T>::to(braw[i][g]) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 
 #pragma unroll

@@ -58,29 +58,35 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(
   const bool live = row < rows;
   const int64_t src = !live ? -1 : row_index != nullptr ? (int64_t)row_index[row] : row;
 
+  // Chunks past the row end are read at the last chunk and dropped: loads
+  // under a per-lane condition are waited for one at a time.
   float4 x[MAXCH];
   if (src >= 0) {
     const TRes* rrow = res + src * ld_res;
+    typename Quad<TRes>::raw rr[MAXCH];
 #pragma unroll
-    for (int j = 0; j < MAXCH; ++j) {
-      const int c = lane + 64 * j;
-      if (FULL || c < nch) {
-        x[j] = Quad<TRes>::to(reinterpret_cast<const typename Quad<TRes>::raw*>(rrow)[c]);
-      } else {
-        x[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-    }
+    for (int j = 0; j < MAXCH; ++j)
+      rr[j] = reinterpret_cast<const typename Quad<TRes>::raw*>(rrow)[FULL ? lane + 64 * j : min(lane + 64 * j, nch - 1)];
     if (delta != nullptr) {
       const TDelta* drow = delta + src * ld_delta;
+      typename Quad<TDelta>::raw dr[MAXCH];
+#pragma unroll
+      for (int j = 0; j < MAXCH; ++j)
+        dr[j] = reinterpret_cast<const typename Quad<TDelta>::raw*>(drow)[FULL ? lane + 64 * j
+                                                                             : min(lane + 64 * j, nch - 1)];
 #pragma unroll
       for (int j = 0; j < MAXCH; ++j) {
-        const int c = lane + 64 * j;
-        if (FULL || c < nch) {
-          float4 d = Quad<TDelta>::to(reinterpret_cast<const typename Quad<TDelta>::raw*>(drow)[c]);
-          x[j].x += d.x; x[j].y += d.y; x[j].z += d.z; x[j].w += d.w;
-        }
+        x[j] = Quad<TRes>::to(rr[j]);
+        const float4 d = Quad<TDelta>::to(dr[j]);
+        x[j].x += d.x; x[j].y += d.y; x[j].z += d.z; x[j].w += d.w;
       }
+    } else {
+#pragma unroll
+      for (int j = 0; j < MAXCH; ++j) x[j] = Quad<TRes>::to(rr[j]);
     }
+#pragma unroll
+    for (int j = 0; j < MAXCH; ++j)
+      if (!FULL && lane + 64 * j >= nch) x[j] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   // gamma / beta staged once per workgroup (4 rows), by every thread before
   // any wave leaves: read from L2 by each wave they were 8 KB per 1024-wide
@@ -177,16 +183,26 @@ __global__ __launch_bounds__(256) void add_layernorm_parts_kernel(
     }
     return;
   }
+  // Every load is unconditional, chunks past the row end read at the last
+  // chunk (and dropped): loads under a per-lane condition are waited for one
+  // at a time.  Wave 0 also fetches gamma / beta up front.
   const int q = (n_parts + 3) / 4, p_lo = min(wave * q, n_parts), p_hi = min(p_lo + q, n_parts);
-  float4 x[MAXCH];
+  int cl[MAXCH];  // clamped chunk index
+#pragma unroll
+  for (int j = 0; j < MAXCH; ++j) cl[j] = min(lane + 64 * j, nch - 1);
+  float4 x[MAXCH], gv[MAXCH], bv[MAXCH];
   if (wave == 0) {
     const TRes* rrow = res + src * ld_res;
+    typename Quad<TRes>::raw rr[MAXCH];
+#pragma unroll
+    for (int j = 0; j < MAXCH; ++j) rr[j] = reinterpret_cast<const typename Quad<TRes>::raw*>(rrow)[cl[j]];
 #pragma unroll
     for (int j = 0; j < MAXCH; ++j) {
-      const int c = lane + 64 * j;
-      x[j] = c < nch ? Quad<TRes>::to(reinterpret_cast<const typename Quad<TRes>::raw*>(rrow)[c])
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
+      gv[j] = reinterpret_cast<const float4*>(gamma)[cl[j]];
+      bv[j] = reinterpret_cast<const float4*>(beta)[cl[j]];
     }
+#pragma unroll
+    for (int j = 0; j < MAXCH; ++j) x[j] = Quad<TRes>::to(rr[j]);
   }
   float4 acc[MAXCH];
   const float* prow = parts + src * ld_parts;
@@ -195,12 +211,9 @@ __global__ __launch_bounds__(256) void add_layernorm_parts_kernel(
 #pragma unroll
     for (int u = 0; u < PER; ++u)
 #pragma unroll
-      for (int j = 0; j < MAXCH; ++j) {
-        const int c = lane + 64 * j;
-        v[u][j] = (p0 + u < p_hi && c < nch)
-                      ? reinterpret_cast<const float4*>(prow + (int64_t)(p0 + u) * part_stride)[c]
-                      : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+      for (int j = 0; j < MAXCH; ++j)
+        v[u][j] = p0 + u < p_hi ? reinterpret_cast<const float4*>(prow + (int64_t)(p0 + u) * part_stride)[cl[j]]
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
       if (p0 + u == p_lo) {
@@ -233,6 +246,7 @@ __global__ __launch_bounds__(256) void add_layernorm_parts_kernel(
 #pragma unroll
   for (int j = 0; j < MAXCH; ++j) {
     x[j].x += acc[j].x; x[j].y += acc[j].y; x[j].z += acc[j].z; x[j].w += acc[j].w;
+    if (lane + 64 * j >= nch) x[j] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   if (res_out != nullptr) {
     float4* orow = reinterpret_cast<float4*>(res_out + row * ld_res_out);
@@ -265,7 +279,7 @@ __global__ __launch_bounds__(256) void add_layernorm_parts_kernel(
       if (zero) {
         y = make_float4(0.f, 0.f, 0.f, 0.f);
       } else {
-        const float4 g = reinterpret_cast<const float4*>(gamma)[c], b = reinterpret_cast<const float4*>(beta)[c];
+        const float4 g = gv[j], b = bv[j];
         y.x = (x[j].x - mean) * rstd * g.x + b.x;
         y.y = (x[j].y - mean) * rstd * g.y + b.y;
         y.z = (x[j].z - mean) * rstd * g.z + b.z;

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede the library load; see module docstring)
 
 LIB_PATH = Path(__file__).with_name("libtjk.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 F32, F16, BF16 = 0, 1, 2
 OK, EINVAL, EUNSUPPORTED = 0, -1, -2
@@ -50,6 +50,9 @@ _SIGNATURES = {
     "tjk_ffn": (_i32, [_vp, _i32, _i64, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32,
                        _i64, _i64, _i64, _i32, _vp]),
     "tjk_ffn_supported": (_i32, [_i64, _i64, _i32, _i32]),
+    "tjk_attn_block": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _i32, _i32, _i32,
+                              _i32, _f32, _i32, _i32, _vp]),
+    "tjk_attn_block_supported": (_i32, [_i64, _i32, _i32, _i64, _i32]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

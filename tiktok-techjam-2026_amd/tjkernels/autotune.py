@@ -36,7 +36,8 @@ import torch
 
 from . import ops
 from .modules import UserOptimizedTransformer
-from .plans import Plan, default_plan, device_arch, fused_ffn_ok, save_plans, set_override, shape_key
+from .plans import (Plan, attn_block_ok, default_plan, device_arch, fused_ffn_ok, save_plans, set_override,
+                    shape_key)
 from .workloads import WORKLOADS, Workload, make_inputs, make_state_dict
 
 HELD_OUT_SEEDS = [777, 4242]
@@ -179,6 +180,8 @@ def tune_workload(w: Workload, trials: int = 2, margin: float = 0.85, iters: int
     knobs = [("attn_plan", attn_plans), ("residual_epilogue", [True, False]), ("cuda_graph", [True, False])]
     if fused_ffn_ok(w.d_model, w.ffn_dim, cur["plan"].compute_dtype):
         knobs.insert(0, ("ffn", ["gemm", "fused"]))
+    if attn_block_ok(w.seq, w.d_model, w.heads, cur["plan"].compute_dtype):
+        knobs.insert(0, ("attn_block", [True, False]))
     for knob, values in knobs:
         for v in values:
             if getattr(cur["plan"], knob) == v:

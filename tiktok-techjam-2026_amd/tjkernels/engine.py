@@ -10,6 +10,9 @@ pre-LN causal encoder over an fp32 residual stream ``res``:
         qkv  = h Wqkv^T + bqkv             one [3d, d] GEMM, rows q | k | v
         ctx  = attention(qkv viewed as [B, S, 3, H, hd])
         res += ctx Wo^T + bo               GEMM residual epilogue
+              (``Plan.attn_block``, sequences of <= 128 tokens: the three
+              in one launch, its per-head partials of ctx Wo^T + bo summed
+              into res by LayerNorm 2)
         FFN:  "gemm"  -- h = LN2(res); mid = gelu_erf(h W1^T + b1) (GEMM
                          epilogue); res += mid W2^T + b2 (residual epilogue)
               "fused" -- one launch: LN2, both GEMMs and GELU with the
@@ -47,7 +50,7 @@ import torch
 
 from . import ops, schedule as sched_mod, tiles
 from .graphs import GraphCache
-from .plans import ATTN_SCHEDULED, Plan, fused_ffn_ok, select_plan
+from .plans import ATTN_SCHEDULED, Plan, attn_block_ok, fused_ffn_ok, select_plan
 
 try:
     from torch.utils.weak import WeakTensorKeyDictionary
@@ -233,6 +236,7 @@ class Workspace:
     mid: Optional[torch.Tensor]      # [T, f] FFN intermediate (two-launch FFN)
     delta: Optional[torch.Tensor]    # [T, d] deferred block output (deferred plans)
     parts: Optional[torch.Tensor]    # [splits, T, d] fp32 FFN partials (fused FFN)
+    attn_parts: Optional[torch.Tensor] = None  # [H, T, d] fp32 out-proj partials (attention block)
 
 
 @dataclass
@@ -249,6 +253,7 @@ class Forward:
     packing: Optional[Packing] = None
     key_mask: Optional[torch.Tensor] = None
     use_sched: bool = False
+    use_block: bool = False
     splits: int = 1
     pending: Optional[torch.Tensor] = None  # what the next LayerNorm adds to res
 
@@ -256,7 +261,7 @@ class Forward:
         t = getattr(self.ws, name)
         if t is None:
             return None
-        return t[:, :self.rows] if name == "parts" else t[:self.rows]
+        return t[:, :self.rows] if name in ("parts", "attn_parts") else t[:self.rows]
 
 
 class Engine:
@@ -325,9 +330,9 @@ class Engine:
 
     # -- per-shape preparation
 
-    def _workspace(self, batch: int, seq: int, plan: Plan, splits: int) -> Workspace:
+    def _workspace(self, batch: int, seq: int, plan: Plan, splits: int, block: bool) -> Workspace:
         fused = plan.ffn == "fused"
-        key = (batch, seq, plan.compute_dtype, plan.residual_epilogue, fused, splits)
+        key = (batch, seq, plan.compute_dtype, plan.residual_epilogue, fused, splits, block)
         ws = self._workspaces.get(key)
         if ws is None:
             t, d, f = batch * seq, self.shape.d_model, self.shape.ffn_dim
@@ -339,7 +344,8 @@ class Engine:
             ws = Workspace(res=buf(t, d, dtype=torch.float32), h=buf(t, d), qkv=buf(t, 3 * d), ctx=buf(t, d),
                            mid=None if fused else buf(t, f),
                            delta=None if plan.residual_epilogue else buf(t, d),
-                           parts=buf(splits, t, d, dtype=torch.float32) if fused and splits > 1 else None)
+                           parts=buf(splits, t, d, dtype=torch.float32) if fused and splits > 1 else None,
+                           attn_parts=buf(self.shape.heads, t, d, dtype=torch.float32) if block else None)
             self._workspaces[key] = ws
         return ws
 
@@ -353,15 +359,22 @@ class Engine:
         rows = packing.tokens if mode == MASK_PREFIX else batch * seq
         splits = (plan.ffn_splits or ffn_slices(rows, shp.ffn_dim)) if fused else 1
         cdt, d, f = plan.compute_dtype, shp.d_model, shp.ffn_dim
+        # the one-launch attention block takes no per-key mask and
+        # sequences of at most 128 tokens; other forwards of the plan run the
+        # QKV GEMM, attention and out-proj GEMM
+        longest = max(packing.lengths) if mode == MASK_PREFIX else seq
+        block = (plan.attn_block and mode != MASK_GENERAL and rows > 0
+                 and attn_block_ok(longest, d, shp.heads, cdt))
         epi_res = ops.EPI_BIAS_RESIDUAL if plan.residual_epilogue else ops.EPI_BIAS
         tp = Tiles(
-            qkv=tiles.gemm_plan(rows, 3 * d, d, cdt, ops.EPI_BIAS, plan.gemm_qkv),
-            out=tiles.gemm_plan(rows, d, d, cdt, epi_res, plan.gemm_out),
+            qkv=-1 if block else tiles.gemm_plan(rows, 3 * d, d, cdt, ops.EPI_BIAS, plan.gemm_qkv),
+            out=-1 if block else tiles.gemm_plan(rows, d, d, cdt, epi_res, plan.gemm_out),
             fc1=-1 if fused else tiles.gemm_plan(rows, f, d, cdt, ops.EPI_BIAS_GELU, plan.gemm_ffn1),
             fc2=-1 if fused else tiles.gemm_plan(rows, d, f, cdt, epi_res, plan.gemm_ffn2))
-        fw = Forward(batch=batch, seq=seq, mode=mode, rows=rows, ws=self._workspace(batch, seq, plan, splits),
-                     tiles=tp, packing=packing if mode == MASK_PREFIX else None,
-                     key_mask=mask if mode == MASK_GENERAL else None, splits=splits)
+        fw = Forward(batch=batch, seq=seq, mode=mode, rows=rows,
+                     ws=self._workspace(batch, seq, plan, splits, block), tiles=tp,
+                     packing=packing if mode == MASK_PREFIX else None,
+                     key_mask=mask if mode == MASK_GENERAL else None, use_block=block, splits=splits)
         if fused:
             fw.pending = fw.view("parts")
         elif not plan.residual_epilogue:
@@ -372,7 +385,7 @@ class Engine:
         # sequences of at most 128 keys the short-sequence plan 4; other plan
         # ids force the plain kernel.
         pk = fw.packing
-        fw.use_sched = (pk is not None and cdt != torch.float32 and rows > 0
+        fw.use_sched = (pk is not None and cdt != torch.float32 and rows > 0 and not block
                         and (plan.attn_plan == ATTN_SCHEDULED
                              or (plan.attn_plan == -1 and 128 < max(pk.lengths) < 2048)))
         if fw.use_sched and pk.attn is None:
@@ -402,15 +415,30 @@ class Engine:
             ops.flash_attention(qkv.view(fw.batch, fw.seq, 3, shp.heads, shp.head_dim), ctx, causal=shp.causal,
                                 key_mask=fw.key_mask, plan=self.plan.attn_plan)
 
+    def _attn_block(self, fw: Forward, blk: BlockWeights) -> None:
+        """QKV GEMM, attention and out-projection in one launch; the
+        out-projection's per-head partials go to attn_parts."""
+        shp, pk = self.shape, fw.packing
+        args = (fw.view("h"), blk.qkv.weight, blk.qkv.bias, blk.out.weight, blk.out.bias, fw.view("attn_parts"),
+                shp.heads)
+        if pk is not None:
+            ops.attn_block(*args, causal=shp.causal, cu_seqlens=pk.cu_seqlens, max_seqlen=max(pk.lengths))
+        else:
+            ops.attn_block(*args, causal=shp.causal, batch=fw.batch, seq=fw.seq)
+
     def _ffn(self, fw: Forward, blk: BlockWeights) -> None:
         plan = self.plan
         res, h, n2 = fw.view("res"), fw.view("h"), blk.norm2
+        # the attention output not yet in res: the attention block's
+        # partials, or the deferred out-proj output
+        attn_pending = fw.view("attn_parts") if fw.use_block else (
+            None if plan.residual_epilogue else fw.view("delta"))
         if plan.ffn == "fused":
             parts = fw.view("parts")
-            if plan.residual_epilogue:
+            if attn_pending is None:
                 ln, a = (n2.weight, n2.bias, n2.eps), res  # LayerNorm 2 inside the kernel
             else:
-                ops.add_layernorm(res, fw.view("delta"), n2.weight, n2.bias, n2.eps, h, res_out=res)
+                ops.add_layernorm(res, attn_pending, n2.weight, n2.bias, n2.eps, h, res_out=res)
                 ln, a = None, h
             if parts is None:
                 ops.ffn(a, blk.fc1.weight, blk.fc1.bias, blk.fc2.weight, blk.fc2.bias, res, ln=ln, accumulate=True)
@@ -420,12 +448,13 @@ class Engine:
             return
         mid = fw.view("mid")
         if plan.residual_epilogue:
-            ops.add_layernorm(res, None, n2.weight, n2.bias, n2.eps, h)
+            ops.add_layernorm(res, attn_pending, n2.weight, n2.bias, n2.eps, h,
+                              res_out=res if attn_pending is not None else None)
             ops.gemm(h, blk.fc1.weight, blk.fc1.bias, mid, ops.EPI_BIAS_GELU, fw.tiles.fc1)
             ops.gemm(mid, blk.fc2.weight, blk.fc2.bias, res, ops.EPI_BIAS_RESIDUAL, fw.tiles.fc2)
         else:
             delta = fw.view("delta")
-            ops.add_layernorm(res, delta, n2.weight, n2.bias, n2.eps, h, res_out=res)
+            ops.add_layernorm(res, attn_pending, n2.weight, n2.bias, n2.eps, h, res_out=res)
             ops.gemm(h, blk.fc1.weight, blk.fc1.bias, mid, ops.EPI_BIAS_GELU, fw.tiles.fc1)
             ops.gemm(mid, blk.fc2.weight, blk.fc2.bias, delta, ops.EPI_BIAS, fw.tiles.fc2)
 
@@ -438,12 +467,15 @@ class Engine:
                 n1 = blk.norm1
                 ops.add_layernorm(res, fw.pending, n1.weight, n1.bias, n1.eps, h,
                                   res_out=res if fw.pending is not None else None)
-            ops.gemm(h, blk.qkv.weight, blk.qkv.bias, fw.view("qkv"), ops.EPI_BIAS, fw.tiles.qkv)
-            self._attention(fw)
-            if self.plan.residual_epilogue:
-                ops.gemm(ctx, blk.out.weight, blk.out.bias, res, ops.EPI_BIAS_RESIDUAL, fw.tiles.out)
+            if fw.use_block:
+                self._attn_block(fw, blk)
             else:
-                ops.gemm(ctx, blk.out.weight, blk.out.bias, fw.view("delta"), ops.EPI_BIAS, fw.tiles.out)
+                ops.gemm(h, blk.qkv.weight, blk.qkv.bias, fw.view("qkv"), ops.EPI_BIAS, fw.tiles.qkv)
+                self._attention(fw)
+                if self.plan.residual_epilogue:
+                    ops.gemm(ctx, blk.out.weight, blk.out.bias, res, ops.EPI_BIAS_RESIDUAL, fw.tiles.out)
+                else:
+                    ops.gemm(ctx, blk.out.weight, blk.out.bias, fw.view("delta"), ops.EPI_BIAS, fw.tiles.out)
             self._ffn(fw, blk)
 
     def _final(self, fw: Forward, out: torch.Tensor, row_mask: Optional[torch.Tensor]) -> None:

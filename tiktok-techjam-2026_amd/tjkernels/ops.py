@@ -260,6 +260,65 @@ def ffn(a: torch.Tensor, w1: torch.Tensor, b1: Optional[torch.Tensor], w2: torch
     return out
 
 
+def attn_block_supported(d_model: int, heads: int, head_dim: int, max_seqlen: int, dtype: torch.dtype) -> bool:
+    """Whether ``attn_block`` takes the shape (tjk_attn_block_supported)."""
+    code = _lib.DTYPE_CODES.get(dtype)
+    return code is not None and bool(_lib.load().tjk_attn_block_supported(d_model, heads, head_dim, max_seqlen, code))
+
+
+def attn_block(x: torch.Tensor, w_qkv: torch.Tensor, b_qkv: Optional[torch.Tensor], w_out: torch.Tensor,
+               b_out: Optional[torch.Tensor], parts: torch.Tensor, heads: int, causal: bool = True,
+               scale: Optional[float] = None, batch: Optional[int] = None, seq: Optional[int] = None,
+               cu_seqlens: Optional[torch.Tensor] = None, max_seqlen: Optional[int] = None,
+               ctx_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """QKV projection, attention and out-projection of one layer in one
+    launch, for sequences of at most 128 tokens: the addmm / flash_attention
+    / addmm of tjkernels/engine.py:245-247 fused.
+
+    ``x`` is h [rows, d]: ``batch`` sequences of ``seq`` rows, or with
+    ``cu_seqlens`` (int32 [B+1]) packed sequences of at most ``max_seqlen``
+    rows.  ``parts`` is [heads, rows, d] fp32: head h's share of the
+    out-projection (head 0 with b_out); ``add_layernorm`` sums them.
+    ``ctx_out`` [rows, d] optionally receives the attention context."""
+    _require_gpu(x, w_qkv, b_qkv, w_out, b_out, parts, cu_seqlens, ctx_out)
+    rows, d = x.shape
+    cdt = x.dtype
+    if tuple(w_qkv.shape) != (3 * d, d) or tuple(w_out.shape) != (d, d):
+        raise TjkError(f"attn_block weight shapes w_qkv{tuple(w_qkv.shape)} w_out{tuple(w_out.shape)} "
+                       f"do not match d={d}")
+    if w_qkv.dtype != cdt or w_out.dtype != cdt or any(b is not None and b.dtype != cdt for b in (b_qkv, b_out)):
+        raise TjkError("attn_block operands must share x's dtype")
+    if not (w_qkv.is_contiguous() and w_out.is_contiguous()) or \
+            any(b is not None and not b.is_contiguous() for b in (b_qkv, b_out)):
+        raise TjkError("attn_block weights and biases must be contiguous")
+    if d % heads:
+        raise TjkError(f"d={d} is not a multiple of heads={heads}")
+    if parts.dtype != torch.float32 or parts.dim() != 3 or parts.shape[0] != heads or parts.shape[1] < rows \
+            or parts.shape[2] != d or parts.stride(2) != 1:
+        raise TjkError(f"attn_block partials must be [heads={heads}, rows, {d}] fp32")
+    if cu_seqlens is not None:
+        if cu_seqlens.dtype != torch.int32 or cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2 \
+                or not cu_seqlens.is_contiguous():
+            raise TjkError("cu_seqlens must be a contiguous int32 [B+1] vector")
+        if max_seqlen is None:
+            raise TjkError("packed attn_block needs max_seqlen")
+        b, s = cu_seqlens.numel() - 1, int(max_seqlen)
+    else:
+        if batch is None or seq is None or batch * seq != rows:
+            raise TjkError("attn_block needs batch * seq == rows (or cu_seqlens)")
+        b, s = int(batch), int(seq)
+    if ctx_out is not None and (ctx_out.dtype != cdt or ctx_out.shape[0] < rows or ctx_out.shape[1] != d):
+        raise TjkError("bad attn_block ctx_out buffer")
+    hd = d // heads
+    status = _lib.load().tjk_attn_block(
+        x.data_ptr(), _rowmajor(x, "x"), w_qkv.data_ptr(), _ptr(b_qkv), w_out.data_ptr(), _ptr(b_out),
+        parts.data_ptr(), parts.stride(1), parts.stride(0), _ptr(ctx_out),
+        _rowmajor(ctx_out, "ctx_out") if ctx_out is not None else 0, _ptr(cu_seqlens), b, s, heads, hd,
+        float(hd ** -0.5 if scale is None else scale), int(bool(causal)), _code(x), _stream(x))
+    check(status, "tjk_attn_block")
+    return parts
+
+
 def gemm_plans(dtype: torch.dtype):
     """[(plan_id, block_m, block_n, waves, k_groups)] available for ``dtype``."""
     import ctypes

@@ -20,6 +20,11 @@ to select, and the product path has no non-HIP fallback):
   the [T, f] intermediate in HBM) or ``"fused"`` (one launch per layer with
   the intermediate in LDS and LayerNorm 2 inside, split over ``ffn_splits``
   f-slices whose partials the next LayerNorm sums; 0 = f / 128);
+* ``attn_block``: for sequences of at most 128 tokens, the QKV GEMM,
+  attention and out-projection of each layer as one launch
+  (``tjk_attn_block``) whose per-head partials LayerNorm 2 sums; forwards
+  it does not take (longer sequences, general masks) use the three
+  launches;
 * ``cuda_graph``: replay the layer body as one hipGraph;
 * ``whole_graph`` (with ``cuda_graph``): capture the first and final
   LayerNorm too, reading x from a static input buffer and writing a static
@@ -34,8 +39,8 @@ to select, and the product path has no non-HIP fallback):
   ``ATTN_SCHEDULED`` (5) the work-list kernel for packed sequences);
 * ``pack_prefix``: run only the valid tokens of prefix masks.
 
-Environment: ``TJ_NO_GRAPH``, ``TJ_WHOLE_GRAPH`` (0 / 1), ``TJ_COMPUTE_DTYPE``, ``TJ_DEFERRED_RESIDUAL``,
-``TJ_NO_PACK``, ``TJ_ATTN_PLAN``, ``TJ_FFN`` (gemm | fused), ``TJ_FFN_SPLITS``;
+Environment: ``TJ_NO_GRAPH``, ``TJ_WHOLE_GRAPH`` (0 / 1), ``TJ_ATTN_BLOCK`` (0 / 1), ``TJ_COMPUTE_DTYPE``,
+``TJ_DEFERRED_RESIDUAL``, ``TJ_NO_PACK``, ``TJ_ATTN_PLAN``, ``TJ_FFN`` (gemm | fused), ``TJ_FFN_SPLITS``;
 ``TJ_GEMM_TUNE=0`` (tjkernels.tiles) skips the measured tile choice.
 Tuned keys carry the GPU architecture (``...@gfx950``).
 """
@@ -75,6 +80,7 @@ class Plan:
     packed_qkv: bool = True
     cuda_graph: bool = True
     whole_graph: bool = False
+    attn_block: bool = False
     residual_epilogue: bool = True
     gemm_qkv: int = -1
     gemm_out: int = -1
@@ -138,6 +144,13 @@ def fused_ffn_ok(d_model: int, ffn_dim: int, compute_dtype: torch.dtype, splits:
     return all(ops.ffn_supported(d_model, ffn_dim, max(ffn_dim // w, 1), compute_dtype) for w in (64, 128))
 
 
+def attn_block_ok(seq: int, d_model: int, heads: int, compute_dtype: torch.dtype) -> bool:
+    """Whether the one-launch attention block takes the shape
+    (tjk_attn_block_supported)."""
+    from . import ops
+    return d_model % heads == 0 and ops.attn_block_supported(d_model, heads, d_model // heads, seq, compute_dtype)
+
+
 def default_plan(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int,
                  layers: int, causal: bool, dtype: torch.dtype, device: torch.device) -> Plan:
     """Heuristic plan used before (or without) autotuning."""
@@ -151,6 +164,10 @@ def default_plan(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int,
     elems = batch * seq * d_model
     graph = elems <= (1 << 20) and elems * dtype.itemsize <= 64 * 1024 * 1024
     fused = batch * seq * ffn_dim <= FUSED_FFN_MAX_ELEMS and fused_ffn_ok(d_model, ffn_dim, dtype)
+    # The one-launch attention block is not the default: measured on MI355X
+    # at C2 it runs 15.1 us per layer, which with the LayerNorm launch that
+    # sums its per-head partials equals the QKV GEMM + attention + out-proj
+    # it replaces (0.1527 vs 0.1530 ms per forward); the autotuner tries it.
     return Plan(compute_dtype=dtype, cuda_graph=graph, ffn="fused" if fused else "gemm", label="heuristic")
 
 
@@ -209,6 +226,8 @@ def _env_adjusted(plan: Plan, d_model: int, ffn_dim: int) -> Plan:
         changes["cuda_graph"] = False
     if env.get("TJ_WHOLE_GRAPH") in ("0", "1"):
         changes["whole_graph"] = env["TJ_WHOLE_GRAPH"] == "1"
+    if env.get("TJ_ATTN_BLOCK") in ("0", "1"):
+        changes["attn_block"] = env["TJ_ATTN_BLOCK"] == "1"
     if env.get("TJ_COMPUTE_DTYPE") in DTYPE_BY_NAME:
         changes["compute_dtype"] = DTYPE_BY_NAME[env["TJ_COMPUTE_DTYPE"]]
     if env.get("TJ_DEFERRED_RESIDUAL") == "1":
