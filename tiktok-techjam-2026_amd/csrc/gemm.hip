@@ -254,6 +254,12 @@ static const GemmPlan kPlans16[] = {
     {kDtl, 64, 64, 2, 2, 128, 2, 0.45, 4},    // 21 16 waves, 128 KB
     {kDtl, 64, 64, 2, 2, 128, 4, 0.45, 2},    // 22 8 waves, 128 KB
     {kDtl, 128, 64, 2, 2, 128, 3, 0.50, 2},   // 23 8 waves, 144 KB
+    // 24, 25: 32-row tiles with K split between two groups of 2 / 1 waves,
+    // for projections of a few hundred rows (C2: 128), whose tiles would
+    // otherwise occupy a few dozen CUs each moving 128 KB of operands: at
+    // 32 x 64 and 32 x 32 a launch spreads over 2x and 4x more CUs.
+    {kDtl, 32, 64, 1, 2, 128, 4, 0.35, 2},    // 24 4 waves, 96 KB
+    {kDtl, 32, 32, 1, 1, 128, 4, 0.30, 2},    // 25 2 waves, 64 KB
 };
 // fp32.
 static const GemmPlan kPlans32[] = {
@@ -392,6 +398,8 @@ static int run_gemm(int plan, int epi, const GemmArgs& g) {
       TJK_GEMM_CASE(21, D2K4, 64, 64, 2, 2)
       TJK_GEMM_CASE(22, D4K2, 64, 64, 2, 2)
       TJK_GEMM_CASE(23, D3K2, 128, 64, 2, 2)
+      TJK_GEMM_CASE(24, D4K2, 32, 64, 1, 2)
+      TJK_GEMM_CASE(25, D4K2, 32, 32, 1, 1)
     }
   }
 #undef TJK_GEMM_CASE

@@ -44,8 +44,9 @@ from . import _lib, ops, timing
 # class 1: 128x128, 256x256 (8 waves), 64x64, 192x128, 192x256, 192x384,
 #          96x128, 192x128 in a 4-slot ring, 64x64 / 128x64 in 8- / 6-slot rings;
 # class 2: 192x128, 128x128, 64x64 (4-slot ring), 128x64 (3-slot ring), each
-#          with K split between two groups of 4 waves.
-CLASS_TILES_16 = {1: (7, 8, 9, 12, 13, 14, 15, 18, 19, 20), 2: (16, 17, 22, 23)}
+#          with K split between two groups of 4 waves; 32x64 and 32x32
+#          (4-slot rings) with K split between two groups of 2 / 1 waves.
+CLASS_TILES_16 = {1: (7, 8, 9, 12, 13, 14, 15, 18, 19, 20), 2: (16, 17, 22, 23, 24, 25)}
 CANDIDATES_32 = (2, 3, 4)  # fp32: class 1 only
 MAX_ENTRIES = 256
 M_BUCKET = 64
