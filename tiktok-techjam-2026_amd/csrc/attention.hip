@@ -246,12 +246,20 @@ __global__ __launch_bounds__(256 * KS) void flash_fwd_kernel(
             }
         }
         if constexpr (KEYMASK) {
+          // every mask byte loaded before any is used (a load under the
+          // key < kend condition would be waited for on its own)
+          uint8_t km[2][16];
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              km[kb][r] = key_mask[(int64_t)b * S + min(k0 + kb * 32 + 16 * (r >> 3) + 8 * hi + (r & 7), S - 1)];
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const int key = k0 + kb * 32 + 16 * (r >> 3) + 8 * hi + (r & 7);
-              const bool keep = key < kend && key_mask[(int64_t)b * S + key] != 0;
+              const bool keep = key < kend && km[kb][r] != 0;
               s[j][kb][r] = keep ? s[j][kb][r] : -INFINITY;
             }
         }
@@ -490,7 +498,7 @@ __global__ __launch_bounds__(64) void flash_short_kernel(
   f32x16 o[HB];
   const float inv = short_attention<T, HDP, MAXK>(
       sK, sV, qf, nkb, lim, scale_log2,
-      [&](int key) { return !KEYMASK || key_mask[(int64_t)b * S + key] != 0; }, o);
+      [&](int key) { return !KEYMASK || key_mask[(int64_t)b * S + min(key, S - 1)] != 0; }, o);
   if (q >= Sb) return;
   T* orow = out + (row0 + q) * ld_out + (int64_t)h * hd;
 #pragma unroll
@@ -768,13 +776,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
   auto mask_tile = [&](int t, f32x16 (&sa)[2]) {
     const int k0 = t * BNK, q = wq0 + l32;
     const int lim = causal ? min(q + 1, kend) : kend;
+    // mask bytes all loaded before any is used (see flash_fwd_kernel)
+    uint8_t km[2][16];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        km[kb][r] = KEYMASK ? key_mask[(int64_t)b * S + min(k0 + kb * 32 + 16 * (r >> 3) + 8 * hi + (r & 7), S - 1)]
+                            : 1;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = k0 + kb * 32 + 16 * (r >> 3) + 8 * hi + (r & 7);
-        bool keep = key < lim;
-        if constexpr (KEYMASK) keep = keep && key_mask[(int64_t)b * S + min(key, S - 1)] != 0;
+        const bool keep = key < lim && km[kb][r] != 0;
         sa[kb][r] = keep ? sa[kb][r] : -INFINITY;
       }
   };

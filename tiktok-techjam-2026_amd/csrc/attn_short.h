@@ -22,7 +22,8 @@ __device__ __forceinline__ int swap_bits_2_3(int x) {
 //   qf  the queries as MFMA B fragments: lane (l32, hi) holds
 //       Q[query l32][16 c + 8 hi + 0..7] in qf[c].
 // A key is admitted when key < lim (per lane, i.e. per query) and
-// keep(key).  Computes S^T = K Q^T per 32-key block, the exact row max
+// keep(key); keep is called for every key 0 .. MAXK - 1, so it must be
+// safe to evaluate past the sequence end.  Computes S^T = K Q^T per 32-key block, the exact row max
 // (lanes l and l ^ 32 hold the two halves of a query's keys), P = 2^(S
 // scale_log2 - max) with its fp32 row sum, and O^T = V^T P^T in 16-key
 // steps.  o receives O^T unnormalised (block hb, register r = hd row
@@ -52,14 +53,20 @@ __device__ __forceinline__ float short_attention(const T* sK, const T* sV,
       for (int c = 0; c < KC; ++c) Mfma<T>::mma(s[kb], Mfma<T>::load(kp + 16 * c), qf[c]);
     }
   }
-  // masks and the row max
+  // masks and the row max; keep() is evaluated for every key first (it may
+  // load: loads under the key < lim condition would be waited for one by one)
+  bool kp[NKB][16];
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) kp[kb][r] = keep(kb * 32 + 16 * (r >> 3) + 8 * hi + (r & 7));
   float mx = -INFINITY;
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int key = kb * 32 + 16 * (r >> 3) + 8 * hi + (r & 7);
-      const bool admit = key < lim && keep(key);
+      const bool admit = key < lim && kp[kb][r];
       s[kb][r] = admit ? s[kb][r] : -INFINITY;
       mx = fmaxf(mx, s[kb][r]);
     }
