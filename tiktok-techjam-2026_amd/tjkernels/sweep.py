@@ -22,6 +22,7 @@ Ablation variants (each against the full stack on the same workloads):
   * plain attention kernel (plan 1)      TJ_ATTN_PLAN=1
   * two-launch FFN (no single-launch)    TJ_FFN=gemm
   * fp32 compute (accuracy escalation)   TJ_COMPUTE_DTYPE=float32
+  * one-launch attention block (opt-in)  TJ_ATTN_BLOCK=1
 
 The report opens with the system it ran on (GPU, its architecture and CU
 count, ROCm / torch versions, host CPU and the cores the CPU baseline may
@@ -51,6 +52,7 @@ LEAVE_ONE = [
     ("plain attention kernel", {"TJ_ATTN_PLAN": "1"}),
     ("two-launch FFN", {"TJ_FFN": "gemm"}),
     ("fp32 compute", {"TJ_COMPUTE_DTYPE": "float32"}),
+    ("one-launch attention block", {"TJ_ATTN_BLOCK": "1"}),
 ]
 
 
