@@ -150,7 +150,7 @@ def test_override_and_env_knobs(monkeypatch):
     assert base.ffn == "gemm"  # d = 1024: the two-launch FFN
     small = plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev)
     assert small.cuda_graph  # launch-bound: replayed as a hipGraph
-    assert small.ffn == "fused"  # C2: one FFN launch per layer
+    assert small.ffn == "gemm"  # C2: two launches measured faster than the single-launch FFN
     tiny = plans_mod.select_plan(2, 64, 128, 4, 512, 2, True, torch.float32, dev)
     assert tiny.ffn == "fused" and tiny.compute_dtype == torch.float32  # C1
     big = plans_mod.select_plan(64, 4096, 1024, 16, 4096, 4, True, torch.bfloat16, dev)
@@ -171,6 +171,10 @@ def test_override_and_env_knobs(monkeypatch):
     p = plans_mod.select_plan(4, 2048, 1024, 16, 4096, 4, True, torch.bfloat16, dev)
     assert not p.pack_prefix and p.attn_plan == 1
     assert plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev).ffn == "gemm"
+    monkeypatch.setenv("TJ_FFN", "fused")
+    assert plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev).ffn == "fused"
+    monkeypatch.setenv("TJ_ATTN_BLOCK", "1")
+    assert plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev).attn_block
     assert plans_mod.Plan.from_json(p.to_json()) == p
 
 
