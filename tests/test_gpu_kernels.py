@@ -38,7 +38,7 @@ def _close(got, ref, rtol, atol):
 
 # ------------------------------------------------------------------ LayerNorm
 
-@pytest.mark.parametrize("n", [96, 128, 512, 768, 1024, 2048, 8192])
+@pytest.mark.parametrize("n", [96, 128, 512, 768, 1024, 1536, 2048, 8192])
 @pytest.mark.parametrize("res_dt,delta_dt,out_dt", [
     ("f32", None, "bf16"), ("bf16", None, "bf16"), ("f32", "bf16", "bf16"),
     ("f32", "f16", "f16"), ("f16", None, "f16"), ("f32", "f32", "f32"), ("f32", None, "f32"),

@@ -331,6 +331,16 @@ static int launch_ln(const void* res, int64_t ld_res, const void* delta, int64_t
     else TJK_LN_LAUNCH(MC, false);                        \
     return check_launch("tjk_add_layernorm");             \
   }
+  // widths of 3 and 6 chunks per lane (d = 768, 1536: C3's model width) run
+  // without per-chunk guards too
+  if (nch == 64 * 3) {
+    TJK_LN_LAUNCH(3, true);
+    return check_launch("tjk_add_layernorm");
+  }
+  if (nch == 64 * 6) {
+    TJK_LN_LAUNCH(6, true);
+    return check_launch("tjk_add_layernorm");
+  }
   TJK_LN_CASE(1)
   TJK_LN_CASE(2)
   TJK_LN_CASE(4)
