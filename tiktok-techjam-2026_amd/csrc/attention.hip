@@ -537,8 +537,16 @@ constexpr int kFaSc1 = 16, kFaSc0Sc1 = 17;
 constexpr int kFaSpinLimit = 1 << 20;  // polls of a split item's flag before giving up (>= 0.1 s)
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-template <typename T, int HDP, bool KEYMASK, bool FULLHD>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ? 2 : 1, HDP <= 64 ? 2 : 1))) void flash_pipe_kernel(
+// NW waves per workgroup own BMQ = 32 NW queries.  NW = 4 (two workgroups
+// per CU at head_dim <= 64, one above).  NW = 8 is the head_dim-128 grid
+// variant: the LDS ring (143 KB) allows one workgroup per CU, so 8 waves
+// put two waves on each SIMD where 4 would leave one -- the second wave's
+// MFMAs and softmax fill the first one's stalls, and every K / V tile staged
+// into LDS serves 256 queries instead of 128.  Its K and V fragments are
+// read just before use (in two halves for S) to stay within the 256
+// registers two waves per SIMD leave each wave.
+template <typename T, int HDP, bool KEYMASK, bool FULLHD, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 64 || NW == 8 ? 2 : 1, HDP <= 64 || NW == 8 ? 2 : 1))) void flash_pipe_kernel(
     const T* __restrict__ qkv, int64_t sb, int64_t ss, int64_t sc, int64_t sh,
     T* __restrict__ out, int64_t ld_out, int B, int S, int H, int hd, float scale_log2,
     int causal, const int32_t* __restrict__ lengths, const uint8_t* __restrict__ key_mask,
@@ -546,12 +554,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
     const int4* __restrict__ work, float* __restrict__ partials, int* __restrict__ flags, int n_slots,
     int grp) {
   static_assert(sizeof(T) == 2, "2-byte element types only");
-  constexpr int BMQ = 128, BNK = 64, NST = 4, VEC = 8;
+  static_assert(NW == 4 || (NW == 8 && HDP == 128), "8 waves for head_dim 128 only");
+  constexpr int NT = 64 * NW, BMQ = 32 * NW, BNK = 64, NST = 4, VEC = 8;
+  constexpr bool LEAN = NW == 8;  // fragments read just before use
   constexpr int LDK = HDP + VEC, LDV = BNK + VEC;
   constexpr int KC = HDP / 16, HB = HDP / 32, CH = HDP / VEC;
   constexpr int KITEMS = BNK * CH, VITEMS = (BNK / 2) * CH;
-  constexpr int KPT = KITEMS / 256, VPT = (VITEMS + 255) / 256;
-  static_assert(KITEMS % 256 == 0, "K tile must split evenly over 256 threads");
+  constexpr int KPT = KITEMS / NT, VPT = (VITEMS + NT - 1) / NT;
+  static_assert(KITEMS % NT == 0, "K tile must split evenly over the threads");
 
   __shared__ __attribute__((aligned(16))) T sK[NST][BNK * LDK];
   __shared__ __attribute__((aligned(16))) T sV[NST][HDP * LDV];
@@ -650,14 +660,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
         __builtin_amdgcn_make_buffer_rsrc((void*)(qbase + 2 * sc + t_elems), (short)0, nrec, 0x00020000);
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
-      const int it = tid + i * 256, key = it / CH, c = it % CH;
+      const int it = tid + i * NT, key = it / CH, c = it % CH;
       const uint32_t off = (uint32_t)key * row_bytes + (uint32_t)(c * 16);
       uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsk, off, 0, 0));
       rk[i] = (FULLHD || c * VEC < hd) ? v : make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
-      const int it = tid + i * 256;
+      const int it = tid + i * NT;
       const int p = it % (BNK / 2), c = it / (BNK / 2);
       const uint32_t off = (uint32_t)(2 * p) * row_bytes + (uint32_t)(c * 16);
       uint4 v0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsv, off, 0, 0));
@@ -680,13 +690,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
     }
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
-      const int it = tid + i * 256, key = it / CH, c = it % CH;
+      const int it = tid + i * NT, key = it / CH, c = it % CH;
       *reinterpret_cast<uint4*>(&sK[st][key * LDK + c * VEC]) = rk[i];
     }
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
-      const int it = tid + i * 256;
-      if (VITEMS % 256 == 0 || it < VITEMS) {
+      const int it = tid + i * NT;
+      if (VITEMS % NT == 0 || it < VITEMS) {
         const int p = it % (BNK / 2), c = it / (BNK / 2);
         PairPack<T>::write(&sV[st][(c * VEC) * LDV + 2 * p], LDV, rv0[i], rv1[i]);
       }
@@ -837,6 +847,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
   // here too, so their LDS latency hides behind the exponentials.
   auto qk_exp = [&](int st, f32x16 (&snext)[2], const f32x16 (&scur_)[2], Frag (&pf)[4], int vst,
                     Frag (&vf)[HB][4]) __attribute__((always_inline)) -> float {
+    if constexpr (LEAN) {
+      // K fragments in two halves of the head dimension, V read in pv
+      constexpr int KH = KC / 2;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) snext[kb][r] = 0.f;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        Frag kf[KH][2];
+#pragma unroll
+        for (int c = 0; c < KH; ++c)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+            kf[c][kb] = Mfma<T>::load(&sK[st][(kb * 32 + krow) * LDK + 8 * hi] + 16 * (half * KH + c));
+#pragma unroll
+        for (int c = 0; c < KH; ++c)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb) Mfma<T>::mma(snext[kb], kf[c][kb], qf[half * KH + c]);
+      }
+      const float lt = exp_pack(scur_, pf);
+#pragma unroll
+      for (int i = 0; i < 2 * KC; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);
+      }
+      (void)vst;
+      (void)vf;
+      return lt;
+    }
     Frag kf[KC][2];
 #pragma unroll
     for (int c = 0; c < KC; ++c)
@@ -889,12 +929,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
     }
     l_run += lt;
   };
-  // O += V^T P^T from the fragments qk_exp read
-  auto pv = [&](const Frag (&vf)[HB][4], const Frag (&pf)[4]) __attribute__((always_inline)) {
+  // O += V^T P^T from the fragments qk_exp read (LEAN: read here, from slot vst)
+  auto pv = [&](const Frag (&vf)[HB][4], const Frag (&pf)[4], int vst) __attribute__((always_inline)) {
+    if constexpr (LEAN) {
 #pragma unroll
-    for (int stp = 0; stp < 4; ++stp)
+      for (int stp = 0; stp < 4; ++stp)
 #pragma unroll
-      for (int hb = 0; hb < HB; ++hb) Mfma<T>::mma(o[hb], vf[hb][stp], pf[stp]);
+        for (int hb = 0; hb < HB; ++hb)
+          Mfma<T>::mma(o[hb], Mfma<T>::load(&sV[vst][(hb * 32 + l32) * LDV + 8 * hi] + 16 * stp), pf[stp]);
+    } else {
+#pragma unroll
+      for (int stp = 0; stp < 4; ++stp)
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb) Mfma<T>::mma(o[hb], vf[hb][stp], pf[stp]);
+    }
   };
 
   // Ring invariant at the top of step t: LDS slots of tiles t and t+1 hold
@@ -932,7 +980,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HDP <= 64 ?
     Frag vf[HB][4];
     const float lt = qk_exp((j + 1) & (NST - 1), sn, sc, pf, j, vf);
     settle(sc, pf, lt);
-    pv(vf, pf);
+    pv(vf, pf, j);
     __syncthreads();
   };
   // four tiles per trip (one turn of the ring), scores ping-pong scur <-> salt
@@ -1113,7 +1161,7 @@ static int launch_sched(const void* qkv, int64_t ss, int64_t sc, int64_t sh, voi
     hipLaunchKernelGGL(clear_words_kernel, dim3(1), dim3(256), 0, st, flags - 1, n_slots + 1);
   }
 #define TJK_PIPE_SCHED(FULL)                                                                                  \
-  hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, false, FULL>), dim3((unsigned)n_work), dim3(256), 0, st,      \
+  hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, false, FULL, 4>), dim3((unsigned)n_work), dim3(256), 0, st,   \
                      (const T*)qkv, (int64_t)0, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, \
                      (const int32_t*)nullptr, (const uint8_t*)nullptr, cu_seqlens, 0,                         \
                      reinterpret_cast<const int4*>(work), partials, flags, n_slots, 1)
@@ -1127,7 +1175,11 @@ static int launch_pipe(const void* qkv, int64_t sb, int64_t ss, int64_t sc, int6
                        int64_t ld_out, int B, int S, int H, int hd, float scale_log2, int causal,
                        const int32_t* lengths, const uint8_t* key_mask, const int32_t* cu_seqlens,
                        hipStream_t st) {
-  const int nqb = (S + 127) / 128;
+  // head_dim 128 without a key mask: 8 waves and 256 queries per workgroup
+  // (see flash_pipe_kernel; with a key mask that variant would spill)
+  constexpr int NW8 = HDP == 128 ? 8 : 4;
+  const int nw = key_mask == nullptr ? NW8 : 4;
+  const int nqb = (S + 32 * nw - 1) / (32 * nw);
   const int64_t nblk = (int64_t)nqb * B * H;
   if (nblk > INT32_MAX) return fail(TJK_EUNSUPPORTED, "tjk_flash_fwd: grid too large");
   // (b, h) pairs per group: all of them while their K / V fit in about half
@@ -1137,14 +1189,14 @@ static int launch_pipe(const void* qkv, int64_t sb, int64_t ss, int64_t sc, int6
   const int64_t kv_pair = (int64_t)S * hd * 2 * (int64_t)sizeof(T);
   const int64_t fit = (int64_t)128 * 1024 * 1024 / (kv_pair > 0 ? kv_pair : 1);
   const int grp = (int)std::max<int64_t>(std::min<int64_t>(B * H, std::max<int64_t>(fit, 8)), 1);
-#define TJK_PIPE(KM, FULL)                                                                                     \
-  hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, KM, FULL>), dim3((unsigned)nblk), dim3(256), 0, st, (const T*)qkv, \
-                     sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, lengths, key_mask,          \
-                     cu_seqlens, nqb, (const int4*)nullptr, (float*)nullptr, (int*)nullptr, 0, grp)
+#define TJK_PIPE(KM, FULL, NWV)                                                                                \
+  hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, KM, FULL, NWV>), dim3((unsigned)nblk), dim3(64 * NWV), 0, st,   \
+                     (const T*)qkv, sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, lengths,  \
+                     key_mask, cu_seqlens, nqb, (const int4*)nullptr, (float*)nullptr, (int*)nullptr, 0, grp)
   if (key_mask != nullptr) {
-    if (hd == HDP) TJK_PIPE(true, true); else TJK_PIPE(true, false);
+    if (hd == HDP) TJK_PIPE(true, true, 4); else TJK_PIPE(true, false, 4);
   } else {
-    if (hd == HDP) TJK_PIPE(false, true); else TJK_PIPE(false, false);
+    if (hd == HDP) TJK_PIPE(false, true, NW8); else TJK_PIPE(false, false, NW8);
   }
 #undef TJK_PIPE
   return check_launch("tjk_flash_fwd");
@@ -1424,7 +1476,7 @@ extern "C" int tjk_flash_sched_occupancy(int head_dim, int dtype) {
   int blocks = 0;
   hipError_t e = hipErrorInvalidValue;
   const bool h16 = dtype == TJK_F16;
-#define TJK_OCC(TT, HDP) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, flash_pipe_kernel<TT, HDP, false, true>, 256, 0)
+#define TJK_OCC(TT, HDP) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, flash_pipe_kernel<TT, HDP, false, true, 4>, 256, 0)
   if (head_dim <= 32) { if (h16) TJK_OCC(f16, 32); else TJK_OCC(bf16, 32); }
   else if (head_dim <= 64) { if (h16) TJK_OCC(f16, 64); else TJK_OCC(bf16, 64); }
   else { if (h16) TJK_OCC(f16, 128); else TJK_OCC(bf16, 128); }
