@@ -2,6 +2,7 @@
 plan dispatcher, the module skeleton, the engine's guards, mask
 classification, and graph-capture failure handling."""
 
+import csv
 import json
 import re
 from pathlib import Path
@@ -430,3 +431,42 @@ def test_gemm_tile_classes_follow_the_library_table():
     assert tiles.k_class(128, 512, 2048, torch.bfloat16) == 2   # C2 FFN2: launch-bound
     assert tiles.k_class(5430, 4096, 1024, torch.bfloat16) == 1  # C4 FFN1
     assert tiles.candidates(96, 512, 128, torch.float32) == tiles.CANDIDATES_32
+
+
+def test_rocprof_summary_groups_forwards_by_rows_and_kernels(tmp_path):
+    """The profile summarizer labels each launch of a forward by position
+    and keeps forwards of the same rows through different kernels (the
+    bench's timed forward and its masked comparison run) in separate
+    groups, with per-label averages over each group's forwards only."""
+    from tjkernels import rocprof_summary as rs
+    names = {
+        "ln_first": "_ZN3tjk20add_layernorm_kernelIDF16bDF16bDF16bLi4ELb1EE",
+        "gemm_qkv": "_ZN3tjk15gemm_dtl_kernelIDF16bLi192ELi384EE",
+        "gemm_out_residual": "_ZN3tjk15gemm_dtl_kernelIDF16bLi96ELi128EE",
+        "add_layernorm": "_ZN3tjk20add_layernorm_kernelIffDF16bLi4ELb1EE",
+        "gemm_ffn1_gelu": "_ZN3tjk15gemm_dtl_kernelIDF16bLi192ELi128EE",
+        "gemm_ffn2_residual": "_ZN3tjk15gemm_dtl_kernelIDF16bLi192ELi128EE",
+        "ln_final": "_ZN3tjk20add_layernorm_kernelIffDF16bLi4ELb1EE",
+    }
+    rows, t = [], 0
+    for attn, dur in (("_ZN3tjk17flash_pipe_kernelIDF16bLi64E", 10), ("_ZN3tjk16flash_fwd_kernelIDF16bLi64E", 30),
+                      ("_ZN3tjk17flash_pipe_kernelIDF16bLi64E", 12)):
+        for lab in rs._labels(1):
+            name = attn if lab == "flash_attention" else names[lab]
+            d = dur if lab == "flash_attention" else 5
+            rows.append({"Kernel_Name": name, "Start_Timestamp": str(t), "End_Timestamp": str(t + d * 1000),
+                         "Grid_Size_X": "4096", "Workgroup_Size_X": "256"})
+            t += d * 1000 + 100
+    trace = tmp_path / "k_kernel_trace.csv"
+    with open(trace, "w", newline="") as fh:
+        w = csv.DictWriter(fh, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    out = rs.summarize(str(trace), layers=1)
+    blocks = [b for b in out.split("\n\n") if b.startswith("forward group")]
+    assert len(blocks) == 2
+    pipe = next(b for b in blocks if "flash_pipe" in b)
+    masked = next(b for b in blocks if "flash_fwd" in b)
+    assert "2 forwards" in pipe and "1 forwards" in masked
+    attn_line = next(line for line in pipe.splitlines() if line.startswith("flash_attention"))
+    assert float(attn_line.split()[2]) == 11.0  # (10 + 12) / 2, the masked run's 30 kept out

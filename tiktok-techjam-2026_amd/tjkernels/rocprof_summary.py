@@ -11,9 +11,11 @@ forward: the forward's launch sequence is fixed (first LayerNorm, then per
 layer QKV GEMM, attention, out-proj GEMM, and either LayerNorm + FFN1 GEMM +
 FFN2 GEMM or the single-launch FFN, LayerNorm, and the final LayerNorm), so
 every complete sequence that starts with the first LayerNorm (the one
-reading the model-dtype input) is split into labelled launches.  Sequences are grouped by the first LayerNorm's grid
-(the packed forward has fewer rows than the all-rows one) and each group is
-reported separately.  HBM bytes per launch are FETCH_SIZE and WRITE_SIZE
+reading the model-dtype input) is split into labelled launches.  Sequences
+are grouped by the first LayerNorm's grid (the packed forward has fewer rows
+than the all-rows one) and by their kernel names (a forward of the same rows
+through other kernels, such as the bench's masked comparison run), and each
+group is reported separately.  HBM bytes per launch are FETCH_SIZE and WRITE_SIZE
 (KiB per dispatch) scaled by what the same counters read for the bench's
 plain 256 MiB copy (``__amd_rocclr_copyBuffer`` of 268435456 bytes read and
 written).  ``--pmc`` takes ``*_counter_collection.csv`` files of runs with
@@ -77,10 +79,13 @@ def _tjk(name: str) -> bool:
     return GEMM in name or FLASH in name or LN in name or FFN in name
 
 
-def _forwards(rows: List[dict], layers: int) -> Dict[int, List[List[Tuple[str, dict]]]]:
-    """{first-LN grid: [forward as [(label, row)]]} from dispatch-ordered rows."""
+def _forwards(rows: List[dict], layers: int) -> Dict[Tuple, List[List[Tuple[str, dict]]]]:
+    """{(first-LN grid, kernel names): [forward as [(label, row)]]} from
+    dispatch-ordered rows.  The names split forwards of one grid that run
+    different kernels (C5's timed forward and the bench's masked comparison
+    run have the same rows)."""
     tjk = [r for r in rows if _tjk(r["Kernel_Name"])]
-    out: Dict[int, List[List[Tuple[str, dict]]]] = collections.defaultdict(list)
+    out: Dict[Tuple, List[List[Tuple[str, dict]]]] = collections.defaultdict(list)
     i = 0
     while i < len(tjk):
         matched = False
@@ -89,7 +94,7 @@ def _forwards(rows: List[dict], layers: int) -> Dict[int, List[List[Tuple[str, d
                 seq = tjk[i:i + len(labels)]
                 if (len(seq) == len(labels) and all(_kind_ok(lab, r["Kernel_Name"]) for lab, r in zip(labels, seq))
                         and not any(_is_first_ln(r["Kernel_Name"]) for r in seq[1:])):
-                    out[_grid(seq[0])].append(list(zip(labels, seq)))
+                    out[(_grid(seq[0]), tuple(r["Kernel_Name"] for r in seq))].append(list(zip(labels, seq)))
                     i += len(labels)
                     matched = True
                     break
@@ -169,7 +174,7 @@ def summarize(trace: str, layers: int = 4, fetch: Optional[str] = None,
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
     groups = _forwards(rows, layers)
     lines = []
-    for grid, fwds in sorted(groups.items()):
+    for (grid, _), fwds in sorted(groups.items()):
         per: Dict[str, List[float]] = collections.defaultdict(list)
         totals = []
         for f in fwds:
