@@ -1327,9 +1327,9 @@ extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s
   // with two key splits per query group (8 waves, merged through LDS).
   // Measured on MI355X (bf16): at hd <= 64 plan 0 is fastest at every
   // length (causal 4 x 2048: 54 vs 60 us; S = 32768: 944 vs 790 TFLOP/s);
-  // at hd 128 plan 1 up to S = 2048 (causal 4 x 2048: 112.5 vs 117.9 us)
-  // and plan 0 from S = 4096 (causal 2 x 4096: 192 vs 197 us, 2 x 8192:
-  // 671 vs 720 us); plans 2 and 3 were slower on every BASELINE shape.
+  // at hd 128 too since its 8-wave workgroups (causal 16 x 512: 50.5 vs
+  // 53.0 us, 4 x 2048: 95.1 vs 122.6 us, 2 x 8192: 615 vs 743 us); plans 2
+  // and 3 were slower on every BASELINE shape.
   // With a key mask plan 0 runs every tile through its masked
   // (unpipelined) loop: plan 1 from S = 2048 (padded C4 with a per-key
   // mask: 129 vs 168 us).  A sequence of one 128-query block has only
@@ -1342,7 +1342,7 @@ extern "C" int tjk_flash_fwd(const void* qkv, int64_t stride_b, int64_t stride_s
     if (seq <= 128)
       plan_id = 4;
     else
-      plan_id = (pipe_ok && (key_mask != nullptr ? seq < 2048 : (head_dim <= 64 || seq >= 4096))) ? 0 : 1;
+      plan_id = (pipe_ok && (key_mask == nullptr || seq < 2048)) ? 0 : 1;
   }
   if (plan_id == 0 && !pipe_ok) plan_id = 1;
   const float scale_log2 = scale * 1.4426950408889634f;
