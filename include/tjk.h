@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define TJK_ABI_VERSION 5
+#define TJK_ABI_VERSION 6
 
 /* dtypes */
 #define TJK_F32 0
@@ -69,15 +69,21 @@ const char* tjk_last_error_string(void);
 /*
  * Fused residual-add + LayerNorm over rows of length n.
  *   x   = res (+ delta)                       computed in fp32
- *   res_out = x            (if res_out != NULL; may alias res when res is fp32)
+ *   res_out = x            (if res_out != NULL), stored in res_out_dtype:
+ *           fp32, or rounded to fp16 / bf16 (a 2-byte residual stream, the
+ *           reference's Plan.residual_dtype, tjkernels/plans.py:33-36; the
+ *           LayerNorm below still normalises the unrounded fp32 x, as the
+ *           reference's kernel does, tjkernels/kernels/layernorm.py:50-60).
+ *           res_out may alias res only in place: same dtype and leading
+ *           dimension, no row_index.
  *   out = (x - mean) * rsqrt(var + eps) * gamma + beta, biased variance,
  *         written in out_dtype; rows whose row_mask byte is 0 are written as 0
  *         (row_mask may be NULL, indexed by row).
  * row_index (may be NULL) makes the call a gather / scatter over `rows`
  * output rows: output row r reads res / delta row row_index[r]; a negative
  * index writes an all-zero output row and leaves res_out's row untouched.
- * res_out must not alias res when row_index is given.
- * res_dtype, delta_dtype, out_dtype in {TJK_F32, TJK_F16, TJK_BF16};
+ * res_dtype, delta_dtype, res_out_dtype, out_dtype in
+ * {TJK_F32, TJK_F16, TJK_BF16};
  * delta may be NULL.  Requires n % 4 == 0, n <= 8192, 8-byte aligned rows.
  * delta_splits > 1 (fp32 delta, n <= 1024): delta is the sum of
  * delta_splits slices delta_split_stride elements apart (the split partials
@@ -88,7 +94,7 @@ const char* tjk_last_error_string(void);
 int tjk_add_layernorm(const void* res, int res_dtype, int64_t ld_res,
                       const void* delta, int delta_dtype, int64_t ld_delta,
                       int delta_splits, int64_t delta_split_stride,
-                      float* res_out, int64_t ld_res_out,
+                      void* res_out, int res_out_dtype, int64_t ld_res_out,
                       void* out, int out_dtype, int64_t ld_out,
                       const float* gamma, const float* beta,
                       int64_t rows, int64_t n, float eps,

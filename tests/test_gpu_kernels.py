@@ -766,6 +766,78 @@ def test_add_layernorm_split_delta(device, n, splits):
             _close(out2[r:r + 1], ref[src:src + 1], 2e-5, 1e-5)
 
 
+@pytest.mark.parametrize("n", [128, 1024, 1536, 2048])
+@pytest.mark.parametrize("res_dt,delta_dt,ro_dt", [
+    ("bf16", None, "f16"), ("f16", "f16", "f16"), ("f16", "bf16", "f16"), ("bf16", "bf16", "bf16"),
+    ("f16", "f32", "f16"), ("f32", "bf16", "bf16"),
+])
+def test_add_layernorm_two_byte_residual(device, n, res_dt, delta_dt, ro_dt):
+    """A 2-byte residual stream (the reference's residual_dtype knob): the
+    stored residual is the fp32 sum res + delta rounded once to its dtype,
+    bit for bit, and the output is the LayerNorm of the unrounded sum (as
+    the reference's kernel normalises its fp32 x, layernorm.py:50-60)."""
+    rows = 37
+    g = _gen(n + 3)
+    res = (torch.randn(rows, n, generator=g) * 3 + 0.5).to(DT[res_dt])
+    delta = None if delta_dt is None else torch.randn(rows, n, generator=g).to(DT[delta_dt])
+    gamma, beta = torch.randn(n, generator=g), torch.randn(n, generator=g)
+    x32 = res.float() + (0 if delta is None else delta.float())
+    ref = oracle.layer_norm(res.double() + (0 if delta is None else delta.double()), gamma.double(),
+                            beta.double(), 1e-5)
+    out = torch.empty(rows, n, dtype=torch.bfloat16, device=device)
+    res_out = torch.full((rows, n), float("nan"), dtype=DT[ro_dt], device=device)
+    ops.add_layernorm(res.to(device), None if delta is None else delta.to(device), gamma.to(device),
+                      beta.to(device), 1e-5, out, res_out=res_out)
+    torch.cuda.synchronize()
+    assert torch.equal(res_out.cpu(), x32.to(DT[ro_dt]))
+    _close(out, ref, OUT_RTOL[torch.bfloat16], 4e-3)
+    # in place (res_out aliases res) when they share the dtype
+    if ro_dt == res_dt:
+        res_d = res.to(device)
+        ops.add_layernorm(res_d, None if delta is None else delta.to(device), gamma.to(device),
+                          beta.to(device), 1e-5, out, res_out=res_d)
+        torch.cuda.synchronize()
+        assert torch.equal(res_d.cpu(), x32.to(DT[ro_dt]))
+
+
+def test_add_layernorm_two_byte_residual_split_delta(device):
+    """Split fp32 partials added to an fp16 residual in place: the fixed
+    summation order, then one rounding of the stored residual."""
+    n, rows, splits = 512, 33, 8
+    g = _gen(99)
+    res = torch.randn(rows, n, generator=g).to(torch.float16)
+    parts = torch.randn(splits, rows, n, generator=g)
+    gamma, beta = torch.randn(n, generator=g), torch.randn(n, generator=g)
+    acc = None
+    q = (splits + 3) // 4
+    for grp in range(4):
+        part = parts[grp * q].clone()
+        for s_ in range(grp * q + 1, grp * q + q):
+            part = part + parts[s_]
+        acc = part if acc is None else acc + part
+    x32 = res.float() + acc
+    res_d = res.to(device)
+    out = torch.empty(rows, n, dtype=torch.float16, device=device)
+    ops.add_layernorm(res_d, parts.to(device), gamma.to(device), beta.to(device), 1e-5, out, res_out=res_d)
+    torch.cuda.synchronize()
+    assert torch.equal(res_d.cpu(), x32.to(torch.float16))
+    ref = oracle.layer_norm(x32.double(), gamma.double(), beta.double(), 1e-5)
+    _close(out, ref, OUT_RTOL[torch.float16], 1e-3)
+
+
+def test_add_layernorm_rejects_cross_dtype_alias(device):
+    """Writing the residual in place in another dtype (or with a row index)
+    would overwrite bytes of rows other waves still read: rejected before
+    any launch."""
+    n, rows = 256, 4
+    buf = torch.zeros(rows, n, dtype=torch.float32, device=device)
+    gamma, beta = torch.ones(n, device=device), torch.zeros(n, device=device)
+    out = torch.empty(rows, n, dtype=torch.float16, device=device)
+    as16 = buf.view(torch.float16)[:, :n]
+    with pytest.raises(ops.TjkError, match="alias"):
+        ops.add_layernorm(buf, None, gamma, beta, 1e-5, out, res_out=as16)
+
+
 # ------------------------------------------------------------ attention block
 
 def _block_case(g, lengths, d, dt):

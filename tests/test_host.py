@@ -37,13 +37,19 @@ def test_abi_rejects_bad_arguments_without_launching():
     assert b"null" in lib.tjk_last_error_string()
     assert lib.tjk_flash_fwd(None, 0, 0, 0, 0, None, 0, 1, 4, 1, 12, 0.5, 1, None, None,
                              None, _lib.BF16, -1, None) < 0
-    assert lib.tjk_add_layernorm(None, 0, 8, None, 0, 0, 1, 0, None, 0, None, 0, 8, None, None,
+    assert lib.tjk_add_layernorm(None, 0, 8, None, 0, 0, 1, 0, None, 0, 0, None, 0, 8, None, None,
                                  2, 6, 1e-5, None, None, None) < 0
     assert b"null pointer" in lib.tjk_last_error_string()
     # split deltas need a stride that keeps the slices apart
     fake = 1 << 20  # never dereferenced: the call is rejected first
-    assert lib.tjk_add_layernorm(fake, 0, 8, fake, 0, 8, 4, 8, None, 0, fake, 0, 8, fake, fake,
+    assert lib.tjk_add_layernorm(fake, 0, 8, fake, 0, 8, 4, 8, None, 0, 0, fake, 0, 8, fake, fake,
                                  2, 8, 1e-5, None, None, None) == _lib.EINVAL
+    # the residual is written in place only in its own dtype and leading dimension
+    assert lib.tjk_add_layernorm(fake, _lib.F32, 8, None, 0, 0, 1, 0, fake, _lib.F16, 8, fake, 0, 8, fake,
+                                 fake, 2, 8, 1e-5, None, None, None) == _lib.EINVAL
+    assert b"alias" in lib.tjk_last_error_string()
+    assert lib.tjk_add_layernorm(fake, _lib.F16, 8, None, 0, 0, 1, 0, fake, 7, 8, fake, 0, 8, fake,
+                                 fake, 2, 8, 1e-5, None, None, None) == _lib.EINVAL  # bad res_out dtype
     # the single-launch FFN's shape gate (f / splits must be 128; d in {128, 256, 512})
     assert lib.tjk_ffn_supported(512, 2048, 16, _lib.F16) == 1
     assert lib.tjk_ffn_supported(128, 512, 4, _lib.F32) == 1
@@ -127,12 +133,20 @@ def test_plan_json_round_trip_and_table(tmp_path, monkeypatch):
 def test_plan_validation_rejects_fallback_backends():
     with pytest.raises(ValueError, match="only 'hip'"):
         Plan(attn="sdpa").validate()
-    with pytest.raises(ValueError, match="float32 residual"):
-        Plan(residual_dtype=torch.float16).validate()
+    with pytest.raises(ValueError, match="residual_dtype"):
+        Plan(residual_dtype=torch.int8).validate()
     with pytest.raises(ValueError, match="ffn="):
         Plan(ffn="torch").validate()
     Plan().validate()
     Plan(ffn="fused").validate()
+    # 2-byte residual streams (the reference's knob) run the deferred scheme:
+    # the GEMM epilogues add into an fp32 residual only
+    for rdt in (torch.float16, torch.bfloat16):
+        p = Plan(residual_dtype=rdt)
+        p.validate()
+        assert p.residual_epilogue and not p.epilogue_residual
+        assert Plan.from_json(p.to_json()) == p
+    assert Plan().epilogue_residual and not Plan(residual_epilogue=False).epilogue_residual
 
 
 def test_override_and_env_knobs(monkeypatch):
@@ -176,6 +190,11 @@ def test_override_and_env_knobs(monkeypatch):
     assert plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev).ffn == "fused"
     monkeypatch.setenv("TJ_ATTN_BLOCK", "1")
     assert plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev).attn_block
+    # TJ_RESIDUAL_DTYPE, plans.py:183-185 of the reference
+    assert plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev).residual_dtype == torch.float32
+    monkeypatch.setenv("TJ_RESIDUAL_DTYPE", "float16")
+    p = plans_mod.select_plan(4, 2048, 1024, 16, 4096, 4, True, torch.bfloat16, dev)
+    assert p.residual_dtype == torch.float16 and not p.epilogue_residual
     assert plans_mod.Plan.from_json(p.to_json()) == p
 
 

@@ -42,12 +42,29 @@ int check_launch(const char* what) {
   return TJK_OK;
 }
 
+// Stores chunk c (4 elements) of the updated residual row in the residual
+// stream's dtype: fp32, or a 2-byte type rounded to nearest even (the
+// reference's residual_dtype knob, tjkernels/plans.py:33-36).  ro_dtype is
+// the same for every lane of a launch, so the branch is uniform.
+__device__ __forceinline__ void store_res_chunk(void* row, int c, int ro_dtype, const float4& v) {
+  if (ro_dtype == TJK_F32)
+    reinterpret_cast<float4*>(row)[c] = v;
+  else if (ro_dtype == TJK_F16)
+    reinterpret_cast<typename Quad<f16>::raw*>(row)[c] = Quad<f16>::from(v);
+  else
+    reinterpret_cast<typename Quad<bf16>::raw*>(row)[c] = Quad<bf16>::from(v);
+}
+
+__device__ __forceinline__ void* res_row(void* base, int ro_dtype, int64_t row, int64_t ld) {
+  return static_cast<char*>(base) + row * ld * (ro_dtype == TJK_F32 ? 4 : 2);
+}
+
 // FULL: n == 256 * MAXCH, every lane's chunks in range (no per-chunk guards).
 template <typename TRes, typename TDelta, typename TOut, int MAXCH, bool FULL>
 __global__ __launch_bounds__(256) void add_layernorm_kernel(
     const TRes* res, int64_t ld_res,  // may alias res_out (in-place update)
     const TDelta* __restrict__ delta, int64_t ld_delta,
-    float* res_out, int64_t ld_res_out,
+    void* res_out, int ro_dtype, int64_t ld_res_out,
     TOut* __restrict__ out, int64_t ld_out,
     const float* __restrict__ gamma, const float* __restrict__ beta,
     int64_t rows, int n, float eps, const int32_t* __restrict__ row_index,
@@ -110,11 +127,11 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(
 
   float s = 0.f;
   if (res_out != nullptr) {
-    float4* orow = reinterpret_cast<float4*>(res_out + row * ld_res_out);
+    void* orow = res_row(res_out, ro_dtype, row, ld_res_out);
 #pragma unroll
     for (int j = 0; j < MAXCH; ++j) {
       const int c = lane + 64 * j;
-      if (FULL || c < nch) orow[c] = x[j];
+      if (FULL || c < nch) store_res_chunk(orow, c, ro_dtype, x[j]);
     }
   }
 #pragma unroll
@@ -165,7 +182,7 @@ template <typename TRes, typename TOut, int MAXCH>
 __global__ __launch_bounds__(256) void add_layernorm_parts_kernel(
     const TRes* res, int64_t ld_res,  // may alias res_out (in-place update)
     const float* __restrict__ parts, int64_t ld_parts, int n_parts, int64_t part_stride,
-    float* res_out, int64_t ld_res_out, TOut* __restrict__ out, int64_t ld_out,
+    void* res_out, int ro_dtype, int64_t ld_res_out, TOut* __restrict__ out, int64_t ld_out,
     const float* __restrict__ gamma, const float* __restrict__ beta, int n, float eps,
     const int32_t* __restrict__ row_index, const uint8_t* __restrict__ row_mask) {
   constexpr int PER = 32 / MAXCH;  // slices per load batch of one wave
@@ -249,10 +266,10 @@ __global__ __launch_bounds__(256) void add_layernorm_parts_kernel(
     if (lane + 64 * j >= nch) x[j] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   if (res_out != nullptr) {
-    float4* orow = reinterpret_cast<float4*>(res_out + row * ld_res_out);
+    void* orow = res_row(res_out, ro_dtype, row, ld_res_out);
 #pragma unroll
     for (int j = 0; j < MAXCH; ++j)
-      if (lane + 64 * j < nch) orow[lane + 64 * j] = x[j];
+      if (lane + 64 * j < nch) store_res_chunk(orow, lane + 64 * j, ro_dtype, x[j]);
   }
   float sm = 0.f;
 #pragma unroll
@@ -292,14 +309,14 @@ __global__ __launch_bounds__(256) void add_layernorm_parts_kernel(
 
 template <typename TRes, typename TOut>
 static int launch_ln_parts(const void* res, int64_t ld_res, const float* parts, int64_t ld_parts, int n_parts,
-                           int64_t part_stride, float* res_out, int64_t ld_res_out, void* out, int64_t ld_out,
+                           int64_t part_stride, void* res_out, int ro_dtype, int64_t ld_res_out, void* out, int64_t ld_out,
                            const float* gamma, const float* beta, int64_t rows, int n, float eps,
                            const int32_t* row_index, const uint8_t* row_mask, hipStream_t stream) {
   const int nch = n / 4;
   const dim3 grid((unsigned)rows), block(256);
 #define TJK_LNP(MC)                                                                                           \
   hipLaunchKernelGGL((add_layernorm_parts_kernel<TRes, TOut, MC>), grid, block, 0, stream, (const TRes*)res,   \
-                     ld_res, parts, ld_parts, n_parts, part_stride, res_out, ld_res_out, (TOut*)out, ld_out, gamma, \
+                     ld_res, parts, ld_parts, n_parts, part_stride, res_out, ro_dtype, ld_res_out, (TOut*)out, ld_out, gamma, \
                      beta, n, eps, row_index, row_mask)
   if (nch <= 64) TJK_LNP(1);
   else if (nch <= 128) TJK_LNP(2);
@@ -310,20 +327,20 @@ static int launch_ln_parts(const void* res, int64_t ld_res, const float* parts, 
 
 template <typename TRes, typename TDelta, typename TOut>
 static int launch_ln(const void* res, int64_t ld_res, const void* delta, int64_t ld_delta, int n_delta,
-                     int64_t delta_stride, float* res_out, int64_t ld_res_out, void* out, int64_t ld_out,
+                     int64_t delta_stride, void* res_out, int ro_dtype, int64_t ld_res_out, void* out, int64_t ld_out,
                      const float* gamma, const float* beta, int64_t rows, int n, float eps,
                      const int32_t* row_index, const uint8_t* row_mask, hipStream_t stream) {
   if constexpr (std::is_same<TDelta, float>::value) {
     if (n_delta > 1)
       return launch_ln_parts<TRes, TOut>(res, ld_res, (const float*)delta, ld_delta, n_delta, delta_stride, res_out,
-                                         ld_res_out, out, ld_out, gamma, beta, rows, n, eps, row_index, row_mask,
+                                         ro_dtype, ld_res_out, out, ld_out, gamma, beta, rows, n, eps, row_index, row_mask,
                                          stream);
   }
   const int nch = n / 4;
   dim3 grid((unsigned)((rows + 3) / 4)), block(256);
 #define TJK_LN_LAUNCH(MC, FULL)                                                                    \
   hipLaunchKernelGGL((add_layernorm_kernel<TRes, TDelta, TOut, MC, FULL>), grid, block, 0, stream,     \
-                     (const TRes*)res, ld_res, (const TDelta*)delta, ld_delta, res_out, ld_res_out, \
+                     (const TRes*)res, ld_res, (const TDelta*)delta, ld_delta, res_out, ro_dtype, ld_res_out, \
                      (TOut*)out, ld_out, gamma, beta, rows, n, eps, row_index, row_mask)
 #define TJK_LN_CASE(MC)                                   \
   if (nch <= 64 * MC) {                                   \
@@ -354,18 +371,18 @@ static int launch_ln(const void* res, int64_t ld_res, const void* delta, int64_t
 
 template <typename TRes, typename TDelta>
 static int dispatch_out(int out_dtype, const void* res, int64_t ld_res, const void* delta,
-                        int64_t ld_delta, int n_delta, int64_t delta_stride, float* res_out, int64_t ld_res_out, void* out,
+                        int64_t ld_delta, int n_delta, int64_t delta_stride, void* res_out, int ro_dtype, int64_t ld_res_out, void* out,
                         int64_t ld_out, const float* gamma, const float* beta, int64_t rows,
                         int n, float eps, const int32_t* row_index, const uint8_t* row_mask, hipStream_t stream) {
   switch (out_dtype) {
     case TJK_F32:
-      return launch_ln<TRes, TDelta, float>(res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ld_res_out, out, ld_out,
+      return launch_ln<TRes, TDelta, float>(res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ro_dtype, ld_res_out, out, ld_out,
                                             gamma, beta, rows, n, eps, row_index, row_mask, stream);
     case TJK_F16:
-      return launch_ln<TRes, TDelta, f16>(res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ld_res_out, out, ld_out,
+      return launch_ln<TRes, TDelta, f16>(res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ro_dtype, ld_res_out, out, ld_out,
                                           gamma, beta, rows, n, eps, row_index, row_mask, stream);
     case TJK_BF16:
-      return launch_ln<TRes, TDelta, bf16>(res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ld_res_out, out, ld_out,
+      return launch_ln<TRes, TDelta, bf16>(res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ro_dtype, ld_res_out, out, ld_out,
                                            gamma, beta, rows, n, eps, row_index, row_mask, stream);
   }
   return fail(TJK_EINVAL, "tjk_add_layernorm: bad out dtype %d", out_dtype);
@@ -373,19 +390,19 @@ static int dispatch_out(int out_dtype, const void* res, int64_t ld_res, const vo
 
 template <typename TRes>
 static int dispatch_delta(int delta_dtype, int out_dtype, const void* res, int64_t ld_res,
-                          const void* delta, int64_t ld_delta, int n_delta, int64_t delta_stride, float* res_out, int64_t ld_res_out,
+                          const void* delta, int64_t ld_delta, int n_delta, int64_t delta_stride, void* res_out, int ro_dtype, int64_t ld_res_out,
                           void* out, int64_t ld_out, const float* gamma, const float* beta,
                           int64_t rows, int n, float eps, const int32_t* row_index,
                           const uint8_t* row_mask, hipStream_t stream) {
   switch (delta_dtype) {
     case TJK_F32:
-      return dispatch_out<TRes, float>(out_dtype, res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ld_res_out, out,
+      return dispatch_out<TRes, float>(out_dtype, res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ro_dtype, ld_res_out, out,
                                        ld_out, gamma, beta, rows, n, eps, row_index, row_mask, stream);
     case TJK_F16:
-      return dispatch_out<TRes, f16>(out_dtype, res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ld_res_out, out,
+      return dispatch_out<TRes, f16>(out_dtype, res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ro_dtype, ld_res_out, out,
                                      ld_out, gamma, beta, rows, n, eps, row_index, row_mask, stream);
     case TJK_BF16:
-      return dispatch_out<TRes, bf16>(out_dtype, res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ld_res_out, out,
+      return dispatch_out<TRes, bf16>(out_dtype, res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ro_dtype, ld_res_out, out,
                                       ld_out, gamma, beta, rows, n, eps, row_index, row_mask, stream);
   }
   return fail(TJK_EINVAL, "tjk_add_layernorm: bad delta dtype %d", delta_dtype);
@@ -402,7 +419,7 @@ extern "C" const char* tjk_last_error_string(void) { return g_err; }
 extern "C" int tjk_add_layernorm(const void* res, int res_dtype, int64_t ld_res,
                                  const void* delta, int delta_dtype, int64_t ld_delta,
                                  int delta_splits, int64_t delta_split_stride,
-                                 float* res_out, int64_t ld_res_out,
+                                 void* res_out, int res_out_dtype, int64_t ld_res_out,
                                  void* out, int out_dtype, int64_t ld_out,
                                  const float* gamma, const float* beta,
                                  int64_t rows, int64_t n, float eps,
@@ -411,6 +428,9 @@ extern "C" int tjk_add_layernorm(const void* res, int res_dtype, int64_t ld_res,
   if (rows < 0 || n <= 0) return fail(TJK_EINVAL, "tjk_add_layernorm: bad shape rows=%lld n=%lld", (long long)rows, (long long)n);
   if (rows == 0) return TJK_OK;
   if (!res || !out || !gamma || !beta) return fail(TJK_EINVAL, "tjk_add_layernorm: null pointer");
+  if (res_out && res_out_dtype != TJK_F32 && res_out_dtype != TJK_F16 && res_out_dtype != TJK_BF16)
+    return fail(TJK_EINVAL, "tjk_add_layernorm: bad res_out dtype %d", res_out_dtype);
+  const int ro_dtype = res_out ? res_out_dtype : TJK_F32;
   if (n % 4 != 0) return fail(TJK_EUNSUPPORTED, "tjk_add_layernorm: n=%lld not a multiple of 4", (long long)n);
   if (n > 8192) return fail(TJK_EUNSUPPORTED, "tjk_add_layernorm: n=%lld exceeds 8192", (long long)n);
   if (ld_res < n || ld_out < n || (delta && ld_delta < n) || (res_out && ld_res_out < n))
@@ -421,14 +441,17 @@ extern "C" int tjk_add_layernorm(const void* res, int res_dtype, int64_t ld_res,
     // Chunks are 4 elements: 8-byte aligned for 2-byte types, 16 for fp32.
     const uintptr_t need_res = 4 * dtype_size(res_dtype) - 1, need_out = 4 * dtype_size(out_dtype) - 1;
     const uintptr_t need_delta = 4 * dtype_size(delta ? delta_dtype : res_dtype) - 1;
+    const uintptr_t need_ro = 4 * dtype_size(ro_dtype) - 1;
     if (((uintptr_t)res & need_res) || ((uintptr_t)out & need_out) || ((uintptr_t)delta & need_delta) ||
-        ((uintptr_t)res_out & 15) || ((uintptr_t)gamma & 15) || ((uintptr_t)beta & 15))
+        ((uintptr_t)res_out & need_ro) || ((uintptr_t)gamma & 15) || ((uintptr_t)beta & 15))
       return fail(TJK_EUNSUPPORTED, "tjk_add_layernorm: misaligned pointer");
   }
-  // A gather / scatter reads rows other than the one it writes: an
-  // in-place residual update would race with other rows' reads.
-  if (row_index && res_out && (const void*)res_out == res)
-    return fail(TJK_EINVAL, "tjk_add_layernorm: row_index with res_out aliasing res");
+  // A gather / scatter reads rows other than the one it writes, and a
+  // residual written in place in another dtype overwrites bytes of other
+  // rows: either would race with other rows' reads.
+  if (res_out && (const void*)res_out == res && (row_index || res_out_dtype != res_dtype || ld_res_out != ld_res))
+    return fail(TJK_EINVAL, "tjk_add_layernorm: res_out may alias res only in place (same dtype and leading "
+                "dimension, no row_index)");
   if (delta && (delta_splits < 1 || (delta_splits > 1 && (delta_split_stride < rows * ld_delta ||
                                                           delta_split_stride % 4 != 0))))
     return fail(TJK_EINVAL, "tjk_add_layernorm: delta_splits=%d needs a split stride >= rows x ld_delta, "
@@ -440,13 +463,13 @@ extern "C" int tjk_add_layernorm(const void* res, int res_dtype, int64_t ld_res,
   const int nd = delta ? delta_splits : 0;
   switch (res_dtype) {
     case TJK_F32:
-      return dispatch_delta<float>(dd, out_dtype, res, ld_res, delta, ld_delta, nd, delta_split_stride, res_out, ld_res_out, out,
+      return dispatch_delta<float>(dd, out_dtype, res, ld_res, delta, ld_delta, nd, delta_split_stride, res_out, ro_dtype, ld_res_out, out,
                                    ld_out, gamma, beta, rows, (int)n, eps, row_index, row_mask, s);
     case TJK_F16:
-      return dispatch_delta<f16>(dd, out_dtype, res, ld_res, delta, ld_delta, nd, delta_split_stride, res_out, ld_res_out, out,
+      return dispatch_delta<f16>(dd, out_dtype, res, ld_res, delta, ld_delta, nd, delta_split_stride, res_out, ro_dtype, ld_res_out, out,
                                  ld_out, gamma, beta, rows, (int)n, eps, row_index, row_mask, s);
     case TJK_BF16:
-      return dispatch_delta<bf16>(dd, out_dtype, res, ld_res, delta, ld_delta, nd, delta_split_stride, res_out, ld_res_out, out,
+      return dispatch_delta<bf16>(dd, out_dtype, res, ld_res, delta, ld_delta, nd, delta_split_stride, res_out, ro_dtype, ld_res_out, out,
                                   ld_out, gamma, beta, rows, (int)n, eps, row_index, row_mask, s);
   }
   return fail(TJK_EINVAL, "tjk_add_layernorm: bad res dtype %d", res_dtype);

@@ -20,7 +20,7 @@ MI355X specifics:
   candidates once per projection shape at run time (``tjkernels.tiles``),
   because with packed prefix-masked tokens the row count M of every
   projection follows the input lengths; ``tune_gemm`` remains as a tool;
-  the plan-level knobs (attention plan, residual epilogue, hipGraph) are
+  the plan-level knobs (attention plan, residual epilogue, hipGraph, residual dtype) are
   tuned by coordinate descent on whole-forward latency measured as the
   harness does (events on the current stream around the module call).
 """
@@ -178,6 +178,11 @@ def tune_workload(w: Workload, trials: int = 2, margin: float = 0.85, iters: int
     # coordinate descent over the plan-level knobs
     attn_plans = [0, 1, 3] + ([4] if w.seq <= 128 else [])
     knobs = [("attn_plan", attn_plans), ("residual_epilogue", [True, False]), ("cuda_graph", [True, False])]
+    if cur["plan"].compute_dtype != torch.float32:
+        # an fp16 residual stream, the reference's candidate
+        # (bench/autotune.py:88); not tried for fp32 compute, whose 1e-4
+        # budget a 2-byte residual cannot hold
+        knobs.append(("residual_dtype", [torch.float32, torch.float16]))
     if fused_ffn_ok(w.d_model, w.ffn_dim, cur["plan"].compute_dtype):
         knobs.insert(0, ("ffn", ["gemm", "fused"]))
     if attn_block_ok(w.seq, w.d_model, w.heads, cur["plan"].compute_dtype):

@@ -3,7 +3,8 @@
 An ``Engine`` lives on the module (set with ``object.__setattr__``, so the
 ``state_dict`` keeps the baseline's keys) and owns packed copies of the
 module's parameters, never the parameters themselves.  A forward is a
-pre-LN causal encoder over an fp32 residual stream ``res``:
+pre-LN causal encoder over a residual stream ``res`` (fp32 unless
+``Plan.residual_dtype`` says otherwise):
 
     res, h = x, LN1(x)                     layer 0: the first LayerNorm
     per layer:
@@ -23,7 +24,10 @@ pre-LN causal encoder over an fp32 residual stream ``res``:
 
 ``Plan.residual_epilogue=False`` writes the out-proj and FFN outputs in the
 compute dtype and lets the following LayerNorm add them, the reference's
-deferred-residual scheme (engine.py:232-264).
+deferred-residual scheme (engine.py:232-264).  A 2-byte ``residual_dtype``
+always runs that scheme (the GEMM epilogues add into fp32 only); the
+LayerNorms store the updated residual rounded to it, and the fused FFN's
+output goes through its partials buffer even unsplit.
 
 Masks (reference engine.py:131-158): NONE -- no mask or every token valid;
 PREFIX -- sequence b valid on its first len_b tokens; GENERAL -- anything
@@ -229,7 +233,7 @@ class Tiles(NamedTuple):
 class Workspace:
     """Activation buffers of one (B, S, plan), sized for every row."""
 
-    res: torch.Tensor                # [T, d] fp32 residual stream
+    res: torch.Tensor                # [T, d] residual stream (Plan.residual_dtype)
     h: torch.Tensor                  # [T, d] LayerNorm output
     qkv: torch.Tensor                # [T, 3d]
     ctx: torch.Tensor                # [T, d] attention output
@@ -332,7 +336,7 @@ class Engine:
 
     def _workspace(self, batch: int, seq: int, plan: Plan, splits: int, block: bool) -> Workspace:
         fused = plan.ffn == "fused"
-        key = (batch, seq, plan.compute_dtype, plan.residual_epilogue, fused, splits, block)
+        key = (batch, seq, plan.compute_dtype, plan.residual_dtype, plan.epilogue_residual, fused, splits, block)
         ws = self._workspaces.get(key)
         if ws is None:
             t, d, f = batch * seq, self.shape.d_model, self.shape.ffn_dim
@@ -341,10 +345,12 @@ class Engine:
             def buf(*dims, dtype=cdt):
                 return torch.empty(dims, dtype=dtype, device=dev)
 
-            ws = Workspace(res=buf(t, d, dtype=torch.float32), h=buf(t, d), qkv=buf(t, 3 * d), ctx=buf(t, d),
+            # the fused FFN adds into an fp32 residual itself when unsplit
+            use_parts = fused and (splits > 1 or plan.residual_dtype != torch.float32)
+            ws = Workspace(res=buf(t, d, dtype=plan.residual_dtype), h=buf(t, d), qkv=buf(t, 3 * d), ctx=buf(t, d),
                            mid=None if fused else buf(t, f),
-                           delta=None if plan.residual_epilogue else buf(t, d),
-                           parts=buf(splits, t, d, dtype=torch.float32) if fused and splits > 1 else None,
+                           delta=None if plan.epilogue_residual else buf(t, d),
+                           parts=buf(splits, t, d, dtype=torch.float32) if use_parts else None,
                            attn_parts=buf(self.shape.heads, t, d, dtype=torch.float32) if block else None)
             self._workspaces[key] = ws
         return ws
@@ -365,7 +371,7 @@ class Engine:
         longest = max(packing.lengths) if mode == MASK_PREFIX else seq
         block = (plan.attn_block and mode != MASK_GENERAL and rows > 0
                  and attn_block_ok(longest, d, shp.heads, cdt))
-        epi_res = ops.EPI_BIAS_RESIDUAL if plan.residual_epilogue else ops.EPI_BIAS
+        epi_res = ops.EPI_BIAS_RESIDUAL if plan.epilogue_residual else ops.EPI_BIAS
         tp = Tiles(
             qkv=-1 if block else tiles.gemm_plan(rows, 3 * d, d, cdt, ops.EPI_BIAS, plan.gemm_qkv),
             out=-1 if block else tiles.gemm_plan(rows, d, d, cdt, epi_res, plan.gemm_out),
@@ -377,7 +383,7 @@ class Engine:
                      key_mask=mask if mode == MASK_GENERAL else None, use_block=block, splits=splits)
         if fused:
             fw.pending = fw.view("parts")
-        elif not plan.residual_epilogue:
+        elif not plan.epilogue_residual:
             fw.pending = fw.view("delta")
         # Packed 2-byte attention of 129 to 2047 keys follows a longest-first
         # work list (attn_plan -1, or ATTN_SCHEDULED to force it); longer
@@ -396,7 +402,7 @@ class Engine:
 
     def _first(self, fw: Forward, x: torch.Tensor) -> None:
         """Layer-0 LN1: reads x (gathering the valid rows of a prefix mask),
-        writes the fp32 residual and h."""
+        writes the residual and h."""
         n1 = self.weights.blocks[0].norm1
         gather = fw.packing.gather if fw.packing is not None else None
         ops.add_layernorm(x.reshape(fw.batch * fw.seq, self.shape.d_model), None, n1.weight, n1.bias, n1.eps,
@@ -432,7 +438,7 @@ class Engine:
         # the attention output not yet in res: the attention block's
         # partials, or the deferred out-proj output
         attn_pending = fw.view("attn_parts") if fw.use_block else (
-            None if plan.residual_epilogue else fw.view("delta"))
+            None if plan.epilogue_residual else fw.view("delta"))
         if plan.ffn == "fused":
             parts = fw.view("parts")
             if attn_pending is None:
@@ -447,7 +453,7 @@ class Engine:
                         ln=ln)
             return
         mid = fw.view("mid")
-        if plan.residual_epilogue:
+        if plan.epilogue_residual:
             ops.add_layernorm(res, attn_pending, n2.weight, n2.bias, n2.eps, h,
                               res_out=res if attn_pending is not None else None)
             ops.gemm(h, blk.fc1.weight, blk.fc1.bias, mid, ops.EPI_BIAS_GELU, fw.tiles.fc1)
@@ -472,7 +478,7 @@ class Engine:
             else:
                 ops.gemm(h, blk.qkv.weight, blk.qkv.bias, fw.view("qkv"), ops.EPI_BIAS, fw.tiles.qkv)
                 self._attention(fw)
-                if self.plan.residual_epilogue:
+                if self.plan.epilogue_residual:
                     ops.gemm(ctx, blk.out.weight, blk.out.bias, res, ops.EPI_BIAS_RESIDUAL, fw.tiles.out)
                 else:
                     ops.gemm(ctx, blk.out.weight, blk.out.bias, fw.view("delta"), ops.EPI_BIAS, fw.tiles.out)

@@ -59,9 +59,10 @@ def add_layernorm(res: torch.Tensor, delta: Optional[torch.Tensor],
                   out: torch.Tensor, res_out: Optional[torch.Tensor] = None,
                   row_mask: Optional[torch.Tensor] = None,
                   row_index: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """x = res (+ delta) in fp32; res_out <- x (optional, fp32); out <- LN(x)
-    (rows with row_mask == 0 written as 0).  Mirrors fused_add_layernorm,
-    tjkernels/kernels/__init__.py:48-70.
+    """x = res (+ delta) in fp32; res_out <- x (optional; fp32, or rounded to
+    a 2-byte res_out, the reference's residual_dtype); out <- LN(x), of the
+    unrounded x (rows with row_mask == 0 written as 0).  Mirrors
+    fused_add_layernorm, tjkernels/kernels/__init__.py:48-70.
 
     With ``row_index`` (int32, one entry per output row) the call is a
     gather / scatter: output row r is computed from input row row_index[r],
@@ -85,8 +86,6 @@ def add_layernorm(res: torch.Tensor, delta: Optional[torch.Tensor],
             raise TjkError("row_index has more entries than out / res_out rows")
     elif out.shape[0] < rows or (res_out is not None and res_out.shape[0] < rows):
         raise TjkError("out / res_out have fewer rows than res")
-    if res_out is not None and res_out.dtype != torch.float32:
-        raise TjkError("res_out must be float32")
     if gamma.dtype != torch.float32 or beta.dtype != torch.float32:
         raise TjkError("gamma/beta must be float32")
     if row_mask is not None and (row_mask.dtype not in (torch.bool, torch.uint8)
@@ -97,7 +96,8 @@ def add_layernorm(res: torch.Tensor, delta: Optional[torch.Tensor],
         res.data_ptr(), _code(res), _rowmajor(res, "res"),
         _ptr(delta), _code(delta) if delta is not None else 0,
         _rowmajor(delta2, "delta") if delta is not None else 0, splits, split_stride,
-        _ptr(res_out), _rowmajor(res_out, "res_out") if res_out is not None else 0,
+        _ptr(res_out), _code(res_out) if res_out is not None else 0,
+        _rowmajor(res_out, "res_out") if res_out is not None else 0,
         out.data_ptr(), _code(out), _rowmajor(out, "out"),
         gamma.data_ptr(), beta.data_ptr(), rows, n, float(eps),
         _ptr(row_index), _ptr(row_mask), _stream(res))

@@ -14,8 +14,12 @@ Knobs, all naming HIP kernels of this build (there is no torch/SDPA backend
 to select, and the product path has no non-HIP fallback):
 
 * ``compute_dtype`` / ``residual_dtype``: GEMM / attention operand dtype and
-  the residual stream's dtype (fp32 only).  An fp32 model runs the IEEE fp32
-  plan, since only fp32 compute holds the 1e-4 budget of fp32 plans;
+  the residual stream's dtype.  An fp32 model runs the IEEE fp32 plan, since
+  only fp32 compute holds the 1e-4 budget of fp32 plans.  A 2-byte residual
+  stream (fp16 / bf16, the reference's knob, tjkernels/plans.py:33-36) runs
+  the deferred scheme whatever ``residual_epilogue`` says: the projections
+  write the compute dtype and each LayerNorm adds, normalises the fp32 sum and
+  stores the residual rounded (tjkernels/kernels/layernorm.py:50-60);
 * ``ffn``: ``"gemm"`` (two GEMM launches, GELU in the first one's epilogue,
   the [T, f] intermediate in HBM) or ``"fused"`` (one launch per layer with
   the intermediate in LDS and LayerNorm 2 inside, split over ``ffn_splits``
@@ -33,14 +37,15 @@ to select, and the product path has no non-HIP fallback):
   two eager LayerNorm launches around the replayed body;
 * ``residual_epilogue``: add the out-proj (and two-launch FFN) outputs into
   the fp32 residual in the GEMM epilogue instead of deferring them to the
-  next LayerNorm (the reference's scheme, engine.py:232-264);
+  next LayerNorm (the reference's scheme, engine.py:232-264); fp32 residual
+  only;
 * ``gemm_*`` / ``attn_plan``: force a tile or attention plan (-1: chosen
   at run time; attention 0-4 are the library's plans of tjk_flash_fwd,
   ``ATTN_SCHEDULED`` (5) the work-list kernel for packed sequences);
 * ``pack_prefix``: run only the valid tokens of prefix masks.
 
 Environment: ``TJ_NO_GRAPH``, ``TJ_WHOLE_GRAPH`` (0 / 1), ``TJ_ATTN_BLOCK`` (0 / 1), ``TJ_COMPUTE_DTYPE``,
-``TJ_DEFERRED_RESIDUAL``, ``TJ_NO_PACK``, ``TJ_ATTN_PLAN``, ``TJ_FFN`` (gemm | fused), ``TJ_FFN_SPLITS``;
+``TJ_RESIDUAL_DTYPE``, ``TJ_DEFERRED_RESIDUAL``, ``TJ_NO_PACK``, ``TJ_ATTN_PLAN``, ``TJ_FFN`` (gemm | fused), ``TJ_FFN_SPLITS``;
 ``TJ_GEMM_TUNE=0`` (tjkernels.tiles) skips the measured tile choice.
 Tuned keys carry the GPU architecture (``...@gfx950``).
 """
@@ -114,9 +119,14 @@ class Plan:
             kwargs[name] = value
         return cls(**kwargs)
 
+    @property
+    def epilogue_residual(self) -> bool:
+        """Whether the GEMM epilogues add into the residual (fp32 only)."""
+        return self.residual_epilogue and self.residual_dtype == torch.float32
+
     def validate(self) -> None:
-        if self.residual_dtype != torch.float32:
-            raise ValueError("only a float32 residual stream is implemented")
+        if self.residual_dtype not in NAME_BY_DTYPE:
+            raise ValueError(f"residual_dtype={self.residual_dtype}: one of {sorted(DTYPE_BY_NAME)}")
         if self.attn != "hip" or self.norm != "hip":
             raise ValueError(f"attn={self.attn!r} norm={self.norm!r}: only 'hip' kernels exist "
                              "(no torch/SDPA fallback in this build)")
@@ -233,6 +243,8 @@ def _env_adjusted(plan: Plan, d_model: int, ffn_dim: int) -> Plan:
         changes["attn_block"] = env["TJ_ATTN_BLOCK"] == "1"
     if env.get("TJ_COMPUTE_DTYPE") in DTYPE_BY_NAME:
         changes["compute_dtype"] = DTYPE_BY_NAME[env["TJ_COMPUTE_DTYPE"]]
+    if env.get("TJ_RESIDUAL_DTYPE") in DTYPE_BY_NAME:
+        changes["residual_dtype"] = DTYPE_BY_NAME[env["TJ_RESIDUAL_DTYPE"]]
     if env.get("TJ_DEFERRED_RESIDUAL") == "1":
         changes["residual_epilogue"] = False
     if env.get("TJ_NO_PACK") == "1":

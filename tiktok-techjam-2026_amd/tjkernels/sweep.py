@@ -185,7 +185,7 @@ def main(argv: Optional[List[str]] = None) -> int:
     ap.add_argument("--cpu", action="store_true", help="also time the CPU baseline (slow for C4/C5)")
     ap.add_argument("--ablation", default="", help="workloads for the leave-one-out ablation")
     ap.add_argument("--timeout", type=float, default=900.0, help="seconds per case")
-    ap.add_argument("--out", default=str(REPO / "gpurun_out" / "sweep"))
+    ap.add_argument("--out", default=str(REPO / "sweep_out"))
     ap.add_argument("--tag", default="main")
     args = ap.parse_args(argv)
     out = Path(args.out)
