@@ -320,8 +320,7 @@ def main() -> int:
         "wait_timeouts": wait_timeouts,
         "ffn": plan.ffn,
         # measured tile plan per projection shape (M bucket x N x K, epilogue)
-        "gemm_tiles": {f"{m}x{n}x{k}/epi{e}": p for (m, n, k, _, e), p in sorted(tiles.chosen().items(),
-                                                                              key=lambda kv: kv[0][:3])},
+        "gemm_tiles": tiles.describe(),
     }
     print(json.dumps(line))
     return 0

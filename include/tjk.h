@@ -28,6 +28,10 @@
  *                         shape gate ffn.py:103-110 -> tjk_ffn_supported)
  *   tjk_flash_fwd_sched <- the grid of (query block, b*h) programs of
  *                         tjkernels/kernels/attention.py:199-217
+ *   tjk_gemm_ln        <- fused_add_layernorm without a pending delta and
+ *                         the addmm after it: LN1 + QKV, tjkernels/engine.py:239-245;
+ *                         LN2 + the FFN's first GEMM, engine.py:249-253 with
+ *                         tjkernels/kernels/__init__.py:88
  *   tjk_attn_block     <- the QKV addmm, flash_attention and out-proj addmm
  *                         (tjkernels/engine.py:245-247) fused for sequences
  *                         of at most 128 tokens, the tiny-shape fusion of
@@ -43,7 +47,7 @@
 extern "C" {
 #endif
 
-#define TJK_ABI_VERSION 6
+#define TJK_ABI_VERSION 7
 
 /* dtypes */
 #define TJK_F32 0
@@ -233,6 +237,30 @@ int tjk_ffn(const void* a, int a_dtype, int64_t lda, const float* ln_gamma, cons
             int64_t f, int dtype, void* stream);
 /* 1 if tjk_ffn takes (d, f, splits, dtype), else 0. */
 int tjk_ffn_supported(int64_t d, int64_t f, int splits, int dtype);
+
+/*
+ * C = epilogue(LayerNorm(res) W^T + b) in one launch: the LayerNorm of a
+ * tjk_add_layernorm call without delta (res fp32 [m, k], gamma / beta fp32,
+ * biased variance, eps) computed inside the GEMM into its resident A
+ * operand, in place of an add+LayerNorm launch followed by tjk_gemm_bias:
+ * the LayerNorm applied in the next GEMM's A-load, for launch-bound row
+ * counts (the tiny-shape fusion of README.md:193-196).  h equals
+ * tjk_add_layernorm's output bit for bit and the K summation is one chain
+ * (K-summation class 1), so C equals tjk_gemm_bias with a class-1 plan on
+ * that h.  W [n, k] nn.Linear layout, bias and C in `dtype` (fp16 / bf16);
+ * epilogue TJK_EPI_BIAS or TJK_EPI_BIAS_GELU; k in {256, 512, 768, 1024}
+ * (tjk_gemm_ln_supported); n % 4 == 0.  plan_id 0-2: 32-row tiles of 32 /
+ * 64 / 128 columns (same bits), -1: the widest giving >= 128 workgroups.
+ * Each column tile recomputes its rows' LayerNorm, so large row counts
+ * belong to the separate launches.
+ */
+int tjk_gemm_ln(const float* res, int64_t ld_res, const float* gamma, const float* beta, float eps,
+                const void* w, int64_t ldw, const void* bias, void* c, int64_t ldc, int64_t m, int64_t n,
+                int64_t k, int dtype, int epilogue, int plan_id, void* stream);
+/* 1 if tjk_gemm_ln takes (k, dtype), else 0. */
+int tjk_gemm_ln_supported(int64_t k, int dtype);
+/* Number of tjk_gemm_ln plans (column tile widths). */
+int tjk_gemm_ln_plan_count(void);
 
 /*
  * Attention block of one layer in one launch, for sequences of at most 128

@@ -838,6 +838,56 @@ def test_add_layernorm_rejects_cross_dtype_alias(device):
         ops.add_layernorm(buf, None, gamma, beta, 1e-5, out, res_out=as16)
 
 
+# ------------------------------------------------- LayerNorm-prologue GEMM
+
+@pytest.mark.parametrize("k", [256, 512, 768, 1024])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_gemm_ln_equals_layernorm_then_gemm(device, k, dt):
+    """tjk_gemm_ln (LayerNorm inside the GEMM) equals tjk_add_layernorm
+    followed by a class-1 GEMM plan bit for bit, for every column-tile plan
+    and both epilogues, on ragged rows and columns; and matches fp64."""
+    g = _gen(k + (dt == torch.float16))
+    for m, n in ((128, 1536), (45, 100), (300, 2048)):
+        res = torch.randn(m, k, generator=g) * 2 + 0.3
+        gamma, beta = torch.randn(k, generator=g), torch.randn(k, generator=g) * 0.1
+        w = (torch.randn(n, k, generator=g) / math.sqrt(k)).to(dt)
+        bias = torch.randn(n, generator=g).to(dt)
+        rd, gd, bd, wd, biasd = (t.to(device) for t in (res, gamma, beta, w, bias))
+        h = torch.empty(m, k, dtype=dt, device=device)
+        ops.add_layernorm(rd, None, gd, bd, 1e-5, h)
+        hx = oracle.layer_norm(res.double(), gamma.double(), beta.double(), 1e-5)
+        for epi in (ops.EPI_BIAS, ops.EPI_BIAS_GELU):
+            want = torch.empty(m, n, dtype=dt, device=device)
+            ops.gemm(h, wd, biasd, want, epi, 9)  # class 1: one K chain
+            for plan in range(ops.gemm_ln_plan_count()):
+                got = torch.full((m, n), float("nan"), dtype=dt, device=device)
+                ops.gemm_ln(rd, gd, bd, 1e-5, wd, biasd, got, epi, plan)
+                torch.cuda.synchronize()
+                assert torch.equal(got.cpu(), want.cpu()), (m, n, epi, plan)
+            ref = hx.to(dt).double() @ w.double().t() + bias.double()
+            if epi == ops.EPI_BIAS_GELU:
+                ref = 0.5 * ref * (1 + torch.erf(ref / math.sqrt(2)))
+            _close(got, ref, OUT_RTOL[dt], 2e-3)
+
+
+def test_gemm_ln_rejects_unsupported(device):
+    """Shapes and epilogues the LayerNorm GEMM does not take are refused
+    before any launch."""
+    res = torch.zeros(32, 640, device=device)
+    gamma, beta = torch.ones(640, device=device), torch.zeros(640, device=device)
+    w = torch.zeros(64, 640, dtype=torch.bfloat16, device=device)
+    out = torch.empty(32, 64, dtype=torch.bfloat16, device=device)
+    with pytest.raises(ops.TjkError, match="not supported"):  # k = 640
+        ops.gemm_ln(res, gamma, beta, 1e-5, w, None, out)
+    assert not ops.gemm_ln_supported(640, torch.bfloat16) and ops.gemm_ln_supported(512, torch.float16)
+    assert not ops.gemm_ln_supported(512, torch.float32)
+    res, gamma, beta = res[:, :512], gamma[:512], beta[:512]
+    w = torch.zeros(64, 512, dtype=torch.bfloat16, device=device)
+    with pytest.raises(ops.TjkError, match="epilogue"):
+        ops.gemm_ln(res.contiguous(), gamma.contiguous(), beta.contiguous(), 1e-5, w, None, out,
+                    ops.EPI_BIAS_RESIDUAL)
+
+
 # ------------------------------------------------------------ attention block
 
 def _block_case(g, lengths, d, dt):

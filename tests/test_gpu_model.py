@@ -334,6 +334,79 @@ def test_deferred_residual_plan_matches(device):
                                           cuda_graph=False, label="deferred"))
 
 
+LN_GEMM_CASES = [
+    dict(id="c2-graph", workload="C2", plan=dict(ffn="gemm", cuda_graph=True)),
+    dict(id="c2-eager", workload="C2", plan=dict(ffn="gemm", cuda_graph=False)),
+    dict(id="ragged-bf16", cfg=(5, 96, 256, 4, 1024, 3, True), dtype=torch.bfloat16, padding=0.6),
+    dict(id="ragged-noncausal-d768", cfg=(3, 64, 768, 12, 1536, 2, False), dtype=torch.float16, padding=0.5),
+]
+
+
+@pytest.mark.parametrize("case", LN_GEMM_CASES, ids=[c["id"] for c in LN_GEMM_CASES])
+def test_layernorm_inside_gemm_plan(device, case, monkeypatch):
+    """Plan.ln_gemm: LayerNorm 1 (after layer 0) and LayerNorm 2 computed
+    inside the QKV and FFN1 GEMMs holds the budget against the oracle -- at
+    C2 (graphed and eager) and on packed ragged sequences (causal and not) --
+    and the fused GEMM is the one that runs."""
+    from tjkernels import ops as ops_mod
+    calls = []
+    real = ops_mod.gemm_ln
+    monkeypatch.setattr(ops_mod, "gemm_ln", lambda *a, **k: calls.append(1) or real(*a, **k))
+    if "workload" in case:
+        w = WORKLOADS[case["workload"]]
+        _run_workload(device, case["workload"], seeds=(1, 2),
+                      plan=Plan(compute_dtype=w.dtype, ln_gemm=True, label="ln", **case["plan"]))
+        assert calls, "the LayerNorm GEMM was not used"
+        return
+    monkeypatch.setenv("TJ_GEMM_TUNE", "0")  # no tile timing: every counted call is the forward's
+    cfg = TransformerConfig(*case["cfg"])
+    dtype = case["dtype"]
+    torch.manual_seed(11)
+    sd = {k: v.to(dtype).float() for k, v in UserOptimizedTransformer(cfg).state_dict().items()}
+    model = _module(cfg, sd, dtype, device)
+    plans_mod.set_override(Plan(compute_dtype=dtype, ln_gemm=True, cuda_graph=False, ffn="gemm", label="ln"))
+    try:
+        for seed in (1, 2):
+            x, mask = _inputs(cfg, dtype, seed=seed, padding=case["padding"])
+            with torch.inference_mode():
+                got = model(x.to(device), mask.to(device)).cpu()
+            ref = oracle.forward(sd, x.float(), mask, cfg.num_heads, cfg.causal, torch.float32)
+            _check(got, ref, mask, dtype)
+        # 2 launches per layer, LayerNorm 1 of layer 0 excepted
+        assert len(calls) == 2 * (2 * cfg.num_layers - 1)
+    finally:
+        plans_mod.set_override(None)
+
+
+def test_layernorm_inside_gemm_graph_equals_eager(device):
+    """With the LayerNorms inside the GEMMs, hipGraph replay == eager bit
+    for bit, replayed twice with eager work between."""
+    cfg = TransformerConfig(2, 128, 512, 8, 2048, 3, True)
+    dtype = torch.float16
+    torch.manual_seed(12)
+    eager = _module(cfg, UserOptimizedTransformer(cfg).state_dict(), dtype, device)
+    graphed = _module(cfg, eager.state_dict(), dtype, device)
+    cases = [_inputs(cfg, dtype, seed=60 + i, padding=0.5 * (i % 2)) for i in range(3)]
+    base = dict(compute_dtype=dtype, ln_gemm=True, ffn="gemm")
+    plans_mod.set_override(Plan(cuda_graph=False, label="e", **base))
+    try:
+        with torch.inference_mode():
+            expected = [eager(x.to(device), m.to(device)).cpu() for x, m in cases]
+    finally:
+        plans_mod.set_override(None)
+    plans_mod.set_override(Plan(cuda_graph=True, label="g", **base))
+    try:
+        with torch.inference_mode():
+            for _ in range(2):
+                for (x, m), want in zip(cases, expected):
+                    got = graphed(x.to(device), m.to(device))
+                    torch.cuda.synchronize()
+                    assert torch.equal(got.cpu(), want)
+                    _ = (got * 2).sum().item()
+    finally:
+        plans_mod.set_override(None)
+
+
 RESIDUAL_CASES = [
     dict(id="c2-fp16-graph-fused", workload="C2", residual=torch.float16,
          plan=dict(ffn="fused", cuda_graph=True)),

@@ -190,6 +190,9 @@ def test_override_and_env_knobs(monkeypatch):
     assert plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev).ffn == "fused"
     monkeypatch.setenv("TJ_ATTN_BLOCK", "1")
     assert plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev).attn_block
+    monkeypatch.setenv("TJ_LN_GEMM", "1")
+    assert plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev).ln_gemm
+    monkeypatch.delenv("TJ_LN_GEMM")
     # TJ_RESIDUAL_DTYPE, plans.py:183-185 of the reference
     assert plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev).residual_dtype == torch.float32
     monkeypatch.setenv("TJ_RESIDUAL_DTYPE", "float16")
@@ -489,3 +492,15 @@ def test_rocprof_summary_groups_forwards_by_rows_and_kernels(tmp_path):
     assert "2 forwards" in pipe and "1 forwards" in masked
     attn_line = next(line for line in pipe.splitlines() if line.startswith("flash_attention"))
     assert float(attn_line.split()[2]) == 11.0  # (10 + 12) / 2, the masked run's 30 kept out
+
+
+def test_tile_choices_describe_both_gemm_kinds(monkeypatch):
+    """bench.py reports the measured tiles of the plain and the LayerNorm
+    GEMMs together, in shape order."""
+    from tjkernels import tiles
+    monkeypatch.setattr(tiles, "_choice", tiles.OrderedDict())
+    tiles._choice[(128, 1536, 512, torch.float16, 0)] = 22
+    tiles._choice[("ln", 128, 2048, 512, torch.float16, 1)] = 1
+    tiles._choice[(64, 512, 512, torch.float16, 2)] = 24
+    assert list(tiles.describe().items()) == [("64x512x512/epi2", 24), ("128x1536x512/epi0", 22),
+                                              ("ln:128x2048x512/epi1", 1)]

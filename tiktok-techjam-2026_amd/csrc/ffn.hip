@@ -251,6 +251,95 @@ struct FfnLayout {
   static_assert(TOTAL <= 160 * KB, "fused FFN exceeds LDS");
 };
 
+// Rows m0 .. m0 + 31 of LayerNorm(res) (res fp32, biased variance) written
+// into LDS in the compute dtype: row r at sa + r * APITCH, its 16-byte
+// chunks placed by res_chunk.  Rows wave, wave + 4, ...: every row's loads
+// are issued at once, then started() runs (the caller's weight copies,
+// which then land during the loads' latency), then the LayerNorm of each
+// row.  Rows past M are written as zeros.
+template <typename T, int D, int APITCH, typename Started>
+__device__ __forceinline__ void layernorm_rows_to_lds(char* sa, const float* __restrict__ res, int64_t lda,
+                                                      const float* __restrict__ gamma,
+                                                      const float* __restrict__ beta, float eps, int m0, int M,
+                                                      Started started) {
+  constexpr int VEC = 16 / (int)sizeof(T), ACH = APITCH / 16;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // lane l owns the 4-element chunks l, l+64, ... of a row
+  constexpr int NCH = D / 4, MAXCH = (NCH + 63) / 64, RPW = kFfnRows / kFfnWaves;
+  float4 x[RPW][MAXCH], gm[MAXCH], bt[MAXCH];
+#pragma unroll
+  for (int j = 0; j < MAXCH; ++j) {
+    const int c = lane + 64 * j;
+    const bool in = NCH % 64 == 0 || c < NCH;
+    gm[j] = in ? reinterpret_cast<const float4*>(gamma)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    bt[j] = in ? reinterpret_cast<const float4*>(beta)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int m = m0 + wave + kFfnWaves * i;
+#pragma unroll
+    for (int j = 0; j < MAXCH; ++j) {
+      const int c = lane + 64 * j;
+      x[i][j] = (m < M && (NCH % 64 == 0 || c < NCH)) ? reinterpret_cast<const float4*>(res + (int64_t)m * lda)[c]
+                                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  started();
+  // the add+LayerNorm kernel's arithmetic, operation for operation, with
+  // the eight rows' wave reductions interleaved
+  const float inv_n = 1.0f / (float)D;
+  float mean[RPW], rstd[RPW];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    float sm = 0.f;
+#pragma unroll
+    for (int j = 0; j < MAXCH; ++j) sm += (x[i][j].x + x[i][j].y) + (x[i][j].z + x[i][j].w);
+    mean[i] = sm;
+  }
+  wave_sum_n<RPW>(mean);
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    mean[i] *= inv_n;
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < MAXCH; ++j) {
+      const int c = lane + 64 * j;
+      if (NCH % 64 == 0 || c < NCH) {
+        const float a = x[i][j].x - mean[i], b = x[i][j].y - mean[i], cc = x[i][j].z - mean[i],
+                    d = x[i][j].w - mean[i];
+        q += (a * a + b * b) + (cc * cc + d * d);
+      }
+    }
+    rstd[i] = q;
+  }
+  wave_sum_n<RPW>(rstd);
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) rstd[i] = 1.0f / sqrtf(rstd[i] * inv_n + eps);
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int r = wave + kFfnWaves * i, m = m0 + r;
+    char* row = sa + r * APITCH;
+#pragma unroll
+    for (int j = 0; j < MAXCH; ++j) {
+      const int c = lane + 64 * j;
+      if (NCH % 64 == 0 || c < NCH) {
+        float4 y;
+        if (m < M) {
+          y.x = (x[i][j].x - mean[i]) * rstd[i] * gm[j].x + bt[j].x;
+          y.y = (x[i][j].y - mean[i]) * rstd[i] * gm[j].y + bt[j].y;
+          y.z = (x[i][j].z - mean[i]) * rstd[i] * gm[j].z + bt[j].z;
+          y.w = (x[i][j].w - mean[i]) * rstd[i] * gm[j].w + bt[j].w;
+        } else {
+          y = make_float4(0.f, 0.f, 0.f, 0.f);  // rows past the input: zeros
+        }
+        // elements 4c .. 4c+3: chunk 4c / VEC, byte (4c % VEC) * size
+        const int ch = (4 * c) / VEC, off = ((4 * c) % VEC) * (int)sizeof(T);
+        *reinterpret_cast<typename Quad<T>::raw*>(row + (res_chunk<ACH>(ch, r) << 4) + off) = Quad<T>::from(y);
+      }
+    }
+  }
+}
+
 template <typename T, int D, int FC, bool LNA>
 __global__ __launch_bounds__(256) void ffn_fused_kernel(
     const void* __restrict__ Av, int64_t lda, const float* __restrict__ gamma, const float* __restrict__ beta,
@@ -301,82 +390,8 @@ __global__ __launch_bounds__(256) void ffn_fused_kernel(
 
   // ---- 1. A rows into LDS (compute dtype)
   if constexpr (LNA) {
-    // rows wave, wave + 4, ...: every row's loads issued at once, then the
-    // LayerNorm of each; lane l owns the 4-element chunks l, l+64, ...
-    constexpr int NCH = D / 4, MAXCH = (NCH + 63) / 64, RPW = kFfnRows / kFfnWaves;
-    const float* res = static_cast<const float*>(Av);
-    float4 x[RPW][MAXCH], gm[MAXCH], bt[MAXCH];
-#pragma unroll
-    for (int j = 0; j < MAXCH; ++j) {
-      const int c = lane + 64 * j;
-      const bool in = NCH % 64 == 0 || c < NCH;
-      gm[j] = in ? reinterpret_cast<const float4*>(gamma)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
-      bt[j] = in ? reinterpret_cast<const float4*>(beta)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-      const int m = m0 + wave + kFfnWaves * i;
-#pragma unroll
-      for (int j = 0; j < MAXCH; ++j) {
-        const int c = lane + 64 * j;
-        x[i][j] = (m < M && (NCH % 64 == 0 || c < NCH)) ? reinterpret_cast<const float4*>(res + (int64_t)m * lda)[c]
-                                                        : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-    }
-    start_copies();
-    // the add+LayerNorm kernel's arithmetic, operation for operation, with
-    // the eight rows' wave reductions interleaved
-    const float inv_n = 1.0f / (float)D;
-    float mean[RPW], rstd[RPW];
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-      float sm = 0.f;
-#pragma unroll
-      for (int j = 0; j < MAXCH; ++j) sm += (x[i][j].x + x[i][j].y) + (x[i][j].z + x[i][j].w);
-      mean[i] = sm;
-    }
-    wave_sum_n<RPW>(mean);
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-      mean[i] *= inv_n;
-      float q = 0.f;
-#pragma unroll
-      for (int j = 0; j < MAXCH; ++j) {
-        const int c = lane + 64 * j;
-        if (NCH % 64 == 0 || c < NCH) {
-          const float a = x[i][j].x - mean[i], b = x[i][j].y - mean[i], cc = x[i][j].z - mean[i],
-                      d = x[i][j].w - mean[i];
-          q += (a * a + b * b) + (cc * cc + d * d);
-        }
-      }
-      rstd[i] = q;
-    }
-    wave_sum_n<RPW>(rstd);
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) rstd[i] = 1.0f / sqrtf(rstd[i] * inv_n + eps);
-#pragma unroll
-    for (int i = 0; i < RPW; ++i) {
-      const int r = wave + kFfnWaves * i, m = m0 + r;
-      char* row = sa + r * Lay::A_PITCH;
-#pragma unroll
-      for (int j = 0; j < MAXCH; ++j) {
-        const int c = lane + 64 * j;
-        if (NCH % 64 == 0 || c < NCH) {
-          float4 y;
-          if (m < M) {
-            y.x = (x[i][j].x - mean[i]) * rstd[i] * gm[j].x + bt[j].x;
-            y.y = (x[i][j].y - mean[i]) * rstd[i] * gm[j].y + bt[j].y;
-            y.z = (x[i][j].z - mean[i]) * rstd[i] * gm[j].z + bt[j].z;
-            y.w = (x[i][j].w - mean[i]) * rstd[i] * gm[j].w + bt[j].w;
-          } else {
-            y = make_float4(0.f, 0.f, 0.f, 0.f);  // rows past the input: zeros
-          }
-          // elements 4c .. 4c+3: chunk 4c / VEC, byte (4c % VEC) * size
-          const int ch = (4 * c) / VEC, off = ((4 * c) % VEC) * (int)sizeof(T);
-          *reinterpret_cast<typename Quad<T>::raw*>(row + (res_chunk<ACH>(ch, r) << 4) + off) = Quad<T>::from(y);
-        }
-      }
-    }
+    layernorm_rows_to_lds<T, D, Lay::A_PITCH>(sa, static_cast<const float*>(Av), lda, gamma, beta, eps, m0, M,
+                                              start_copies);
   } else {
     const T* A = static_cast<const T*>(Av);
     constexpr int PER = kFfnRows * ACH / 256;
@@ -490,6 +505,115 @@ static int launch_ffn(int64_t d, const void* a, int64_t lda, const float* gamma,
                                f, splits, s);
 }
 
+// ------------------------------------------------- LayerNorm-prologue GEMM
+//
+// C = epi(LayerNorm(res) W^T + b) for a launch of a few hundred rows (the
+// QKV and FFN1 projections at C2's 128 tokens), in place of an
+// add+LayerNorm launch followed by the GEMM: a workgroup owns 32 rows and
+// BN columns, computes the LayerNorm of its rows into the resident A operand
+// (layernorm_rows_to_lds, bit for bit the add+LayerNorm kernel's h) while
+// the first W tiles load, and streams W through a 4-slot LDS ring.  Each
+// column tile recomputes its rows' LayerNorm (64 KB of fp32 at d = 512, from
+// L2), which is why this is for launch-bound row counts only.  The K
+// summation is one chain of K tiles in order, the GEMM's K-summation class 1:
+// with the same h the result equals the class-1 GEMM plans bit for bit.
+template <typename T, int D, int BN, int EPI>
+struct LnGemmLayout {
+  static constexpr int A_PITCH = D * (int)sizeof(T), A_BYTES = kFfnRows * A_PITCH;
+  static constexpr int WN = Min<BN / 32, kFfnWaves>::v;  // waves computing
+  // W ring deep enough for every K tile (up to 8) to be in flight at once:
+  // the launch is latency-bound, and a shallower ring waits out the DMA
+  // latency again every few K tiles
+  static constexpr int STAGES = Min<Min<D / 64, 8>::v, (160 * 1024 - A_BYTES) / (BN * 128)>::v;
+  typedef FfnPhase<T, BN, 128, STAGES, WN> P;
+  static constexpr int STAGE_EPI = kFfnWaves * EpiStage<T, EPI, P::FN>::BYTES;
+  static constexpr int RING = Max<P::LDS, STAGE_EPI>::v;  // the epilogue staging overlays the ring
+  static constexpr int TOTAL = RING + A_BYTES;
+  static_assert(TOTAL <= 160 * 1024, "LayerNorm-prologue GEMM exceeds LDS");
+};
+
+template <typename T, int D, int BN, int EPI>
+__global__ __launch_bounds__(256) void gemm_ln_kernel(
+    const float* __restrict__ res, int64_t ld_res, const float* __restrict__ gamma, const float* __restrict__ beta,
+    float eps, const T* __restrict__ W, int64_t ldw, const T* __restrict__ bias, T* __restrict__ C, int64_t ldc,
+    int M, int N, int nrb, int ncb) {
+  typedef LnGemmLayout<T, D, BN, EPI> Lay;
+  typedef typename Lay::P P;
+  __shared__ __attribute__((aligned(1024))) char smem[Lay::TOTAL];
+  char* ring = smem;
+  char* sa = smem + Lay::RING;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // XCD-contiguous logical order, column-tile-major: the row blocks of one
+  // column tile (which stream the same W rows) run on one XCD
+  const int t = xcd_remap(blockIdx.x, nrb * ncb);
+  const int n0 = (t / nrb) * BN, m0 = (t % nrb) * kFfnRows;
+
+  WStream<T, BN, 128, Lay::STAGES, Lay::WN, Lay::A_PITCH> ws(ring, W + (int64_t)n0 * ldw, ldw, min(BN, N - n0),
+                                                             D / P::BK);
+  layernorm_rows_to_lds<T, D, Lay::A_PITCH>(sa, res, ld_res, gamma, beta, eps, m0, M, [&]() { ws.prologue(); });
+  __syncthreads();
+  f32x16 acc[P::FN][1];
+  zero_acc<T, 1, P::FN>(acc);
+  ws.accumulate(sa, acc);
+  if (wave < Lay::WN)
+    epilogue<T, EPI, 1, P::FN>(acc, bias, C, ldc, M, N, m0, n0 + wave * P::WTN, lane,
+                               ring + wave * EpiStage<T, EPI, P::FN>::BYTES);
+}
+
+// Column tiles of the plans: 32, 64 or 128 columns (1, 2 or 4 waves
+// computing; all four load rows and copy W).
+constexpr int kLnGemmPlans = 3;
+constexpr int kLnGemmBn[kLnGemmPlans] = {32, 64, 128};
+
+template <typename T, int D, int BN>
+static int launch_gemm_ln_bn(const float* res, int64_t ld_res, const float* gamma, const float* beta, float eps,
+                             const void* w, int64_t ldw, const void* bias, void* c, int64_t ldc, int M, int N,
+                             int epi, hipStream_t s) {
+  const int nrb = (M + kFfnRows - 1) / kFfnRows, ncb = (N + BN - 1) / BN;
+  const dim3 grid((unsigned)(nrb * ncb)), block(256);
+  if (epi == TJK_EPI_BIAS_GELU)
+    hipLaunchKernelGGL((gemm_ln_kernel<T, D, BN, TJK_EPI_BIAS_GELU>), grid, block, 0, s, res, ld_res, gamma, beta,
+                       eps, (const T*)w, ldw, (const T*)bias, (T*)c, ldc, M, N, nrb, ncb);
+  else
+    hipLaunchKernelGGL((gemm_ln_kernel<T, D, BN, TJK_EPI_BIAS>), grid, block, 0, s, res, ld_res, gamma, beta, eps,
+                       (const T*)w, ldw, (const T*)bias, (T*)c, ldc, M, N, nrb, ncb);
+  return check_launch("tjk_gemm_ln");
+}
+
+template <typename T, int D>
+static int launch_gemm_ln_d(int plan, const float* res, int64_t ld_res, const float* gamma, const float* beta,
+                            float eps, const void* w, int64_t ldw, const void* bias, void* c, int64_t ldc, int M,
+                            int N, int epi, hipStream_t s) {
+  switch (plan) {
+    case 0:
+      return launch_gemm_ln_bn<T, D, 32>(res, ld_res, gamma, beta, eps, w, ldw, bias, c, ldc, M, N, epi, s);
+    case 1:
+      return launch_gemm_ln_bn<T, D, 64>(res, ld_res, gamma, beta, eps, w, ldw, bias, c, ldc, M, N, epi, s);
+    default:
+      return launch_gemm_ln_bn<T, D, 128>(res, ld_res, gamma, beta, eps, w, ldw, bias, c, ldc, M, N, epi, s);
+  }
+}
+
+template <typename T>
+static int launch_gemm_ln(int64_t k, int plan, const float* res, int64_t ld_res, const float* gamma,
+                          const float* beta, float eps, const void* w, int64_t ldw, const void* bias, void* c,
+                          int64_t ldc, int M, int N, int epi, hipStream_t s) {
+  switch (k) {
+    case 256:
+      return launch_gemm_ln_d<T, 256>(plan, res, ld_res, gamma, beta, eps, w, ldw, bias, c, ldc, M, N, epi, s);
+    case 512:
+      return launch_gemm_ln_d<T, 512>(plan, res, ld_res, gamma, beta, eps, w, ldw, bias, c, ldc, M, N, epi, s);
+    case 768:
+      return launch_gemm_ln_d<T, 768>(plan, res, ld_res, gamma, beta, eps, w, ldw, bias, c, ldc, M, N, epi, s);
+    default:
+      return launch_gemm_ln_d<T, 1024>(plan, res, ld_res, gamma, beta, eps, w, ldw, bias, c, ldc, M, N, epi, s);
+  }
+}
+
+static bool gemm_ln_shape_ok(int64_t k, int dtype) {
+  return (dtype == TJK_F16 || dtype == TJK_BF16) && (k == 256 || k == 512 || k == 768 || k == 1024);
+}
+
 }  // namespace tjk
 
 using namespace tjk;
@@ -538,4 +662,51 @@ extern "C" int tjk_ffn(const void* a, int a_dtype, int64_t lda, const float* ln_
       return launch_ffn<bf16>(d, a, lda, ln_gamma, ln_beta, ln_eps, w1, b1, w2, b2, out, ld_out, split_stride,
                               accumulate, M, fi, splits, s);
   }
+}
+
+extern "C" int tjk_gemm_ln_supported(int64_t k, int dtype) { return gemm_ln_shape_ok(k, dtype) ? 1 : 0; }
+
+extern "C" int tjk_gemm_ln_plan_count(void) { return kLnGemmPlans; }
+
+extern "C" int tjk_gemm_ln(const float* res, int64_t ld_res, const float* gamma, const float* beta, float eps,
+                           const void* w, int64_t ldw, const void* bias, void* c, int64_t ldc, int64_t m, int64_t n,
+                           int64_t k, int dtype, int epilogue, int plan_id, void* stream) {
+  if (m < 0 || n < 0 || k <= 0) return fail(TJK_EINVAL, "tjk_gemm_ln: bad shape m=%lld n=%lld k=%lld",
+                                            (long long)m, (long long)n, (long long)k);
+  if (!gemm_ln_shape_ok(k, dtype))
+    return fail(TJK_EUNSUPPORTED, "tjk_gemm_ln: k=%lld dtype=%d not supported (fp16 / bf16, k in {256, 512, 768, "
+                "1024})", (long long)k, dtype);
+  if (epilogue != TJK_EPI_BIAS && epilogue != TJK_EPI_BIAS_GELU)
+    return fail(TJK_EINVAL, "tjk_gemm_ln: epilogue %d (bias or bias + GELU only)", epilogue);
+  if (plan_id < -1 || plan_id >= kLnGemmPlans)
+    return fail(TJK_EINVAL, "tjk_gemm_ln: plan %d out of range [-1,%d)", plan_id, kLnGemmPlans);
+  if (m == 0 || n == 0) return TJK_OK;
+  if (!res || !gamma || !beta || !w || !c) return fail(TJK_EINVAL, "tjk_gemm_ln: null pointer");
+  if (m > INT32_MAX / 2 || n > INT32_MAX || n * ldw * dtype_size(dtype) >= kPastEnd)
+    return fail(TJK_EUNSUPPORTED, "tjk_gemm_ln: shape exceeds the 32-bit buffer range");
+  if (n % 4) return fail(TJK_EUNSUPPORTED, "tjk_gemm_ln: n=%lld must be a multiple of 4", (long long)n);
+  const int es = dtype_size(dtype);
+  if (ld_res < k || ldw < k || ldc < n) return fail(TJK_EINVAL, "tjk_gemm_ln: leading dimension too small");
+  if (ld_res % 4 || (ldw * es) % 16 || ldc % 4)
+    return fail(TJK_EUNSUPPORTED, "tjk_gemm_ln: rows must stay 16-byte aligned (ldc a multiple of 4)");
+  if (((uintptr_t)res & 15) || ((uintptr_t)gamma & 15) || ((uintptr_t)beta & 15) || ((uintptr_t)w & 15) ||
+      ((uintptr_t)c & (4 * es - 1)) || ((uintptr_t)bias & (4 * es - 1)))
+    return fail(TJK_EUNSUPPORTED, "tjk_gemm_ln: misaligned pointer");
+  int plan = plan_id;
+  if (plan < 0) {
+    // the widest column tile that still gives a launch of >= 128 workgroups
+    const int64_t nrb = (m + kFfnRows - 1) / kFfnRows;
+    plan = 0;
+    for (int p = kLnGemmPlans - 1; p > 0; --p)
+      if (nrb * ((n + kLnGemmBn[p] - 1) / kLnGemmBn[p]) >= 128) {
+        plan = p;
+        break;
+      }
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == TJK_F16)
+    return launch_gemm_ln<f16>(k, plan, res, ld_res, gamma, beta, eps, w, ldw, bias, c, ldc, (int)m, (int)n,
+                               epilogue, s);
+  return launch_gemm_ln<bf16>(k, plan, res, ld_res, gamma, beta, eps, w, ldw, bias, c, ldc, (int)m, (int)n,
+                              epilogue, s);
 }

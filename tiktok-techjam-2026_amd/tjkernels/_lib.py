@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede the library load; see module docstring)
 
 LIB_PATH = Path(__file__).with_name("libtjk.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 F32, F16, BF16 = 0, 1, 2
 OK, EINVAL, EUNSUPPORTED = 0, -1, -2
@@ -53,6 +53,10 @@ _SIGNATURES = {
     "tjk_attn_block": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _i32, _i32, _i32,
                               _i32, _f32, _i32, _i32, _vp]),
     "tjk_attn_block_supported": (_i32, [_i64, _i32, _i32, _i64, _i32]),
+    "tjk_gemm_ln": (_i32, [_vp, _i64, _vp, _vp, _f32, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32,
+                           _i32, _vp]),
+    "tjk_gemm_ln_supported": (_i32, [_i64, _i32]),
+    "tjk_gemm_ln_plan_count": (_i32, []),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

@@ -183,6 +183,10 @@ def tune_workload(w: Workload, trials: int = 2, margin: float = 0.85, iters: int
         # (bench/autotune.py:88); not tried for fp32 compute, whose 1e-4
         # budget a 2-byte residual cannot hold
         knobs.append(("residual_dtype", [torch.float32, torch.float16]))
+    if ops.gemm_ln_supported(w.d_model, cur["plan"].compute_dtype):
+        # LayerNorms inside the QKV / FFN1 GEMMs (takes effect with the
+        # two-launch FFN and residual epilogues)
+        knobs.insert(0, ("ln_gemm", [False, True]))
     if fused_ffn_ok(w.d_model, w.ffn_dim, cur["plan"].compute_dtype):
         knobs.insert(0, ("ffn", ["gemm", "fused"]))
     if attn_block_ok(w.seq, w.d_model, w.heads, cur["plan"].compute_dtype):

@@ -227,6 +227,8 @@ class Tiles(NamedTuple):
     out: int
     fc1: int
     fc2: int
+    qkv_ln: int = -1  # tjk_gemm_ln plans (LayerNorm inside the GEMM)
+    fc1_ln: int = -1
 
 
 @dataclass
@@ -258,6 +260,7 @@ class Forward:
     key_mask: Optional[torch.Tensor] = None
     use_sched: bool = False
     use_block: bool = False
+    ln_in_gemm: bool = False  # LayerNorms 1 (after layer 0) and 2 inside the QKV / FFN1 GEMMs
     splits: int = 1
     pending: Optional[torch.Tensor] = None  # what the next LayerNorm adds to res
 
@@ -372,15 +375,23 @@ class Engine:
         block = (plan.attn_block and mode != MASK_GENERAL and rows > 0
                  and attn_block_ok(longest, d, shp.heads, cdt))
         epi_res = ops.EPI_BIAS_RESIDUAL if plan.epilogue_residual else ops.EPI_BIAS
+        # LayerNorm inside the QKV / FFN1 GEMMs needs nothing pending for
+        # either LayerNorm: residual epilogues, the two-launch FFN and no
+        # attention block
+        ln_in = (plan.ln_gemm and plan.epilogue_residual and not fused and not block and rows > 0
+                 and ops.gemm_ln_supported(d, cdt))
         tp = Tiles(
             qkv=-1 if block else tiles.gemm_plan(rows, 3 * d, d, cdt, ops.EPI_BIAS, plan.gemm_qkv),
             out=-1 if block else tiles.gemm_plan(rows, d, d, cdt, epi_res, plan.gemm_out),
-            fc1=-1 if fused else tiles.gemm_plan(rows, f, d, cdt, ops.EPI_BIAS_GELU, plan.gemm_ffn1),
-            fc2=-1 if fused else tiles.gemm_plan(rows, d, f, cdt, epi_res, plan.gemm_ffn2))
+            fc1=-1 if fused or ln_in else tiles.gemm_plan(rows, f, d, cdt, ops.EPI_BIAS_GELU, plan.gemm_ffn1),
+            fc2=-1 if fused else tiles.gemm_plan(rows, d, f, cdt, epi_res, plan.gemm_ffn2),
+            qkv_ln=tiles.gemm_ln_plan(rows, 3 * d, d, cdt, ops.EPI_BIAS) if ln_in else -1,
+            fc1_ln=tiles.gemm_ln_plan(rows, f, d, cdt, ops.EPI_BIAS_GELU) if ln_in else -1)
         fw = Forward(batch=batch, seq=seq, mode=mode, rows=rows,
                      ws=self._workspace(batch, seq, plan, splits, block), tiles=tp,
                      packing=packing if mode == MASK_PREFIX else None,
-                     key_mask=mask if mode == MASK_GENERAL else None, use_block=block, splits=splits)
+                     key_mask=mask if mode == MASK_GENERAL else None, use_block=block, splits=splits,
+                     ln_in_gemm=ln_in)
         if fused:
             fw.pending = fw.view("parts")
         elif not plan.epilogue_residual:
@@ -454,9 +465,13 @@ class Engine:
             return
         mid = fw.view("mid")
         if plan.epilogue_residual:
-            ops.add_layernorm(res, attn_pending, n2.weight, n2.bias, n2.eps, h,
-                              res_out=res if attn_pending is not None else None)
-            ops.gemm(h, blk.fc1.weight, blk.fc1.bias, mid, ops.EPI_BIAS_GELU, fw.tiles.fc1)
+            if fw.ln_in_gemm:  # LayerNorm 2 inside the FFN1 GEMM
+                ops.gemm_ln(res, n2.weight, n2.bias, n2.eps, blk.fc1.weight, blk.fc1.bias, mid,
+                            ops.EPI_BIAS_GELU, fw.tiles.fc1_ln)
+            else:
+                ops.add_layernorm(res, attn_pending, n2.weight, n2.bias, n2.eps, h,
+                                  res_out=res if attn_pending is not None else None)
+                ops.gemm(h, blk.fc1.weight, blk.fc1.bias, mid, ops.EPI_BIAS_GELU, fw.tiles.fc1)
             ops.gemm(mid, blk.fc2.weight, blk.fc2.bias, res, ops.EPI_BIAS_RESIDUAL, fw.tiles.fc2)
         else:
             delta = fw.view("delta")
@@ -469,14 +484,22 @@ class Engine:
         part the hipGraph captures (fixed buffers only)."""
         res, h, ctx = fw.view("res"), fw.view("h"), fw.view("ctx")
         for i, blk in enumerate(self.weights.blocks):
-            if i > 0:
+            # LayerNorm 1 of the layers after the first: inside the QKV GEMM,
+            # or a launch of its own
+            ln_qkv = i > 0 and fw.ln_in_gemm
+            if i > 0 and not ln_qkv:
                 n1 = blk.norm1
                 ops.add_layernorm(res, fw.pending, n1.weight, n1.bias, n1.eps, h,
                                   res_out=res if fw.pending is not None else None)
             if fw.use_block:
                 self._attn_block(fw, blk)
             else:
-                ops.gemm(h, blk.qkv.weight, blk.qkv.bias, fw.view("qkv"), ops.EPI_BIAS, fw.tiles.qkv)
+                if ln_qkv:
+                    n1 = blk.norm1
+                    ops.gemm_ln(res, n1.weight, n1.bias, n1.eps, blk.qkv.weight, blk.qkv.bias, fw.view("qkv"),
+                                ops.EPI_BIAS, fw.tiles.qkv_ln)
+                else:
+                    ops.gemm(h, blk.qkv.weight, blk.qkv.bias, fw.view("qkv"), ops.EPI_BIAS, fw.tiles.qkv)
                 self._attention(fw)
                 if self.plan.epilogue_residual:
                     ops.gemm(ctx, blk.out.weight, blk.out.bias, res, ops.EPI_BIAS_RESIDUAL, fw.tiles.out)

@@ -129,6 +129,41 @@ def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], out: to
     return out
 
 
+def gemm_ln_supported(k: int, dtype: torch.dtype) -> bool:
+    """Whether tjk_gemm_ln takes a K (= d_model) and compute dtype."""
+    code = _lib.DTYPE_CODES.get(dtype)
+    return code is not None and bool(_lib.load().tjk_gemm_ln_supported(k, code))
+
+
+def gemm_ln_plan_count() -> int:
+    return int(_lib.load().tjk_gemm_ln_plan_count())
+
+
+def gemm_ln(res: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: float, w: torch.Tensor,
+            bias: Optional[torch.Tensor], out: torch.Tensor, epilogue: int = EPI_BIAS,
+            plan: int = -1) -> torch.Tensor:
+    """out = epi(LayerNorm(res) @ w.T + bias) in one launch: the LayerNorm of
+    ``add_layernorm`` without delta (fp32 ``res``) applied inside the GEMM,
+    for launch-bound row counts; the add+LayerNorm launch and the GEMM of
+    tjkernels/engine.py:239-245 (LN1 + QKV) and :249-253 (LN2 + the FFN's
+    first GEMM) in one.  Equals add_layernorm then a class-1 ``gemm`` bit
+    for bit."""
+    _require_gpu(res, gamma, beta, w, bias, out)
+    m, k = res.shape
+    n, k2 = w.shape
+    if k != k2 or out.shape[0] != m or out.shape[1] != n:
+        raise TjkError(f"gemm_ln shape mismatch res{tuple(res.shape)} w{tuple(w.shape)} out{tuple(out.shape)}")
+    if res.dtype != torch.float32 or gamma.dtype != torch.float32 or beta.dtype != torch.float32:
+        raise TjkError("gemm_ln reads the fp32 residual and fp32 gamma / beta")
+    if out.dtype != w.dtype or (bias is not None and bias.dtype != w.dtype):
+        raise TjkError("gemm_ln: w, bias and out share the compute dtype")
+    status = _lib.load().tjk_gemm_ln(res.data_ptr(), _rowmajor(res, "res"), gamma.data_ptr(), beta.data_ptr(),
+                                     float(eps), w.data_ptr(), _rowmajor(w, "w"), _ptr(bias), out.data_ptr(),
+                                     _rowmajor(out, "out"), m, n, k, _code(w), epilogue, plan, _stream(res))
+    check(status, "tjk_gemm_ln")
+    return out
+
+
 def flash_attention(qkv: torch.Tensor, out: torch.Tensor, causal: bool = True,
                     scale: Optional[float] = None, lengths: Optional[torch.Tensor] = None,
                     key_mask: Optional[torch.Tensor] = None, plan: int = -1,

@@ -29,6 +29,11 @@ to select, and the product path has no non-HIP fallback):
   (``tjk_attn_block``) whose per-head partials LayerNorm 2 sums; forwards
   it does not take (longer sequences, general masks) use the three
   launches;
+* ``ln_gemm``: compute LayerNorm 1 (layers after the first) and LayerNorm 2
+  inside the QKV and FFN1 GEMMs (``tjk_gemm_ln``) instead of as launches of
+  their own, where nothing is pending for them (residual epilogues, the
+  two-launch FFN, no attention block); for launch-bound row counts, since
+  every column tile recomputes its rows' LayerNorm;
 * ``cuda_graph``: replay the layer body as one hipGraph;
 * ``whole_graph`` (with ``cuda_graph``): capture the first and final
   LayerNorm too, reading x from a static input buffer and writing a static
@@ -44,7 +49,8 @@ to select, and the product path has no non-HIP fallback):
   ``ATTN_SCHEDULED`` (5) the work-list kernel for packed sequences);
 * ``pack_prefix``: run only the valid tokens of prefix masks.
 
-Environment: ``TJ_NO_GRAPH``, ``TJ_WHOLE_GRAPH`` (0 / 1), ``TJ_ATTN_BLOCK`` (0 / 1), ``TJ_COMPUTE_DTYPE``,
+Environment: ``TJ_NO_GRAPH``, ``TJ_WHOLE_GRAPH`` (0 / 1), ``TJ_ATTN_BLOCK`` (0 / 1), ``TJ_LN_GEMM`` (0 / 1),
+``TJ_COMPUTE_DTYPE``,
 ``TJ_RESIDUAL_DTYPE``, ``TJ_DEFERRED_RESIDUAL``, ``TJ_NO_PACK``, ``TJ_ATTN_PLAN``, ``TJ_FFN`` (gemm | fused), ``TJ_FFN_SPLITS``;
 ``TJ_GEMM_TUNE=0`` (tjkernels.tiles) skips the measured tile choice.
 Tuned keys carry the GPU architecture (``...@gfx950``).
@@ -89,6 +95,7 @@ class Plan:
     cuda_graph: bool = True
     whole_graph: bool = False
     attn_block: bool = False
+    ln_gemm: bool = False
     residual_epilogue: bool = True
     gemm_qkv: int = -1
     gemm_out: int = -1
@@ -241,6 +248,8 @@ def _env_adjusted(plan: Plan, d_model: int, ffn_dim: int) -> Plan:
         changes["whole_graph"] = env["TJ_WHOLE_GRAPH"] == "1"
     if env.get("TJ_ATTN_BLOCK") in ("0", "1"):
         changes["attn_block"] = env["TJ_ATTN_BLOCK"] == "1"
+    if env.get("TJ_LN_GEMM") in ("0", "1"):
+        changes["ln_gemm"] = env["TJ_LN_GEMM"] == "1"
     if env.get("TJ_COMPUTE_DTYPE") in DTYPE_BY_NAME:
         changes["compute_dtype"] = DTYPE_BY_NAME[env["TJ_COMPUTE_DTYPE"]]
     if env.get("TJ_RESIDUAL_DTYPE") in DTYPE_BY_NAME:

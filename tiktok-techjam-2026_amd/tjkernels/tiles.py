@@ -22,6 +22,11 @@ whatever the timing picks.  ``k_class`` chooses the K split when a launch of
 split to shorten the serial chain of K tiles (the launch-bound projections
 of C2 and C3's FFN2: 10.6 -> 8.5 us and 26.1 -> 23.0 us measured on MI355X).
 
+The LayerNorm-prologue GEMM (``tjk_gemm_ln``, LayerNorm computed inside
+the GEMM for launch-bound row counts) has its own plans, 32-row tiles of
+32 / 64 / 128 columns that all sum K in one chain: ``gemm_ln_plan`` times
+them the same way (any pick gives the same bits).
+
 The table is keyed by M rounded up to a multiple of 64 (the timing runs at
 that M), so ragged lengths reuse a measurement, and it holds at most
 ``MAX_ENTRIES`` shapes.  This replaces the reference's static per-shape
@@ -68,27 +73,34 @@ def candidates(m: int, n: int, k: int, dtype: torch.dtype) -> Tuple[int, ...]:
     return CLASS_TILES_16[k_class(m, n, k, dtype)]
 
 
-def _time_plan(a, w, bias, out, epi, plan, reps) -> float:
-    return timing.launch_ms(lambda: ops.gemm(a, w, bias, out, epi, plan), reps)
-
-
-def _measure(m: int, n: int, k: int, dtype: torch.dtype, epilogue: int) -> int:
+def _measure(m: int, n: int, k: int, dtype: torch.dtype, epilogue: int, ln: bool = False) -> int:
     dev = torch.device("cuda", torch.cuda.current_device())
     g = torch.Generator(device=dev)
     g.manual_seed(m * 7919 + n * 31 + k)
-    a = torch.randn(m, k, device=dev, generator=g).to(dtype)
+    a = torch.randn(m, k, device=dev, generator=g)  # fp32: the LayerNorm GEMM's residual
+    if not ln:
+        a = a.to(dtype)
     w = (torch.randn(n, k, device=dev, generator=g) * k ** -0.5).to(dtype)
     bias = torch.zeros(n, device=dev, dtype=dtype)
+    gamma, beta = torch.ones(k, device=dev), torch.zeros(k, device=dev)
     out = torch.empty(m, n, device=dev,
                       dtype=torch.float32 if epilogue == ops.EPI_BIAS_RESIDUAL else dtype)
+    if ln:
+        def run(plan):
+            ops.gemm_ln(a, gamma, beta, 1e-5, w, bias, out, epilogue, plan)
+        plans = tuple(range(ops.gemm_ln_plan_count()))
+    else:
+        def run(plan):
+            ops.gemm(a, w, bias, out, epilogue, plan)
+        plans = candidates(m, n, k, dtype)
     # about 1.5 ms of GPU work per measurement (estimated at 500 TFLOP/s):
     # with 0.4 ms and three rounds the packed C4 FFN1 / FFN2 picks moved
     # between tiles 2-5% apart from one process to the next
     reps = max(3, min(64, int(1.5e-3 / (2.0 * m * n * k / 500e12))))
     cands = []
-    for cand in candidates(m, n, k, dtype):
+    for cand in plans:
         try:
-            ops.gemm(a, w, bias, out, epilogue, cand)  # warm; rejects shapes it does not take
+            run(cand)  # warm; rejects shapes it does not take
         except _lib.TjkError:  # e.g. K % 64 != 0
             continue
         cands.append(cand)
@@ -100,7 +112,7 @@ def _measure(m: int, n: int, k: int, dtype: torch.dtype, epilogue: int) -> int:
     times = {c: float("inf") for c in cands}
     for rnd in range(5):
         for cand in (cands if rnd % 2 == 0 else cands[::-1]):
-            times[cand] = min(times[cand], _time_plan(a, w, bias, out, epilogue, cand, reps))
+            times[cand] = min(times[cand], timing.launch_ms(lambda: run(cand), reps))
     best, best_ms = cands[0], times[cands[0]]
     for cand in cands[1:]:  # earlier (larger-reuse) candidates win near ties
         if times[cand] < best_ms * 0.98:
@@ -127,9 +139,39 @@ def gemm_plan(m: int, n: int, k: int, dtype: torch.dtype, epilogue: int, forced:
     return plan
 
 
+def gemm_ln_plan(m: int, n: int, k: int, dtype: torch.dtype, epilogue: int, forced: int = -1) -> int:
+    """Column-tile plan of tjk_gemm_ln for out[m, n] = epi(LN(res[m, k]) w[n, k]^T + b)."""
+    if forced >= 0 or m == 0:
+        return forced
+    mb = -(-m // M_BUCKET) * M_BUCKET
+    key = ("ln", mb, n, k, dtype, epilogue)
+    plan = _choice.get(key)
+    if plan is not None:
+        _choice.move_to_end(key)
+        return plan
+    if os.environ.get("TJ_GEMM_TUNE") == "0" or torch.cuda.is_current_stream_capturing():
+        return -1
+    plan = _measure(mb, n, k, dtype, epilogue, ln=True)
+    _choice[key] = plan
+    while len(_choice) > MAX_ENTRIES:
+        _choice.popitem(last=False)
+    return plan
+
+
 def chosen() -> dict:
-    """{(M bucket, N, K, dtype, epilogue): tile} measured so far."""
+    """{(M bucket, N, K, dtype, epilogue): tile} measured so far (the
+    LayerNorm GEMM's entries keyed ("ln", M bucket, N, K, dtype, epilogue))."""
     return dict(_choice)
+
+
+def describe() -> dict:
+    """The choices as {"MxNxK/epiE": tile}, LayerNorm GEMM entries prefixed
+    "ln:", in shape order."""
+    out = {}
+    for key, plan in sorted(_choice.items(), key=lambda kv: (kv[0][0] == "ln", kv[0][-5:-2])):
+        m, n, k, _, e = key[-5:]
+        out[f"{'ln:' if key[0] == 'ln' else ''}{m}x{n}x{k}/epi{e}"] = plan
+    return out
 
 
 def reset() -> None:
