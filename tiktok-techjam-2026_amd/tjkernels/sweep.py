@@ -23,6 +23,8 @@ Ablation variants (each against the full stack on the same workloads):
   * two-launch FFN (no single-launch)    TJ_FFN=gemm
   * fp32 compute (accuracy escalation)   TJ_COMPUTE_DTYPE=float32
   * one-launch attention block (opt-in)  TJ_ATTN_BLOCK=1
+  * LayerNorm inside the GEMMs (opt-in)  TJ_LN_GEMM=1
+  * fp16 residual stream (opt-in)        TJ_RESIDUAL_DTYPE=float16
 
 The report opens with the system it ran on (GPU, its architecture and CU
 count, ROCm / torch versions, host CPU and the cores the CPU baseline may
@@ -53,6 +55,8 @@ LEAVE_ONE = [
     ("two-launch FFN", {"TJ_FFN": "gemm"}),
     ("fp32 compute", {"TJ_COMPUTE_DTYPE": "float32"}),
     ("one-launch attention block", {"TJ_ATTN_BLOCK": "1"}),
+    ("LayerNorm inside the GEMMs", {"TJ_LN_GEMM": "1"}),
+    ("fp16 residual stream", {"TJ_RESIDUAL_DTYPE": "float16"}),
 ]
 
 
