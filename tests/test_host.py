@@ -161,10 +161,11 @@ def test_override_and_env_knobs(monkeypatch):
     monkeypatch.setattr(plans_mod, "TUNED", plans_mod.PlanTable(Path("/nonexistent/plans.json")))
     dev = torch.device("cuda", 0)
     base = plans_mod.select_plan(4, 2048, 1024, 16, 4096, 4, True, torch.bfloat16, dev)
-    assert not base.cuda_graph and base.compute_dtype == torch.bfloat16 and base.residual_epilogue
+    # C4: launched eagerly, outputs deferred to the next LayerNorm (the reference's scheme)
+    assert not base.cuda_graph and base.compute_dtype == torch.bfloat16 and not base.residual_epilogue
     assert base.ffn == "gemm"  # d = 1024: the two-launch FFN
     small = plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev)
-    assert small.cuda_graph  # launch-bound: replayed as a hipGraph
+    assert small.cuda_graph and small.residual_epilogue  # launch-bound: replayed as a hipGraph
     assert small.ffn == "gemm"  # C2: two launches measured faster than the single-launch FFN
     tiny = plans_mod.select_plan(2, 64, 128, 4, 512, 2, True, torch.float32, dev)
     assert tiny.ffn == "fused" and tiny.compute_dtype == torch.float32  # C1
@@ -190,6 +191,9 @@ def test_override_and_env_knobs(monkeypatch):
     assert plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev).ffn == "fused"
     monkeypatch.setenv("TJ_ATTN_BLOCK", "1")
     assert plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev).attn_block
+    monkeypatch.setenv("TJ_DEFERRED_RESIDUAL", "0")
+    assert plans_mod.select_plan(4, 2048, 1024, 16, 4096, 4, True, torch.bfloat16, dev).residual_epilogue
+    monkeypatch.setenv("TJ_DEFERRED_RESIDUAL", "1")
     monkeypatch.setenv("TJ_LN_GEMM", "1")
     assert plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev).ln_gemm
     monkeypatch.delenv("TJ_LN_GEMM")
@@ -504,3 +508,15 @@ def test_tile_choices_describe_both_gemm_kinds(monkeypatch):
     tiles._choice[(64, 512, 512, torch.float16, 2)] = 24
     assert list(tiles.describe().items()) == [("64x512x512/epi2", 24), ("128x1536x512/epi0", 22),
                                               ("ln:128x2048x512/epi1", 1)]
+
+
+def test_rocprof_summary_labels_deferred_projections():
+    """Out-proj / FFN2 launches without the residual epilogue (EPI 0) are
+    labelled by what they are."""
+    from tjkernels import rocprof_summary as rs
+    epi2 = "_ZN3tjk15gemm_dtl_kernelIDF16bLi192ELi128ELi2ELi2ELi128ELi4ELi2ELi1EEEvPKT_lS3_lS3_Pvliii"
+    epi0 = "_ZN3tjk15gemm_dtl_kernelIDF16bLi96ELi128ELi1ELi4ELi128ELi2ELi0ELi1EEEvPKT_lS3_lS3_Pvliii"
+    assert rs._gemm_epilogue(epi2) == 2 and rs._gemm_epilogue(epi0) == 0
+    assert rs._relabel("gemm_ffn2_residual", epi2) == "gemm_ffn2_residual"
+    assert rs._relabel("gemm_out_residual", epi0) == "gemm_out"
+    assert rs._relabel("gemm_qkv", epi0) == "gemm_qkv"

@@ -54,7 +54,7 @@ import torch
 
 from . import ops, schedule as sched_mod, tiles
 from .graphs import GraphCache
-from .plans import ATTN_SCHEDULED, Plan, attn_block_ok, fused_ffn_ok, select_plan
+from .plans import ATTN_SCHEDULED, LN_GEMM_MAX_ROWS, Plan, attn_block_ok, fused_ffn_ok, select_plan
 
 try:
     from torch.utils.weak import WeakTensorKeyDictionary
@@ -378,8 +378,8 @@ class Engine:
         # LayerNorm inside the QKV / FFN1 GEMMs needs nothing pending for
         # either LayerNorm: residual epilogues, the two-launch FFN and no
         # attention block
-        ln_in = (plan.ln_gemm and plan.epilogue_residual and not fused and not block and rows > 0
-                 and ops.gemm_ln_supported(d, cdt))
+        ln_in = (plan.ln_gemm and plan.epilogue_residual and not fused and not block
+                 and 0 < rows <= LN_GEMM_MAX_ROWS and ops.gemm_ln_supported(d, cdt))
         tp = Tiles(
             qkv=-1 if block else tiles.gemm_plan(rows, 3 * d, d, cdt, ops.EPI_BIAS, plan.gemm_qkv),
             out=-1 if block else tiles.gemm_plan(rows, d, d, cdt, epi_res, plan.gemm_out),

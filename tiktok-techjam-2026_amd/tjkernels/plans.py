@@ -32,8 +32,9 @@ to select, and the product path has no non-HIP fallback):
 * ``ln_gemm``: compute LayerNorm 1 (layers after the first) and LayerNorm 2
   inside the QKV and FFN1 GEMMs (``tjk_gemm_ln``) instead of as launches of
   their own, where nothing is pending for them (residual epilogues, the
-  two-launch FFN, no attention block); for launch-bound row counts, since
-  every column tile recomputes its rows' LayerNorm;
+  two-launch FFN, no attention block) and the forward has at most
+  ``LN_GEMM_MAX_ROWS`` rows, since every column tile recomputes its rows'
+  LayerNorm;
 * ``cuda_graph``: replay the layer body as one hipGraph;
 * ``whole_graph`` (with ``cuda_graph``): capture the first and final
   LayerNorm too, reading x from a static input buffer and writing a static
@@ -51,7 +52,7 @@ to select, and the product path has no non-HIP fallback):
 
 Environment: ``TJ_NO_GRAPH``, ``TJ_WHOLE_GRAPH`` (0 / 1), ``TJ_ATTN_BLOCK`` (0 / 1), ``TJ_LN_GEMM`` (0 / 1),
 ``TJ_COMPUTE_DTYPE``,
-``TJ_RESIDUAL_DTYPE``, ``TJ_DEFERRED_RESIDUAL``, ``TJ_NO_PACK``, ``TJ_ATTN_PLAN``, ``TJ_FFN`` (gemm | fused), ``TJ_FFN_SPLITS``;
+``TJ_RESIDUAL_DTYPE``, ``TJ_DEFERRED_RESIDUAL`` (0 / 1), ``TJ_NO_PACK``, ``TJ_ATTN_PLAN``, ``TJ_FFN`` (gemm | fused), ``TJ_FFN_SPLITS``;
 ``TJ_GEMM_TUNE=0`` (tjkernels.tiles) skips the measured tile choice.
 Tuned keys carry the GPU architecture (``...@gfx950``).
 """
@@ -79,6 +80,11 @@ ATTN_SCHEDULED = 5
 # 0.097 ms with two launches; C2 (2^18) 0.147 against 0.140 ms, since the
 # 32-row K-split GEMM tiles made the two launches cheaper.
 FUSED_FFN_MAX_ELEMS = 1 << 17
+
+# The LayerNorm GEMM (Plan.ln_gemm) recomputes each row's LayerNorm once per
+# 32-column tile, so the engine applies it up to this many rows only (C2:
+# 128); at C4's 5430 rows it measured 2.31 against 0.89 ms per forward.
+LN_GEMM_MAX_ROWS = 512
 
 
 @dataclass(frozen=True)
@@ -188,7 +194,13 @@ def default_plan(batch: int, seq: int, d_model: int, heads: int, ffn_dim: int,
     # at C2 it runs 15.1 us per layer, which with the LayerNorm launch that
     # sums its per-head partials equals the QKV GEMM + attention + out-proj
     # it replaces (0.1527 vs 0.1530 ms per forward); the autotuner tries it.
-    return Plan(compute_dtype=dtype, cuda_graph=graph, ffn="fused" if fused else "gemm", label="heuristic")
+    # Shapes launched eagerly defer the out-proj / FFN2 outputs to the next
+    # LayerNorm (the reference's scheme) instead of adding them into the
+    # residual in the GEMM epilogue: measured at C4 0.879 against 0.887 ms
+    # (three alternating runs each, same tiles), within noise at C5; the
+    # graphed small shapes keep the epilogue (C2 0.1400 against 0.1406 ms).
+    return Plan(compute_dtype=dtype, cuda_graph=graph, ffn="fused" if fused else "gemm",
+                residual_epilogue=graph, label="heuristic")
 
 
 class PlanTable:
@@ -254,8 +266,8 @@ def _env_adjusted(plan: Plan, d_model: int, ffn_dim: int) -> Plan:
         changes["compute_dtype"] = DTYPE_BY_NAME[env["TJ_COMPUTE_DTYPE"]]
     if env.get("TJ_RESIDUAL_DTYPE") in DTYPE_BY_NAME:
         changes["residual_dtype"] = DTYPE_BY_NAME[env["TJ_RESIDUAL_DTYPE"]]
-    if env.get("TJ_DEFERRED_RESIDUAL") == "1":
-        changes["residual_epilogue"] = False
+    if env.get("TJ_DEFERRED_RESIDUAL") in ("0", "1"):
+        changes["residual_epilogue"] = env["TJ_DEFERRED_RESIDUAL"] == "0"
     if env.get("TJ_NO_PACK") == "1":
         changes["pack_prefix"] = False
     if env.get("TJ_FFN") in FFN_KINDS:

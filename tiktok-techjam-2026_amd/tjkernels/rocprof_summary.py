@@ -37,6 +37,7 @@ from __future__ import annotations
 import argparse
 import collections
 import csv
+import re
 from typing import Dict, List, Optional, Tuple
 
 # add_layernorm_kernel and add_layernorm_parts_kernel (the split-delta sum
@@ -60,6 +61,21 @@ def _labels(layers: int, fused: bool = False) -> List[str]:
         seq += ["ffn_fused"] if fused else ["add_layernorm", "gemm_ffn1_gelu", "gemm_ffn2_residual"]
     seq.append("ln_final")
     return seq
+
+
+def _gemm_epilogue(name: str) -> Optional[int]:
+    """EPI template argument of a gemm_dtl_kernel<T, BM, BN, WM, WN, BKB,
+    STAGES, EPI, KSPLIT> name (2: residual read-modify-write)."""
+    ints = re.findall(r"Li(\d+)E", name.split(GEMM, 1)[1]) if GEMM in name else []
+    return int(ints[6]) if len(ints) >= 8 else None
+
+
+def _relabel(label: str, name: str) -> str:
+    # the out-proj / FFN2 of a deferred-residual plan write their output for
+    # the next LayerNorm instead of adding into the residual
+    if label.endswith("_residual") and _gemm_epilogue(name) not in (None, 2):
+        return label[:-len("_residual")]
+    return label
 
 
 def _kind_ok(label: str, name: str) -> bool:
@@ -94,7 +110,8 @@ def _forwards(rows: List[dict], layers: int) -> Dict[Tuple, List[List[Tuple[str,
                 seq = tjk[i:i + len(labels)]
                 if (len(seq) == len(labels) and all(_kind_ok(lab, r["Kernel_Name"]) for lab, r in zip(labels, seq))
                         and not any(_is_first_ln(r["Kernel_Name"]) for r in seq[1:])):
-                    out[(_grid(seq[0]), tuple(r["Kernel_Name"] for r in seq))].append(list(zip(labels, seq)))
+                    out[(_grid(seq[0]), tuple(r["Kernel_Name"] for r in seq))].append(
+                        [(_relabel(lab, r["Kernel_Name"]), r) for lab, r in zip(labels, seq)])
                     i += len(labels)
                     matched = True
                     break

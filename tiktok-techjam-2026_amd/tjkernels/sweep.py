@@ -17,6 +17,7 @@ CPU oracle and the CPU baseline (with ``--cpu``).
 Ablation variants (each against the full stack on the same workloads):
   * without hipGraph capture             TJ_NO_GRAPH=1
   * deferred residual (reference scheme) TJ_DEFERRED_RESIDUAL=1
+  * residual added in the GEMM epilogues  TJ_DEFERRED_RESIDUAL=0
   * library tile rule, no measured tiles TJ_GEMM_TUNE=0
   * padded rows computed (no packing)    TJ_NO_PACK=1
   * plain attention kernel (plan 1)      TJ_ATTN_PLAN=1
@@ -49,6 +50,7 @@ LEAVE_ONE = [
     ("full stack (heuristic plan)", {}),
     ("without hipGraph capture", {"TJ_NO_GRAPH": "1"}),
     ("deferred residual", {"TJ_DEFERRED_RESIDUAL": "1"}),
+    ("residual in the GEMM epilogues", {"TJ_DEFERRED_RESIDUAL": "0"}),
     ("library tile rule", {"TJ_GEMM_TUNE": "0"}),
     ("padded rows computed", {"TJ_NO_PACK": "1"}),
     ("plain attention kernel", {"TJ_ATTN_PLAN": "1"}),
