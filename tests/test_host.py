@@ -161,8 +161,7 @@ def test_override_and_env_knobs(monkeypatch):
     monkeypatch.setattr(plans_mod, "TUNED", plans_mod.PlanTable(Path("/nonexistent/plans.json")))
     dev = torch.device("cuda", 0)
     base = plans_mod.select_plan(4, 2048, 1024, 16, 4096, 4, True, torch.bfloat16, dev)
-    # C4: launched eagerly, outputs deferred to the next LayerNorm (the reference's scheme)
-    assert not base.cuda_graph and base.compute_dtype == torch.bfloat16 and not base.residual_epilogue
+    assert not base.cuda_graph and base.compute_dtype == torch.bfloat16 and base.residual_epilogue
     assert base.ffn == "gemm"  # d = 1024: the two-launch FFN
     small = plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev)
     assert small.cuda_graph and small.residual_epilogue  # launch-bound: replayed as a hipGraph
@@ -192,7 +191,7 @@ def test_override_and_env_knobs(monkeypatch):
     monkeypatch.setenv("TJ_ATTN_BLOCK", "1")
     assert plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev).attn_block
     monkeypatch.setenv("TJ_DEFERRED_RESIDUAL", "0")
-    assert plans_mod.select_plan(4, 2048, 1024, 16, 4096, 4, True, torch.bfloat16, dev).residual_epilogue
+    assert plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev).residual_epilogue
     monkeypatch.setenv("TJ_DEFERRED_RESIDUAL", "1")
     monkeypatch.setenv("TJ_LN_GEMM", "1")
     assert plans_mod.select_plan(1, 128, 512, 8, 2048, 4, True, torch.float16, dev).ln_gemm
