@@ -82,6 +82,11 @@ def _attn_flops(qkv, causal, cu_seqlens=None):
     return 4.0 * h * hd * pairs
 
 
+# The traffic-calibration GEMM (see _breakdown): M x N x K bf16, tile plan 9
+# (64 x 64, direct-to-LDS).  tjkernels.rocprof_summary finds it by its grid.
+GEMM_CALIB_M, GEMM_CALIB_N, GEMM_CALIB_K, GEMM_CALIB_PLAN = 64, 65536, 1024, 9
+
+
 def _breakdown(engine, x, mask):
     """Per-kernel-class time of one eager forward: each tjk launch bracketed
     by HIP events on the current stream (the launch stream).  Also returns,
@@ -149,6 +154,18 @@ def _breakdown(engine, x, mask):
     dst.copy_(src)
     torch.cuda.synchronize()
     del src, dst
+    # A GEMM of known traffic checks that scale on the GEMMs' own access
+    # pattern (LDS DMA of 128-byte row pieces): 64 rows against a 128 MiB
+    # weight (65536 x 1024 bf16) that each 64-column tile reads once, so the
+    # fetch is the weight plus one copy of the 128 KiB A (and its bias) per XCD.
+    ga = torch.randn(GEMM_CALIB_M, GEMM_CALIB_K, device=x.device).to(torch.bfloat16)
+    gw = torch.randn(GEMM_CALIB_N, GEMM_CALIB_K, device=x.device).to(torch.bfloat16)
+    gb = torch.zeros(GEMM_CALIB_N, dtype=torch.bfloat16, device=x.device)
+    gc = torch.empty(GEMM_CALIB_M, GEMM_CALIB_N, dtype=torch.bfloat16, device=x.device)
+    torch.cuda.synchronize()
+    ops.gemm(ga, gw, gb, gc, ops.EPI_BIAS, GEMM_CALIB_PLAN)
+    torch.cuda.synchronize()
+    del ga, gw, gb, gc
     for label, flops, s0, s1 in events:
         c = classes.setdefault(label, {"ms": 0.0, "launches": 0, "flops": 0.0})
         c["ms"] += s0.elapsed_time(s1)

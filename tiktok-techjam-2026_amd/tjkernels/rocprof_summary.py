@@ -124,11 +124,35 @@ def _dur_us(r: dict) -> float:
     return (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
 
 
+# bench.py's traffic-calibration GEMM: 64 x 65536 x 1024 bf16 in 64 x 64
+# tiles (1024 workgroups of 256 threads); bytes it must fetch: the weight
+# once, plus the 128 KiB A and 128 KiB bias once per XCD
+CALIB_GEMM_GRID = 1024 * 256
+CALIB_GEMM_FETCH = 65536 * 1024 * 2 + 8 * (64 * 1024 * 2 + 65536 * 2)
+CALIB_GEMM_WRITE = 64 * 65536 * 2
+
+
 def _counter(path: str) -> Tuple[List[dict], Optional[float]]:
     rows = list(csv.DictReader(open(path)))
     rows.sort(key=lambda r: int(r["Dispatch_Id"]))
     copies = [float(r["Counter_Value"]) for r in rows if r["Kernel_Name"] == COPY]
     return rows, (max(copies) if copies else None)
+
+
+def _calib_gemm_kib(rows: List[dict]) -> Optional[float]:
+    """Counter value of the calibration GEMM: the first 64 x 64-tile GEMM
+    dispatch of its grid after the calibration copy (rows in dispatch
+    order; other launches of the same grid, e.g. 256 x 256 tiles of 8 waves,
+    are not it)."""
+    copies = [i for i, r in enumerate(rows) if r["Kernel_Name"] == COPY]
+    if not copies:
+        return None
+    big = max(copies, key=lambda i: float(rows[i]["Counter_Value"]))
+    for r in rows[big + 1:]:
+        name = r["Kernel_Name"]
+        if GEMM in name and _grid(r) == CALIB_GEMM_GRID and "Li64ELi64ELi2ELi2ELi128ELi2ELi0E" in name:
+            return float(r["Counter_Value"])
+    return None
 
 
 def _pmc_by_label(paths: List[str], layers: int) -> Dict[str, Dict[str, float]]:
@@ -220,6 +244,12 @@ def summarize(trace: str, layers: int = 4, fetch: Optional[str] = None,
                 return "\n".join(lines)
             factor = calib_bytes / (copy_kib * 1024.0)
             lines.append(f"  {tag}: calibration copy reads {copy_kib:.0f} KiB -> scale x{factor:.3f}")
+            gemm_kib = _calib_gemm_kib(crow)
+            if gemm_kib:
+                want = CALIB_GEMM_FETCH if tag == "fetch" else CALIB_GEMM_WRITE
+                got = gemm_kib * 1024.0 * factor
+                lines.append(f"  {tag}: calibration GEMM reads {gemm_kib:.0f} KiB x{factor:.3f} = "
+                             f"{got / 2**20:.1f} MiB against {want / 2**20:.1f} MiB known ({got / want:.3f})")
             gr = _forwards(crow, layers)
             grid = min(gr) if gr else None
             acc: Dict[str, List[float]] = collections.defaultdict(list)
