@@ -148,14 +148,27 @@ __global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
   tile_coords(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, pid_m, pid_n);
   const int m0 = pid_m * BM, n0 = pid_n * BN;
 
-  // Residual reads issued ahead of the operand DMAs, where their registers
-  // fit beside the accumulators (plus ~144 for fragments and addresses)
-  // without lowering the occupancy the LDS ring allows.
-  constexpr int WAVES_PER_SIMD = (NW * KSPLIT / 4) * (160 * 1024 / G::LDS);
+  // Bias and residual reads issued ahead of the operand DMAs, where their
+  // registers fit beside the accumulators (plus ~144 for fragments and
+  // addresses) without lowering the occupancy the LDS ring allows: their
+  // round trip then overlaps the main loop instead of ending the launch,
+  // which matters most for the short launches of a few hundred rows.  Wave
+  // tiles above 4 blocks of 32 x 32 keep the bias loads in the epilogue and
+  // prefetch only the residual, and only without a K split: there the
+  // fragments already bring the wave close to its 256 architectural
+  // registers (measured: 256 x 256 and 128 x 256 tiles spilled).
+  constexpr int WG_PER_CU = 160 * 1024 / G::LDS;
+  constexpr int WAVES_PER_SIMD = (WG_PER_CU * NW * KSPLIT + 3) / 4 > 1 ? (WG_PER_CU * NW * KSPLIT + 3) / 4 : 1;
+  constexpr int BUDGET = 512 / WAVES_PER_SIMD - FM * FN * 16 - 144;
+  constexpr int BIAS_REGS = FN * 4 * (int)sizeof(typename Quad<T>::raw) / 4;
   constexpr int PRE_REGS = FM * ResPrefetch<FM, FN>::NIT * 4;
-  constexpr bool PREFETCH = EPI == TJK_EPI_BIAS_RESIDUAL && KSPLIT == 1 &&
-                            FM * FN * 16 + PRE_REGS + 144 <= 512 / WAVES_PER_SIMD;
+  constexpr bool SMALL = sizeof(T) == 2 && FM * FN <= 4;
+  constexpr bool BIAS_PRE = SMALL && BIAS_REGS <= BUDGET;
+  constexpr bool PREFETCH = EPI == TJK_EPI_BIAS_RESIDUAL && (KSPLIT == 1 || SMALL) &&
+                            PRE_REGS + (BIAS_PRE ? BIAS_REGS : 0) <= BUDGET;
   typedef typename std::conditional<PREFETCH, ResPrefetch<FM, FN>, NoPrefetch>::type Pre;
+  BiasRaw<T, FN> bpre;
+  if constexpr (BIAS_PRE) bpre.load(bias, N, n0 + wn * G::WTN, lane);
   Pre pre;
   if constexpr (PREFETCH)
     pre.load(static_cast<const float*>(Cv), ldc, M, N, m0 + wm * G::WTM, n0 + wn * G::WTN, lane);
@@ -194,7 +207,8 @@ __global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
     }
   }
   epilogue<T, EPI, FM, FN, Pre>(acc, bias, Cv, ldc, M, N, m0 + wm * G::WTM, n0 + wn * G::WTN, lane,
-                                smem + XCH + wave * EpiStage<T, EPI, FN>::BYTES, pre);
+                                smem + XCH + wave * EpiStage<T, EPI, FN>::BYTES, pre,
+                                BIAS_PRE ? &bpre : nullptr);
 }
 
 // ------------------------------------------------------------------ plans

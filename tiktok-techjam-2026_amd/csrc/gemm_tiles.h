@@ -97,13 +97,42 @@ struct ResPrefetch {
   __device__ __forceinline__ float4 get(int j, int it) const { return r[j][it]; }
 };
 
+// The bias pieces of a wave's columns nw.. (the epilogue's layout: lane
+// (l32, hi) needs columns nw + 32 i + 8 g + 4 hi .. +3), raw.  All loads go
+// out before any is used -- one memory round trip; a load under a per-lane
+// condition would be waited for on its own, one round trip per load -- with
+// columns past N clamped into range (N % 4 == 0, N >= 4) and zeroed when
+// converted.  A kernel whose registers allow it loads them before its main
+// loop, which takes that round trip off the end of the launch.
+template <typename T, int FN>
+struct BiasRaw {
+  typedef typename Quad<T>::raw Raw;
+  Raw r[FN][4];
+  __device__ __forceinline__ void load(const T* __restrict__ bias, int N, int nw, int lane) {
+    const int hi = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) r[i][g] = Raw{};
+    if (bias != nullptr) {
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          r[i][g] = *reinterpret_cast<const Raw*>(bias + min(nw + i * 32 + g * 8 + hi * 4, N - 4));
+    }
+  }
+};
+
 // Stores this wave's (32 FM) x (32 FN) block at rows mw.., columns nw.. of
 // C (rows >= M and columns >= N dropped).  `stage` is the wave's private
-// EpiStage<T, EPI, FN>::BYTES of LDS.
+// EpiStage<T, EPI, FN>::BYTES of LDS.  `bpre`, when given, holds the bias
+// pieces already loaded (BiasRaw::load with the same bias, N, nw, lane).
 template <typename T, int EPI, int FM, int FN, typename Pre = NoPrefetch>
 __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* __restrict__ bias,
                                          void* __restrict__ Cv, int64_t ldc, int M, int N, int mw, int nw,
-                                         int lane, char* __restrict__ stage, const Pre& pre = Pre()) {
+                                         int lane, char* __restrict__ stage, const Pre& pre = Pre(),
+                                         const BiasRaw<T, FN>* bpre = nullptr) {
   typedef EpiStage<T, EPI, FN> E;
   typedef typename E::S S;
   constexpr int LPR = E::WTN / E::SV;  // 16-byte pieces per staged row
@@ -115,30 +144,17 @@ __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* _
   // that keeps every row 16-byte aligned; otherwise pieces go out as halves.
   const bool a16 = ((uintptr_t)Cv & 15) == 0 && (ldc % E::SV) == 0;
 
-  // Bias of this wave's columns.  All loads go out before any is used --
-  // one memory round trip; a load under a per-lane condition would be
-  // waited for on its own, one round trip per load -- with columns past N
-  // clamped into range and zeroed afterwards (N % 4 == 0, N >= 4).
-  typedef typename Quad<T>::raw Raw;
-  Raw braw[FN][4];
-#pragma unroll
-  for (int i = 0; i < FN; ++i)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) braw[i][g] = Raw{};
-  if (bias != nullptr) {
-#pragma unroll
-    for (int i = 0; i < FN; ++i)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        braw[i][g] = *reinterpret_cast<const Raw*>(bias + min(nw + i * 32 + g * 8 + hi * 4, N - 4));
-  }
+  // bias of this wave's columns (loaded here unless the caller did)
+  BiasRaw<T, FN> own;
+  if (bpre == nullptr) own.load(bias, N, nw, lane);
+  const BiasRaw<T, FN>& braw = bpre != nullptr ? *bpre : own;
   float4 bv[FN][4];
 #pragma unroll
   for (int i = 0; i < FN; ++i)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int n = nw + i * 32 + g * 8 + hi * 4;
-      bv[i][g] = n < N ? Quad<T>::to(braw[i][g]) : make_float4(0.f, 0.f, 0.f, 0.f);
+      bv[i][g] = n < N ? Quad<T>::to(braw.r[i][g]) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 
 #pragma unroll
