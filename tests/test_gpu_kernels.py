@@ -116,8 +116,8 @@ def _gemm_case(device, m, n, k, dt, epi, plan, seed=0):
 # Plans of the staged kernel take any K % 8 == 0; direct-to-LDS plans need
 # K % 64 == 0 (bf16/fp16) and reject other K with TJK_EUNSUPPORTED.
 # Plans 18-20 use 4-, 8- and 6-slot rings with the spread DMA schedule;
-# 16, 17 and 21-25 split K between 2 or 4 wave groups of one workgroup.
-STAGED16, DTL16, DTL16_K32 = range(0, 6), list(range(6, 26)), ()
+# 16, 17 and 21-27 split K between 2 or 4 wave groups of one workgroup.
+STAGED16, DTL16, DTL16_K32 = range(0, 6), list(range(6, 28)), ()
 STAGED32, DTL32 = range(0, 2), range(2, 5)
 
 
@@ -137,13 +137,14 @@ def test_gemm_plans(device, plan, dt):
             _gemm_case(device, 64, 64, 40, dt, ops.EPI_BIAS, plan)
 
 
-@pytest.mark.parametrize("plan", [15, 18, 19, 20, 21, 22, 23, 24, 25])
+@pytest.mark.parametrize("plan", [15, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27])
 @pytest.mark.parametrize("epi", [ops.EPI_BIAS_GELU, ops.EPI_BIAS_RESIDUAL])
 def test_gemm_deep_ring_and_prefetch_plans(device, plan, epi):
     # Deep rings (18-20): K from one tile (fewer tiles than ring slots) to a
-    # long pipeline.  Plans 15 and 18 read the residual before the main loop.
-    # K-split plans (21-23): fewer K tiles than groups, and counts that do
-    # not divide evenly between the groups.
+    # long pipeline.  Plans 15 and 18 read the residual before the main loop,
+    # the small K-split tiles (22-27) the residual and the bias.  K-split
+    # plans (21-27): fewer K tiles than groups, and counts that do not divide
+    # evenly between the groups.
     for m, n, k in ((200, 256, 64), (300, 384, 192), (5430, 1024, 4096), (1000, 516, 1024), (128, 512, 2048)):
         _gemm_case(device, m, n, k, torch.bfloat16, epi, plan)
 

@@ -453,7 +453,9 @@ def test_gemm_tile_classes_follow_the_library_table():
         cls = tiles.k_class(m, n, k, torch.bfloat16)
         assert cls == tiles.k_class(m, n, k, torch.bfloat16)
         assert set(tiles.candidates(m, n, k, torch.bfloat16)) == set(tiles.CLASS_TILES_16[cls])
-    assert tiles.k_class(128, 512, 2048, torch.bfloat16) == 2   # C2 FFN2: launch-bound
+    assert tiles.k_class(128, 512, 2048, torch.bfloat16) == 4   # C2 FFN2: launch-bound, long K
+    assert tiles.k_class(128, 1536, 512, torch.bfloat16) == 2   # C2 QKV
+    assert tiles.k_class(2442, 768, 3072, torch.bfloat16) == 2  # C3 FFN2
     assert tiles.k_class(5430, 4096, 1024, torch.bfloat16) == 1  # C4 FFN1
     assert tiles.candidates(96, 512, 128, torch.float32) == tiles.CANDIDATES_32
 

@@ -274,6 +274,12 @@ static const GemmPlan kPlans16[] = {
     // 32 x 64 and 32 x 32 a launch spreads over 2x and 4x more CUs.
     {kDtl, 32, 64, 1, 2, 128, 4, 0.35, 2},    // 24 4 waves, 96 KB
     {kDtl, 32, 32, 1, 1, 128, 4, 0.30, 2},    // 25 2 waves, 64 KB
+    // 26, 27: the 32-row tiles with K split between four groups, for a
+    // launch of a few dozen tiles with long K (C2's FFN2, K = 2048): each
+    // group streams every 4th K tile, so a workgroup has four rings' worth
+    // of K tiles in flight and the serial chain is a quarter of K.
+    {kDtl, 32, 32, 1, 1, 128, 4, 0.30, 4},    // 26 4 waves, 128 KB
+    {kDtl, 32, 64, 1, 2, 128, 3, 0.35, 4},    // 27 8 waves, 144 KB
 };
 // fp32.
 static const GemmPlan kPlans32[] = {
@@ -369,6 +375,8 @@ typedef DtlLauncher<128, 2, 2> D2K2;
 typedef DtlLauncher<128, 2, 4> D2K4;
 typedef DtlLauncher<128, 4, 2> D4K2;
 typedef DtlLauncher<128, 3, 2> D3K2;
+typedef DtlLauncher<128, 4, 4> D4K4;
+typedef DtlLauncher<128, 3, 4> D3K4;
 typedef DtlLauncher<128, 4> D4;
 typedef DtlLauncher<128, 6> D6;
 typedef DtlLauncher<128, 8> D8;
@@ -414,6 +422,8 @@ static int run_gemm(int plan, int epi, const GemmArgs& g) {
       TJK_GEMM_CASE(23, D3K2, 128, 64, 2, 2)
       TJK_GEMM_CASE(24, D4K2, 32, 64, 1, 2)
       TJK_GEMM_CASE(25, D4K2, 32, 32, 1, 1)
+      TJK_GEMM_CASE(26, D4K4, 32, 32, 1, 1)
+      TJK_GEMM_CASE(27, D3K4, 32, 64, 1, 2)
     }
   }
 #undef TJK_GEMM_CASE

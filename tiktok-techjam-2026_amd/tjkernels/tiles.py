@@ -12,7 +12,9 @@ the order in which they add up the K dimension:
 
 * class 1: one accumulator per output element, K tiles in order;
 * class 2: two wave groups take alternate K tiles and their two sums are
-  added at the end (the in-workgroup K split).
+  added at the end (the in-workgroup K split);
+* class 4: four wave groups take every 4th K tile, their sums added in group
+  order at the end.
 
 Every plan of a class produces the same bits for the same inputs, so the
 class is fixed by the shape (``k_class``) and only tiles within it are
@@ -20,7 +22,9 @@ timed.  Two processes, or two boxes, therefore compute identical outputs
 whatever the timing picks.  ``k_class`` chooses the K split when a launch of
 128 x 64 tiles fits in one round of the CUs and K is long enough for the
 split to shorten the serial chain of K tiles (the launch-bound projections
-of C2 and C3's FFN2: 10.6 -> 8.5 us and 26.1 -> 23.0 us measured on MI355X).
+of C2 and C3's FFN2: 10.6 -> 8.5 us and 26.1 -> 23.0 us measured on MI355X),
+and the four-way split when one round of 32 x 64 tiles covers the launch and
+K >= 2048 (C2's FFN2).
 
 The LayerNorm-prologue GEMM (``tjk_gemm_ln``, LayerNorm computed inside
 the GEMM for launch-bound row counts) has its own plans, 32-row tiles of
@@ -50,8 +54,10 @@ from . import _lib, ops, timing
 #          96x128, 192x128 in a 4-slot ring, 64x64 / 128x64 in 8- / 6-slot rings;
 # class 2: 192x128, 128x128, 64x64 (4-slot ring), 128x64 (3-slot ring), each
 #          with K split between two groups of 4 waves; 32x64 and 32x32
-#          (4-slot rings) with K split between two groups of 2 / 1 waves.
-CLASS_TILES_16 = {1: (7, 8, 9, 12, 13, 14, 15, 18, 19, 20), 2: (16, 17, 22, 23, 24, 25)}
+#          (4-slot rings) with K split between two groups of 2 / 1 waves;
+# class 4: 64x64 (2-slot rings), 32x32 (4-slot) and 32x64 (3-slot) with K split
+#          between four groups of 4 / 1 / 2 waves.
+CLASS_TILES_16 = {1: (7, 8, 9, 12, 13, 14, 15, 18, 19, 20), 2: (16, 17, 22, 23, 24, 25), 4: (21, 26, 27)}
 CANDIDATES_32 = (2, 3, 4)  # fp32: class 1 only
 MAX_ENTRIES = 256
 M_BUCKET = 64
@@ -63,6 +69,8 @@ def k_class(m: int, n: int, k: int, dtype: torch.dtype) -> int:
     """K-summation class of the tile used for out[m, n] = a[m, k] w[n, k]^T."""
     if dtype == torch.float32:
         return 1
+    if ((m + 31) // 32) * ((n + 63) // 64) <= 256 and k >= 2048:
+        return 4
     one_round = ((m + 127) // 128) * ((n + 63) // 64) <= 256
     return 2 if one_round and k >= 512 else 1
 
