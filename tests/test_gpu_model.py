@@ -414,6 +414,10 @@ RESIDUAL_CASES = [
          plan=dict(ffn="fused", cuda_graph=True, attn_block=True)),
     dict(id="c3-fp16", workload="C3", residual=torch.float16, plan=dict(cuda_graph=False)),
     dict(id="c4-fp16", workload="C4", residual=torch.float16, plan=dict(cuda_graph=False)),
+    # f = 128 at 1024 rows: the single-launch FFN runs one f-slice, whose
+    # output goes through the partials buffer since the residual is 2-byte
+    dict(id="unsplit-fused-ffn", cfg=(8, 128, 256, 4, 128, 2, True), dtype=torch.bfloat16, padding=0.0,
+         residual=torch.float16, plan=dict(ffn="fused", cuda_graph=True)),
 ]
 # A bf16 residual stream is accepted by the plan but does not hold C4's
 # budget: 1241 of 8.4M elements out, max |d| 0.058 on this kernel set, and a
@@ -429,9 +433,29 @@ def test_two_byte_residual_plans(device, case):
     the workload's budget against the oracle: the deferred scheme with the
     two-launch and the single-launch FFN, the attention block, packed ragged
     sequences (C3, C4) and graph replay (C2)."""
-    w = WORKLOADS[case["workload"]]
-    plan = Plan(compute_dtype=w.dtype, residual_dtype=case["residual"], label=case["id"], **case["plan"])
-    _run_workload(device, case["workload"], seeds=(1, 2), plan=plan)
+    if "workload" in case:
+        w = WORKLOADS[case["workload"]]
+        plan = Plan(compute_dtype=w.dtype, residual_dtype=case["residual"], label=case["id"], **case["plan"])
+        _run_workload(device, case["workload"], seeds=(1, 2), plan=plan)
+        return
+    from tjkernels.engine import ffn_slices
+    cfg = TransformerConfig(*case["cfg"])
+    dtype = case["dtype"]
+    assert ffn_slices(cfg.batch_size * cfg.seq_len, cfg.ffn_dim) == 1
+    torch.manual_seed(13)
+    sd = {k: v.to(dtype).float() for k, v in UserOptimizedTransformer(cfg).state_dict().items()}
+    model = _module(cfg, sd, dtype, device)
+    plans_mod.set_override(Plan(compute_dtype=dtype, residual_dtype=case["residual"], label=case["id"],
+                                **case["plan"]))
+    try:
+        for seed in (1, 2):
+            x, mask = _inputs(cfg, dtype, seed=seed, padding=case["padding"])
+            with torch.inference_mode():
+                got = model(x.to(device), mask.to(device)).cpu()
+            ref = oracle.forward(sd, x.float(), mask, cfg.num_heads, cfg.causal, torch.float32)
+            _check(got, ref, mask, dtype)
+    finally:
+        plans_mod.set_override(None)
 
 
 def test_two_byte_residual_graph_equals_eager_and_env(device, monkeypatch):
