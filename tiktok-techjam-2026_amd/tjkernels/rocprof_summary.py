@@ -120,6 +120,13 @@ def _forwards(rows: List[dict], layers: int) -> Dict[Tuple, List[List[Tuple[str,
     return out
 
 
+def _timed(groups: Dict[Tuple, list]) -> Tuple:
+    """Key of the forward group the bench times: the one with the most
+    forwards (its warm-up, breakdown and timed steps; the bench's masked
+    comparison forward runs once or twice and may share the first grid)."""
+    return max(groups, key=lambda k: (len(groups[k]), k))
+
+
 def _dur_us(r: dict) -> float:
     return (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
 
@@ -156,7 +163,7 @@ def _calib_gemm_kib(rows: List[dict]) -> Optional[float]:
 
 
 def _pmc_by_label(paths: List[str], layers: int) -> Dict[str, Dict[str, float]]:
-    """{label: {counter: mean per dispatch}} over the first forward group of
+    """{label: {counter: mean per dispatch}} over the timed forward group of
     each multi-counter counter-collection file."""
     out: Dict[str, Dict[str, float]] = collections.defaultdict(dict)
     for path in paths:
@@ -172,7 +179,7 @@ def _pmc_by_label(paths: List[str], layers: int) -> Dict[str, Dict[str, float]]:
         if not groups:
             continue
         acc: Dict[str, Dict[str, List[float]]] = collections.defaultdict(lambda: collections.defaultdict(list))
-        for f in groups[min(groups)]:
+        for f in groups[_timed(groups)]:
             for lab, r in f:
                 for name, v in r["_counters"].items():
                     acc[lab][name].append(v)
@@ -251,7 +258,7 @@ def summarize(trace: str, layers: int = 4, fetch: Optional[str] = None,
                 lines.append(f"  {tag}: calibration GEMM reads {gemm_kib:.0f} KiB x{factor:.3f} = "
                              f"{got / 2**20:.1f} MiB against {want / 2**20:.1f} MiB known ({got / want:.3f})")
             gr = _forwards(crow, layers)
-            grid = min(gr) if gr else None
+            grid = _timed(gr) if gr else None
             acc: Dict[str, List[float]] = collections.defaultdict(list)
             for f in gr.get(grid, []):
                 for lab, r in f:
