@@ -32,6 +32,10 @@
 // (tjk_add_layernorm's delta_splits, in a fixed order), which is where the
 // reference adds its deferred FFN output (tjkernels/engine.py:232-264): no
 // cross-workgroup reduction, no waiting, deterministic results.
+//
+// The same resident-A machinery gives tjk_gemm_ln (end of this file): one
+// GEMM whose A operand is the LayerNorm of the fp32 residual, computed in the
+// kernel (LayerNorm applied in the GEMM's A-load).
 
 #include "gemm_tiles.h"
 
