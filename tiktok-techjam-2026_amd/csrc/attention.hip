@@ -534,8 +534,25 @@ __global__ __launch_bounds__(64) void flash_short_kernel(
 // Cache-policy bits of buffer loads / stores (sc0 = 1, sc1 = 16): sc1 makes
 // an access device-coherent, sc0 sc1 on a store writes through to memory.
 constexpr int kFaSc1 = 16, kFaSc0Sc1 = 17;
+typedef __attribute__((address_space(3))) void lds_void;
+
 constexpr int kFaSpinLimit = 1 << 20;  // polls of a split item's flag before giving up (>= 0.1 s)
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer descriptor over `bytes` bytes at p (stride 0, raw dword access).
+__device__ __forceinline__ u32x4 fa_rsrc(const void* p, int bytes) {
+  const uint64_t a = (uint64_t)p;
+  return u32x4{(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, (uint32_t)bytes, 0x00020000u};
+}
+// One LDS DMA: each lane copies 16 bytes at voff of the descriptor's range to
+// LDS byte lds_addr + 16 * lane.  Issued as inline asm so that the compiler
+// does not track it: for an LDS read it cannot tell apart from a DMA's
+// destination (the transposing ds_read_b64_tr_b16 carries no alias
+// information) it would otherwise wait for every copy in flight.  The ring's
+// own s_waitcnt vmcnt + s_barrier order the copies against the reads.
+__device__ __forceinline__ void fa_lds_dma16(u32x4 rsrc, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rsrc), "{m0}"(lds_addr));
+}
 
 // NW waves per workgroup own BMQ = 32 NW queries.  NW = 4 (two workgroups
 // per CU at head_dim <= 64, one above).  NW = 8 is the head_dim-128 grid
@@ -563,8 +580,35 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
   constexpr int KPT = KITEMS / NT, VPT = (VITEMS + NT - 1) / NT;
   static_assert(KITEMS % NT == 0, "K tile must split evenly over the threads");
 
-  __shared__ __attribute__((aligned(16))) T sK[NST][BNK * LDK];
-  __shared__ __attribute__((aligned(16))) T sV[NST][HDP * LDV];
+  // K / V ring.  DMA (head_dim 64 / 128 with the full head dimension, no
+  // key mask, 4 waves): tiles are copied straight into LDS by buffer_load
+  // ... lds, K and V both key-major with 128- / 256-byte rows whose 16-byte
+  // chunks are XOR-swizzled by row, and V^T fragments are gathered with the
+  // transposing ds_read_b64_tr_b16.  Otherwise tiles pass through registers,
+  // V stored transposed.  (The 8-wave head-dim-128 kernel keeps the register
+  // path: its DMA form measured no faster.)
+  constexpr bool DMA = FULLHD && !KEYMASK && HDP >= 64 && NW == 4;
+  constexpr int RB = HDP * (int)sizeof(T);  // DMA: bytes per K / V row
+  constexpr int CPR = RB / 16, RPI = 64 / CPR, TILE_B = BNK * RB;
+  char* smem;  // DMA ring: slot st holds K at st * 2 TILE_B, V TILE_B later
+  T (*sK)[BNK * LDK];
+  T (*sV)[HDP * LDV];
+  int* s_flag;  // the split-item merge's published flag
+  if constexpr (DMA) {
+    __shared__ __attribute__((aligned(1024))) char ring[NST * 2 * TILE_B + 16];
+    smem = ring;
+    sK = nullptr;
+    sV = nullptr;
+    s_flag = reinterpret_cast<int*>(ring + NST * 2 * TILE_B);
+  } else {
+    __shared__ __attribute__((aligned(16))) T k_ring[NST][BNK * LDK];
+    __shared__ __attribute__((aligned(16))) T v_ring[NST][HDP * LDV];
+    __shared__ int flag;
+    smem = nullptr;
+    sK = k_ring;
+    sV = v_ring;
+    s_flag = &flag;
+  }
 
   const int BH = B * H;
   // Work item: from the scheduled list (bh, qb, key tiles [t_lo, t_hi),
@@ -704,6 +748,89 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
   };
   auto load_kv = [&](int t) __attribute__((always_inline)) { load_kv_into(t, rk, rv0, rv1); };
   auto store_kv = [&](int st) __attribute__((always_inline)) { store_kv_from(st, rk, rv0, rv1); };
+
+  // DMA path: chunk c of row r sits at physical chunk c ^ swz(r), which
+  // spreads the fragment reads of 16 consecutive rows over all banks.
+  // DMA instruction q of this wave fills the 1 KB block q*NW + wave of a
+  // tile: rows (q*NW + wave)*RPI + lane/CPR, lane's chunk landing at byte
+  // 16*lane, so it fetches logical chunk (lane % CPR) ^ swz(row).
+  constexpr int NDK = DMA ? TILE_B / 1024 / NW : 1;  // DMA instructions per wave per K (or V) tile
+  constexpr int NDT = 2 * NDK;                      // ... per K + V tile
+  static_assert(!DMA || NDK * 1024 * NW == TILE_B, "K / V tile must split over the waves");
+  auto swz = [](int r) __attribute__((always_inline)) {
+    return CPR == 8 ? ((r & 7) ^ ((r >> 3) & 1)) : (r & 15);
+  };
+  uint32_t dvoff[NDK];
+  const uint32_t lds_ring = (uint32_t)(uintptr_t)(lds_void*)smem;
+#pragma unroll
+  for (int q = 0; q < NDK; ++q) {
+    const int r = (q * NW + wave) * RPI + lane / CPR;
+    dvoff[q] = (uint32_t)r * row_bytes + (uint32_t)(((lane % CPR) ^ swz(r)) << 4);
+  }
+  // K and V of key tile t into ring slot st (a tile past the item's range
+  // gets an empty descriptor and moves nothing)
+  auto dma_kv = [&](int t, int st) __attribute__((always_inline)) {
+    const int64_t t_elems = (int64_t)t * BNK * ss;
+    const int nrec = t < t_hi ? span - (int)(t_elems * (int64_t)sizeof(T)) : 0;
+    const u32x4 rsk = fa_rsrc(qbase + sc + t_elems, nrec), rsv = fa_rsrc(qbase + 2 * sc + t_elems, nrec);
+    const uint32_t kb = lds_ring + (uint32_t)(st * 2 * TILE_B + wave * 1024);
+#pragma unroll
+    for (int q = 0; q < NDK; ++q) fa_lds_dma16(rsk, dvoff[q], kb + q * NW * 1024);
+#pragma unroll
+    for (int q = 0; q < NDK; ++q) fa_lds_dma16(rsv, dvoff[q], kb + TILE_B + q * NW * 1024);
+  };
+  // end of a ring step: this wave's copies of the tile two ahead have landed
+  // (only the newest tile's may still be in flight) and its LDS reads are
+  // done, then everyone's
+  auto step_barrier = [&]() __attribute__((always_inline)) {
+    if constexpr (DMA) {
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(NDT) : "memory");
+      asm volatile("s_barrier" ::: "memory");
+    } else {
+      __syncthreads();
+    }
+  };
+  typedef typename Mfma<T>::frag FragT;
+  // K fragment: row `row` of slot st, 16-byte chunk `ch` (8 head-dim elements)
+  auto kfrag = [&](int st, int row, int ch) __attribute__((always_inline)) -> FragT {
+    if constexpr (DMA)
+      return *reinterpret_cast<const FragT*>(smem + st * 2 * TILE_B + row * RB + ((ch ^ swz(row)) << 4));
+    else
+      return Mfma<T>::load(&sK[st][row * LDK + 8 * ch]);
+  };
+  // V^T fragment of the PV product: lane (l32, hi) gets V[keys 16 stp + 8 hi
+  // + 0..7][head-dim row hb*32 + l32].  DMA: two transposing reads of four
+  // keys each; in a group of 16 lanes, source lane s points at key
+  // kbase + s/4, head-dim elements c0 + 4 (s%4) .. +3, and lane i receives
+  // keys kbase + 0..3 of element c0 + i.  Read rd of step stp in block hb:
+  // key 16 stp + 8 hi + 4 rd + g (g = (lane & 15) / 4), element
+  // hb*32 + 16 ((lane >> 4) & 1) + 4 (lane & 3), i.e. chunk ch = 4 hb + 2
+  // ((lane >> 4) & 1) + ((lane & 3) >> 1), 8-byte half lane & 1.  Bit 2 of
+  // ch ^ swz(key) is hb ^ rd for every lane (bit 3 as well at 16 chunks per
+  // row, XOR hi), so the address is a per-lane base (two: +-2 chunks of
+  // 64 bytes by hi at 16 chunks) plus a compile-time offset.
+  const int vg = (lane & 15) >> 2;
+  const int vlow = ((2 * ((lane >> 4) & 1) + ((lane & 3) >> 1)) ^ vg ^ (CPR == 8 ? hi : 0)) & 3;
+  const int vlb = (8 * hi + vg) * RB + 16 * vlow + 8 * (lane & 1);
+  const int vlane[2] = {vlb + (CPR == 16 ? 128 * hi : 0), vlb - (CPR == 16 ? 128 * hi : 0)};
+  auto vfrag = [&](int st, int hb, int stp) __attribute__((always_inline)) -> FragT {
+    if constexpr (DMA) {
+      typedef short v4s __attribute__((ext_vector_type(4)));
+      const char* vb = smem + st * 2 * TILE_B + TILE_B;
+      v4s part[2];
+#pragma unroll
+      for (int rd = 0; rd < 2; ++rd) {
+        const int c = hb ^ rd;
+        part[rd] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4s*)(vb + (16 * stp + 4 * rd) * RB + 64 * c + vlane[(c >> 1) & 1]));
+      }
+      typedef short v8s __attribute__((ext_vector_type(8)));
+      const v8s both = {part[0][0], part[0][1], part[0][2], part[0][3], part[1][0], part[1][1], part[1][2], part[1][3]};
+      return __builtin_bit_cast(FragT, both);
+    } else {
+      return Mfma<T>::load(&sV[st][(hb * 32 + l32) * LDV + 8 * hi] + 16 * stp);
+    }
+  };
   // ring slot of key tile tt (slot 0 holds the item's first tile)
   auto slot_of = [&](int tt) { return (tt - t_lo) & (NST - 1); };
 
@@ -713,11 +840,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
     // LDS latency overlaps instead of being waited out before every MFMA
     typename Mfma<T>::frag kf[2][KC];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const T* kp = &sK[st][(kb * 32 + krow) * LDK + 8 * hi];
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int c = 0; c < KC; ++c) kf[kb][c] = Mfma<T>::load(kp + 16 * c);
-    }
+      for (int c = 0; c < KC; ++c) kf[kb][c] = kfrag(st, kb * 32 + krow, 2 * c + hi);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -775,11 +900,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
 #pragma unroll
     for (int stp = 0; stp < 4; ++stp) l_run = Mfma<T>::sum8(pf[stp], l_run);
 #pragma unroll
-    for (int hb = 0; hb < HB; ++hb) {
-      const T* vp = &sV[st][(hb * 32 + l32) * LDV + 8 * hi];
+    for (int hb = 0; hb < HB; ++hb)
 #pragma unroll
-      for (int stp = 0; stp < 4; ++stp) Mfma<T>::mma(o[hb], Mfma<T>::load(vp + 16 * stp), pf[stp]);
-    }
+      for (int stp = 0; stp < 4; ++stp) Mfma<T>::mma(o[hb], vfrag(st, hb, stp), pf[stp]);
   };
 
   // register r of block kb is key k0 + kb*32 + 16*(r/8) + 8*hi + r%8
@@ -861,7 +984,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
         for (int c = 0; c < KH; ++c)
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb)
-            kf[c][kb] = Mfma<T>::load(&sK[st][(kb * 32 + krow) * LDK + 8 * hi] + 16 * (half * KH + c));
+            kf[c][kb] = kfrag(st, kb * 32 + krow, 2 * (half * KH + c) + hi);
 #pragma unroll
         for (int c = 0; c < KH; ++c)
 #pragma unroll
@@ -881,13 +1004,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
 #pragma unroll
     for (int c = 0; c < KC; ++c)
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) kf[c][kb] = Mfma<T>::load(&sK[st][(kb * 32 + krow) * LDK + 8 * hi] + 16 * c);
+      for (int kb = 0; kb < 2; ++kb) kf[c][kb] = kfrag(st, kb * 32 + krow, 2 * c + hi);
 #pragma unroll
-    for (int hb = 0; hb < HB; ++hb) {
-      const T* vp = &sV[vst][(hb * 32 + l32) * LDV + 8 * hi];
+    for (int hb = 0; hb < HB; ++hb)
 #pragma unroll
-      for (int stp = 0; stp < 4; ++stp) vf[hb][stp] = Mfma<T>::load(vp + 16 * stp);
-    }
+      for (int stp = 0; stp < 4; ++stp) vf[hb][stp] = vfrag(vst, hb, stp);
     // every fragment read issued together, one wait for all of them
 #pragma unroll
     for (int c = 0; c < KC; ++c)
@@ -936,7 +1057,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
       for (int stp = 0; stp < 4; ++stp)
 #pragma unroll
         for (int hb = 0; hb < HB; ++hb)
-          Mfma<T>::mma(o[hb], Mfma<T>::load(&sV[vst][(hb * 32 + l32) * LDV + 8 * hi] + 16 * stp), pf[stp]);
+          Mfma<T>::mma(o[hb], vfrag(vst, hb, stp), pf[stp]);
     } else {
 #pragma unroll
       for (int stp = 0; stp < 4; ++stp)
@@ -950,17 +1071,30 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
   // previous step), and sc holds S(t).  A step first stores tile t+2 into
   // the slot tile t-2 freed, then loads tile t+3, so every global load has
   // a whole step to land; one barrier per step orders the slot reuse.
-  {
-    // both first tiles in flight at once (one global latency, not two)
-    uint4 rk1[KPT], rv01[VPT], rv11[VPT];
-    load_kv(t_lo);
-    load_kv_into(t_lo + 1, rk1, rv01, rv11);
-    store_kv(0);
-    store_kv_from(1, rk1, rv01, rv11);
+  if constexpr (DMA) {
+    // the first three tiles in flight at once; the first two have landed
+    // at the barrier
+    dma_kv(t_lo, 0);
+    dma_kv(t_lo + 1, 1);
+    dma_kv(t_lo + 2, 2);
+    step_barrier();
+  } else {
+    {
+      // both first tiles in flight at once (one global latency, not two)
+      uint4 rk1[KPT], rv01[VPT], rv11[VPT];
+      load_kv(t_lo);
+      load_kv_into(t_lo + 1, rk1, rv01, rv11);
+      store_kv(0);
+      store_kv_from(1, rk1, rv01, rv11);
+    }
+    __syncthreads();
+    load_kv(t_lo + 2);
   }
-  __syncthreads();
-  load_kv(t_lo + 2);
 
+  // The compiler does not see the ring's copies (inline asm) and waits for
+  // the Q loads before their first use: here, once, not in the interior loop
+  // (where its wait would cover every copy in flight on each pass).
+  if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
   f32x16 scur[2];
   if (t_hi > t_lo) qk(0, scur);
   // Interior tiles: every key below the workgroup's first query and inside
@@ -975,13 +1109,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
   Frag pf[4];
   // one interior step; j is tile t's ring slot (a constant in the unrolled loop)
   auto istep = [&](int tt, int j, const f32x16 (&sc)[2], f32x16 (&sn)[2]) __attribute__((always_inline)) {
-    store_kv((j + 2) & (NST - 1));
-    load_kv(tt + 3);
+    if constexpr (DMA) {
+      dma_kv(tt + 3, (j + 3) & (NST - 1));
+    } else {
+      store_kv((j + 2) & (NST - 1));
+      load_kv(tt + 3);
+    }
     Frag vf[HB][4];
     const float lt = qk_exp((j + 1) & (NST - 1), sn, sc, pf, j, vf);
     settle(sc, pf, lt);
     pv(vf, pf, j);
-    __syncthreads();
+    step_barrier();
   };
   // four tiles per trip (one turn of the ring), scores ping-pong scur <-> salt
   for (; t + 3 < n_int; t += 4) {
@@ -1008,8 +1146,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
     }
   }
   for (; t < t_hi; ++t) {
-    store_kv(slot_of(t + 2));
-    load_kv(t + 3);
+    if constexpr (DMA) {
+      dma_kv(t + 3, slot_of(t + 3));
+    } else {
+      store_kv(slot_of(t + 2));
+      load_kv(t + 3);
+    }
     f32x16 snext[2];
     const bool act_next = t + 1 < t_hi && (!causal || (t + 1) * BNK <= wq0 + 31);
     if (act_next) qk(slot_of(t + 1), snext);
@@ -1020,12 +1162,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
       if (KEYMASK || (causal && t * BNK + BNK - 1 > wq0) || t * BNK + BNK > kend) mask_tile(t, scur);
       softmax_pv(slot_of(t), scur);
     }
-    __syncthreads();
+    step_barrier();
     if (act_next) {
       scur[0] = snext[0];
       scur[1] = snext[1];
     }
   }
+  // no copy may still be writing this workgroup's LDS when it ends
+  if constexpr (DMA) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // normalise and store: register r of block hb is hd row hb*32 + 8*(r/4) + 4*hi + r%4
   const int q = wq0 + l32;
@@ -1079,7 +1223,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
     //   O = O_hi a_hi + O_lo a_lo,  l = l_hi a_hi + l_lo a_lo,
     //   a_x = 2^(m_x - max(m_lo, m_hi)),  in this order every time.
     const int ps = -2 - slot;
-    __shared__ int s_published;
+    int& s_published = *s_flag;
     if (tid == 0) {
       int v = __hip_atomic_load(&flags[ps], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       for (int spins = 0; v != 1 && spins < kFaSpinLimit; ++spins) {
