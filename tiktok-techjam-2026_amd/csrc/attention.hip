@@ -749,8 +749,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
   auto load_kv = [&](int t) __attribute__((always_inline)) { load_kv_into(t, rk, rv0, rv1); };
   auto store_kv = [&](int st) __attribute__((always_inline)) { store_kv_from(st, rk, rv0, rv1); };
 
-  // DMA path: chunk c of row r sits at physical chunk c ^ swz(r), which
-  // spreads the fragment reads of 16 consecutive rows over all banks.
+  // DMA path: chunk c of row r sits at physical chunk c ^ swz(r).  With row
+  // bits r0..r3, swz = r1 | r3 << 1 | (r1 ^ r2) << 2 at 8 chunks per row and
+  // r0 | r1 << 1 | (r0 ^ r2) << 2 | (r1 ^ r3) << 3 at 16.  Both spread
+  // the K fragment reads (16 lanes, rows 0..15 of a block, one logical chunk)
+  // over all 64 banks.  They also spread each half-wave of a transposing V
+  // read (4 consecutive rows, 64 bytes of each): the rows' 64-byte blocks
+  // land in distinct bank ranges (the row-major swizzle r & 15 gave 4-way
+  // conflicts there, 6 extra cycles per read at 16 chunks, 2 at 8).
   // DMA instruction q of this wave fills the 1 KB block q*NW + wave of a
   // tile: rows (q*NW + wave)*RPI + lane/CPR, lane's chunk landing at byte
   // 16*lane, so it fetches logical chunk (lane % CPR) ^ swz(row).
@@ -758,7 +764,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
   constexpr int NDT = 2 * NDK;                      // ... per K + V tile
   static_assert(!DMA || NDK * 1024 * NW == TILE_B, "K / V tile must split over the waves");
   auto swz = [](int r) __attribute__((always_inline)) {
-    return CPR == 8 ? ((r & 7) ^ ((r >> 3) & 1)) : (r & 15);
+    const int r0 = r & 1, r1 = (r >> 1) & 1, r2 = (r >> 2) & 1, r3 = (r >> 3) & 1;
+    return CPR == 8 ? (r1 | (r3 << 1) | ((r1 ^ r2) << 2)) : (r0 | (r1 << 1) | ((r0 ^ r2) << 2) | ((r1 ^ r3) << 3));
   };
   uint32_t dvoff[NDK];
   const uint32_t lds_ring = (uint32_t)(uintptr_t)(lds_void*)smem;
@@ -803,16 +810,20 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
   // keys each; in a group of 16 lanes, source lane s points at key
   // kbase + s/4, head-dim elements c0 + 4 (s%4) .. +3, and lane i receives
   // keys kbase + 0..3 of element c0 + i.  Read rd of step stp in block hb:
-  // key 16 stp + 8 hi + 4 rd + g (g = (lane & 15) / 4), element
-  // hb*32 + 16 ((lane >> 4) & 1) + 4 (lane & 3), i.e. chunk ch = 4 hb + 2
-  // ((lane >> 4) & 1) + ((lane & 3) >> 1), 8-byte half lane & 1.  Bit 2 of
-  // ch ^ swz(key) is hb ^ rd for every lane (bit 3 as well at 16 chunks per
-  // row, XOR hi), so the address is a per-lane base (two: +-2 chunks of
-  // 64 bytes by hi at 16 chunks) plus a compile-time offset.
-  const int vg = (lane & 15) >> 2;
-  const int vlow = ((2 * ((lane >> 4) & 1) + ((lane & 3) >> 1)) ^ vg ^ (CPR == 8 ? hi : 0)) & 3;
+  // key 16 stp + 8 hi + 4 rd + g (g = (lane & 15) / 4 = g0 + 2 g1), element
+  // hb*32 + 16 b4 + 4 (lane & 3) (b4 = (lane >> 4) & 1), i.e. chunk
+  // ch = 4 hb + 2 b4 + b1 (b1 = (lane & 3) >> 1), 8-byte half lane & 1.  In
+  // ch ^ swz(key) the bits below 2 depend on the lane only, and the bits from
+  // 2 up are c ^ x, c = hb ^ rd for every lane and x a per-lane value, so the
+  // address is one of HB per-lane bases (by c) plus a compile-time offset.
+  const int vg = (lane & 15) >> 2, g0 = vg & 1, g1 = vg >> 1;
+  const int b4 = (lane >> 4) & 1, b1 = (lane & 3) >> 1;
+  const int vlow = CPR == 8 ? ((b1 ^ g1) | ((b4 ^ hi) << 1)) : ((b1 ^ g0) | ((b4 ^ g1) << 1));
+  const int vx = CPR == 8 ? g1 : (g0 | ((g1 ^ hi) << 1));
   const int vlb = (8 * hi + vg) * RB + 16 * vlow + 8 * (lane & 1);
-  const int vlane[2] = {vlb + (CPR == 16 ? 128 * hi : 0), vlb - (CPR == 16 ? 128 * hi : 0)};
+  int vlane[HB];
+#pragma unroll
+  for (int c = 0; c < HB; ++c) vlane[c] = vlb + 64 * (c ^ vx);
   auto vfrag = [&](int st, int hb, int stp) __attribute__((always_inline)) -> FragT {
     if constexpr (DMA) {
       typedef short v4s __attribute__((ext_vector_type(4)));
@@ -822,7 +833,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
       for (int rd = 0; rd < 2; ++rd) {
         const int c = hb ^ rd;
         part[rd] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) v4s*)(vb + (16 * stp + 4 * rd) * RB + 64 * c + vlane[(c >> 1) & 1]));
+            (__attribute__((address_space(3))) v4s*)(vb + (16 * stp + 4 * rd) * RB + vlane[c]));
       }
       typedef short v8s __attribute__((ext_vector_type(8)));
       const v8s both = {part[0][0], part[0][1], part[0][2], part[0][3], part[1][0], part[1][1], part[1][2], part[1][3]};
