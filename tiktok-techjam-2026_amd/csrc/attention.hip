@@ -581,13 +581,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
   static_assert(KITEMS % NT == 0, "K tile must split evenly over the threads");
 
   // K / V ring.  DMA (head_dim 64 / 128 with the full head dimension, no
-  // key mask, 4 waves): tiles are copied straight into LDS by buffer_load
-  // ... lds, K and V both key-major with 128- / 256-byte rows whose 16-byte
-  // chunks are XOR-swizzled by row, and V^T fragments are gathered with the
-  // transposing ds_read_b64_tr_b16.  Otherwise tiles pass through registers,
-  // V stored transposed.  (The 8-wave head-dim-128 kernel keeps the register
-  // path: its DMA form measured no faster.)
-  constexpr bool DMA = FULLHD && !KEYMASK && HDP >= 64 && NW == 4;
+  // key mask): tiles are copied straight into LDS by buffer_load ... lds, K
+  // and V both key-major with 128- / 256-byte rows whose 16-byte chunks are
+  // XOR-swizzled by row, and V^T fragments are gathered with the transposing
+  // ds_read_b64_tr_b16.  Otherwise tiles pass through registers, V stored
+  // transposed.
+  constexpr bool DMA = FULLHD && !KEYMASK && HDP >= 64;
   constexpr int RB = HDP * (int)sizeof(T);  // DMA: bytes per K / V row
   constexpr int CPR = RB / 16, RPI = 64 / CPR, TILE_B = BNK * RB;
   char* smem;  // DMA ring: slot st holds K at st * 2 TILE_B, V TILE_B later
