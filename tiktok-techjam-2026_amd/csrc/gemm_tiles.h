@@ -12,21 +12,29 @@ namespace tjk {
 constexpr int kGroupM = 8;
 
 // GELU(v) = 0.5 v (1 + erf(v / sqrt 2)) with erf from Abramowitz & Stegun,
-// Handbook of Mathematical Functions, eq. 7.1.26 (|error| <= 1.5e-7): for
-// z >= 0, erf z = 1 - t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-z^2) with
-// t = 1 / (1 + p z), and erf(-z) = -erf(z).  Branch-free (one reciprocal, one
-// exp2) -- the library erff branches on |z| and measured ~35 VALU
-// instructions per value with divergent lanes, most of the FFN1 epilogue.
+// Handbook of Mathematical Functions, eq. 7.1.28 (|error| <= 3e-7): for
+// z >= 0, erf z = 1 - (1 + a1 z + a2 z^2 + ... + a6 z^6)^-16, and
+// erf(-z) = -erf(z).  The polynomial is taken in |v| (coefficients
+// a_i / sqrt(2)^i), the 16th power by four squarings: one reciprocal and no
+// exponential, where eq. 7.1.26 needs both (the transcendental instructions
+// run at a quarter of the VALU rate, and the epilogue of an FFN1 tile is
+// VALU-bound).  Branch-free -- the library erff branches on |z| and measured
+// ~35 VALU instructions per value with divergent lanes.
 __device__ __forceinline__ float gelu_erf(float v) {
-  const float z = fabsf(v) * 0.70710678118654752440f;
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
-  float poly = fmaf(1.061405429f, t, -1.453152027f);
-  poly = fmaf(poly, t, 1.421413741f);
-  poly = fmaf(poly, t, -0.284496736f);
-  poly = fmaf(poly, t, 0.254829592f);
-  poly *= t;
-  const float e = __builtin_amdgcn_exp2f(-(z * z) * 1.4426950408889634f);  // exp(-z^2)
-  const float erf_v = copysignf(fmaf(-poly, e, 1.0f), v);
+  const float u = fabsf(v);
+  // a1..a6 = 0.0705230784, 0.0422820123, 0.0092705272, 0.0001520143,
+  // 0.0002765672, 0.0000430638, each divided by sqrt(2)^i
+  float p = fmaf(u, 5.382975e-06f, 4.8890637e-05f);
+  p = fmaf(p, u, 3.8003574e-05f);
+  p = fmaf(p, u, 3.2776264e-03f);
+  p = fmaf(p, u, 2.1141006e-02f);
+  p = fmaf(p, u, 4.9867347e-02f);
+  p = fmaf(p, u, 1.0f);
+  p *= p;
+  p *= p;
+  p *= p;
+  p *= p;  // p^16 (inf for large |v|: the reciprocal is then 0)
+  const float erf_v = copysignf(1.0f - __builtin_amdgcn_rcpf(p), v);
   const float hv = 0.5f * v;
   return fmaf(hv, erf_v, hv);
 }
