@@ -1077,10 +1077,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
   };
 
   // Ring invariant at the top of step t: LDS slots of tiles t and t+1 hold
-  // them, the staging registers hold tile t+2 (its loads in flight since the
-  // previous step), and sc holds S(t).  A step first stores tile t+2 into
-  // the slot tile t-2 freed, then loads tile t+3, so every global load has
-  // a whole step to land; one barrier per step orders the slot reuse.
+  // them, and sc holds S(t).  Register path: the staging registers hold tile
+  // t+2 (its loads in flight since the previous step); a step first stores
+  // tile t+2 into the slot tile t-2 freed, then loads tile t+3.  DMA path:
+  // tile t+2's copies are in flight into its slot; a step first issues tile
+  // t+3's copies into the slot tile t-1 freed.  Either way every global load
+  // has a whole step to land; one barrier per step orders the slot reuse.
   if constexpr (DMA) {
     // the first three tiles in flight at once; the first two have landed
     // at the barrier
