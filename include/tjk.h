@@ -8,9 +8,13 @@
  *     negative       invalid argument / unsupported shape or dtype
  *                    (nothing was launched; see tjk_last_error_string())
  *     positive       a hipError_t from the launch
- * No entry point allocates memory, synchronizes the host, or keeps mutable
- * global state, so all of them are safe inside hipGraph stream capture and
- * reentrant across streams.  Row-major layouts throughout.
+ * No entry point allocates memory or synchronizes the host, and all but one
+ * keep no mutable global state, so they are safe inside hipGraph stream
+ * capture and reentrant across streams.  The exception is
+ * tjk_flash_fwd_sched_static: it keeps a per-device table of its static
+ * workspace's address, filled once under a mutex, and every call on one
+ * device shares that workspace, so calls that overlap on one device race.
+ * Row-major layouts throughout.
  *
  * Reference interfaces replaced (paths relative to the reference repository):
  *   tjk_add_layernorm  <- fused_add_layernorm, tjkernels/kernels/__init__.py:48-70
@@ -47,7 +51,7 @@
 extern "C" {
 #endif
 
-#define TJK_ABI_VERSION 7
+#define TJK_ABI_VERSION 8
 
 /* dtypes */
 #define TJK_F32 0
@@ -86,6 +90,10 @@ const char* tjk_last_error_string(void);
  * row_index (may be NULL) makes the call a gather / scatter over `rows`
  * output rows: output row r reads res / delta row row_index[r]; a negative
  * index writes an all-zero output row and leaves res_out's row untouched.
+ * src_rows is the number of rows res and delta hold (read only with a
+ * row_index): an entry >= src_rows is treated like a negative one (zero
+ * row, nothing read) and counted, once per output row, in *index_errors
+ * (an int on the device, may be NULL; never reset by the call).
  * res_dtype, delta_dtype, res_out_dtype, out_dtype in
  * {TJK_F32, TJK_F16, TJK_BF16};
  * delta may be NULL.  Requires n % 4 == 0, n <= 8192, 8-byte aligned rows.
@@ -102,7 +110,8 @@ int tjk_add_layernorm(const void* res, int res_dtype, int64_t ld_res,
                       void* out, int out_dtype, int64_t ld_out,
                       const float* gamma, const float* beta,
                       int64_t rows, int64_t n, float eps,
-                      const int32_t* row_index, const uint8_t* row_mask, void* stream);
+                      const int32_t* row_index, int64_t src_rows, int* index_errors,
+                      const uint8_t* row_mask, void* stream);
 
 /*
  * C[m, n] = epilogue(sum_k A[m, k] * W[n, k] + bias[n]) -- W in nn.Linear
@@ -138,7 +147,9 @@ int tjk_gemm_plan_info(int dtype, int id, int* block_m, int* block_n, int* waves
  *              sequences; sequence b is rows cu_seqlens[b] .. cu_seqlens[b+1]-1
  *              of both the QKV buffer (row stride stride_s; stride_b unused)
  *              and `out`; only its own rows are read or written.  Exclusive
- *              with key_mask.
+ *              with key_mask.  The kernels bound what they read by it: a
+ *              length above seq is taken as seq, a negative one as 0, a
+ *              negative start as 0; the buffers must hold cu_seqlens[B] rows.
  * A query row with no admissible key is written as 0.
  * head_dim in [1, 128], head_dim % 8 == 0 (16-byte aligned rows).
  * plan_id: -1 chooses; 0 software-pipelined (2-byte types); 1 / 2 one / two
@@ -228,8 +239,8 @@ int tjk_flash_sched_occupancy(int head_dim, int dtype);
  * out + s * split_stride; tjk_add_layernorm(delta_splits = splits) then adds
  * their sum to the residual.  With splits == 1 and accumulate != 0 the
  * result is added into `out` (the fp32 residual) instead.
- * Supported: f / splits == 128; d in {128, 256, 512} (fp32: 128, 256); see
- * tjk_ffn_supported.  b1 / b2 may be NULL.
+ * Supported: f / splits in {64, 128}; d in {128, 256, 512} (fp32: 128,
+ * 256); see tjk_ffn_supported.  b1 / b2 may be NULL.
  */
 int tjk_ffn(const void* a, int a_dtype, int64_t lda, const float* ln_gamma, const float* ln_beta,
             float ln_eps, const void* w1, const void* b1, const void* w2, const void* b2, float* out,
@@ -275,7 +286,8 @@ int tjk_gemm_ln_plan_count(void);
  * their sum -- the out-projection output -- to the residual.  ctx_out (may
  * be NULL; leading dimension ld_ctx) also receives the context [rows, d].
  * Sequences: `batch` of `seq` tokens each (rows b*seq ..), or with
- * cu_seqlens (int32 [batch+1]) packed back to back, every length <= seq.
+ * cu_seqlens (int32 [batch+1]) packed back to back, every length <= seq
+ * (longer ones taken as seq, as in tjk_flash_fwd).
  * The same Q / K / V give the same context bits as tjk_flash_fwd plan 4.
  * Supported: see tjk_attn_block_supported (bf16 / fp16, head_dim 64,
  * d_model = 64 heads in {128, 256, 384, 512}, seq <= 128).

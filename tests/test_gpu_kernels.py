@@ -272,6 +272,40 @@ def test_add_layernorm_gather_scatter(device, out_dt):
                           row_index=torch.arange(8, dtype=torch.int32, device=device))
 
 
+
+@pytest.mark.parametrize("split_delta", [False, True])
+def test_add_layernorm_index_past_source_rows(device, split_delta):
+    """A row_index entry at or past the rows the call declares for res /
+    delta is not followed: that output row is written as zeros and counted
+    in the error word, once per row.  The indices used still point inside
+    the allocation (res is a prefix view of a larger tensor), so a broken
+    bound cannot read outside it."""
+    n, full, declared = 256, 24, 10
+    g = _gen(17)
+    base = torch.randn(full, n, generator=g).to(device)
+    res = base[:declared]
+    gamma, beta = torch.randn(n, generator=g).to(device), torch.randn(n, generator=g).to(device)
+    delta = None
+    if split_delta:
+        delta = torch.randn(3, full, n, generator=g).to(device)[:, :declared]
+    index = torch.tensor([0, 9, 10, 23, -1, 5, 12, 9], dtype=torch.int32, device=device)
+    errors = torch.zeros(1, dtype=torch.int32, device=device)
+    out = torch.full((index.numel(), n), float("nan"), dtype=torch.float32, device=device)
+    for _ in range(2):
+        ops.add_layernorm(res, delta, gamma, beta, 1e-5, out, row_index=index, index_errors=errors)
+    torch.cuda.synchronize()
+    assert errors.item() == 2 * 3  # entries 10, 23 and 12, on each of the two calls
+    got, idx = out.cpu(), index.cpu()
+    bad = idx >= declared
+    assert (got[bad] == 0).all() and (got[idx < 0] == 0).all()
+    x = res.double().cpu()
+    if split_delta:
+        x = x + delta.double().cpu().sum(0)
+    ref = oracle.layer_norm(x, gamma.double().cpu(), beta.double().cpu(), 1e-5)
+    ok = (idx >= 0) & ~bad
+    _close(got[ok], ref[idx[ok].long()], OUT_RTOL[torch.float32], 1e-5)
+
+
 # ------------------------------------------------------------------ attention
 
 def _attn_ref(qkv, causal, key_mask=None):
@@ -529,6 +563,28 @@ def test_flash_packed_sequences(device, dt, hd, causal):
             ref = _attn_ref(qkv[cu[b]:cu[b + 1]].unsqueeze(0), causal)
             _close(got[cu[b]:cu[b + 1]], ref, tol, tol)
         assert (got[t:] == 7.0).all(), "rows past the packed tokens were written"
+
+
+def test_flash_packed_length_above_seq_is_clamped(device):
+    """A packed sequence whose cu_seqlens length exceeds the launch's seq is
+    taken as seq rows long: its first seq rows get the attention of those
+    rows, the rows past them are neither read nor written.  The buffer holds
+    every row cu_seqlens names, so a broken clamp stays inside it."""
+    heads, hd, seq = 2, 64, 40
+    cu = [0, 70, 80]  # lengths 70 (> seq) and 10
+    g = _gen(23)
+    qkv = torch.randn(cu[-1], 3, heads, hd, generator=g).to(torch.bfloat16)
+    want0 = _attn_ref(qkv[0:seq][None], True)
+    want1 = _attn_ref(qkv[70:80][None], True)
+    cu_d = torch.tensor(cu, dtype=torch.int32, device=device)
+    for plan in range(5):  # every kernel: pipelined (0), grid (1-3), short (4)
+        out = torch.full((cu[-1], heads * hd), 7.0, dtype=torch.bfloat16, device=device)
+        ops.flash_attention(qkv.to(device), out, causal=True, cu_seqlens=cu_d, max_seqlen=seq, plan=plan)
+        torch.cuda.synchronize()
+        got = out.cpu().float()
+        assert (got[seq:70] == 7.0).all(), plan
+        assert (got[0:seq] - want0).abs().max() < 2e-2, plan
+        assert (got[70:80] - want1).abs().max() < 2e-2, plan
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])

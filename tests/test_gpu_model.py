@@ -235,6 +235,47 @@ def test_graph_equals_eager(device, dtype, ffn, whole):
         plans_mod.set_override(None)
 
 
+def test_whole_graph_hot_key_survives_cache_churn(device):
+    """Whole-forward capture: one key replayed between more new keys than
+    the graph cache holds keeps the static input / output it was captured
+    on, so each of its replays matches eager bit for bit (prefix lengths
+    are part of the key, so every new lengths tuple is a new graph)."""
+    cfg = TransformerConfig(2, 64, 128, 4, 256, 2, True)
+    dtype = torch.float16
+    torch.manual_seed(9)
+    eager = _module(cfg, UserOptimizedTransformer(cfg).state_dict(), dtype, device)
+    graphed = _module(cfg, eager.state_dict(), dtype, device)
+
+    def case(lengths, seed):
+        g = torch.Generator()
+        g.manual_seed(seed)
+        x = torch.randn(cfg.batch_size, cfg.seq_len, cfg.d_model, generator=g)
+        mask = torch.arange(cfg.seq_len)[None, :] < torch.tensor(lengths)[:, None]
+        return x.masked_fill(~mask[..., None], 0).to(dtype), mask
+
+    hot = case((64, 40), 1)
+    others = [case((64, 10 + 3 * i), 2 + i) for i in range(7)]
+    plans_mod.set_override(Plan(compute_dtype=dtype, cuda_graph=False, label="eager"))
+    try:
+        with torch.inference_mode():
+            want_hot = eager(hot[0].to(device), hot[1].to(device)).cpu()
+            want = [eager(x.to(device), m.to(device)).cpu() for x, m in others]
+    finally:
+        plans_mod.set_override(None)
+    plans_mod.set_override(Plan(compute_dtype=dtype, cuda_graph=True, whole_graph=True, label="whole"))
+    try:
+        with torch.inference_mode():
+            graphed(hot[0].to(device), hot[1].to(device))
+            graphed._tj_engine._graphs.max_entries = 3
+            for (x, m), w in zip(others, want):
+                got = graphed(hot[0].to(device), hot[1].to(device)).cpu()
+                assert torch.equal(got, want_hot)
+                assert torch.equal(graphed(x.to(device), m.to(device)).cpu(), w)
+            assert len(graphed._tj_engine._graphs) <= 3
+    finally:
+        plans_mod.set_override(None)
+
+
 BLOCK_CASES = [
     dict(id="c2-graph", workload="C2"),
     dict(id="ragged-causal", cfg=(6, 128, 256, 4, 512, 2, True), dtype=torch.bfloat16, padding=0.7),

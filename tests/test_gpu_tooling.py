@@ -2,9 +2,11 @@
 
 The autotuner mirrors the reference's bench/autotune.py:61-246: a plan is
 admitted only if no element uses more than ``margin`` of its budget
-max(atol, rtol |ref|) on the trial and held-out seeds; an inadmissible
-heuristic escalates to fp32 compute (:203-217); a knob change is kept only
-when it stays admissible and is at least 2% faster.  The sweep runs
+max(atol, rtol |ref|) on the trial and held-out seeds, measured here
+against the CPU oracle's outputs on those seeds (the reference measures
+against its baseline model, :120-131); an inadmissible heuristic escalates
+to fp32 compute (:203-217); a knob change is kept only when it stays
+admissible and is at least 2% faster.  The sweep runs
 ``bench.py`` per workload in its own process (bench/run_all.py:41-112).
 """
 
@@ -13,8 +15,9 @@ from pathlib import Path
 import pytest
 import torch
 
-from tjkernels import autotune, plans as plans_mod, sweep
-from tjkernels.workloads import WORKLOADS
+from oracle import model as oracle
+from tjkernels import autotune, ops as ops_mod, plans as plans_mod, sweep
+from tjkernels.workloads import WORKLOADS, make_inputs, make_state_dict
 
 pytestmark = pytest.mark.gpu
 
@@ -25,12 +28,24 @@ def _select(w, tmp_table, monkeypatch):
                                  torch.device("cuda", 0))
 
 
+def _oracle_refs(w, trials):
+    """The CPU oracle's fp32 outputs on the gate's inputs, in gate_seeds
+    order: the tuner's reference, independent of every plan it judges."""
+    sd = make_state_dict(w, seed=0)
+    refs = []
+    for seed in autotune.gate_seeds(trials):
+        x, mask, _ = make_inputs(w, seed=seed)
+        refs.append(oracle.forward(sd, x, mask, w.heads, w.causal, torch.float32))
+    return refs
+
+
 def test_autotune_admits_records_and_selects_a_plan(device, tmp_path, monkeypatch):
     w = WORKLOADS["C2"]
-    out = autotune.tune_workload(w, trials=1, margin=0.85, iters=5, verbose=False)
+    out = autotune.tune_workload(w, trials=1, margin=0.85, iters=5, verbose=False,
+                                 references=_oracle_refs(w, 1))
     assert out is not None
     key, plan, res = out
-    assert res["usage"] <= 0.85 and res["latency_ms"] > 0
+    assert res["usage"] <= 0.85 and res["latency_ms"] > 0  # measured against the oracle
     assert plan.compute_dtype == torch.float16 and plan.label == "autotuned"
     plan.validate()
     table = tmp_path / "plans.json"
@@ -39,19 +54,49 @@ def test_autotune_admits_records_and_selects_a_plan(device, tmp_path, monkeypatc
 
 
 def test_autotune_escalates_to_fp32_when_the_gate_rejects_fp16(device, tmp_path, monkeypatch):
-    """A margin no fp16 plan can meet (1% of the budget: fp16 rounding alone
-    uses more) but the fp32 plan can: the tuner escalates, records an fp32
-    plan, and select_plan then picks it."""
+    """A margin of 3.3% of the budget, measured against the CPU oracle: the
+    fp16 heuristic plan uses more (4.3% at C2 on the gate's seeds: fp16
+    activations) and is rejected; the fp32 escalation uses less (2.4%: its
+    output is still rounded to the model's fp16, which alone costs up to
+    2^-11 |ref| against a budget of 2e-2 |ref|) and is admitted.  The tuner
+    records the fp32 plan and select_plan then picks it."""
     w = WORKLOADS["C2"]
-    out = autotune.tune_workload(w, trials=1, margin=0.01, iters=5, verbose=False)
+    margin = 0.033
+    log = []
+    out = autotune.tune_workload(w, trials=1, margin=margin, iters=5, verbose=False,
+                                 references=_oracle_refs(w, 1), log=log)
+    first, esc = log[0], log[1]
+    assert first["tag"] == "heuristic" and first["plan"].compute_dtype == torch.float16
+    assert first["usage"] > margin, f"the fp16 plan used only {first['usage']:.4f} of its budget"
+    assert esc["tag"] == "escalate-fp32" and esc["usage"] <= margin, f"fp32 plan used {esc['usage']:.4f}"
     assert out is not None, "the fp32 escalation was not admitted"
     key, plan, res = out
     assert plan.compute_dtype == torch.float32 and plan.label == "autotuned-fp32"
-    assert res["usage"] <= 0.01
+    assert res["usage"] <= margin
     table = tmp_path / "plans.json"
     plans_mod.save_plans({key: plan}, table)
     chosen = _select(w, table, monkeypatch)
     assert chosen.compute_dtype == torch.float32 and chosen == plan
+
+
+def test_autotune_gate_rejects_a_corrupted_plan(device, monkeypatch):
+    """A planted error common to every plan -- every LayerNorm launched with
+    eps = 0.5 instead of the module's 1e-5 -- is rejected by the gate
+    measured against the oracle.  A gate referenced to this build's own
+    fp32 plan (computed with the same planted error) admits it, which is
+    why the tuner takes its reference from the caller."""
+    w = WORKLOADS["C2"]
+    plan = plans_mod.default_plan(w.batch, w.seq, w.d_model, w.heads, w.ffn_dim, w.layers, w.causal, w.dtype,
+                                  torch.device("cuda", 0))
+    ev = autotune._Evaluator(w, 1, 2, references=_oracle_refs(w, 1))
+    good = ev.evaluate(plan)
+    assert good["usage"] <= 0.85
+    real = ops_mod.add_layernorm
+    monkeypatch.setattr(ops_mod, "add_layernorm", lambda *a, **k: real(*a[:4], 0.5, *a[5:], **k))
+    bad = ev.evaluate(plan)
+    assert bad["usage"] > 1.0, f"the corrupted plan used only {bad['usage']:.2f} of its budget"
+    self_ref = autotune._Evaluator(w, 1, 2)  # its fp32 reference carries the same error
+    assert self_ref.evaluate(plan)["usage"] <= 0.85
 
 
 def test_sweep_runs_bench_in_a_subprocess(device, tmp_path):

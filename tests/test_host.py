@@ -38,18 +38,22 @@ def test_abi_rejects_bad_arguments_without_launching():
     assert lib.tjk_flash_fwd(None, 0, 0, 0, 0, None, 0, 1, 4, 1, 12, 0.5, 1, None, None,
                              None, _lib.BF16, -1, None) < 0
     assert lib.tjk_add_layernorm(None, 0, 8, None, 0, 0, 1, 0, None, 0, 0, None, 0, 8, None, None,
-                                 2, 6, 1e-5, None, None, None) < 0
+                                 2, 6, 1e-5, None, 0, None, None, None) < 0
     assert b"null pointer" in lib.tjk_last_error_string()
     # split deltas need a stride that keeps the slices apart
     fake = 1 << 20  # never dereferenced: the call is rejected first
     assert lib.tjk_add_layernorm(fake, 0, 8, fake, 0, 8, 4, 8, None, 0, 0, fake, 0, 8, fake, fake,
-                                 2, 8, 1e-5, None, None, None) == _lib.EINVAL
+                                 2, 8, 1e-5, None, 0, None, None, None) == _lib.EINVAL
     # the residual is written in place only in its own dtype and leading dimension
     assert lib.tjk_add_layernorm(fake, _lib.F32, 8, None, 0, 0, 1, 0, fake, _lib.F16, 8, fake, 0, 8, fake,
-                                 fake, 2, 8, 1e-5, None, None, None) == _lib.EINVAL
+                                 fake, 2, 8, 1e-5, None, 0, None, None, None) == _lib.EINVAL
     assert b"alias" in lib.tjk_last_error_string()
     assert lib.tjk_add_layernorm(fake, _lib.F16, 8, None, 0, 0, 1, 0, fake, 7, 8, fake, 0, 8, fake,
-                                 fake, 2, 8, 1e-5, None, None, None) == _lib.EINVAL  # bad res_out dtype
+                                 fake, 2, 8, 1e-5, None, 0, None, None, None) == _lib.EINVAL  # bad res_out dtype
+    # a row_index needs a source-row count it is bounded by
+    assert lib.tjk_add_layernorm(fake, _lib.F32, 8, None, 0, 0, 1, 0, None, 0, 0, fake, 0, 8, fake,
+                                 fake, 2, 8, 1e-5, fake, -1, None, None, None) == _lib.EINVAL
+    assert b"src_rows" in lib.tjk_last_error_string()
     # the single-launch FFN's shape gate (f / splits must be 128; d in {128, 256, 512})
     assert lib.tjk_ffn_supported(512, 2048, 16, _lib.F16) == 1
     assert lib.tjk_ffn_supported(128, 512, 4, _lib.F32) == 1
@@ -274,6 +278,20 @@ def test_packing_row_maps():
     empty = build_packing((0, 0), 4, torch.device("cpu"))
     assert empty.tokens == 0 and empty.gather.numel() == 0 and (empty.scatter == -1).all()
 
+
+
+def test_static_attention_workspace_rejects_too_many_slots():
+    """tjk_flash_fwd_sched_static refuses a work list whose split slots
+    exceed its static array before it makes any HIP call, so no device
+    pointer is needed (NULL everywhere, no stream)."""
+    lib = _lib.load()
+    cap = lib.tjk_flash_sched_static_bytes()
+    per_slot = lib.tjk_flash_partial_bytes(128, 1)
+    too_many = cap // per_slot + 1
+    assert lib.tjk_flash_partial_bytes(128, too_many) > cap
+    rc = lib.tjk_flash_fwd_sched_static(None, 384, 128, 128, None, 128, 1, 128, 1, 128, 0.1, 1, None, None, 1,
+                                        too_many, _lib.BF16, None)
+    assert rc == _lib.EUNSUPPORTED and b"static" in lib.tjk_last_error_string()
 
 def test_graph_capture_failure_degrades_to_eager(capsys):
     cache = GraphCache()

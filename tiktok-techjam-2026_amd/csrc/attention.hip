@@ -106,8 +106,8 @@ __global__ __launch_bounds__(256 * KS) void flash_fwd_kernel(
   int Sb = S;
   int64_t row0 = (int64_t)b * S, boff = (int64_t)b * sb;
   if (cu_seqlens != nullptr) {
-    row0 = cu_seqlens[b];
-    Sb = cu_seqlens[b + 1] - cu_seqlens[b];
+    row0 = max(cu_seqlens[b], 0);
+    Sb = min(max(cu_seqlens[b + 1] - cu_seqlens[b], 0), S);  // bounded by the launch's sequence length
     boff = row0 * ss;
   }
   const T* qbase = qkv + boff + (int64_t)h * sh;
@@ -423,8 +423,8 @@ __global__ __launch_bounds__(64) void flash_short_kernel(
   int Sb = S;
   int64_t row0 = (int64_t)b * S, boff = (int64_t)b * sb;
   if (cu_seqlens != nullptr) {
-    row0 = cu_seqlens[b];
-    Sb = cu_seqlens[b + 1] - cu_seqlens[b];
+    row0 = max(cu_seqlens[b], 0);
+    Sb = min(max(cu_seqlens[b + 1] - cu_seqlens[b], 0), S);  // bounded by the launch's sequence length
     boff = row0 * ss;
   }
   const T* qbase = qkv + boff + (int64_t)h * sh;
@@ -656,8 +656,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
   int Sb = S;
   int64_t row0 = (int64_t)b * S, boff = (int64_t)b * sb;
   if (cu_seqlens != nullptr) {
-    row0 = cu_seqlens[b];
-    Sb = cu_seqlens[b + 1] - cu_seqlens[b];
+    row0 = max(cu_seqlens[b], 0);
+    Sb = min(max(cu_seqlens[b + 1] - cu_seqlens[b], 0), S);  // bounded by the launch's sequence length
     boff = row0 * ss;
   }
   const T* qbase = qkv + boff + (int64_t)h * sh;

@@ -100,8 +100,8 @@ __global__ __launch_bounds__(256) void attn_block_kernel(
   int L = S;
   int64_t r0 = (int64_t)b * S;
   if (cu_seqlens != nullptr) {
-    r0 = cu_seqlens[b];
-    L = cu_seqlens[b + 1] - cu_seqlens[b];
+    r0 = max(cu_seqlens[b], 0);
+    L = min(max(cu_seqlens[b + 1] - cu_seqlens[b], 0), S);  // bounded by the launch's sequence length
   }
   L = min(L, kAbMaxK);  // the entry point requires lengths <= 128; this keeps LDS indices in range
   const int q0 = 32 * qb;

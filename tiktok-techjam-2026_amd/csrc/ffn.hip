@@ -344,11 +344,14 @@ __device__ __forceinline__ void layernorm_rows_to_lds(char* sa, const float* __r
   }
 }
 
+// Av and out are not __restrict__: with LayerNorm 2 inside (LNA) and an
+// unsplit accumulating launch they are the same fp32 residual, read into LDS
+// before the barrier that precedes every store to out.
 template <typename T, int D, int FC, bool LNA>
 __global__ __launch_bounds__(256) void ffn_fused_kernel(
-    const void* __restrict__ Av, int64_t lda, const float* __restrict__ gamma, const float* __restrict__ beta,
+    const void* Av, int64_t lda, const float* __restrict__ gamma, const float* __restrict__ beta,
     float eps, const T* __restrict__ W1, const T* __restrict__ b1, const T* __restrict__ W2,
-    const T* __restrict__ b2, float* __restrict__ out, int64_t ldo, int64_t split_stride, int accumulate, int M,
+    const T* __restrict__ b2, float* out, int64_t ldo, int64_t split_stride, int accumulate, int M,
     int f, int nrb, int splits) {
   typedef FfnLayout<T, D, FC> Lay;
   typedef typename Lay::P1 P1;

@@ -12,7 +12,9 @@
 // of tjkernels/engine.py:267-268) writes padded rows as exact zeros.
 //
 // A row index turns the kernel into a gather / scatter: output row r reads
-// input row row_index[r], or is written as zeros when the index is negative.
+// input row row_index[r], or is written as zeros when the index is negative
+// or not below the input's row count (the latter also counted in an error
+// word).
 // The engine uses it to pack the valid tokens of prefix-masked sequences
 // into consecutive rows (first LayerNorm) and to put them back in [B, S]
 // order with zero padded rows (final LayerNorm).
@@ -59,6 +61,24 @@ __device__ __forceinline__ void* res_row(void* base, int ro_dtype, int64_t row, 
   return static_cast<char*>(base) + row * ld * (ro_dtype == TJK_F32 ? 4 : 2);
 }
 
+// The gather / scatter map of a launch: output row r reads input row
+// index[r] (index == NULL: row r).  An entry at or past src_rows (the rows
+// res / delta hold) is not followed: the row is written as a hole (zeros)
+// and counted in *errors (if not NULL), once per row, by the calling lane.
+struct RowMap {
+  const int32_t* __restrict__ index;
+  int64_t src_rows;
+  int* errors;
+};
+
+__device__ __forceinline__ int64_t map_row(const RowMap& rm, int64_t row, bool count) {
+  if (rm.index == nullptr) return row;
+  const int64_t s = rm.index[row];
+  if (s < rm.src_rows) return s;
+  if (count && rm.errors != nullptr) atomicAdd(rm.errors, 1);
+  return -1;
+}
+
 // FULL: n == 256 * MAXCH, every lane's chunks in range (no per-chunk guards).
 template <typename TRes, typename TDelta, typename TOut, int MAXCH, bool FULL>
 __global__ __launch_bounds__(256) void add_layernorm_kernel(
@@ -67,13 +87,12 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(
     void* res_out, int ro_dtype, int64_t ld_res_out,
     TOut* __restrict__ out, int64_t ld_out,
     const float* __restrict__ gamma, const float* __restrict__ beta,
-    int64_t rows, int n, float eps, const int32_t* __restrict__ row_index,
-    const uint8_t* __restrict__ row_mask) {
+    int64_t rows, int n, float eps, RowMap rmap, const uint8_t* __restrict__ row_mask) {
   const int lane = threadIdx.x & 63;
   const int nch = n >> 2;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const bool live = row < rows;
-  const int64_t src = !live ? -1 : row_index != nullptr ? (int64_t)row_index[row] : row;
+  const int64_t src = !live ? -1 : map_row(rmap, row, lane == 0);
 
   // Chunks past the row end are read at the last chunk and dropped: loads
   // under a per-lane condition are waited for one at a time.
@@ -184,12 +203,12 @@ __global__ __launch_bounds__(256) void add_layernorm_parts_kernel(
     const float* __restrict__ parts, int64_t ld_parts, int n_parts, int64_t part_stride,
     void* res_out, int ro_dtype, int64_t ld_res_out, TOut* __restrict__ out, int64_t ld_out,
     const float* __restrict__ gamma, const float* __restrict__ beta, int n, float eps,
-    const int32_t* __restrict__ row_index, const uint8_t* __restrict__ row_mask) {
+    RowMap rmap, const uint8_t* __restrict__ row_mask) {
   constexpr int PER = 32 / MAXCH;  // slices per load batch of one wave
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nch = n >> 2;
   const int64_t row = blockIdx.x;
-  const int64_t src = row_index != nullptr ? (int64_t)row_index[row] : row;
+  const int64_t src = map_row(rmap, row, threadIdx.x == 0);
   __shared__ float4 s_sum[3][MAXCH][64];
   if (src < 0) {  // scatter hole: an exact zero row
     if (wave == 0) {
@@ -311,13 +330,13 @@ template <typename TRes, typename TOut>
 static int launch_ln_parts(const void* res, int64_t ld_res, const float* parts, int64_t ld_parts, int n_parts,
                            int64_t part_stride, void* res_out, int ro_dtype, int64_t ld_res_out, void* out, int64_t ld_out,
                            const float* gamma, const float* beta, int64_t rows, int n, float eps,
-                           const int32_t* row_index, const uint8_t* row_mask, hipStream_t stream) {
+                           const RowMap& rmap, const uint8_t* row_mask, hipStream_t stream) {
   const int nch = n / 4;
   const dim3 grid((unsigned)rows), block(256);
 #define TJK_LNP(MC)                                                                                           \
   hipLaunchKernelGGL((add_layernorm_parts_kernel<TRes, TOut, MC>), grid, block, 0, stream, (const TRes*)res,   \
                      ld_res, parts, ld_parts, n_parts, part_stride, res_out, ro_dtype, ld_res_out, (TOut*)out, ld_out, gamma, \
-                     beta, n, eps, row_index, row_mask)
+                     beta, n, eps, rmap, row_mask)
   if (nch <= 64) TJK_LNP(1);
   else if (nch <= 128) TJK_LNP(2);
   else TJK_LNP(4);
@@ -329,11 +348,11 @@ template <typename TRes, typename TDelta, typename TOut>
 static int launch_ln(const void* res, int64_t ld_res, const void* delta, int64_t ld_delta, int n_delta,
                      int64_t delta_stride, void* res_out, int ro_dtype, int64_t ld_res_out, void* out, int64_t ld_out,
                      const float* gamma, const float* beta, int64_t rows, int n, float eps,
-                     const int32_t* row_index, const uint8_t* row_mask, hipStream_t stream) {
+                     const RowMap& rmap, const uint8_t* row_mask, hipStream_t stream) {
   if constexpr (std::is_same<TDelta, float>::value) {
     if (n_delta > 1)
       return launch_ln_parts<TRes, TOut>(res, ld_res, (const float*)delta, ld_delta, n_delta, delta_stride, res_out,
-                                         ro_dtype, ld_res_out, out, ld_out, gamma, beta, rows, n, eps, row_index, row_mask,
+                                         ro_dtype, ld_res_out, out, ld_out, gamma, beta, rows, n, eps, rmap, row_mask,
                                          stream);
   }
   const int nch = n / 4;
@@ -341,7 +360,7 @@ static int launch_ln(const void* res, int64_t ld_res, const void* delta, int64_t
 #define TJK_LN_LAUNCH(MC, FULL)                                                                    \
   hipLaunchKernelGGL((add_layernorm_kernel<TRes, TDelta, TOut, MC, FULL>), grid, block, 0, stream,     \
                      (const TRes*)res, ld_res, (const TDelta*)delta, ld_delta, res_out, ro_dtype, ld_res_out, \
-                     (TOut*)out, ld_out, gamma, beta, rows, n, eps, row_index, row_mask)
+                     (TOut*)out, ld_out, gamma, beta, rows, n, eps, rmap, row_mask)
 #define TJK_LN_CASE(MC)                                   \
   if (nch <= 64 * MC) {                                   \
     if (nch == 64 * MC) TJK_LN_LAUNCH(MC, true);          \
@@ -373,17 +392,17 @@ template <typename TRes, typename TDelta>
 static int dispatch_out(int out_dtype, const void* res, int64_t ld_res, const void* delta,
                         int64_t ld_delta, int n_delta, int64_t delta_stride, void* res_out, int ro_dtype, int64_t ld_res_out, void* out,
                         int64_t ld_out, const float* gamma, const float* beta, int64_t rows,
-                        int n, float eps, const int32_t* row_index, const uint8_t* row_mask, hipStream_t stream) {
+                        int n, float eps, const RowMap& rmap, const uint8_t* row_mask, hipStream_t stream) {
   switch (out_dtype) {
     case TJK_F32:
       return launch_ln<TRes, TDelta, float>(res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ro_dtype, ld_res_out, out, ld_out,
-                                            gamma, beta, rows, n, eps, row_index, row_mask, stream);
+                                            gamma, beta, rows, n, eps, rmap, row_mask, stream);
     case TJK_F16:
       return launch_ln<TRes, TDelta, f16>(res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ro_dtype, ld_res_out, out, ld_out,
-                                          gamma, beta, rows, n, eps, row_index, row_mask, stream);
+                                          gamma, beta, rows, n, eps, rmap, row_mask, stream);
     case TJK_BF16:
       return launch_ln<TRes, TDelta, bf16>(res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ro_dtype, ld_res_out, out, ld_out,
-                                           gamma, beta, rows, n, eps, row_index, row_mask, stream);
+                                           gamma, beta, rows, n, eps, rmap, row_mask, stream);
   }
   return fail(TJK_EINVAL, "tjk_add_layernorm: bad out dtype %d", out_dtype);
 }
@@ -392,18 +411,18 @@ template <typename TRes>
 static int dispatch_delta(int delta_dtype, int out_dtype, const void* res, int64_t ld_res,
                           const void* delta, int64_t ld_delta, int n_delta, int64_t delta_stride, void* res_out, int ro_dtype, int64_t ld_res_out,
                           void* out, int64_t ld_out, const float* gamma, const float* beta,
-                          int64_t rows, int n, float eps, const int32_t* row_index,
+                          int64_t rows, int n, float eps, const RowMap& rmap,
                           const uint8_t* row_mask, hipStream_t stream) {
   switch (delta_dtype) {
     case TJK_F32:
       return dispatch_out<TRes, float>(out_dtype, res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ro_dtype, ld_res_out, out,
-                                       ld_out, gamma, beta, rows, n, eps, row_index, row_mask, stream);
+                                       ld_out, gamma, beta, rows, n, eps, rmap, row_mask, stream);
     case TJK_F16:
       return dispatch_out<TRes, f16>(out_dtype, res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ro_dtype, ld_res_out, out,
-                                     ld_out, gamma, beta, rows, n, eps, row_index, row_mask, stream);
+                                     ld_out, gamma, beta, rows, n, eps, rmap, row_mask, stream);
     case TJK_BF16:
       return dispatch_out<TRes, bf16>(out_dtype, res, ld_res, delta, ld_delta, n_delta, delta_stride, res_out, ro_dtype, ld_res_out, out,
-                                      ld_out, gamma, beta, rows, n, eps, row_index, row_mask, stream);
+                                      ld_out, gamma, beta, rows, n, eps, rmap, row_mask, stream);
   }
   return fail(TJK_EINVAL, "tjk_add_layernorm: bad delta dtype %d", delta_dtype);
 }
@@ -423,9 +442,11 @@ extern "C" int tjk_add_layernorm(const void* res, int res_dtype, int64_t ld_res,
                                  void* out, int out_dtype, int64_t ld_out,
                                  const float* gamma, const float* beta,
                                  int64_t rows, int64_t n, float eps,
-                                 const int32_t* row_index, const uint8_t* row_mask, void* stream) {
+                                 const int32_t* row_index, int64_t src_rows, int* index_errors,
+                                 const uint8_t* row_mask, void* stream) {
   g_err[0] = 0;
   if (rows < 0 || n <= 0) return fail(TJK_EINVAL, "tjk_add_layernorm: bad shape rows=%lld n=%lld", (long long)rows, (long long)n);
+  if (row_index && src_rows < 0) return fail(TJK_EINVAL, "tjk_add_layernorm: negative src_rows with a row_index");
   if (rows == 0) return TJK_OK;
   if (!res || !out || !gamma || !beta) return fail(TJK_EINVAL, "tjk_add_layernorm: null pointer");
   if (res_out && res_out_dtype != TJK_F32 && res_out_dtype != TJK_F16 && res_out_dtype != TJK_BF16)
@@ -459,18 +480,19 @@ extern "C" int tjk_add_layernorm(const void* res, int res_dtype, int64_t ld_res,
   if (delta && delta_splits > 1 && (n > 1024 || delta_dtype != TJK_F32))
     return fail(TJK_EUNSUPPORTED, "tjk_add_layernorm: split deltas are fp32 rows of n <= 1024");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const RowMap rmap{row_index, row_index ? src_rows : rows, index_errors};
   const int dd = delta ? delta_dtype : res_dtype;
   const int nd = delta ? delta_splits : 0;
   switch (res_dtype) {
     case TJK_F32:
       return dispatch_delta<float>(dd, out_dtype, res, ld_res, delta, ld_delta, nd, delta_split_stride, res_out, ro_dtype, ld_res_out, out,
-                                   ld_out, gamma, beta, rows, (int)n, eps, row_index, row_mask, s);
+                                   ld_out, gamma, beta, rows, (int)n, eps, rmap, row_mask, s);
     case TJK_F16:
       return dispatch_delta<f16>(dd, out_dtype, res, ld_res, delta, ld_delta, nd, delta_split_stride, res_out, ro_dtype, ld_res_out, out,
-                                 ld_out, gamma, beta, rows, (int)n, eps, row_index, row_mask, s);
+                                 ld_out, gamma, beta, rows, (int)n, eps, rmap, row_mask, s);
     case TJK_BF16:
       return dispatch_delta<bf16>(dd, out_dtype, res, ld_res, delta, ld_delta, nd, delta_split_stride, res_out, ro_dtype, ld_res_out, out,
-                                  ld_out, gamma, beta, rows, (int)n, eps, row_index, row_mask, s);
+                                  ld_out, gamma, beta, rows, (int)n, eps, rmap, row_mask, s);
   }
   return fail(TJK_EINVAL, "tjk_add_layernorm: bad res dtype %d", res_dtype);
 }

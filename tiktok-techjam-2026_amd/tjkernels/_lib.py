@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede the library load; see module docstring)
 
 LIB_PATH = Path(__file__).with_name("libtjk.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 F32, F16, BF16 = 0, 1, 2
 OK, EINVAL, EUNSUPPORTED = 0, -1, -2
@@ -31,7 +31,7 @@ _SIGNATURES = {
     "tjk_abi_version": (_i32, []),
     "tjk_last_error_string": (ctypes.c_char_p, []),
     "tjk_add_layernorm": (_i32, [_vp, _i32, _i64, _vp, _i32, _i64, _i32, _i64, _vp, _i32, _i64, _vp, _i32, _i64,
-                                 _vp, _vp, _i64, _i64, _f32, _vp, _vp, _vp]),
+                                 _vp, _vp, _i64, _i64, _f32, _vp, _i64, _vp, _vp, _vp]),
     "tjk_gemm_bias": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64,
                              _i32, _i32, _i32, _vp]),
     "tjk_gemm_plan_count": (_i32, [_i32]),

@@ -288,8 +288,6 @@ class Engine:
         self._packings: "OrderedDict[Tuple[int, Tuple[int, ...]], Packing]" = OrderedDict()
         self._static_masks: Dict[Tuple[int, int], torch.Tensor] = {}
         self._forwards: "OrderedDict[Tuple, Forward]" = OrderedDict()
-        # static input / output of whole-forward graphs, per graph key
-        self._graph_io: "OrderedDict[Tuple, Tuple[torch.Tensor, torch.Tensor]]" = OrderedDict()
         self.check_waits = os.environ.get("TJ_CHECK_WAITS") == "1"
 
     # compatibility names used by tools and tests
@@ -618,29 +616,7 @@ class Engine:
                 self._forwards.popitem(last=False)
         row_mask = static_mask.reshape(-1) if mode == MASK_GENERAL else None
         if self.plan.whole_graph:
-            # the buffers a graph was captured on live and die with it: a key
-            # the graph cache no longer holds gets new buffers and a new capture
-            io = self._graph_io.get(key)
-            if io is None or key not in self._graphs:
-                io = (torch.empty_like(x), torch.empty((batch, seq, d), dtype=self.dtype, device=x.device))
-                self._graph_io[key] = io
-                while len(self._graph_io) > self._graphs.max_entries:
-                    self._graph_io.popitem(last=False)
-            x_in, y_out = io
-
-            def whole() -> None:
-                self._first(fw, x_in)
-                self._body(fw)
-                self._final(fw, y_out, row_mask)
-
-            x_in.copy_(x)
-            graph = self._graphs.get(key, whole, keepalive=(packing, fw, io))
-            if graph is not None:
-                graph.replay()
-            else:
-                whole()
-            self._check(fw)
-            return y_out.clone()
+            return self._forward_whole_graph(x, fw, key, packing, row_mask)
         graph = self._graphs.get(key, lambda: self._body(fw), keepalive=(packing, fw))
         self._first(fw, x)
         if graph is not None:
@@ -651,6 +627,44 @@ class Engine:
         self._final(fw, out, row_mask)
         self._check(fw)
         return out
+
+    def _forward_whole_graph(self, x: torch.Tensor, fw: Forward, key: Tuple, packing: Optional[Packing],
+                             row_mask: Optional[torch.Tensor]) -> torch.Tensor:
+        """One replay of a graph that holds both LayerNorms too: x is copied
+        into the graph's static input and its static output is cloned.  The
+        static buffers are part of the graph entry (its keepalive), so they
+        are evicted together with the graph and never separately: a replay
+        always reads and writes the buffers it was captured on."""
+        found, graph = self._graphs.lookup(key)
+        if found and graph is not None:
+            _, fw_g, (x_in, y_out) = graph.keepalive
+            x_in.copy_(x)
+            graph.replay()
+            self._check(fw_g)
+            return y_out.clone()
+        if found:  # the capture failed before: eager launches on fresh buffers
+            out = torch.empty_like(x)
+            self._first(fw, x)
+            self._body(fw)
+            self._final(fw, out, row_mask)
+            self._check(fw)
+            return out
+        io = (torch.empty_like(x), torch.empty_like(x))
+        x_in, y_out = io
+
+        def whole() -> None:
+            self._first(fw, x_in)
+            self._body(fw)
+            self._final(fw, y_out, row_mask)
+
+        x_in.copy_(x)
+        graph = self._graphs.get(key, whole, keepalive=(packing, fw, io))
+        if graph is not None:
+            graph.replay()
+        else:
+            whole()
+        self._check(fw)
+        return y_out.clone()
 
 
 def get_engine(module: torch.nn.Module) -> Engine:

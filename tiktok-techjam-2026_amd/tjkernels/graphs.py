@@ -19,7 +19,7 @@ from __future__ import annotations
 
 import warnings
 from collections import OrderedDict
-from typing import Callable, Hashable, Optional
+from typing import Callable, Hashable, Optional, Tuple
 
 import torch
 
@@ -82,6 +82,14 @@ class GraphCache:
         if len(self._entries) > self.max_entries:
             self._entries.popitem(last=False)
         return entry
+
+    def lookup(self, key: Hashable) -> Tuple[bool, Optional[CapturedGraph]]:
+        """(key present, its graph or None for a failed capture), marking the
+        key as the most recently used; no capture happens."""
+        if key not in self._entries:
+            return False, None
+        self._entries.move_to_end(key)
+        return True, self._entries[key]
 
     def __contains__(self, key: Hashable) -> bool:
         return key in self._entries

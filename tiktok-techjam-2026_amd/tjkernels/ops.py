@@ -58,7 +58,8 @@ def add_layernorm(res: torch.Tensor, delta: Optional[torch.Tensor],
                   gamma: torch.Tensor, beta: torch.Tensor, eps: float,
                   out: torch.Tensor, res_out: Optional[torch.Tensor] = None,
                   row_mask: Optional[torch.Tensor] = None,
-                  row_index: Optional[torch.Tensor] = None) -> torch.Tensor:
+                  row_index: Optional[torch.Tensor] = None,
+                  index_errors: Optional[torch.Tensor] = None) -> torch.Tensor:
     """x = res (+ delta) in fp32; res_out <- x (optional; fp32, or rounded to
     a 2-byte res_out, the reference's residual_dtype); out <- LN(x), of the
     unrounded x (rows with row_mask == 0 written as 0).  Mirrors
@@ -66,13 +67,18 @@ def add_layernorm(res: torch.Tensor, delta: Optional[torch.Tensor],
 
     With ``row_index`` (int32, one entry per output row) the call is a
     gather / scatter: output row r is computed from input row row_index[r],
-    or written as zeros when the index is negative; ``out`` (and ``res_out``)
-    then have ``row_index.numel()`` rows.
+    or written as zeros when the index is negative or not below the rows
+    ``res`` (and ``delta``) hold -- the latter also counted in
+    ``index_errors`` (a one-element int32 device tensor) when given;
+    ``out`` (and ``res_out``) then have ``row_index.numel()`` rows.
 
     A 3-D ``delta`` [splits, rows, n] (the fused FFN's split partials) is
     summed over its first dimension, in order, before it is added."""
-    _require_gpu(res, delta, gamma, beta, out, res_out, row_mask, row_index)
+    _require_gpu(res, delta, gamma, beta, out, res_out, row_mask, row_index, index_errors)
     rows, n = res.shape
+    src_rows = rows if delta is None else min(rows, delta.shape[-2])
+    if index_errors is not None and (index_errors.dtype != torch.int32 or index_errors.numel() < 1):
+        raise TjkError("index_errors must be an int32 device tensor of at least one element")
     splits, split_stride, delta2 = 1, 0, delta
     if delta is not None and delta.dim() == 3:
         splits, split_stride, delta2 = delta.shape[0], delta.stride(0), delta[0]
@@ -100,7 +106,7 @@ def add_layernorm(res: torch.Tensor, delta: Optional[torch.Tensor],
         _rowmajor(res_out, "res_out") if res_out is not None else 0,
         out.data_ptr(), _code(out), _rowmajor(out, "out"),
         gamma.data_ptr(), beta.data_ptr(), rows, n, float(eps),
-        _ptr(row_index), _ptr(row_mask), _stream(res))
+        _ptr(row_index), src_rows, _ptr(index_errors), _ptr(row_mask), _stream(res))
     check(status, "tjk_add_layernorm")
     return out
 
