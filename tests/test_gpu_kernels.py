@@ -117,7 +117,7 @@ def _gemm_case(device, m, n, k, dt, epi, plan, seed=0):
 # K % 64 == 0 (bf16/fp16) and reject other K with TJK_EUNSUPPORTED.
 # Plans 18-20 use 4-, 8- and 6-slot rings with the spread DMA schedule;
 # 16, 17 and 21-27 split K between 2 or 4 wave groups of one workgroup.
-STAGED16, DTL16, DTL16_K32 = range(0, 6), list(range(6, 28)), ()
+STAGED16, DTL16, DTL16_K32 = range(0, 6), list(range(6, 33)), ()
 STAGED32, DTL32 = range(0, 2), range(2, 5)
 
 
@@ -137,14 +137,16 @@ def test_gemm_plans(device, plan, dt):
             _gemm_case(device, 64, 64, 40, dt, ops.EPI_BIAS, plan)
 
 
-@pytest.mark.parametrize("plan", [15, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27])
+@pytest.mark.parametrize("plan", [15, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27, 28, 29, 30, 31, 32])
 @pytest.mark.parametrize("epi", [ops.EPI_BIAS_GELU, ops.EPI_BIAS_RESIDUAL])
 def test_gemm_deep_ring_and_prefetch_plans(device, plan, epi):
     # Deep rings (18-20): K from one tile (fewer tiles than ring slots) to a
     # long pipeline.  Plans 15 and 18 read the residual before the main loop,
     # the small K-split tiles (22-27) the residual and the bias.  K-split
     # plans (21-27): fewer K tiles than groups, and counts that do not divide
-    # evenly between the groups.
+    # evenly between the groups.  Wave-specialized plans (28-32): K tiles
+    # fewer than, equal to and more than the ring's slots, so the loader
+    # waves' tail (no further tile to issue) runs at every ring depth.
     for m, n, k in ((200, 256, 64), (300, 384, 192), (5430, 1024, 4096), (1000, 516, 1024), (128, 512, 2048)):
         _gemm_case(device, m, n, k, torch.bfloat16, epi, plan)
 

@@ -211,14 +211,194 @@ __global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
                                 BIAS_PRE ? &bpre : nullptr);
 }
 
+
+// ---------------------------------------------------- wave-specialized GEMM
+//
+// The direct-to-LDS main loop above issues its DMA from the waves that run
+// the MFMAs.  When the per-CU DMA rate saturates (measured on MI355X:
+// ~35-44 B/clk per CU for buffer_load ... lds), a wave stalls at the issue
+// of its next DMA instruction and, issuing in order, its MFMAs stall with
+// it: the loop then takes about the DMA-only time plus the MFMA-only time
+// (1.5x the larger of the two at the packed C4 shapes).  Here the two jobs
+// go to different waves of the workgroup:
+//   * NW = WM x WN compute waves read fragments from the ring and issue the
+//     MFMAs (the same fragment reads, MFMA order and epilogue as
+//     gemm_dtl_kernel, so the results are bitwise those of the class-1
+//     plans);
+//   * L loader waves only issue the LDS DMA of K tile kt + STAGES - 1 and
+//     wait for tile kt + 1 to land.
+// One barrier per K tile (B_kt, before the compute waves' last 16-deep step
+// of tile kt) orders them: after B_kt tile kt + 1 has landed and tile kt's
+// slot is free.  A final barrier ends the ring before the epilogue reuses
+// its LDS; the loader waves then exit.
+template <typename T, int BM, int BN, int WM, int WN, int STAGES, int L, int EPI>
+__global__ __launch_bounds__((WM * WN + L) * 64) void gemm_ws_kernel(
+    const T* __restrict__ A, int64_t lda, const T* __restrict__ W, int64_t ldw,
+    const T* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K) {
+  constexpr int BKB = 128;
+  typedef DtlGeom<T, BM, BN, WM, WN, BKB, STAGES, 1> G;
+  constexpr int NW = G::NW, KS = G::KS, CPS = G::CPS, WTM = G::WTM, WTN = G::WTN, FM = G::FM, FN = G::FN;
+  constexpr int STAGE = G::STAGE;
+  constexpr int NINST = (BM + BN) / G::RPI;  // 1 KB DMA instructions per K tile
+  constexpr int NL = NINST / L;              // per loader wave
+  static_assert(NINST % L == 0 && BM % G::RPI == 0, "DMA rows split over the loader waves");
+  static_assert(STAGES >= 2 && (STAGES - 2) * NL <= 63, "vmcnt range");
+  constexpr int STG = NW * EpiStage<T, EPI, FN>::BYTES;
+  constexpr int LDS = STAGES * STAGE > STG ? STAGES * STAGE : STG;
+  __shared__ __attribute__((aligned(1024))) char smem[LDS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  int pid_m, pid_n;
+  tile_coords(blockIdx.x, (M + BM - 1) / BM, (N + BN - 1) / BN, pid_m, pid_n);
+  const int m0 = pid_m * BM, n0 = pid_n * BN;
+  const int nk = K / G::BK;
+
+  if (wave >= NW) {
+    // ------------------------------------------------------------ loaders
+    const int lw = wave - NW;
+    const int64_t a_rows = min((int64_t)BM, (int64_t)(M - m0));
+    const int64_t w_rows = min((int64_t)BN, (int64_t)(N - n0));
+    const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(A + (int64_t)m0 * lda), (short)0, (int)(a_rows * lda * (int64_t)sizeof(T)), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(W + (int64_t)n0 * ldw), (short)0, (int)(w_rows * ldw * (int64_t)sizeof(T)), 0x00020000);
+    // instruction q of loader lw fills rows (q L + lw) RPI .. +RPI-1 of the
+    // stacked (A; W) tile; lane l lands at byte 16 l: row + l / CPR,
+    // physical chunk l % CPR, so it fetches logical chunk (l % CPR) ^ swz(row)
+    auto dma = [&](int t, int q) {
+      char* sb = smem + (t % STAGES) * STAGE;
+      const int base = (q * L + lw) * G::RPI;  // wave-uniform
+      const uint32_t kb = (uint32_t)(t * BKB);
+      if (base < BM) {
+        const int r = base + lane / G::CPR;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rsa, (lds_void*)(sb + base * BKB), 16,
+            (uint32_t)(r * lda * (int64_t)sizeof(T)) + (uint32_t)(((lane % G::CPR) ^ swz<BKB>(r)) << 4) + kb, 0, 0, 0);
+      } else {
+        const int r = base - BM + lane / G::CPR;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rsw, (lds_void*)(sb + base * BKB), 16,
+            (uint32_t)(r * ldw * (int64_t)sizeof(T)) + (uint32_t)(((lane % G::CPR) ^ swz<BKB>(r)) << 4) + kb, 0, 0, 0);
+      }
+    };
+    for (int t = 0; t < STAGES - 1 && t < nk; ++t) {
+#pragma unroll
+      for (int q = 0; q < NL; ++q) dma(t, q);
+    }
+    // tile 0 landed (the tiles issued after it may still be in flight)
+    if (nk >= STAGES - 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"((STAGES - 2) * NL) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // B_-1
+    for (int k = 0; k < nk; ++k) {
+      // tile k + STAGES - 1 into the slot tile k - 1 freed at B_{k-1};
+      // then tile k + 1 landed before B_k
+      const int t = k + STAGES - 1;
+      if (t < nk) {
+#pragma unroll
+        for (int q = 0; q < NL; ++q) dma(t, q);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((STAGES - 2) * NL) : "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      __builtin_amdgcn_s_barrier();  // B_k
+    }
+    __builtin_amdgcn_s_barrier();  // B_final
+    return;
+  }
+
+  // ------------------------------------------------------------- compute
+  const int wm = wave / WN, wn = wave % WN;
+  const int l32 = lane & 31, hi = lane >> 5;
+  // The epilogue's bias and residual reads go out before the main loop where
+  // the registers allow (accumulators, two fragment sets and address
+  // registers counted against the per-wave share of the register file):
+  // their round trip then overlaps the main loop.
+  constexpr int WPS = (NW + L + 3) / 4;  // waves per SIMD (one workgroup per CU)
+  constexpr int AVAIL = (512 / WPS) & ~7;
+  // (the residual first: its read-modify-write is most of a residual
+  // epilogue; 36 overhead registers, 44 with a ring whose slot count is not
+  // a power of two, keeps every plan here free of spills)
+  constexpr int USED = FM * FN * 16 + 2 * (FM + FN) * 4 + ((STAGES & (STAGES - 1)) ? 44 : 36);
+  constexpr int BIAS_REGS = FN * 4 * (int)sizeof(typename Quad<T>::raw) / 4;
+  constexpr int PRE_REGS = FM * ResPrefetch<FM, FN>::NIT * 4;
+  constexpr bool PREFETCH = EPI == TJK_EPI_BIAS_RESIDUAL && USED + PRE_REGS <= AVAIL;
+  constexpr bool BIAS_PRE = USED + BIAS_REGS + (PREFETCH ? PRE_REGS : 0) <= AVAIL;
+  typedef typename std::conditional<PREFETCH, ResPrefetch<FM, FN>, NoPrefetch>::type Pre;
+  BiasRaw<T, FN> bpre;
+  if constexpr (BIAS_PRE) bpre.load(bias, N, n0 + wn * WTN, lane);
+  Pre pre;
+  if constexpr (PREFETCH)
+    pre.load(static_cast<const float*>(Cv), ldc, M, N, m0 + wm * WTM, n0 + wn * WTN, lane);
+  const int sw = swz<BKB>(l32);
+  typedef typename Mfma<T>::frag Frag;
+  auto frag_at = [&](const char* rowbase, int ks) -> Frag {
+    return *reinterpret_cast<const Frag*>(rowbase + (((CPS * ks + hi) ^ sw) << 4));
+  };
+  f32x16 acc[FN][FM];
+  zero_acc<T, FM, FN>(acc);
+  constexpr int NMF = FN * FM, NDS = FN + FM;
+  constexpr int NSLOT = NMF > NDS ? NMF : NDS;
+  Frag fa[2][FM], fw[2][FN];
+  __builtin_amdgcn_s_barrier();  // B_-1: tile 0 landed
+  __builtin_amdgcn_sched_barrier(0);
+  {
+    const char* sa = smem + (wm * WTM + l32) * BKB;
+    const char* sw_ = smem + BM * BKB + (wn * WTN + l32) * BKB;
+#pragma unroll
+    for (int j = 0; j < FM; ++j) fa[0][j] = frag_at(sa + j * 32 * BKB, 0);
+#pragma unroll
+    for (int i = 0; i < FN; ++i) fw[0][i] = frag_at(sw_ + i * 32 * BKB, 0);
+  }
+  // Same schedule as dtl_accumulate: MFMA m of a step, then fragment read m
+  // of the next step; the barrier precedes the last step of a tile, whose
+  // fragments are in registers, and the next tile's first fragments are
+  // read during the last step's MFMAs.  (The slot after the last tile is
+  // read too; those fragments are never used.)
+  for (int kt = 0; kt < nk; ++kt) {
+    const char* st = smem + (kt % STAGES) * STAGE;
+    const char* sa = st + (wm * WTM + l32) * BKB;
+    const char* sw_ = st + BM * BKB + (wn * WTN + l32) * BKB;
+    const char* nx = smem + ((kt + 1) % STAGES) * STAGE;
+    const char* na = nx + (wm * WTM + l32) * BKB;
+    const char* nw = nx + BM * BKB + (wn * WTN + l32) * BKB;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int b = ks & 1;
+      const bool last = ks + 1 == KS;
+      const char* ra = last ? na : sa;
+      const char* rw = last ? nw : sw_;
+      const int rks = last ? 0 : ks + 1;
+      if (last) {
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // my reads of slot kt are done
+        __builtin_amdgcn_s_barrier();                        // B_kt
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int m = 0; m < NSLOT; ++m) {
+        if (m < NMF) Mfma<T>::mma(acc[m / FM][m % FM], fw[b][m / FM], fa[b][m % FM]);
+        if (m < FM) fa[b ^ 1][m] = frag_at(ra + m * 32 * BKB, rks);
+        else if (m < NDS) fw[b ^ 1][m - FM] = frag_at(rw + (m - FM) * 32 * BKB, rks);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();  // B_final: every ring read done, every DMA landed
+  epilogue<T, EPI, FM, FN, Pre>(acc, bias, Cv, ldc, M, N, m0 + wm * WTM, n0 + wn * WTN, lane,
+                                smem + wave * EpiStage<T, EPI, FN>::BYTES, pre, BIAS_PRE ? &bpre : nullptr);
+}
+
 // ------------------------------------------------------------------ plans
 
-enum { kStaged = 0, kDtl = 1 };
+enum { kStaged = 0, kDtl = 1, kWs = 2 };
 
 struct GemmPlan {
   int kind, bm, bn, wm, wn, bkb, stages;
-  double eff;      // prior used by auto_plan
-  int ksplit = 1;  // K groups per workgroup (direct-to-LDS kernel)
+  double eff;       // prior used by auto_plan
+  int ksplit = 1;   // K groups per workgroup (direct-to-LDS kernel)
+  int loaders = 0;  // DMA-only waves (wave-specialized kernel)
 };
 
 // 2-byte types (bf16/fp16), BK = 64.  Measured on MI355X (bf16, C4/C5
@@ -280,6 +460,15 @@ static const GemmPlan kPlans16[] = {
     // of K tiles in flight and the serial chain is a quarter of K.
     {kDtl, 32, 32, 1, 1, 128, 4, 0.30, 4},    // 26 4 waves, 128 KB
     {kDtl, 32, 64, 1, 2, 128, 3, 0.35, 4},    // 27 8 waves, 144 KB
+    // 28-32: wave-specialized (gemm_ws_kernel): WM x WN compute waves plus 4
+    // DMA-only loader waves.  Measured on the packed C4 projections against
+    // the best plan above: FFN2 (5430 x 1024 x 4096) 51 against 55.5 us,
+    // out-proj 20.6 against 22.0 us, FFN1 59.7 against 60.2 us; QKV no gain.
+    {kWs, 192, 128, 2, 2, 128, 4, 0.85, 1, 4},  // 28 wave tile 96x64, 160 KB
+    {kWs, 192, 128, 2, 4, 128, 3, 0.85, 1, 4},  // 29 wave tile 96x32, 120 KB
+    {kWs, 192, 128, 2, 4, 128, 4, 0.85, 1, 4},  // 30 wave tile 96x32, 160 KB
+    {kWs, 192, 256, 2, 4, 128, 2, 0.85, 1, 4},  // 31 wave tile 96x64, 112 KB
+    {kWs, 128, 256, 2, 4, 128, 3, 0.85, 1, 4},  // 32 wave tile 64x64, 144 KB
 };
 // fp32.
 static const GemmPlan kPlans32[] = {
@@ -321,7 +510,7 @@ static int auto_plan(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) 
   int best = 0;
   double best_cost = 1e300;
   for (int i = 0; i < count; ++i) {
-    if (p[i].kind == kDtl && !dtl_ok(p[i], K, lda, ldw, sizeof(T))) continue;
+    if (p[i].kind != kStaged && !dtl_ok(p[i], K, lda, ldw, sizeof(T))) continue;
     const int64_t tiles = ((M + p[i].bm - 1) / p[i].bm) * ((N + p[i].bn - 1) / p[i].bn);
     const int64_t rounds = (tiles + 255) / 256;
     const double cost = (double)rounds * p[i].bm * p[i].bn / p[i].eff;
@@ -369,6 +558,17 @@ static int launch_epi(int epi, const GemmArgs& g) {
   }
 }
 
+template <int STAGES, int L> struct WsLauncher {
+  template <typename T, int BM, int BN, int WM, int WN, int EPI>
+  static int go(const GemmArgs& g) {
+    const dim3 grid(((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN));
+    hipLaunchKernelGGL((gemm_ws_kernel<T, BM, BN, WM, WN, STAGES, L, EPI>), grid, dim3((WM * WN + L) * 64), 0,
+                       g.s, (const T*)g.a, g.lda, (const T*)g.w, g.ldw, (const T*)g.bias, g.c, g.ldc, g.M, g.N,
+                       g.K);
+    return TJK_OK;
+  }
+};
+
 typedef Launcher<kStaged> St;
 typedef DtlLauncher<128, 2> D2;
 typedef DtlLauncher<128, 2, 2> D2K2;
@@ -380,6 +580,9 @@ typedef DtlLauncher<128, 3, 4> D3K4;
 typedef DtlLauncher<128, 4> D4;
 typedef DtlLauncher<128, 6> D6;
 typedef DtlLauncher<128, 8> D8;
+typedef WsLauncher<4, 4> W4;
+typedef WsLauncher<3, 4> W3;
+typedef WsLauncher<2, 4> W2;
 
 template <typename T>
 static int run_gemm(int plan, int epi, const GemmArgs& g) {
@@ -424,6 +627,11 @@ static int run_gemm(int plan, int epi, const GemmArgs& g) {
       TJK_GEMM_CASE(25, D4K2, 32, 32, 1, 1)
       TJK_GEMM_CASE(26, D4K4, 32, 32, 1, 1)
       TJK_GEMM_CASE(27, D3K4, 32, 64, 1, 2)
+      TJK_GEMM_CASE(28, W4, 192, 128, 2, 2)
+      TJK_GEMM_CASE(29, W3, 192, 128, 2, 4)
+      TJK_GEMM_CASE(30, W4, 192, 128, 2, 4)
+      TJK_GEMM_CASE(31, W2, 192, 256, 2, 4)
+      TJK_GEMM_CASE(32, W3, 128, 256, 2, 4)
     }
   }
 #undef TJK_GEMM_CASE
@@ -468,7 +676,7 @@ extern "C" int tjk_gemm_plan_info(int dtype, int id, int* block_m, int* block_n,
   if (id < 0 || id >= count) return fail(TJK_EINVAL, "tjk_gemm_plan_info: plan %d out of range", id);
   if (block_m) *block_m = p[id].bm;
   if (block_n) *block_n = p[id].bn;
-  if (waves) *waves = p[id].wm * p[id].wn * p[id].ksplit;
+  if (waves) *waves = p[id].wm * p[id].wn * p[id].ksplit + p[id].loaders;
   if (k_groups) *k_groups = p[id].ksplit;
   return TJK_OK;
 }

@@ -51,13 +51,17 @@ from . import _lib, ops, timing
 
 # Direct-to-LDS plans of the 2-byte table by K order (ids of tjk_gemm_plan_info):
 # class 1: 128x128, 256x256 (8 waves), 64x64, 192x128, 192x256, 192x384,
-#          96x128, 192x128 in a 4-slot ring, 64x64 / 128x64 in 8- / 6-slot rings;
+#          96x128, 192x128 in a 4-slot ring, 64x64 / 128x64 in 8- / 6-slot rings,
+#          and the wave-specialized tiles (compute waves + DMA-only loader
+#          waves): 192x128 with 4 compute waves in a 4-slot ring, with 8 in 3-
+#          and 4-slot rings, 192x256 with 8 in 2 slots, 128x256 with 8 in 3;
 # class 2: 192x128, 128x128, 64x64 (4-slot ring), 128x64 (3-slot ring), each
 #          with K split between two groups of 4 waves; 32x64 and 32x32
 #          (4-slot rings) with K split between two groups of 2 / 1 waves;
 # class 4: 64x64 (2-slot rings), 32x32 (4-slot) and 32x64 (3-slot) with K split
 #          between four groups of 4 / 1 / 2 waves.
-CLASS_TILES_16 = {1: (7, 8, 9, 12, 13, 14, 15, 18, 19, 20), 2: (16, 17, 22, 23, 24, 25), 4: (21, 26, 27)}
+CLASS_TILES_16 = {1: (7, 8, 9, 12, 13, 14, 15, 18, 19, 20, 28, 29, 30, 31, 32), 2: (16, 17, 22, 23, 24, 25),
+                  4: (21, 26, 27)}
 CANDIDATES_32 = (2, 3, 4)  # fp32: class 1 only
 MAX_ENTRIES = 256
 M_BUCKET = 64
