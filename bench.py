@@ -18,7 +18,10 @@ Also reported:
   algorithmic FLOPs per launch over its average launch time, against the
   MI355X dense peak; ``traffic`` from the committed rocprofv3 FETCH_SIZE /
   WRITE_SIZE summary when present;
-* ``breakdown``: per-kernel-class time of one eager forward;
+* ``breakdown``: per-kernel-class kernel time of one eager forward: every
+  launch of the forward replayed on its own, back to back behind a spin
+  kernel, HIP events on the launch stream (so no inter-launch gap or host
+  launch cost enters), summed over the class's launches;
 * ``cpu_baseline``: the CPU oracle (fp32 restatement of the reference
   forward) timed on the host's cores on a bounded sample (one sequence:
   one warmup run, then the median of three, scaled to a whole forward);
@@ -88,11 +91,15 @@ GEMM_CALIB_M, GEMM_CALIB_N, GEMM_CALIB_K, GEMM_CALIB_PLAN = 64, 65536, 1024, 9
 
 
 def _breakdown(engine, x, mask):
-    """Per-kernel-class time of one eager forward: each tjk launch bracketed
-    by HIP events on the current stream (the launch stream).  Also returns,
-    per class, the exact call of its last launch so it can be replayed."""
+    """Per-kernel-class kernel time of one eager forward.  The forward runs
+    once with every tjk launch recorded (its exact call); each recorded call
+    is then replayed on its own, back to back behind a spin kernel
+    (``_kernel_avg_ms``), and its average launch time is summed into its
+    class.  Events bracketing the launches inside the forward would also
+    count the gaps between launches.  Also returns, per class, the call of
+    its last launch."""
     import torch
-    from tjkernels import ops, timing
+    from tjkernels import ops
     classes, calls = {}, {}
     orig = {name: getattr(ops, name) for name in ("gemm", "flash_attention", "flash_attention_sched",
                                                   "add_layernorm", "ffn")}
@@ -122,11 +129,8 @@ def _breakdown(engine, x, mask):
                 flops = 4.0 * a[0].shape[0] * a[1].shape[0] * a[1].shape[1]
             else:
                 flops = 0.0
-            s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s0.record()
             r = fn(*a, **k)
-            s1.record()
-            events.append((label, flops, s0, s1))
+            events.append((label, flops, (fn, a, k)))
             calls[label] = (fn, a, k)
             return r
         return inner
@@ -136,17 +140,17 @@ def _breakdown(engine, x, mask):
     for name, fn in orig.items():
         setattr(ops, name, wrap(name, fn))
     try:
-        for _ in range(3):  # warm, then keep the last pass
+        for _ in range(2):  # warm, then keep the last pass
             events.clear()
-            torch.cuda.synchronize()
-            # queue the whole forward behind a spin kernel so each launch's
-            # events read its GPU time, not the host's launch overhead
-            timing.queue_ahead(5.0)
             engine._forward_impl(x, mask, mode, packing)
         torch.cuda.synchronize()
     finally:
         for name, fn in orig.items():
             setattr(ops, name, fn)
+    # Replays write the forward's workspaces again (a residual epilogue adds
+    # into the residual once more per replay); the forward's output was read
+    # before, and every later forward recomputes them from x.
+    timed = [(label, flops, _kernel_avg_ms(call, reps=20)) for label, flops, call in events]
     # A plain copy of known size (256 MiB read + 256 MiB written): its rocprof
     # FETCH_SIZE / WRITE_SIZE readings calibrate the HBM-traffic counters.
     src = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device=x.device)
@@ -166,9 +170,9 @@ def _breakdown(engine, x, mask):
     ops.gemm(ga, gw, gb, gc, ops.EPI_BIAS, GEMM_CALIB_PLAN)
     torch.cuda.synchronize()
     del ga, gw, gb, gc
-    for label, flops, s0, s1 in events:
+    for label, flops, ms in timed:
         c = classes.setdefault(label, {"ms": 0.0, "launches": 0, "flops": 0.0})
-        c["ms"] += s0.elapsed_time(s1)
+        c["ms"] += ms
         c["launches"] += 1
         c["flops"] += flops
     return classes, calls

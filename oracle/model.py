@@ -38,7 +38,7 @@ import torch
 
 __all__ = [
     "layer_norm", "gelu_erf", "attention", "block", "forward",
-    "baseline_module", "compare_outputs", "budget_usage",
+    "compare_outputs", "budget_usage",
 ]
 
 
@@ -124,20 +124,6 @@ def forward(state_dict: Dict[str, torch.Tensor], x: torch.Tensor,
             xb = xb.masked_fill(~mb[..., None], 0.0)
         outs.append(xb)
     return torch.cat(outs, dim=0)
-
-
-def baseline_module(config):
-    """An ``nn.Module`` with the reference's parameter tree whose forward is
-    the restatement above, run in the parameters' dtype on the CPU."""
-    from tjkernels.modules import TransformerLayout  # parameter tree only
-
-    class BaselineTransformer(TransformerLayout):
-        def forward(self, x, valid_token_mask=None):
-            dtype = next(self.parameters()).dtype
-            return forward(self.state_dict(), x, valid_token_mask,
-                           self.config.num_heads, self.config.causal, dtype=dtype)
-
-    return BaselineTransformer(config)
 
 
 def compare_outputs(reference: torch.Tensor, optimized: torch.Tensor,

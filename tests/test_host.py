@@ -539,3 +539,7 @@ def test_rocprof_summary_labels_deferred_projections():
     assert rs._relabel("gemm_ffn2_residual", epi2) == "gemm_ffn2_residual"
     assert rs._relabel("gemm_out_residual", epi0) == "gemm_out"
     assert rs._relabel("gemm_qkv", epi0) == "gemm_qkv"
+    # the wave-specialized kernel <T, BM, BN, WM, WN, STAGES, L, EPI> counts as a GEMM launch too
+    ws2 = "_ZN3tjk14gemm_ws_kernelIDF16bLi192ELi128ELi2ELi4ELi4ELi4ELi2EEEvPKT_lS3_lS3_Pvliii"
+    assert rs._gemm_epilogue(ws2) == 2 and rs._kind_ok("gemm_out_residual", ws2)
+    assert rs._relabel("gemm_out_residual", ws2) == "gemm_out_residual" and rs._tjk(ws2)

@@ -286,7 +286,7 @@ struct DtlGeom {
   static constexpr int NDMA = DA + DW;                // DMA instructions per wave per tile
   static constexpr int LDS = KSPLIT * STAGES * STAGE; // ring bytes
   static_assert(DA * RPI * NW == BM && DW * RPI * NW == BN, "tile rows must split over the waves");
-  static_assert(STAGES >= 2 && (STAGES - 1) * NDMA <= 63, "vmcnt range");
+  static_assert(STAGES >= 2 && 2 * (STAGES - 1) * NDMA <= 63, "vmcnt range");
   static_assert(KS % 2 == 0, "fragment double buffer alternates per 16-deep step");
 };
 
@@ -343,10 +343,23 @@ __device__ __forceinline__ void dtl_accumulate(
     voff_w[i] = (uint32_t)(r * ldw * (int64_t)sizeof(T)) + (uint32_t)(((lane % CPR) ^ swz<BKB>(r)) << 4);
   }
   const int nit = (kt1 - kt0 + KSPLIT - 1) / KSPLIT;  // ring steps per group
+  // Eight-wave tiles with 96 x 96 (or larger) wave tiles issue every DMA
+  // instruction from waves 0-3 (one per SIMD), twice their share, and none
+  // from waves 4-7: a wave whose DMA cannot issue yet stalls its own in-order
+  // MFMAs, and with the issue on one wave of each SIMD the other keeps the
+  // matrix pipe busy meanwhile.  Measured (A/B of two builds, one box):
+  // 192 x 384 tiles 37.3 -> 36.85 us on the packed C4 QKV, 79.3 -> 78.0 us
+  // at 5430 x 4096 x 1024 with GELU, 898 -> 886 us at 8192^3; the 8-wave
+  // 256 x 256 tile (128 x 64 wave tiles) got 1-2.5% slower with it and 192 x 128
+  // / 192 x 256 ones no faster, so they keep the even split.  The math is
+  // untouched.
+  constexpr bool ASYM = NW == 8 && KSPLIT == 1 && FM * FN >= 9;
+  constexpr int NDW = ASYM ? 2 * NDMA : NDMA;  // DMA instructions per issuing wave per tile
+  const bool issuer = !ASYM || wave < NW / 2;
   // DMA instruction q (q < DA: A rows, else W rows) of this group's step it
   // into its slot; past the segment it points outside the range and moves
   // nothing.
-  auto dma = [&](int it, int q) {
+  auto dma1 = [&](int it, int q) {
     char* sb = gsm + (it % STAGES) * STAGE;
     const int kt = kt0 + it * KSPLIT + kg;
     const uint32_t kb = kt < kt1 ? (uint32_t)(kt * BKB) : (uint32_t)kPastEnd;
@@ -356,6 +369,35 @@ __device__ __forceinline__ void dtl_accumulate(
     else
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_void*)(sb + BM * BKB + ((q - DA) * NW + wave) * 1024),
                                                16, (uint32_t)(voff_w[q - DA] + kb), 0, 0, 0);
+  };
+  // asymmetric issue: instruction q' of issuing wave w covers rows
+  // (q' NW/2 + w) RPI .. +RPI-1 of the stacked (A; W) tile, q' < 2 NDMA
+  auto dma2 = [&](int it, int q2) {
+    char* sb = gsm + (it % STAGES) * STAGE;
+    const int kt = kt0 + it * KSPLIT + kg;
+    const uint32_t kb = kt < kt1 ? (uint32_t)(kt * BKB) : (uint32_t)kPastEnd;
+    const int base = (q2 * (NW / 2) + wave) * RPI;  // wave-uniform
+    if (base < BM) {
+      const int r = base + lane / CPR;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsa, (lds_void*)(sb + base * BKB), 16,
+          (uint32_t)(r * lda * (int64_t)sizeof(T)) + (uint32_t)(((lane % CPR) ^ swz<BKB>(r)) << 4) + kb, 0, 0, 0);
+    } else {
+      const int r = base - BM + lane / CPR;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsw, (lds_void*)(sb + BM * BKB + (base - BM) * BKB), 16,
+          (uint32_t)(r * ldw * (int64_t)sizeof(T)) + (uint32_t)(((lane % CPR) ^ swz<BKB>(r)) << 4) + kb, 0, 0, 0);
+    }
+  };
+  auto dma = [&](int it, int q) {
+    if constexpr (ASYM) {
+      if (issuer) {
+        dma2(it, 2 * q);
+        dma2(it, 2 * q + 1);
+      }
+    } else {
+      dma1(it, q);
+    }
   };
 
   // Fragment reads: row (base + l32), logical chunk c at physical c ^ swz(l32).
@@ -382,7 +424,7 @@ __device__ __forceinline__ void dtl_accumulate(
   for (int t = 0; t < PRE; ++t)
 #pragma unroll
     for (int q = 0; q < NDMA; ++q) dma(t, q);
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"((PRE - 1) * NDMA) : "memory");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"((PRE - 1) * NDW) : "memory");
   asm volatile("s_barrier" ::: "memory");
   constexpr int NMF = FN * FM, NDS = FN + FM;  // MFMAs and fragment reads per step
   constexpr int NSLOT = NMF > NDS ? NMF : NDS;
@@ -423,7 +465,7 @@ __device__ __forceinline__ void dtl_accumulate(
         // kt+STAGES.  Inline asm with a memory clobber keeps the compiler
         // from moving LDS accesses across either instruction.
         __builtin_amdgcn_sched_barrier(0);
-        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((STAGES - 2) * NDMA) : "memory");  // tile kt+1 landed
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((STAGES - 2) * NDW) : "memory");  // tile kt+1 landed
         asm volatile("s_barrier" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
       }

@@ -41,8 +41,14 @@ import re
 from typing import Dict, List, Optional, Tuple
 
 # add_layernorm_kernel and add_layernorm_parts_kernel (the split-delta sum
-# after the single-launch FFN) both count as LayerNorm launches
+# after the single-launch FFN) both count as LayerNorm launches; a GEMM
+# launch is the direct-to-LDS kernel or the wave-specialized one
 GEMM, FLASH, LN, FFN = "gemm_dtl_kernel", "flash_", "add_layernorm", "ffn_fused_kernel"
+GEMM_WS = "gemm_ws_kernel"
+
+
+def _is_gemm(name: str) -> bool:
+    return GEMM in name or GEMM_WS in name
 COPY = "__amd_rocclr_copyBuffer"
 
 
@@ -65,9 +71,11 @@ def _labels(layers: int, fused: bool = False) -> List[str]:
 
 def _gemm_epilogue(name: str) -> Optional[int]:
     """EPI template argument of a gemm_dtl_kernel<T, BM, BN, WM, WN, BKB,
-    STAGES, EPI, KSPLIT> name (2: residual read-modify-write)."""
-    ints = re.findall(r"Li(\d+)E", name.split(GEMM, 1)[1]) if GEMM in name else []
-    return int(ints[6]) if len(ints) >= 8 else None
+    STAGES, EPI, KSPLIT> or gemm_ws_kernel<T, BM, BN, WM, WN, STAGES, L, EPI>
+    name, the seventh integer in both (2: residual read-modify-write)."""
+    kern = GEMM if GEMM in name else GEMM_WS if GEMM_WS in name else None
+    ints = re.findall(r"Li(\d+)E", name.split(kern, 1)[1]) if kern else []
+    return int(ints[6]) if len(ints) >= 7 else None
 
 
 def _relabel(label: str, name: str) -> str:
@@ -79,7 +87,7 @@ def _relabel(label: str, name: str) -> str:
 
 
 def _kind_ok(label: str, name: str) -> bool:
-    return ((GEMM in name) == label.startswith("gemm") and (FLASH in name) == (label == "flash_attention")
+    return (_is_gemm(name) == label.startswith("gemm") and (FLASH in name) == (label == "flash_attention")
             and (FFN in name) == (label == "ffn_fused"))
 
 
@@ -92,7 +100,7 @@ def _wg(r: dict) -> int:
 
 
 def _tjk(name: str) -> bool:
-    return GEMM in name or FLASH in name or LN in name or FFN in name
+    return _is_gemm(name) or FLASH in name or LN in name or FFN in name
 
 
 def _forwards(rows: List[dict], layers: int) -> Dict[Tuple, List[List[Tuple[str, dict]]]]:
