@@ -177,6 +177,39 @@ def test_gemm_k_order_classes_are_bitwise_identical(device, epi):
                 assert torch.equal(out, outs[0]), f"class {cls}: plan {plan} differs from plan {plans[0]}"
 
 
+@pytest.mark.parametrize("epi", [ops.EPI_BIAS, ops.EPI_BIAS_GELU, ops.EPI_BIAS_RESIDUAL])
+@pytest.mark.parametrize("plan", [9, 14, 16, 21, 29])
+def test_gemm_write_through_launch_equals_plain(device, epi, plan):
+    """A launch whose output reaches 4 MiB stores it written through the L2
+    (cache policy sc1), a smaller one with plain stores.  Rows do not depend
+    on the launch's other rows, so with the tile plan fixed the first rows of
+    a 2112-row launch (4.1 MiB of bf16, 8.3 MiB of fp32) are bitwise those of
+    a 1000-row one (2.0 / 3.9 MiB); the large launch also against fp64."""
+    n, k, big, small = 1024, 512, 2112, 1000
+    g = _gen(23 + plan)
+    a = torch.randn(big, k, generator=g).bfloat16()
+    w = (torch.randn(n, k, generator=g) / math.sqrt(k)).bfloat16()
+    b = torch.randn(n, generator=g).bfloat16()
+    r0 = torch.randn(big, n, generator=g)
+    outs = []
+    for m in (big, small):
+        if epi == ops.EPI_BIAS_RESIDUAL:
+            out = r0[:m].to(device)
+        else:
+            out = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=device)
+        ops.gemm(a[:m].to(device), w.to(device), b.to(device), out, epi, plan)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][:small], outs[1])
+    ref = a.double() @ w.double().t() + b.double()
+    if epi == ops.EPI_BIAS_GELU:
+        ref = 0.5 * ref * (1 + torch.erf(ref / math.sqrt(2)))
+    if epi == ops.EPI_BIAS_RESIDUAL:
+        ref = ref + r0.double()
+    rtol = 2e-5 if epi == ops.EPI_BIAS_RESIDUAL else OUT_RTOL[torch.bfloat16]
+    _close(outs[0], ref, rtol, 1e-4)
+
+
 @pytest.mark.parametrize("plan", list(STAGED32) + list(DTL32))
 def test_gemm_fp32_plans(device, plan):
     _gemm_case(device, 257, 516, 256, torch.float32, ops.EPI_BIAS, plan)
@@ -273,6 +306,74 @@ def test_add_layernorm_gather_scatter(device, out_dt):
                           torch.empty(8, n, device=device), res_out=r,
                           row_index=torch.arange(8, dtype=torch.int32, device=device))
 
+
+
+@pytest.mark.parametrize("case", ["delta", "gather", "scatter", "split", "two_byte"])
+def test_add_layernorm_write_through_launch_equals_plain(device, case):
+    """A LayerNorm launch whose normalised output reaches 4 MiB is the
+    write-through instantiation (stores with cache policy sc1, gamma / beta
+    loaded before the row); a smaller one the plain instantiation.  Each
+    output row depends on its own input row only, so the first rows of a
+    2176-row launch (4.25 MiB of bf16 at n = 1024; fp32 output: 8.5 MiB) are
+    bitwise those of a 600-row one; the large launch also against fp64.
+    Covers the row kernel (delta, row mask, fp32 and 2-byte residual
+    output, gather and scatter with holes) and the split-delta kernel."""
+    n, big, small = 1024, 2176, 600
+    g = _gen(31)
+    gamma, beta = torch.randn(n, generator=g).to(device), torch.randn(n, generator=g).to(device)
+    res = (torch.randn(big, n, generator=g) * 2).to(device)
+    delta = torch.randn(big, n, generator=g).bfloat16().to(device)
+    parts = torch.randn(8, big, n, generator=g).to(device)
+    mask = (torch.rand(big, generator=g) > 0.2).to(device)
+    index = torch.randperm(big, generator=g).to(torch.int32)
+    index[::7] = -1
+    index = index.to(device)
+    out_dt = torch.float32 if case == "gather" else torch.bfloat16
+
+    def run(m):
+        out = torch.full((m, n), float("nan"), dtype=out_dt, device=device)
+        ro = None
+        if case == "delta":
+            ro = torch.empty(m, n, device=device)
+            ops.add_layernorm(res[:m], delta[:m], gamma, beta, 1e-5, out, res_out=ro, row_mask=mask[:m])
+        elif case == "gather":
+            ro = torch.empty(m, n, device=device)
+            ops.add_layernorm(res.bfloat16(), None, gamma, beta, 1e-5, out, res_out=ro,
+                              row_index=index[:m].clamp(min=0))
+        elif case == "scatter":
+            ops.add_layernorm(res, None, gamma, beta, 1e-5, out, row_index=index[:m])
+        elif case == "split":
+            ro = res[:m].clone()
+            ops.add_layernorm(ro, parts[:, :m], gamma, beta, 1e-5, out, res_out=ro)
+        else:  # two_byte: bf16 residual stream in and out
+            ro = torch.empty(m, n, dtype=torch.bfloat16, device=device)
+            ops.add_layernorm(res[:m].bfloat16(), delta[:m], gamma, beta, 1e-5, out, res_out=ro)
+        return out, ro
+
+    (ob, rb), (os_, rs) = run(big), run(small)
+    torch.cuda.synchronize()
+    assert torch.equal(ob[:small], os_)
+    if rb is not None:
+        assert torch.equal(rb[:small], rs)
+    # the large launch against fp64
+    x = res.double().cpu()
+    rows = torch.arange(big)
+    if case == "delta" or case == "two_byte":
+        x = (res.bfloat16() if case == "two_byte" else res).double().cpu() + delta.double().cpu()
+    elif case == "gather":
+        rows = index.cpu().clamp(min=0).long()
+        x = res.bfloat16().double().cpu()
+    elif case == "scatter":
+        rows = index.cpu().long()
+    elif case == "split":
+        x = x + parts.double().cpu().sum(0)
+    ref = oracle.layer_norm(x[rows.clamp(min=0)], gamma.double().cpu(), beta.double().cpu(), 1e-5)
+    if case == "delta":
+        ref = ref.masked_fill(~mask.cpu()[:, None], 0.0)
+    if case == "scatter":
+        ref = ref.masked_fill((rows < 0)[:, None], 0.0)
+        assert (ob.cpu()[rows < 0] == 0).all()
+    _close(ob, ref, OUT_RTOL[out_dt], 1e-5 if out_dt == torch.float32 else 4e-3)
 
 
 @pytest.mark.parametrize("split_delta", [False, True])

@@ -537,7 +537,6 @@ constexpr int kFaSc1 = 16, kFaSc0Sc1 = 17;
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kFaSpinLimit = 1 << 20;  // polls of a split item's flag before giving up (>= 0.1 s)
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // Buffer descriptor over `bytes` bytes at p (stride 0, raw dword access).
 __device__ __forceinline__ u32x4 fa_rsrc(const void* p, int bytes) {

@@ -151,6 +151,8 @@ __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* _
   // 16-byte output pieces need a 16-byte aligned C and a leading dimension
   // that keeps every row 16-byte aligned; otherwise pieces go out as halves.
   const bool a16 = ((uintptr_t)Cv & 15) == 0 && (ldc % E::SV) == 0;
+  constexpr int OB = E::F32OUT ? 4 : (int)sizeof(T);  // output bytes per element
+  const bool wt = (int64_t)M * N * OB >= kWtMinBytes;
 
   // bias of this wave's columns (loaded here unless the caller did)
   BiasRaw<T, FN> own;
@@ -182,34 +184,40 @@ __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* _
         else
           *reinterpret_cast<typename Quad<T>::raw*>(dst) = Quad<T>::from(v);
       }
+    // rows mw + 32 j .. of this block, from column nw
+    const int64_t rb0 = (int64_t)(mw + 32 * j) * ldc + nw;
+    const RowOut rows(static_cast<char*>(Cv) + rb0 * OB, ((int64_t)M * ldc - rb0) * OB, wt);
+    with_wt(rows.wt, [&](auto wt_tag) {
+      const auto wr = rows.writer<decltype(wt_tag)::value>();
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      const int pc = lane + 64 * it;  // piece index: row pc / LPR, piece pc % LPR
-      if (NPC % 64 != 0 && pc >= NPC) break;
-      const int rr = pc / LPR, cc = (pc % LPR) * E::SV;
-      const int m = mw + 32 * j + rr, n = nw + cc;
-      const uint4 piece = *reinterpret_cast<const uint4*>(st + rr * E::PITCH + cc);
-      if (m < M && n < N) {
-        if constexpr (EPI == TJK_EPI_BIAS_RESIDUAL) {
-          // fp32 pieces never straddle N (N % 4 == 0)
-          const float4 a = __builtin_bit_cast(float4, piece);
-          float4* r = reinterpret_cast<float4*>(static_cast<float*>(Cv) + (int64_t)m * ldc + n);
-          float4 o = Pre::on ? pre.get(j, it) : *r;
-          o.x += a.x; o.y += a.y; o.z += a.z; o.w += a.w;
-          *r = o;
-        } else if constexpr (EPI == kEpiStoreF32) {
-          *reinterpret_cast<uint4*>(static_cast<float*>(Cv) + (int64_t)m * ldc + n) = piece;
-        } else {
-          T* c = static_cast<T*>(Cv) + (int64_t)m * ldc + n;
-          if (E::SV == 4 || (a16 && n + E::SV <= N)) {
-            *reinterpret_cast<uint4*>(c) = piece;
-          } else {  // 2-byte types: halves of 4 elements (N % 4 == 0)
-            *reinterpret_cast<uint2*>(c) = make_uint2(piece.x, piece.y);
-            if (n + 4 < N) *reinterpret_cast<uint2*>(c + 4) = make_uint2(piece.z, piece.w);
+      for (int it = 0; it < NIT; ++it) {
+        const int pc = lane + 64 * it;  // piece index: row pc / LPR, piece pc % LPR
+        if (NPC % 64 != 0 && pc >= NPC) break;
+        const int rr = pc / LPR, cc = (pc % LPR) * E::SV;
+        const int m = mw + 32 * j + rr, n = nw + cc;
+        const uint4 piece = *reinterpret_cast<const uint4*>(st + rr * E::PITCH + cc);
+        const int off = (int)(((int64_t)rr * ldc + cc) * OB);
+        if (m < M && n < N) {
+          if constexpr (EPI == TJK_EPI_BIAS_RESIDUAL) {
+            // fp32 pieces never straddle N (N % 4 == 0)
+            const float4 a = __builtin_bit_cast(float4, piece);
+            float4 o = Pre::on ? pre.get(j, it) : *reinterpret_cast<const float4*>(rows.p + off);
+            o.x += a.x; o.y += a.y; o.z += a.z; o.w += a.w;
+            wr.put(off, o);
+          } else if constexpr (EPI == kEpiStoreF32) {
+            wr.put(off, piece);
+          } else {
+            if (E::SV == 4 || (a16 && n + E::SV <= N)) {
+              wr.put(off, piece);
+            } else {  // 2-byte types: halves of 4 elements (N % 4 == 0)
+              T* c = static_cast<T*>(Cv) + (int64_t)m * ldc + n;
+              *reinterpret_cast<uint2*>(c) = make_uint2(piece.x, piece.y);
+              if (n + 4 < N) *reinterpret_cast<uint2*>(c + 4) = make_uint2(piece.z, piece.w);
+            }
           }
         }
       }
-    }
+    });
   }
 }
 

@@ -48,17 +48,31 @@ int check_launch(const char* what) {
 // stream's dtype: fp32, or a 2-byte type rounded to nearest even (the
 // reference's residual_dtype knob, tjkernels/plans.py:33-36).  ro_dtype is
 // the same for every lane of a launch, so the branch is uniform.
-__device__ __forceinline__ void store_res_chunk(void* row, int c, int ro_dtype, const float4& v) {
+// `row` is the wave's output row (res_row); a wave's stores cover whole row
+// segments.
+template <typename W>
+__device__ __forceinline__ void store_res_chunk(const W& row, int c, int ro_dtype, const float4& v) {
   if (ro_dtype == TJK_F32)
-    reinterpret_cast<float4*>(row)[c] = v;
+    row.put(c * 16, v);
   else if (ro_dtype == TJK_F16)
-    reinterpret_cast<typename Quad<f16>::raw*>(row)[c] = Quad<f16>::from(v);
+    row.put(c * 8, Quad<f16>::from(v));
   else
-    reinterpret_cast<typename Quad<bf16>::raw*>(row)[c] = Quad<bf16>::from(v);
+    row.put(c * 8, Quad<bf16>::from(v));
 }
 
-__device__ __forceinline__ void* res_row(void* base, int ro_dtype, int64_t row, int64_t ld) {
-  return static_cast<char*>(base) + row * ld * (ro_dtype == TJK_F32 ? 4 : 2);
+// Stores into row `row` (n elements) of the residual output, written
+// through the L2 when WT.
+template <bool WT>
+__device__ __forceinline__ auto res_row(void* base, int ro_dtype, int64_t row, int64_t ld, int n) {
+  const int es = ro_dtype == TJK_F32 ? 4 : 2;
+  return RowOut(static_cast<char*>(base) + row * ld * es, (int64_t)n * es, WT).writer<WT>();
+}
+
+// Stores into row `row` (n elements) of the normalised output, written
+// through the L2 when WT.
+template <bool WT, typename TOut>
+__device__ __forceinline__ auto out_row(TOut* out, int64_t row, int64_t ld, int n) {
+  return RowOut(out + row * ld, (int64_t)n * (int64_t)sizeof(TOut), WT).writer<WT>();
 }
 
 // The gather / scatter map of a launch: output row r reads input row
@@ -80,7 +94,7 @@ __device__ __forceinline__ int64_t map_row(const RowMap& rm, int64_t row, bool c
 }
 
 // FULL: n == 256 * MAXCH, every lane's chunks in range (no per-chunk guards).
-template <typename TRes, typename TDelta, typename TOut, int MAXCH, bool FULL>
+template <typename TRes, typename TDelta, typename TOut, int MAXCH, bool FULL, bool WT>
 __global__ __launch_bounds__(256) void add_layernorm_kernel(
     const TRes* res, int64_t ld_res,  // may alias res_out (in-place update)
     const TDelta* __restrict__ delta, int64_t ld_delta,
@@ -93,6 +107,25 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const bool live = row < rows;
   const int64_t src = !live ? -1 : map_row(rmap, row, lane == 0);
+
+  // gamma / beta staged once per workgroup (4 rows), by every thread before
+  // any wave leaves: read from L2 by each wave they were 8 KB per 1024-wide
+  // row, more than the row itself.  In launches large enough to write
+  // through (WT) and up to 2048-wide rows, their loads go out first, in
+  // flight together with the row's (measured: 6.4 -> 4.9 us per C4
+  // LayerNorm together with the write-through stores; in launches of a few
+  // hundred rows, 0.1 us slower).
+  constexpr int GPT = (64 * MAXCH + 255) / 256;  // gamma / beta chunks per thread
+  constexpr bool EARLY = WT && GPT <= 2;
+  float4 gl[EARLY ? GPT : 1], bl[EARLY ? GPT : 1];
+  if constexpr (EARLY) {
+#pragma unroll
+    for (int u = 0; u < GPT; ++u) {
+      const int c = min((int)threadIdx.x + 256 * u, nch - 1);
+      gl[u] = reinterpret_cast<const float4*>(gamma)[c];
+      bl[u] = reinterpret_cast<const float4*>(beta)[c];
+    }
+  }
 
   // Chunks past the row end are read at the last chunk and dropped: loads
   // under a per-lane condition are waited for one at a time.
@@ -124,33 +157,43 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(
     for (int j = 0; j < MAXCH; ++j)
       if (!FULL && lane + 64 * j >= nch) x[j] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  // gamma / beta staged once per workgroup (4 rows), by every thread before
-  // any wave leaves: read from L2 by each wave they were 8 KB per 1024-wide
-  // row, more than the row itself
   __shared__ float4 s_gamma[64 * MAXCH], s_beta[64 * MAXCH];
-  for (int c = threadIdx.x; c < nch; c += 256) {
-    s_gamma[c] = reinterpret_cast<const float4*>(gamma)[c];
-    s_beta[c] = reinterpret_cast<const float4*>(beta)[c];
+  if constexpr (EARLY) {
+#pragma unroll
+    for (int u = 0; u < GPT; ++u) {
+      const int c = (int)threadIdx.x + 256 * u;
+      if (c < nch) {
+        s_gamma[c] = gl[u];
+        s_beta[c] = bl[u];
+      }
+    }
+  } else {
+    for (int c = threadIdx.x; c < nch; c += 256) {
+      s_gamma[c] = reinterpret_cast<const float4*>(gamma)[c];
+      s_beta[c] = reinterpret_cast<const float4*>(beta)[c];
+    }
   }
   __syncthreads();
   if (!live) return;
+  constexpr int OB = (int)sizeof(typename Quad<TOut>::raw);  // bytes per output chunk
   if (src < 0) {  // scatter hole: an exact zero row, nothing read
-    typename Quad<TOut>::raw* yrow = reinterpret_cast<typename Quad<TOut>::raw*>(out + row * ld_out);
+    const auto w = out_row<WT>(out, row, ld_out, n);
 #pragma unroll
     for (int j = 0; j < MAXCH; ++j) {
       const int c = lane + 64 * j;
-      if (FULL || c < nch) yrow[c] = Quad<TOut>::from(make_float4(0.f, 0.f, 0.f, 0.f));
+      if (FULL || c < nch)
+        w.put(c * OB, Quad<TOut>::from(make_float4(0.f, 0.f, 0.f, 0.f)));
     }
     return;
   }
 
   float s = 0.f;
   if (res_out != nullptr) {
-    void* orow = res_row(res_out, ro_dtype, row, ld_res_out);
+    const auto w = res_row<WT>(res_out, ro_dtype, row, ld_res_out, n);
 #pragma unroll
     for (int j = 0; j < MAXCH; ++j) {
       const int c = lane + 64 * j;
-      if (FULL || c < nch) store_res_chunk(orow, c, ro_dtype, x[j]);
+      if (FULL || c < nch) store_res_chunk(w, c, ro_dtype, x[j]);
     }
   }
 #pragma unroll
@@ -170,7 +213,7 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(
   const float rstd = 1.0f / sqrtf(var + eps);
   const bool zero = row_mask != nullptr && row_mask[row] == 0;
 
-  typename Quad<TOut>::raw* yrow = reinterpret_cast<typename Quad<TOut>::raw*>(out + row * ld_out);
+  const auto w = out_row<WT>(out, row, ld_out, n);
 #pragma unroll
   for (int j = 0; j < MAXCH; ++j) {
     const int c = lane + 64 * j;
@@ -185,7 +228,7 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(
         y.z = (x[j].z - mean) * rstd * g.z + b.z;
         y.w = (x[j].w - mean) * rstd * g.w + b.w;
       }
-      yrow[c] = Quad<TOut>::from(y);
+      w.put(c * OB, Quad<TOut>::from(y));
     }
   }
 }
@@ -197,14 +240,15 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(
 // S_3) (waves without slices skipped), and normalises the row with the row
 // kernel's arithmetic.  Spreading one row's slices over four waves keeps a
 // launch of a few hundred rows from waiting out n_delta / 4 load latencies.
-template <typename TRes, typename TOut, int MAXCH>
+template <typename TRes, typename TOut, int MAXCH, bool WT>
 __global__ __launch_bounds__(256) void add_layernorm_parts_kernel(
     const TRes* res, int64_t ld_res,  // may alias res_out (in-place update)
     const float* __restrict__ parts, int64_t ld_parts, int n_parts, int64_t part_stride,
     void* res_out, int ro_dtype, int64_t ld_res_out, TOut* __restrict__ out, int64_t ld_out,
-    const float* __restrict__ gamma, const float* __restrict__ beta, int n, float eps,
+    const float* __restrict__ gamma, const float* __restrict__ beta, int64_t rows, int n, float eps,
     RowMap rmap, const uint8_t* __restrict__ row_mask) {
   constexpr int PER = 32 / MAXCH;  // slices per load batch of one wave
+  constexpr int OB = (int)sizeof(typename Quad<TOut>::raw);  // bytes per output chunk
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nch = n >> 2;
   const int64_t row = blockIdx.x;
@@ -212,10 +256,11 @@ __global__ __launch_bounds__(256) void add_layernorm_parts_kernel(
   __shared__ float4 s_sum[3][MAXCH][64];
   if (src < 0) {  // scatter hole: an exact zero row
     if (wave == 0) {
-      typename Quad<TOut>::raw* yrow = reinterpret_cast<typename Quad<TOut>::raw*>(out + row * ld_out);
+      const auto w = out_row<WT>(out, row, ld_out, n);
 #pragma unroll
       for (int j = 0; j < MAXCH; ++j)
-        if (lane + 64 * j < nch) yrow[lane + 64 * j] = Quad<TOut>::from(make_float4(0.f, 0.f, 0.f, 0.f));
+        if (lane + 64 * j < nch)
+          w.put((lane + 64 * j) * OB, Quad<TOut>::from(make_float4(0.f, 0.f, 0.f, 0.f)));
     }
     return;
   }
@@ -285,10 +330,10 @@ __global__ __launch_bounds__(256) void add_layernorm_parts_kernel(
     if (lane + 64 * j >= nch) x[j] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
   if (res_out != nullptr) {
-    void* orow = res_row(res_out, ro_dtype, row, ld_res_out);
+    const auto w = res_row<WT>(res_out, ro_dtype, row, ld_res_out, n);
 #pragma unroll
     for (int j = 0; j < MAXCH; ++j)
-      if (lane + 64 * j < nch) store_res_chunk(orow, lane + 64 * j, ro_dtype, x[j]);
+      if (lane + 64 * j < nch) store_res_chunk(w, lane + 64 * j, ro_dtype, x[j]);
   }
   float sm = 0.f;
 #pragma unroll
@@ -306,7 +351,7 @@ __global__ __launch_bounds__(256) void add_layernorm_parts_kernel(
   const float var = wave_sum(qq) * inv_n;
   const float rstd = 1.0f / sqrtf(var + eps);
   const bool zero = row_mask != nullptr && row_mask[row] == 0;
-  typename Quad<TOut>::raw* yrow = reinterpret_cast<typename Quad<TOut>::raw*>(out + row * ld_out);
+  const auto w = out_row<WT>(out, row, ld_out, n);
 #pragma unroll
   for (int j = 0; j < MAXCH; ++j) {
     const int c = lane + 64 * j;
@@ -321,7 +366,7 @@ __global__ __launch_bounds__(256) void add_layernorm_parts_kernel(
         y.z = (x[j].z - mean) * rstd * g.z + b.z;
         y.w = (x[j].w - mean) * rstd * g.w + b.w;
       }
-      yrow[c] = Quad<TOut>::from(y);
+      w.put(c * OB, Quad<TOut>::from(y));
     }
   }
 }
@@ -333,14 +378,23 @@ static int launch_ln_parts(const void* res, int64_t ld_res, const float* parts, 
                            const RowMap& rmap, const uint8_t* row_mask, hipStream_t stream) {
   const int nch = n / 4;
   const dim3 grid((unsigned)rows), block(256);
-#define TJK_LNP(MC)                                                                                           \
-  hipLaunchKernelGGL((add_layernorm_parts_kernel<TRes, TOut, MC>), grid, block, 0, stream, (const TRes*)res,   \
+  const bool wt = rows * n * (int64_t)sizeof(TOut) >= kWtMinBytes;
+#define TJK_LNP1(MC, WT)                                                                                      \
+  hipLaunchKernelGGL((add_layernorm_parts_kernel<TRes, TOut, MC, WT>), grid, block, 0, stream, (const TRes*)res, \
                      ld_res, parts, ld_parts, n_parts, part_stride, res_out, ro_dtype, ld_res_out, (TOut*)out, ld_out, gamma, \
-                     beta, n, eps, rmap, row_mask)
+                     beta, rows, n, eps, rmap, row_mask)
+#define TJK_LNP(MC)            \
+  do {                         \
+    if (wt)                    \
+      TJK_LNP1(MC, true);      \
+    else                       \
+      TJK_LNP1(MC, false);     \
+  } while (0)
   if (nch <= 64) TJK_LNP(1);
   else if (nch <= 128) TJK_LNP(2);
   else TJK_LNP(4);
 #undef TJK_LNP
+#undef TJK_LNP1
   return check_launch("tjk_add_layernorm");
 }
 
@@ -357,10 +411,18 @@ static int launch_ln(const void* res, int64_t ld_res, const void* delta, int64_t
   }
   const int nch = n / 4;
   dim3 grid((unsigned)((rows + 3) / 4)), block(256);
-#define TJK_LN_LAUNCH(MC, FULL)                                                                    \
-  hipLaunchKernelGGL((add_layernorm_kernel<TRes, TDelta, TOut, MC, FULL>), grid, block, 0, stream,     \
+  const bool wt = rows * n * (int64_t)sizeof(TOut) >= kWtMinBytes;
+#define TJK_LN_LAUNCH1(MC, FULL, WT)                                                                   \
+  hipLaunchKernelGGL((add_layernorm_kernel<TRes, TDelta, TOut, MC, FULL, WT>), grid, block, 0, stream,     \
                      (const TRes*)res, ld_res, (const TDelta*)delta, ld_delta, res_out, ro_dtype, ld_res_out, \
                      (TOut*)out, ld_out, gamma, beta, rows, n, eps, rmap, row_mask)
+#define TJK_LN_LAUNCH(MC, FULL)        \
+  do {                                 \
+    if (wt)                            \
+      TJK_LN_LAUNCH1(MC, FULL, true);  \
+    else                               \
+      TJK_LN_LAUNCH1(MC, FULL, false); \
+  } while (0)
 #define TJK_LN_CASE(MC)                                   \
   if (nch <= 64 * MC) {                                   \
     if (nch == 64 * MC) TJK_LN_LAUNCH(MC, true);          \
@@ -385,6 +447,7 @@ static int launch_ln(const void* res, int64_t ld_res, const void* delta, int64_t
   TJK_LN_CASE(32)
 #undef TJK_LN_CASE
 #undef TJK_LN_LAUNCH
+#undef TJK_LN_LAUNCH1
   return fail(TJK_EUNSUPPORTED, "tjk_add_layernorm: n=%d exceeds 8192", n);
 }
 
