@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define TJK_ABI_VERSION 8
+#define TJK_ABI_VERSION 9
 
 /* dtypes */
 #define TJK_F32 0
@@ -171,7 +171,11 @@ int tjk_flash_plan_count(int dtype);
  * Scheduled flash attention over packed sequences (bf16 / fp16): the same
  * math as tjk_flash_fwd with cu_seqlens, but the workgroups follow a work
  * list built by the caller (from the host-known lengths), so long query
- * blocks can start first and be split over their key range.
+ * blocks can start first and be split over their key range.  The launch
+ * runs n_lists workgroups (1 <= n_lists <= n_work); workgroup w runs items
+ * w, w + n_lists, w + 2*n_lists, ... (< n_work) back to back, in that order
+ * (n_lists == n_work: one item per workgroup).  An item { -1, *, *, * } is
+ * a hole (padding of a shorter list) and is skipped.
  *   work[4*i .. 4*i+3] = { b*heads + h, qb, t_lo | t_hi << 16, slot }
  *     query block qb (queries 128*qb .. 128*qb+127 of sequence b, head h)
  *     over key tiles t_lo .. t_hi-1 (64 keys each; t_hi is clipped to the
@@ -181,8 +185,12 @@ int tjk_flash_plan_count(int dtype);
  *     offset and sum per query) in partials slot s, the second (slot -2-s)
  *     waits for it, merges it into its own ((O_hi a_hi + O_lo a_lo) /
  *     (l_hi a_hi + l_lo a_lo), in that order, so results are deterministic)
- *     and writes the output rows.  The first half must precede the second in
- *     the list (workgroups are dispatched in list order).
+ *     and writes the output rows.  The first half must run first: with one
+ *     item per workgroup, before the second in the list (workgroups are
+ *     dispatched in list order); with lists, at the head of a list (index
+ *     < n_lists), and all n_lists workgroups must fit on the device at once.
+ *     A second half's wait is bounded: a list breaking these rules costs
+ *     NaN rows and an error count, never a hang.
  * Every (query block, key tile) pair of every sequence must be covered
  * exactly once.  partials holds partials_bytes >=
  * tjk_flash_partial_bytes(head_dim, n_slots) bytes: the n_slots partials,
@@ -199,8 +207,8 @@ int tjk_flash_plan_count(int dtype);
 int tjk_flash_fwd_sched(const void* qkv, int64_t stride_s, int64_t stride_c, int64_t stride_h,
                         void* out, int64_t ld_out, int batch, int max_seqlen, int heads,
                         int head_dim, float scale, int causal, const int32_t* cu_seqlens,
-                        const int32_t* work, int n_work, float* partials, size_t partials_bytes,
-                        int n_slots, int dtype, void* stream);
+                        const int32_t* work, int n_work, int n_lists, float* partials,
+                        size_t partials_bytes, int n_slots, int dtype, void* stream);
 size_t tjk_flash_partial_bytes(int head_dim, int n_slots);
 
 /*
@@ -219,7 +227,8 @@ size_t tjk_flash_partial_bytes(int head_dim, int n_slots);
 int tjk_flash_fwd_sched_static(const void* qkv, int64_t stride_s, int64_t stride_c, int64_t stride_h,
                                void* out, int64_t ld_out, int batch, int max_seqlen, int heads,
                                int head_dim, float scale, int causal, const int32_t* cu_seqlens,
-                               const int32_t* work, int n_work, int n_slots, int dtype, void* stream);
+                               const int32_t* work, int n_work, int n_lists, int n_slots, int dtype,
+                               void* stream);
 size_t tjk_flash_sched_static_bytes(void);
 /* Workgroups of the scheduled kernel resident per CU (> 0), or a negative /
  * hipError_t status. */

@@ -741,6 +741,49 @@ def test_flash_scheduled(device, dt, hd, causal):
             assert torch.equal(again.cpu(), got), "split merge is not deterministic"
 
 
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("hd", [64, 128])
+def test_flash_scheduled_lists(device, causal, hd):
+    """More items than workgroups: 16 lists (build_schedule's slots), each
+    workgroup running its items back to back, with split items' first halves
+    at list heads (causal: 6 splits).  Against fp64, bitwise repeatable, no
+    wait timed out and every flag cleared; without splits, bitwise equal to
+    one workgroup per item (the same items, the same arithmetic)."""
+    from tjkernels import schedule as sched_mod
+    lengths, h, dt = [1000] + [64] * 8, 2, torch.bfloat16
+    cu = [0]
+    for n in lengths:
+        cu.append(cu[-1] + n)
+    t = cu[-1]
+    qkv = torch.randn(t, 3, h, hd, generator=_gen(hd + int(causal))).to(dt)
+    cu_d = torch.tensor(cu, dtype=torch.int32, device=device)
+    sched = sched_mod.build_schedule(lengths, h, hd, causal, dt, device, slots=16, min_split=2,
+                                     split_factor=1.0, lists=True)
+    assert sched.n_lists == 16 and sched.work.shape[0] > 16
+    assert (sched.n_slots == 6) == causal and (sched.n_slots == 0) == (not causal)
+    outs = []
+    for _ in range(2):
+        out = torch.full((t, h * hd), 7.0, dtype=dt, device=device)
+        ops.flash_attention_sched(qkv.to(device), out, cu_d, max(lengths), sched, causal=causal)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    assert sched_mod.error_count(sched) == 0
+    hdp = 64 if hd <= 64 else 128
+    assert int(sched.partials.view(torch.int32)[sched.n_slots * 128 * (hdp + 2):].abs().sum()) == 0
+    got = outs[0].cpu()
+    for b, n in enumerate(lengths):
+        ref = _attn_ref(qkv[cu[b]:cu[b + 1]].unsqueeze(0), causal)
+        _close(got[cu[b]:cu[b + 1]], ref, 1e-2, 1e-2)
+    if not causal:
+        one = sched_mod.build_schedule(lengths, h, hd, causal, dt, device, slots=100000, min_split=1 << 14)
+        assert one.n_lists == 0
+        per_item = torch.full((t, h * hd), 7.0, dtype=dt, device=device)
+        ops.flash_attention_sched(qkv.to(device), per_item, cu_d, max(lengths), one, causal=causal)
+        torch.cuda.synchronize()
+        assert torch.equal(per_item, outs[0])
+
+
 def test_flash_scheduled_reports_items_it_cannot_run(device):
     """Failure handling, forced from the host with lists validate_work would
     reject (written straight to the device): an item for a (b, h) outside

@@ -66,8 +66,12 @@ def test_abi_rejects_bad_arguments_without_launching():
     assert lib.tjk_ffn(fake, _lib.F16, 512, None, None, 0.0, fake, None, fake, None, fake, 512, 0, 16, 1,
                        16, 512, 2048, _lib.F16, None) == _lib.EINVAL  # accumulate with 16 splits
     # scheduled attention: split slots without enough partials bytes
-    assert lib.tjk_flash_fwd_sched(fake, 192, 64, 64, fake, 64, 1, 128, 1, 64, 0.125, 1, fake, fake, 2,
+    assert lib.tjk_flash_fwd_sched(fake, 192, 64, 64, fake, 64, 1, 128, 1, 64, 0.125, 1, fake, fake, 2, 2,
                                    fake, 16, 1, _lib.BF16, None) == _lib.EINVAL
+    # the lists of a work list: 1 .. n_work of them
+    for n_lists in (0, 3, -1):
+        assert lib.tjk_flash_fwd_sched(fake, 192, 64, 64, fake, 64, 1, 128, 1, 64, 0.125, 1, fake, fake, 2,
+                                       n_lists, None, 0, 0, _lib.BF16, None) == _lib.EINVAL
     # empty work is a successful no-op
     assert lib.tjk_gemm_bias(None, 8, None, 8, None, None, 8, 0, 4, 8, _lib.BF16, 0, -1, None) == 0
     assert lib.tjk_gemm_plan_count(_lib.BF16) >= 4
@@ -289,7 +293,7 @@ def test_static_attention_workspace_rejects_too_many_slots():
     per_slot = lib.tjk_flash_partial_bytes(128, 1)
     too_many = cap // per_slot + 1
     assert lib.tjk_flash_partial_bytes(128, too_many) > cap
-    rc = lib.tjk_flash_fwd_sched_static(None, 384, 128, 128, None, 128, 1, 128, 1, 128, 0.1, 1, None, None, 1,
+    rc = lib.tjk_flash_fwd_sched_static(None, 384, 128, 128, None, 128, 1, 128, 1, 128, 0.1, 1, None, None, 1, 1,
                                         too_many, _lib.BF16, None)
     assert rc == _lib.EUNSUPPORTED and b"static" in lib.tjk_last_error_string()
 
@@ -456,6 +460,47 @@ def test_work_list_validation_rejects_broken_lists():
     for name, bad in cases.items():
         with pytest.raises(ValueError):
             validate_work(bad, lengths, heads, True, n_slots)
+
+
+def test_attention_lists_balance_items_and_head_split_halves():
+    """pack_lists deals every item of build_items' list exactly once into
+    n_lists lists laid out item-major (item j of list w at j * n_lists + w,
+    HOLE padding), first halves of split items at list heads, largest cost
+    first into the least-loaded list: no list ends more than one item's cost
+    above the lightest (the LPT bound), and at the C4 lengths the heaviest
+    list is the longest single item.  validate_work accepts the layout and
+    rejects a first half moved off a list head."""
+    from tjkernels.schedule import HOLE, ITEM_OVERHEAD, build_items, pack_lists, validate_work
+    for lengths, heads, slots, n_lists, split in (([1380, 1710, 1054, 1286], 16, 512, 512, 2.0),
+                                                  ([300, 70, 0, 260, 129, 1], 3, 32, 16, 1.0)):
+        work, n_slots = build_items(lengths, heads, True, slots, min_split=2, split_factor=split)
+        assert (n_slots > 0) == (n_lists == 16)
+        laid = pack_lists(work, n_lists)
+        assert len(laid) % n_lists == 0
+        items = [w for w in laid if w != HOLE]
+        assert sorted(items) == sorted(w[1:] for w in work)
+        validate_work(laid, lengths, heads, True, n_slots, n_lists)
+        heads_ = [laid[i] for i in range(n_lists)]
+        assert {w[1:] for w in work if w[5] >= 0} <= set(heads_)
+        load = [0] * n_lists
+        last = [0] * n_lists
+        for j, w in enumerate(laid):
+            if w != HOLE:
+                load[j % n_lists] += w[3] - w[2] + ITEM_OVERHEAD
+                last[j % n_lists] = w[3] - w[2] + ITEM_OVERHEAD
+        assert all(load[i] - last[i] <= min(load) for i in range(n_lists)), "an item went to a heavier list"
+        if n_slots == 0:
+            assert max(load) == max(w[0] for w in work) + ITEM_OVERHEAD
+        if n_slots:
+            first = next(j for j in range(n_lists) if laid[j][4] >= 0)
+            moved = list(laid)
+            moved[first], moved[first + n_lists] = moved[first + n_lists], moved[first]
+            with pytest.raises(ValueError):
+                validate_work(moved, lengths, heads, True, n_slots, n_lists)
+    work, n_slots = build_items([300, 260], 2, True, 8, min_split=2, split_factor=0.5)
+    assert n_slots == 8
+    with pytest.raises(ValueError):  # more split items than lists
+        pack_lists(work, 7)
 
 
 def test_gemm_tile_classes_follow_the_library_table():

@@ -40,7 +40,8 @@ def _run(lib, fn, qkv, cu_d, sched, lengths, heads, hd, dt, static):
     out = torch.full((t, heads * hd), 7.0, dtype=dt, device=qkv.device)
     ss, sc, sh, _ = qkv.stride()
     args = [qkv.data_ptr(), ss, sc, sh, out.data_ptr(), out.stride(0), len(lengths), max(lengths), heads, hd,
-            hd ** -0.5, 1, cu_d.data_ptr(), sched.work.data_ptr(), sched.work.shape[0]]
+            hd ** -0.5, 1, cu_d.data_ptr(), sched.work.data_ptr(), sched.work.shape[0],
+            sched.n_lists or sched.work.shape[0]]
     if static:
         rc = lib.tjk_flash_fwd_sched_static(*args, sched.n_slots, _lib.DTYPE_CODES[dt], _stream())
     else:

@@ -567,7 +567,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
     T* __restrict__ out, int64_t ld_out, int B, int S, int H, int hd, float scale_log2,
     int causal, const int32_t* __restrict__ lengths, const uint8_t* __restrict__ key_mask,
     const int32_t* __restrict__ cu_seqlens, int nqb,
-    const int4* __restrict__ work, float* __restrict__ partials, int* __restrict__ flags, int n_slots,
+    const int4* __restrict__ work, int n_work, float* __restrict__ partials, int* __restrict__ flags, int n_slots,
     int grp) {
   static_assert(sizeof(T) == 2, "2-byte element types only");
   static_assert(NW == 4 || (NW == 8 && HDP == 128), "8 waves for head_dim 128 only");
@@ -609,43 +609,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
   }
 
   const int BH = B * H;
-  // Work item: from the scheduled list (bh, qb, key tiles [t_lo, t_hi),
-  // slot), else from the grid (every key tile, longest first).  slot -1: a
-  // whole item; slot s >= 0: the first half of a key-split item, which
-  // publishes its partial in slot s; slot -2 - s: the second half, which
-  // merges partial s into its own before the store.
-  int bh, qb, t_lo = 0, t_hi = 1 << 30, slot = -1;
-  bool bad_slot = false;
-  if (work != nullptr) {
-    const int4 it = work[blockIdx.x];
-    bh = it.x;
-    qb = it.y;
-    t_lo = it.z & 0xffff;
-    t_hi = it.z >> 16;
-    slot = it.w;
-    // An item outside the launch's (b, h) range cannot be placed: it is
-    // counted in the error word and dropped.  A slot outside [0, n_slots)
-    // (or its second-half image) has no partial to publish or merge: the
-    // item's rows are written as NaN and counted.
-    if (bh < 0 || bh >= BH || qb < 0 || t_lo > t_hi) {
-      if (flags != nullptr && threadIdx.x == 0)
-        __hip_atomic_fetch_add(&flags[-1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return;
-    }
-    if (slot != -1 && (slot >= n_slots || slot < -1 - n_slots)) {
-      bad_slot = true;
-      slot = -1;
-    }
-  } else {
-    // Longest query blocks first within groups of `grp` (b, h) pairs: a
-    // group's blocks run together, which bounds the K/V the blocks in
-    // flight stream (grp = B*H: one group, longest first over everything).
-    const int gi = blockIdx.x / (grp * nqb), r = blockIdx.x % (grp * nqb);
-    const int gsize = min(grp, BH - gi * grp);
-    const int rank = r / gsize;
-    bh = gi * grp + r % gsize;
-    qb = causal ? nqb - 1 - rank : rank;
-  }
+  // One work item: query block qb of (b, h) = bh over key tiles [t_lo,
+  // t_hi).  slot -1: a whole item; slot s >= 0: the first half of a
+  // key-split item, which publishes its partial in slot s; slot -2 - s: the
+  // second half, which merges partial s into its own before the store.
+  // bad_slot: the listed slot was outside [0, n_slots) (the rows are written
+  // as NaN and counted).
+  auto run_item = [&](int bh, int qb, int t_lo, int t_hi, int slot, bool bad_slot) __attribute__((always_inline)) {
   const int b = bh / H, h = bh % H;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hi = lane >> 5;
@@ -1299,6 +1269,39 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
     __syncthreads();  // every wave has read the partial
     if (tid == 0) __hip_atomic_store(&flags[-2 - slot], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  };
+
+  // Scheduled (the 4-wave kernel without a key mask; the other
+  // instantiations are launched on the grid only and carry one copy of the
+  // item code): workgroup w runs items w, w + gridDim.x, w + 2 gridDim.x,
+  // ... of the list, in that order.  An item whose (b, h) is -1 is a hole
+  // (a shorter list's padding).  An item outside the launch's (b, h) range
+  // cannot be placed: it is counted in the error word and dropped.  A slot
+  // outside [0, n_slots) (or its second-half image) has no partial to
+  // publish or merge: the item's rows are written as NaN and counted.
+  if (!KEYMASK && NW == 4 && work != nullptr) {
+    for (int j = blockIdx.x; j < n_work; j += gridDim.x) {
+      const int4 it = work[j];
+      if (it.x == -1) continue;
+      const int t_lo = it.z & 0xffff, t_hi = it.z >> 16;
+      if (it.x < 0 || it.x >= BH || it.y < 0 || t_lo > t_hi) {
+        if (flags != nullptr && threadIdx.x == 0)
+          __hip_atomic_fetch_add(&flags[-1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        continue;
+      }
+      const bool bad_slot = it.w != -1 && (it.w >= n_slots || it.w < -1 - n_slots);
+      run_item(it.x, it.y, t_lo, t_hi, bad_slot ? -1 : it.w, bad_slot);
+      __syncthreads();  // the next item refills the K / V ring and the LDS flag
+    }
+  } else {
+    // Longest query blocks first within groups of `grp` (b, h) pairs: a
+    // group's blocks run together, which bounds the K/V the blocks in
+    // flight stream (grp = B*H: one group, longest first over everything).
+    const int gi = blockIdx.x / (grp * nqb), r = blockIdx.x % (grp * nqb);
+    const int gsize = min(grp, BH - gi * grp);
+    const int rank = r / gsize;
+    run_item(gi * grp + r % gsize, causal ? nqb - 1 - rank : rank, 0, 1 << 30, -1, false);
+  }
 }
 
 __global__ __launch_bounds__(256) void clear_words_kernel(int* p, int n) {
@@ -1308,7 +1311,8 @@ __global__ __launch_bounds__(256) void clear_words_kernel(int* p, int n) {
 template <typename T, int HDP>
 static int launch_sched(const void* qkv, int64_t ss, int64_t sc, int64_t sh, void* out, int64_t ld_out,
                         int B, int S, int H, int hd, float scale_log2, int causal, const int32_t* cu_seqlens,
-                        const int32_t* work, int n_work, float* partials, int n_slots, bool clear, hipStream_t st) {
+                        const int32_t* work, int n_work, int n_lists, float* partials, int n_slots, bool clear,
+                        hipStream_t st) {
   // [n_slots partial slots][error word][n_slots flags]; flags[-1] is the error word
   int* flags = partials != nullptr ? reinterpret_cast<int*>(partials + (size_t)n_slots * 128 * (HDP + 2)) + 1 : nullptr;
   if (clear && flags != nullptr) {
@@ -1316,10 +1320,10 @@ static int launch_sched(const void* qkv, int64_t ss, int64_t sc, int64_t sh, voi
     hipLaunchKernelGGL(clear_words_kernel, dim3(1), dim3(256), 0, st, flags - 1, n_slots + 1);
   }
 #define TJK_PIPE_SCHED(FULL)                                                                                  \
-  hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, false, FULL, 4>), dim3((unsigned)n_work), dim3(256), 0, st,   \
+  hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, false, FULL, 4>), dim3((unsigned)n_lists), dim3(256), 0, st,  \
                      (const T*)qkv, (int64_t)0, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, \
                      (const int32_t*)nullptr, (const uint8_t*)nullptr, cu_seqlens, 0,                         \
-                     reinterpret_cast<const int4*>(work), partials, flags, n_slots, 1)
+                     reinterpret_cast<const int4*>(work), n_work, partials, flags, n_slots, 1)
   if (hd == HDP) TJK_PIPE_SCHED(true); else TJK_PIPE_SCHED(false);
 #undef TJK_PIPE_SCHED
   return check_launch("tjk_flash_fwd_sched");
@@ -1347,7 +1351,7 @@ static int launch_pipe(const void* qkv, int64_t sb, int64_t ss, int64_t sc, int6
 #define TJK_PIPE(KM, FULL, NWV)                                                                                \
   hipLaunchKernelGGL((flash_pipe_kernel<T, HDP, KM, FULL, NWV>), dim3((unsigned)nblk), dim3(64 * NWV), 0, st,   \
                      (const T*)qkv, sb, ss, sc, sh, (T*)out, ld_out, B, S, H, hd, scale_log2, causal, lengths,  \
-                     key_mask, cu_seqlens, nqb, (const int4*)nullptr, (float*)nullptr, (int*)nullptr, 0, grp)
+                     key_mask, cu_seqlens, nqb, (const int4*)nullptr, 0, (float*)nullptr, (int*)nullptr, 0, grp)
   if (key_mask != nullptr) {
     if (hd == HDP) TJK_PIPE(true, true, 4); else TJK_PIPE(true, false, 4);
   } else {
@@ -1525,11 +1529,13 @@ extern "C" size_t tjk_flash_partial_bytes(int head_dim, int n_slots) {
 static int flash_sched_entry(const char* who, const void* qkv, int64_t stride_s, int64_t stride_c,
                              int64_t stride_h, void* out, int64_t ld_out, int batch, int max_seqlen, int heads,
                              int head_dim, float scale, int causal, const int32_t* cu_seqlens, const int32_t* work,
-                             int n_work, float* partials, size_t partials_bytes, int n_slots, int dtype,
+                             int n_work, int n_lists, float* partials, size_t partials_bytes, int n_slots, int dtype,
                              bool clear, hipStream_t st) {
   if (batch < 0 || max_seqlen < 0 || heads <= 0 || head_dim <= 0 || n_work < 0 || n_slots < 0)
     return fail(TJK_EINVAL, "%s: bad shape or counts", who);
   if (n_work == 0) return TJK_OK;
+  if (n_lists <= 0 || n_lists > n_work)
+    return fail(TJK_EINVAL, "%s: n_lists=%d must be in [1, n_work=%d]", who, n_lists, n_work);
   if (!qkv || !out || !cu_seqlens || !work) return fail(TJK_EINVAL, "%s: null pointer", who);
   if ((n_slots > 0 || partials) && (!partials || partials_bytes < tjk_flash_partial_bytes(head_dim, n_slots)))
     return fail(TJK_EINVAL, "%s: %d split slots need %zu bytes of partials (got %zu)", who, n_slots,
@@ -1549,7 +1555,7 @@ static int flash_sched_entry(const char* who, const void* qkv, int64_t stride_s,
   const float scale_log2 = scale * 1.4426950408889634f;
 #define TJK_SCHED(TT, HDP)                                                                                  \
   return launch_sched<TT, HDP>(qkv, stride_s, stride_c, stride_h, out, ld_out, batch, max_seqlen, heads, \
-                               head_dim, scale_log2, causal, cu_seqlens, work, n_work, partials, n_slots, \
+                               head_dim, scale_log2, causal, cu_seqlens, work, n_work, n_lists, partials, n_slots, \
                                clear, st)
   if (dtype == TJK_F16) {
     if (head_dim <= 32) TJK_SCHED(f16, 32);
@@ -1565,10 +1571,10 @@ static int flash_sched_entry(const char* who, const void* qkv, int64_t stride_s,
 extern "C" int tjk_flash_fwd_sched(const void* qkv, int64_t stride_s, int64_t stride_c, int64_t stride_h,
                                    void* out, int64_t ld_out, int batch, int max_seqlen, int heads,
                                    int head_dim, float scale, int causal, const int32_t* cu_seqlens,
-                                   const int32_t* work, int n_work, float* partials, size_t partials_bytes,
-                                   int n_slots, int dtype, void* stream) {
+                                   const int32_t* work, int n_work, int n_lists, float* partials,
+                                   size_t partials_bytes, int n_slots, int dtype, void* stream) {
   return flash_sched_entry("tjk_flash_fwd_sched", qkv, stride_s, stride_c, stride_h, out, ld_out, batch, max_seqlen,
-                           heads, head_dim, scale, causal, cu_seqlens, work, n_work, partials, partials_bytes,
+                           heads, head_dim, scale, causal, cu_seqlens, work, n_work, n_lists, partials, partials_bytes,
                            n_slots, dtype, false, reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -1611,7 +1617,8 @@ extern "C" size_t tjk_flash_sched_static_bytes(void) { return kSchedScratchBytes
 extern "C" int tjk_flash_fwd_sched_static(const void* qkv, int64_t stride_s, int64_t stride_c, int64_t stride_h,
                                           void* out, int64_t ld_out, int batch, int max_seqlen, int heads,
                                           int head_dim, float scale, int causal, const int32_t* cu_seqlens,
-                                          const int32_t* work, int n_work, int n_slots, int dtype, void* stream) {
+                                          const int32_t* work, int n_work, int n_lists, int n_slots, int dtype,
+                                          void* stream) {
   if (head_dim <= 0 || n_slots < 0) return fail(TJK_EINVAL, "tjk_flash_fwd_sched_static: bad shape or counts");
   const size_t need = tjk_flash_partial_bytes(head_dim, n_slots);
   if (need > kSchedScratchBytes)
@@ -1622,7 +1629,7 @@ extern "C" int tjk_flash_fwd_sched_static(const void* qkv, int64_t stride_s, int
   const int rc = scratch_on_current_device(&ws);
   if (rc != TJK_OK) return rc;
   return flash_sched_entry("tjk_flash_fwd_sched_static", qkv, stride_s, stride_c, stride_h, out, ld_out, batch,
-                           max_seqlen, heads, head_dim, scale, causal, cu_seqlens, work, n_work, ws,
+                           max_seqlen, heads, head_dim, scale, causal, cu_seqlens, work, n_work, n_lists, ws,
                            kSchedScratchBytes, n_slots, dtype, true, reinterpret_cast<hipStream_t>(stream));
 }
 

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede the library load; see module docstring)
 
 LIB_PATH = Path(__file__).with_name("libtjk.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 F32, F16, BF16 = 0, 1, 2
 OK, EINVAL, EUNSUPPORTED = 0, -1, -2
@@ -41,10 +41,10 @@ _SIGNATURES = {
                              _f32, _i32, _vp, _vp, _vp, _i32, _i32, _vp]),
     "tjk_flash_plan_count": (_i32, [_i32]),
     "tjk_flash_fwd_sched": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _f32, _i32,
-                                   _vp, _vp, _i32, _vp, ctypes.c_size_t, _i32, _i32, _vp]),
+                                   _vp, _vp, _i32, _i32, _vp, ctypes.c_size_t, _i32, _i32, _vp]),
     "tjk_flash_partial_bytes": (ctypes.c_size_t, [_i32, _i32]),
     "tjk_flash_fwd_sched_static": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i32, _i32, _i32, _i32, _f32, _i32,
-                                          _vp, _vp, _i32, _i32, _i32, _vp]),
+                                          _vp, _vp, _i32, _i32, _i32, _i32, _vp]),
     "tjk_flash_sched_static_bytes": (ctypes.c_size_t, []),
     "tjk_flash_sched_occupancy": (_i32, [_i32, _i32]),
     "tjk_ffn": (_i32, [_vp, _i32, _i64, _vp, _vp, _f32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32,

@@ -241,6 +241,7 @@ def flash_attention_sched(qkv: torch.Tensor, out: torch.Tensor, cu_seqlens: torc
         qkv.data_ptr(), ss, sc, sh, out.data_ptr(), _rowmajor(out, "out"), cu_seqlens.numel() - 1,
         int(max_seqlen), h, hd, float(hd ** -0.5 if scale is None else scale), int(bool(causal)),
         cu_seqlens.data_ptr(), schedule.work.data_ptr(), schedule.work.shape[0],
+        schedule.n_lists or schedule.work.shape[0],
         schedule.partials.data_ptr(), schedule.partials.numel() * schedule.partials.element_size(),
         schedule.n_slots, _code(qkv), _stream(qkv))
     check(status, "tjk_flash_fwd_sched")

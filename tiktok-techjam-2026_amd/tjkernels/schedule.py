@@ -22,16 +22,40 @@ is throughput-bound (the softmax VALU work of a 64-key tile is about twice
 its MFMA time) and each half pays its own Q load and pipeline fill, so the
 default ``split_factor`` = 2 only splits lists dominated by a few very long
 items.
+
+With more items than resident workgroups, one workgroup per item leaves
+the last items to start when the first ones end: at the C4 lengths (720
+items, 512 resident workgroups) a per-workgroup timeline showed the
+shortest items dispatched ~21 us into a 33 us launch, each paying ~2 us
+of Q load and ring fill before its first tile, and finishing last.  So
+``pack_lists`` can deal the items into at most as many lists as workgroups
+are resident (largest cost first, each to the list with the least cost so
+far, a cost being its key tiles plus ``ITEM_OVERHEAD``); the kernel then
+runs one list per workgroup, its items back to back, and every list starts
+at once.  First halves of split items go first, one at the head of each of
+as many lists, so a second half never waits on an item queued behind it.
+That pays where one workgroup fills a CU (head_dim 128: a CU otherwise
+idles from one item's end to the next one's first tile); with two
+workgroups per CU (head_dim <= 64) it measured slower than one workgroup
+per item, and balancing the lists per CU (the two workgroups of a CU, the
+older one faster, K/V of a head kept on one XCD's L2) did not change that:
+the cost is each item's start (Q load and ring fill, ~2-3 us), which a list
+runs in series like a new workgroup does (``build_schedule``).
 """
 
 from __future__ import annotations
 
+import heapq
 from dataclasses import dataclass
-from typing import List, Sequence, Tuple
+from typing import List, Optional, Sequence, Tuple
 
 import torch
 
 BMQ, BNK = 128, 64
+# An item's fixed cost (Q load, K/V ring fill, output store) in key tiles,
+# for balancing lists: ~2 us against ~1.2 us per tile at C4.
+ITEM_OVERHEAD = 2
+HOLE = (-1, 0, 0, 0, -1)  # (b*H + h, qb, t_lo, t_hi, slot) padding a shorter list
 
 
 @dataclass
@@ -42,6 +66,7 @@ class AttentionSchedule:
     max_item: int           # largest item, in key tiles
     total: int              # key tiles over all items
     error_index: int = 0    # int32 index of the kernel's error word in `partials`
+    n_lists: int = 0        # workgroups: list w is items w, w + n_lists, ...; 0 = one per item
 
 
 def _key_tiles(n: int, qb: int, causal: bool) -> int:
@@ -50,16 +75,24 @@ def _key_tiles(n: int, qb: int, causal: bool) -> int:
 
 
 def validate_work(work: Sequence[Tuple[int, int, int, int]], lengths: Sequence[int], heads: int,
-                  causal: bool, n_slots: int) -> None:
+                  causal: bool, n_slots: int, n_lists: int = 0) -> None:
     """Raise ValueError unless ``work`` [(b*H + h, qb, t_lo, t_hi, slot)] --
-    in issue order -- is a list the scheduled kernel can run: every item
-    inside the launch, every (b, h, query block) covered by exactly one
-    whole item or by one split pair whose halves tile its key range, first
-    half (slot s) before second half (slot -2 - s), every slot in
-    [0, n_slots) used by exactly one pair."""
+    in array order, workgroup w running items w, w + n_lists, ... (n_lists
+    0: one item per workgroup, in issue order) -- is a list the scheduled
+    kernel can run: every item a ``HOLE`` or inside the launch, every
+    (b, h, query block) covered by exactly one whole item or by one split
+    pair whose halves tile its key range, every slot in [0, n_slots) used by
+    exactly one pair, and each first half (slot s) ahead of its second half
+    (slot -2 - s): before it in issue order, or at the head of a list when
+    workgroups run lists."""
+    lists = n_lists > 0 and n_lists < len(work)
+    if n_lists < 0 or n_lists > max(len(work), 1):
+        raise ValueError(f"n_lists={n_lists} outside [0, {len(work)}]")
     cover = {}
     first_at, second_at = {}, {}
     for pos, (bh, qb, lo, hi, slot) in enumerate(work):
+        if (bh, qb, lo, hi, slot) == HOLE:
+            continue
         if not 0 <= bh < len(lengths) * heads:
             raise ValueError(f"item {pos}: (b, h) index {bh} outside the launch")
         n = lengths[bh // heads]
@@ -71,6 +104,8 @@ def validate_work(work: Sequence[Tuple[int, int, int, int]], lengths: Sequence[i
         if slot >= 0:
             if slot >= n_slots or slot in first_at:
                 raise ValueError(f"item {pos}: first-half slot {slot} invalid or repeated")
+            if lists and pos >= n_lists:
+                raise ValueError(f"item {pos}: first half of slot {slot} not at the head of a list")
             first_at[slot] = (pos, bh, qb)
         elif slot <= -2:
             s = -2 - slot
@@ -83,7 +118,7 @@ def validate_work(work: Sequence[Tuple[int, int, int, int]], lengths: Sequence[i
     for s in range(n_slots):
         if s not in first_at or s not in second_at:
             raise ValueError(f"slot {s} lacks a first or second half")
-        if first_at[s][0] > second_at[s][0] or first_at[s][1:] != second_at[s][1:]:
+        if (not lists and first_at[s][0] > second_at[s][0]) or first_at[s][1:] != second_at[s][1:]:
             raise ValueError(f"slot {s}: halves out of order or of different query blocks")
     for b, n in enumerate(lengths):
         for h in range(heads):
@@ -134,23 +169,67 @@ def build_items(lengths: Sequence[int], heads: int, causal: bool, slots: int, mi
     return work, n_slots
 
 
+def pack_lists(work: Sequence[Tuple[int, int, int, int, int, int]], n_lists: int
+               ) -> List[Tuple[int, int, int, int, int]]:
+    """Deal ``work`` [(cost, b*H + h, qb, t_lo, t_hi, slot)] (build_items'
+    order) into ``n_lists`` lists and lay them out for the kernel: item j of
+    list w at position j * n_lists + w, shorter lists padded with ``HOLE``.
+    First halves of split items are dealt first, one at the head of each of
+    as many lists (there must be at most n_lists of them); then every other
+    item, largest cost first, goes to the list with the least cost so far
+    (ties: the lower list), a cost being tiles + ITEM_OVERHEAD.  A pure
+    function of its input."""
+    firsts = [w for w in work if w[5] >= 0]
+    if len(firsts) > n_lists:
+        raise ValueError(f"{len(firsts)} split items need as many lists (got {n_lists})")
+    rest = sorted((w for w in work if w[5] < 0), key=lambda w: (-w[0], w[1], w[2], w[3]))
+    lists: List[List[Tuple[int, int, int, int, int]]] = [[] for _ in range(n_lists)]
+    heap = [(0, i) for i in range(n_lists)]
+    for i, w in enumerate(firsts):
+        lists[i].append(w[1:])
+        heap[i] = (w[0] + ITEM_OVERHEAD, i)
+    heapq.heapify(heap)
+    for w in rest:
+        load, i = heapq.heappop(heap)
+        lists[i].append(w[1:])
+        heapq.heappush(heap, (load + w[0] + ITEM_OVERHEAD, i))
+    depth = max((len(li) for li in lists), default=0)
+    return [lists[i][j] if j < len(lists[i]) else HOLE for j in range(depth) for i in range(n_lists)]
+
+
 def build_schedule(lengths: Sequence[int], heads: int, head_dim: int, causal: bool,
                    dtype: torch.dtype, device: torch.device, slots: int = 0,
-                   min_split: int = 6, split_factor: float = 2.0) -> AttentionSchedule:
-    """``slots`` (resident workgroups) defaults to CUs x the kernel's occupancy."""
+                   min_split: int = 6, split_factor: float = 2.0,
+                   lists: Optional[bool] = None) -> AttentionSchedule:
+    """``slots`` (resident workgroups) defaults to CUs x the kernel's
+    occupancy.  ``lists``: run the items as per-workgroup lists when there
+    are more than ``slots`` of them (None: only where one workgroup fills a
+    CU, head_dim 128).  Measured on MI355X: 2 x 4096 tokens at head_dim 128
+    (256 lists) 193 -> 184 us; at head_dim 64 with two workgroups per CU the
+    packed C4 lengths ran 34.1 us as one workgroup per item against 35.0 as
+    lists -- there the CU's other workgroup already covers a new one's start,
+    and the hardware hands the next item to whichever workgroup ends first."""
     from . import _lib
     lib = _lib.load()
+    occ = lib.tjk_flash_sched_occupancy(head_dim, _lib.DTYPE_CODES[dtype])
+    _lib.check(0 if occ > 0 else (occ or -1), "tjk_flash_sched_occupancy")
     if slots <= 0:
-        occ = lib.tjk_flash_sched_occupancy(head_dim, _lib.DTYPE_CODES[dtype])
-        _lib.check(0 if occ > 0 else (occ or -1), "tjk_flash_sched_occupancy")
         slots = occ * torch.cuda.get_device_properties(device).multi_processor_count
+    if lists is None:
+        lists = occ == 1
     work, n_slots = build_items(lengths, heads, causal, slots, min_split, split_factor)
-    validate_work([(bh, qb, lo, hi, slot) for _, bh, qb, lo, hi, slot in work], lengths, heads, causal, n_slots)
-    w = torch.tensor([(bh, qb, lo | (hi << 16), slot) for _, bh, qb, lo, hi, slot in work] or [(0, 0, 0, -1)],
-                     dtype=torch.int32)[:len(work)]
+    items = [(bh, qb, lo, hi, slot) for _, bh, qb, lo, hi, slot in work]
+    n_lists = 0
+    if lists and len(work) > slots and n_slots <= slots:
+        n_lists = slots
+        items = pack_lists(work, n_lists)
+    validate_work(items, lengths, heads, causal, n_slots, n_lists)
+    w = torch.tensor([(bh, qb, (lo | (hi << 16)) if bh >= 0 else 0, slot) for bh, qb, lo, hi, slot in items]
+                     or [(0, 0, 0, -1)], dtype=torch.int32)[:len(items)]
     nbytes = lib.tjk_flash_partial_bytes(head_dim, n_slots)
     hdp = 32 if head_dim <= 32 else 64 if head_dim <= 64 else 128
     return AttentionSchedule(work=w.contiguous().to(device), n_slots=n_slots,
                              partials=torch.zeros((nbytes + 15) // 4, dtype=torch.float32, device=device),
                              max_item=max((c for c, *_ in work), default=0),
-                             total=sum(c for c, *_ in work), error_index=n_slots * BMQ * (hdp + 2))
+                             total=sum(c for c, *_ in work), error_index=n_slots * BMQ * (hdp + 2),
+                             n_lists=n_lists)
