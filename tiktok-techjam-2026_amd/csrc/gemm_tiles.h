@@ -11,32 +11,35 @@ namespace tjk {
 
 constexpr int kGroupM = 8;
 
-// GELU(v) = 0.5 v (1 + erf(v / sqrt 2)) with erf from Abramowitz & Stegun,
-// Handbook of Mathematical Functions, eq. 7.1.28 (|error| <= 3e-7): for
-// z >= 0, erf z = 1 - (1 + a1 z + a2 z^2 + ... + a6 z^6)^-16, and
-// erf(-z) = -erf(z).  The polynomial is taken in |v| (coefficients
-// a_i / sqrt(2)^i), the 16th power by four squarings: one reciprocal and no
-// exponential, where eq. 7.1.26 needs both (the transcendental instructions
-// run at a quarter of the VALU rate, and the epilogue of an FFN1 tile is
-// VALU-bound).  Branch-free -- the library erff branches on |z| and measured
-// ~35 VALU instructions per value with divergent lanes.
+// GELU(v) = v Phi(v) with erf from Abramowitz & Stegun, Handbook of
+// Mathematical Functions, eq. 7.1.28 (|error| <= 3e-7): for z >= 0,
+// erfc z = (1 + a1 z + a2 z^2 + ... + a6 z^6)^-16.  With u = |v| and
+// h = erfc(u / sqrt 2) / 2, Phi(v) = 1 - h for v >= 0 and h for v < 0, so
+// GELU(v) = max(v, 0) - u h: one FMA after the reciprocal, exact in the
+// negative tail (no 1 - erf cancellation).  The polynomial is taken in u
+// (coefficients a_i / sqrt(2)^i) and scaled by 2^(1/16), so that its 16th
+// power (four squarings) is 2 (1 + ...)^16 and its reciprocal is h: one
+// reciprocal and no exponential, where eq. 7.1.26 needs both (the
+// transcendental instructions run at a quarter of the VALU rate, and the
+// epilogue of an FFN1 tile is VALU-bound).  Branch-free -- the library
+// erff branches on |z| and measured ~35 VALU instructions per value with
+// divergent lanes.
 __device__ __forceinline__ float gelu_erf(float v) {
   const float u = fabsf(v);
-  // a1..a6 = 0.0705230784, 0.0422820123, 0.0092705272, 0.0001520143,
-  // 0.0002765672, 0.0000430638, each divided by sqrt(2)^i
-  float p = fmaf(u, 5.382975e-06f, 4.8890637e-05f);
-  p = fmaf(p, u, 3.8003574e-05f);
-  p = fmaf(p, u, 3.2776264e-03f);
-  p = fmaf(p, u, 2.1141006e-02f);
-  p = fmaf(p, u, 4.9867347e-02f);
-  p = fmaf(p, u, 1.0f);
+  // 2^(1/16) x (1, a1 / sqrt 2, ..., a6 / sqrt(2)^6), a1..a6 = 0.0705230784,
+  // 0.0422820123, 0.0092705272, 0.0001520143, 0.0002765672, 0.0000430638
+  float p = fmaf(u, 5.62129981e-06f, 5.1055209e-05f);
+  p = fmaf(p, u, 3.9686136e-05f);
+  p = fmaf(p, u, 3.42273922e-03f);
+  p = fmaf(p, u, 2.20769979e-02f);
+  p = fmaf(p, u, 5.20751625e-02f);
+  p = fmaf(p, u, 1.04427373f);
   p *= p;
   p *= p;
   p *= p;
-  p *= p;  // p^16 (inf for large |v|: the reciprocal is then 0)
-  const float erf_v = copysignf(1.0f - __builtin_amdgcn_rcpf(p), v);
-  const float hv = 0.5f * v;
-  return fmaf(hv, erf_v, hv);
+  p *= p;  // 2 (1 + ...)^16 (inf for large |v|: the reciprocal is then 0)
+  const float h = __builtin_amdgcn_rcpf(p);
+  return fmaf(-u, h, fmaxf(v, 0.0f));
 }
 
 // Bijection from hardware workgroup id to a tile order in which XCD x gets
