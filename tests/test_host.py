@@ -425,6 +425,18 @@ def test_mask_memo_follows_in_place_updates(monkeypatch):
     lengths[0] = 9  # clamped to S
     _, info = eng._decode_mask(torch.zeros(2, 6, 32), lengths)
     assert info.mode == MASK_NONE
+    # a mask created under inference mode has no version counter: it is
+    # classified on every call, so an in-place update is still seen
+    with torch.inference_mode():
+        imask = torch.arange(6)[None, :] < torch.tensor([[3], [6]])
+    assert imask.is_inference()
+    calls.clear()
+    _, info = eng._decode_mask(torch.zeros(2, 6, 32), imask)
+    assert (info.mode, info.lengths) == (MASK_PREFIX, (3, 6))
+    with torch.inference_mode():
+        imask[0, 3] = True
+    _, info = eng._decode_mask(torch.zeros(2, 6, 32), imask)
+    assert (info.mode, info.lengths) == (MASK_PREFIX, (4, 6)) and len(calls) == 2
 
 
 def test_work_list_validation_rejects_broken_lists():

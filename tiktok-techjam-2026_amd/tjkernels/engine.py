@@ -137,15 +137,19 @@ class TensorMemo:
     """Host-side facts derived from a device tensor (one sync each),
     remembered per tensor object and recomputed when the tensor's version
     counter shows an in-place update since.  Tensors created under
-    ``torch.inference_mode`` have no version counter: for them the memo is
-    per object only, as the reference's (engine.py:139-141), so such a
-    tensor must not be updated in place between forwards."""
+    ``torch.inference_mode`` have no version counter, so an in-place update
+    could not be seen: for them the facts are derived again on every call
+    (one host sync per forward).  The reference memoises them per object
+    (engine.py:139-141), where a stale entry only mislabels the mask mode;
+    here a stale entry would be stale prefix lengths, i.e. wrong rows."""
 
     def __init__(self) -> None:
         self._memo = WeakTensorKeyDictionary() if WeakTensorKeyDictionary is not None else {}
 
     def get(self, t: torch.Tensor, derive):
         version = _version(t)
+        if version is None:
+            return derive(t)
         hit = self._memo.get(t)
         if hit is not None and hit[0] == version:
             return hit[1]
