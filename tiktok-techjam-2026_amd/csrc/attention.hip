@@ -1251,7 +1251,44 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
       __hip_atomic_fetch_add(&flags[-1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     inv = __builtin_nanf("");
   }
-  if (q < Sb) {
+  // DMA ring: the wave's 32 x HDP block goes through LDS and out as 16-byte
+  // pieces of whole rows, 8 lanes per 128 bytes, so a launch that writes 4
+  // MiB or more can write them through the L2 (its 8-byte pieces 2 KB apart,
+  // stored straight from the accumulator layout, measured 4 us slower per C4
+  // launch written through, one by one).  Needs 16-byte aligned rows.
+  const bool staged = DMA && ((uintptr_t)out & 15) == 0 && (ld_out % 8) == 0;
+  if (staged) {
+    // The ring is free once every wave's copies have landed (the copies of
+    // tiles past the item write zeros too) and every wave is past its last
+    // tile.
+    __syncthreads();
+    constexpr int OP = HDP * 2 + 16;             // staged row pitch (bytes)
+    constexpr int PPR = HDP * 2 / 16;            // 16-byte pieces per row
+    constexpr int NPASS = 32 * PPR / 64;         // store instructions per wave
+    char* stg = smem + wave * 32 * OP;
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 v = make_float4(o[hb][4 * g] * inv, o[hb][4 * g + 1] * inv, o[hb][4 * g + 2] * inv,
+                                     o[hb][4 * g + 3] * inv);
+        *reinterpret_cast<typename Quad<T>::raw*>(stg + l32 * OP + (hb * 32 + 8 * g + 4 * hi) * 2) =
+            Quad<T>::from(v);
+      }
+    const int nrow = min(Sb - wq0, 32);
+    const RowOut rows(out + (row0 + wq0) * ld_out + (int64_t)h * hd,
+                      nrow > 0 ? ((int64_t)(nrow - 1) * ld_out + HDP) * (int64_t)sizeof(T) : 0,
+                      (int64_t)B * S * H * HDP * (int64_t)sizeof(T) >= kWtMinBytes);
+    with_wt(rows.wt, [&](auto wt_tag) {
+      const auto w = rows.writer<decltype(wt_tag)::value>();
+#pragma unroll
+      for (int ps = 0; ps < NPASS; ++ps) {
+        const int idx = lane + 64 * ps, r = idx / PPR, pc = idx % PPR;
+        const uint4 piece = *reinterpret_cast<const uint4*>(stg + r * OP + pc * 16);
+        if (r < nrow) w.put((int)(((int64_t)r * ld_out + pc * 8) * (int64_t)sizeof(T)), piece);
+      }
+    });
+  } else if (q < Sb) {
     T* orow = out + (row0 + q) * ld_out + (int64_t)h * hd;
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb)
