@@ -741,6 +741,44 @@ def test_flash_scheduled(device, dt, hd, causal):
             assert torch.equal(again.cpu(), got), "split merge is not deterministic"
 
 
+@pytest.mark.parametrize("hd", [64, 128])
+def test_flash_output_staging_matches_direct_stores(device, hd):
+    """The direct-to-LDS kernels stage each wave's output block through LDS
+    and store whole-row pieces when the output rows are 16-byte aligned
+    (written through the L2 for launches of 4 MiB or more); an output view
+    whose rows are only 8-byte aligned takes the direct per-lane stores.
+    Both give the same bits, on the grid path (a ragged last query block:
+    waves with fewer than 32 rows) and on the scheduled path, and neither
+    writes outside its rows and columns."""
+    from tjkernels.schedule import build_schedule
+    h, dt = 4, torch.bfloat16
+    g = _gen(hd + 5)
+    # the second case writes 2 x 2048 x 4 x 128 x 2 bytes = 4 MiB at hd 128 (written through)
+    for seqs in ((300, 77), (2048, 2048)):
+        t = sum(seqs)
+        qkv = torch.randn(t, 3, h, hd, generator=g).to(dt).to(device)
+        cu = torch.tensor([0, seqs[0], t], dtype=torch.int32, device=device)
+        sched = build_schedule(list(seqs), h, hd, True, dt, device)
+        outs = {}
+        for col0 in (0, 4):  # rows 16-byte aligned (staged), 8-byte aligned (direct)
+            for name in ("sched", "grid"):
+                buf = torch.full((t + 3, h * hd + 8), float("nan"), dtype=dt, device=device)
+                view = buf[:t, col0:col0 + h * hd]
+                assert (view.data_ptr() % 16 == 0) == (col0 == 0) and view.stride(0) % 8 == 0
+                if name == "sched":
+                    ops.flash_attention_sched(qkv, view, cu, max(seqs), sched)
+                else:
+                    ops.flash_attention(qkv, view, causal=True, plan=0, cu_seqlens=cu, max_seqlen=max(seqs))
+                torch.cuda.synchronize()
+                assert torch.isfinite(view.float()).all(), f"{name}: a row or column was not written"
+                rest = buf.clone()
+                rest[:t, col0:col0 + h * hd] = 0
+                assert torch.isnan(rest.float()[rest != 0]).all(), f"{name}: wrote outside its output"
+                outs[(name, col0)] = view.clone()
+        for name in ("sched", "grid"):
+            assert torch.equal(outs[(name, 0)], outs[(name, 4)]), f"{name}: staged and direct stores differ"
+
+
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("hd", [64, 128])
 def test_flash_scheduled_lists(device, causal, hd):
