@@ -62,19 +62,39 @@ constexpr int kEpiStoreF32 = 3;
 // instruction would scatter 8-16 byte pieces over 32 rows (32 L2 requests
 // per instruction), which measured slower than the whole K=1024 main loop.
 // Instead each wave applies bias / GELU in registers, transposes one 32-row
-// block at a time through a private LDS region (row pitch padded by one
-// 16-byte piece) and writes whole row segments: 16 bytes per lane, WTN
-// contiguous elements per row.  The residual epilogue stages fp32 and does
-// its read-modify-write of the fp32 residual with the same row-contiguous
-// pieces; kEpiStoreF32 stages fp32 and stores it.
+// block at a time through a private LDS region and writes whole row
+// segments: 16 bytes per lane, WTN contiguous elements per row.  The
+// residual epilogue stages fp32 and does its read-modify-write of the fp32
+// residual with the same row-contiguous pieces; kEpiStoreF32 stages fp32
+// and stores it.
+//
+// The staging is written and read in 16-byte pieces.  Measured on MI355X
+// (SQ_LDS_BANK_CONFLICT of probe kernels), a 16-byte LDS write serves 8
+// lanes per cycle over 32 banks and a 16-byte read 32 lanes per cycle over
+// 128 banks.  A staged row holds LPR pieces (a multiple of 4) with no
+// padding, and piece p of row r sits at slot r LPR + (p ^ x(r)), x(r) =
+// r & 7 if LPR % 8 == 0, else (r >> 1) & 3.  A write puts one piece of each
+// of 8 consecutive rows per cycle, which the XOR spreads over the 8 bank
+// groups; a read takes 32 consecutive pieces in row-major order, and the
+// XOR only permutes pieces within aligned groups of 8 (or 4) that every
+// such window covers whole.  In fp32 each lane's four columns are one
+// piece.  In a 2-byte type a piece's two halves sit in lanes l32 and
+// l32 + 32, so pieces g = 2k, 2k + 1 trade halves (v_permlane32_swap) and
+// each lane writes a whole piece.  (8-byte writes from rows padded by one
+// piece counted ~7 conflict cycles per write and ~4 per read in the probe.)
 template <typename T, int EPI, int FN>
 struct EpiStage {
   static constexpr bool F32OUT = EPI == TJK_EPI_BIAS_RESIDUAL || EPI == kEpiStoreF32;
   typedef typename std::conditional<F32OUT, float, T>::type S;  // staged type
   static constexpr int WTN = FN * 32;
   static constexpr int SV = 16 / (int)sizeof(S);  // elements per 16-byte piece
-  static constexpr int PITCH = WTN + SV;          // staged row pitch (elements)
-  static constexpr int BYTES = 32 * PITCH * (int)sizeof(S);  // LDS bytes per wave
+  static constexpr int LPR = WTN / SV;            // pieces per staged row
+  static constexpr int BYTES = 32 * LPR * 16;     // LDS bytes per wave
+  static_assert(LPR % 4 == 0, "staged rows of whole 4-piece groups");
+  static constexpr int G = LPR % 8 == 0 ? 8 : 4;  // pieces per XOR group
+  static __device__ __forceinline__ int x(int r) { return G == 8 ? (r & 7) : ((r >> 1) & 3); }
+  // byte offset of piece p of staged row r
+  static __device__ __forceinline__ int at(int r, int p) { return (r * LPR + (p ^ x(r))) * 16; }
 };
 
 // The residual pieces (TJK_EPI_BIAS_RESIDUAL) a wave's epilogue will
@@ -145,11 +165,9 @@ __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* _
                                          int lane, char* __restrict__ stage, const Pre& pre = Pre(),
                                          const BiasRaw<T, FN>* bpre = nullptr) {
   typedef EpiStage<T, EPI, FN> E;
-  typedef typename E::S S;
-  constexpr int LPR = E::WTN / E::SV;  // 16-byte pieces per staged row
+  constexpr int LPR = E::LPR;          // 16-byte pieces per staged row
   constexpr int NPC = 32 * LPR;        // pieces per 32-row block
   constexpr int NIT = (NPC + 63) / 64; // read instructions per block
-  S* st = reinterpret_cast<S*>(stage);
   const int l32 = lane & 31, hi = lane >> 5;
   // 16-byte output pieces need a 16-byte aligned C and a leading dimension
   // that keeps every row 16-byte aligned; otherwise pieces go out as halves.
@@ -170,23 +188,54 @@ __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* _
       bv[i][g] = n < N ? Quad<T>::to(braw.r[i][g]) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 
+  // columns 32 i + 8 g + 4 hi .. +3 of this lane's row, bias / GELU applied
+  auto value = [&](int j, int i, int g) __attribute__((always_inline)) {
+    float4 v = make_float4(acc[i][j][4 * g + 0] + bv[i][g].x, acc[i][j][4 * g + 1] + bv[i][g].y,
+                           acc[i][j][4 * g + 2] + bv[i][g].z, acc[i][j][4 * g + 3] + bv[i][g].w);
+    if (EPI == TJK_EPI_BIAS_GELU) {
+      v.x = gelu_erf(v.x); v.y = gelu_erf(v.y); v.z = gelu_erf(v.z); v.w = gelu_erf(v.w);
+    }
+    return v;
+  };
+
+  // Staging offsets, the same for every 32-row block.  Writes: piece C + hi
+  // of row l32 (C even, a compile-time value) sits at C ^ wx with
+  // wx = x(l32) ^ hi, i.e. at the constant C & ~(G - 1) plus one of G / 2
+  // per-lane offsets.  Reads: one offset per read instruction.
+  char* const wrow = stage + l32 * LPR * 16;
+  const int wx = E::x(l32) ^ hi;
+  auto wslot = [&](int c) __attribute__((always_inline)) {
+    return wrow + 16 * ((c & ~(E::G - 1)) + ((c & (E::G - 1)) ^ wx));
+  };
+  int roff[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int pc = min(lane + 64 * it, NPC - 1);
+    roff[it] = E::at(pc / LPR, pc % LPR);
+  }
+
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
 #pragma unroll
-    for (int i = 0; i < FN; ++i)
+    for (int i = 0; i < FN; ++i) {
+      if constexpr (E::SV == 4) {  // fp32 staged: a lane's four columns are one piece
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        float4 v = make_float4(acc[i][j][4 * g + 0] + bv[i][g].x, acc[i][j][4 * g + 1] + bv[i][g].y,
-                               acc[i][j][4 * g + 2] + bv[i][g].z, acc[i][j][4 * g + 3] + bv[i][g].w);
-        if (EPI == TJK_EPI_BIAS_GELU) {
-          v.x = gelu_erf(v.x); v.y = gelu_erf(v.y); v.z = gelu_erf(v.z); v.w = gelu_erf(v.w);
+        for (int g = 0; g < 4; ++g) *reinterpret_cast<float4*>(wslot(8 * i + 2 * g)) = value(j, i, g);
+      } else {
+        static_assert(sizeof(typename Quad<T>::raw) == 8, "2-byte staged type");
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          // lane (l32, 0) ends with piece 4 i + 2 k of row l32, lane (l32, 1)
+          // with piece 4 i + 2 k + 1: the swap trades the upper lanes' half
+          // of the first for the lower lanes' half of the second
+          const typename Quad<T>::raw x = Quad<T>::from(value(j, i, 2 * k));
+          const typename Quad<T>::raw y = Quad<T>::from(value(j, i, 2 * k + 1));
+          const auto s0 = __builtin_amdgcn_permlane32_swap(x.x, y.x, false, false);
+          const auto s1 = __builtin_amdgcn_permlane32_swap(x.y, y.y, false, false);
+          *reinterpret_cast<uint4*>(wslot(4 * i + 2 * k)) = make_uint4(s0[0], s1[0], s0[1], s1[1]);
         }
-        S* dst = st + l32 * E::PITCH + i * 32 + g * 8 + hi * 4;
-        if constexpr (E::F32OUT)
-          *reinterpret_cast<float4*>(dst) = v;
-        else
-          *reinterpret_cast<typename Quad<T>::raw*>(dst) = Quad<T>::from(v);
       }
+    }
     // rows mw + 32 j .. of this block, from column nw
     const int64_t rb0 = (int64_t)(mw + 32 * j) * ldc + nw;
     const RowOut rows(static_cast<char*>(Cv) + rb0 * OB, ((int64_t)M * ldc - rb0) * OB, wt);
@@ -198,7 +247,7 @@ __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* _
         if (NPC % 64 != 0 && pc >= NPC) break;
         const int rr = pc / LPR, cc = (pc % LPR) * E::SV;
         const int m = mw + 32 * j + rr, n = nw + cc;
-        const uint4 piece = *reinterpret_cast<const uint4*>(st + rr * E::PITCH + cc);
+        const uint4 piece = *reinterpret_cast<const uint4*>(stage + roff[it]);
         const int off = (int)(((int64_t)rr * ldc + cc) * OB);
         if (m < M && n < N) {
           if constexpr (EPI == TJK_EPI_BIAS_RESIDUAL) {
