@@ -112,3 +112,64 @@ def test_sweep_runs_bench_in_a_subprocess(device, tmp_path):
     assert "gfx" in str(info.get("arch", "")), info
     assert "System:" in sweep.system_header(info)
     assert "| C1 | PASS |" in sweep.sweep_table([r])
+
+
+def test_tile_step_pins_tiles_at_the_bench_rows_only(device):
+    """The autotuner's tile step times each projection's tiles inside whole
+    forwards on the bench input and pins the winners with tile_rows = that
+    input's row bucket.  A forward on the bench input then runs exactly the
+    pinned tiles and gives the bits of the run-time picks (same K-summation
+    class); a forward with another row count times its own tiles."""
+    from dataclasses import replace
+    from tjkernels import UserOptimizedTransformer, tiles
+    from tjkernels.engine import MASK_PREFIX, reset_engines
+    w = WORKLOADS["C3"]
+    base = plans_mod.default_plan(w.batch, w.seq, w.d_model, w.heads, w.ffn_dim, w.layers, w.causal, w.dtype,
+                                  torch.device("cuda", 0))
+    base = replace(base, cuda_graph=False)
+    ev = autotune._Evaluator(w, 1, 3)
+    best = autotune.tune_tiles(ev, ev.evaluate(base), w, rounds=1)
+    pinned = best["plan"]
+    rows = ev.bench_rows(pinned)
+    mb = -(-rows // tiles.M_BUCKET) * tiles.M_BUCKET
+    assert pinned.tile_rows == mb
+    shapes = autotune._tile_shapes(w, pinned, rows)
+    assert [s[0] for s in shapes] == ["gemm_qkv", "gemm_out", "gemm_ffn1", "gemm_ffn2"]
+    for name, n, k, _ in shapes:
+        assert getattr(pinned, name) in tiles.candidates(mb, n, k, pinned.compute_dtype), name
+
+    model = UserOptimizedTransformer(w.config)
+    model.load_state_dict(make_state_dict(w, seed=0), strict=True)
+    model = model.to(device=device, dtype=w.dtype).eval()
+    xb, maskb = ev.bench_input
+    x2, mask2, len2 = make_inputs(w, seed=5)
+    x2, mask2 = x2.to(device, w.dtype), mask2.to(device)
+    rows2 = int(len2.sum())
+    assert -(-rows2 // tiles.M_BUCKET) * tiles.M_BUCKET != mb  # another row bucket
+    lens_b = tuple(int(n) for n in maskb.sum(1).tolist())
+    outs = {}
+    try:
+        for tag, plan in (("pinned", pinned),
+                          ("run-time", replace(pinned, tile_rows=0, gemm_qkv=-1, gemm_out=-1, gemm_ffn1=-1,
+                                               gemm_ffn2=-1))):
+            plans_mod.set_override(plan)
+            reset_engines(model)
+            with torch.inference_mode():
+                outs[tag] = (model(xb, maskb).clone(), model(x2, mask2).clone())
+            if tag == "pinned":
+                eng = model._tj_engine  # its plan is the pinned one now
+
+                def prepared(lengths):
+                    return eng._prepare(w.batch, w.seq, MASK_PREFIX, eng._packing(lengths, w.seq), None).tiles
+
+                t = prepared(lens_b)
+                assert (t.qkv, t.out, t.fc1, t.fc2) == (pinned.gemm_qkv, pinned.gemm_out, pinned.gemm_ffn1,
+                                                        pinned.gemm_ffn2)
+                t2 = prepared(tuple(int(n) for n in len2.tolist()))  # another row count: run-time picks
+                d, f = w.d_model, w.ffn_dim
+                assert t2.qkv == tiles.gemm_plan(rows2, 3 * d, d, w.dtype, ops_mod.EPI_BIAS)
+                assert t2.fc1 == tiles.gemm_plan(rows2, f, d, w.dtype, ops_mod.EPI_BIAS_GELU)
+    finally:
+        plans_mod.set_override(None)
+    assert torch.equal(outs["pinned"][0], outs["run-time"][0])
+    assert torch.equal(outs["pinned"][1], outs["run-time"][1])

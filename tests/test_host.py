@@ -600,3 +600,16 @@ def test_rocprof_summary_labels_deferred_projections():
     ws2 = "_ZN3tjk14gemm_ws_kernelIDF16bLi192ELi128ELi2ELi4ELi4ELi4ELi2EEEvPKT_lS3_lS3_Pvliii"
     assert rs._gemm_epilogue(ws2) == 2 and rs._kind_ok("gemm_out_residual", ws2)
     assert rs._relabel("gemm_out_residual", ws2) == "gemm_out_residual" and rs._tjk(ws2)
+
+
+def test_plan_tile_rows_round_trip_and_validation():
+    """Plan.tile_rows (the row bucket the autotuner measured the gemm_*
+    tiles at) survives plans.json and must be a row count >= 0."""
+    from dataclasses import replace
+    from tjkernels.plans import Plan
+    p = replace(Plan(), gemm_qkv=14, gemm_out=30, gemm_ffn1=31, gemm_ffn2=29, tile_rows=5440, label="autotuned")
+    q = Plan.from_json(json.loads(json.dumps(p.to_json())))
+    assert q == p and q.tile_rows == 5440
+    assert Plan.from_json({"label": "older table"}).tile_rows == 0  # entries written before the field
+    with pytest.raises(ValueError, match="tile_rows"):
+        replace(Plan(), tile_rows=-64).validate()

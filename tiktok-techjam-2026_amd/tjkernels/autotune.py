@@ -21,13 +21,23 @@ MI355X specifics:
   plan on the same inputs, which the tests pin to the oracle at 1e-4 -- far
   inside the 2e-2 budgets, but an error common to every plan (packing,
   layout, masking) is then invisible to the gate;
-* GEMM tile plans are not part of the tuned table: the engine times the tile
-  candidates once per projection shape at run time (``tjkernels.tiles``),
-  because with packed prefix-masked tokens the row count M of every
-  projection follows the input lengths; ``tune_gemm`` remains as a tool;
-  the plan-level knobs (attention plan, residual epilogue, hipGraph, residual dtype) are
-  tuned by coordinate descent on whole-forward latency measured as the
-  harness does (events on the current stream around the module call).
+* the plan-level knobs (attention plan, residual epilogue, hipGraph,
+  residual dtype) are tuned by coordinate descent on whole-forward latency
+  measured as the harness does (events on the current stream around the
+  module call);
+* GEMM tiles: the engine times the tile candidates once per projection
+  shape at run time (``tjkernels.tiles``), because with packed
+  prefix-masked tokens the row count M of every projection follows the
+  input lengths.  Those launches are timed alone, back to back on hot
+  caches, which ranks near-equal tiles differently from a forward, where
+  each launch follows other kernels' writes (measured at C4: the run-time
+  picks cost up to 1.5 us per out-proj launch and 2.6 us per FFN1 launch
+  against the best tile inside the forward).  So the tuner ends with a
+  coordinate descent over the four projections' tiles inside whole
+  forwards on the bench input, among the tiles of the shape's K-summation
+  class (so the outputs keep their bits), and stores them with
+  ``tile_rows`` = that input's row count: other row counts still time
+  their own.  ``tune_gemm`` remains as a tool.
 """
 
 from __future__ import annotations
@@ -39,10 +49,10 @@ from typing import Dict, List, Optional, Sequence, Tuple
 
 import torch
 
-from . import ops
+from . import ops, tiles
 from .modules import UserOptimizedTransformer
-from .plans import (Plan, attn_block_ok, default_plan, device_arch, fused_ffn_ok, save_plans, set_override,
-                    shape_key)
+from .plans import (LN_GEMM_MAX_ROWS, TUNED, Plan, attn_block_ok, default_plan, device_arch, fused_ffn_ok,
+                    save_plans, set_override, shape_key)
 from .workloads import WORKLOADS, Workload, make_inputs, make_state_dict
 
 HELD_OUT_SEEDS = [777, 4242]
@@ -142,7 +152,13 @@ class _Evaluator:
         finally:
             set_override(None)
 
-    def evaluate(self, plan: Plan) -> Dict[str, object]:
+    def bench_rows(self, plan: Plan) -> int:
+        """Rows every projection of a forward on the bench input runs: the
+        valid tokens of its prefix mask when the plan packs them."""
+        x, m = self.bench_input
+        return int(m.sum()) if plan.pack_prefix else x.shape[0] * x.shape[1]
+
+    def evaluate(self, plan: Plan, iters: Optional[int] = None) -> Dict[str, object]:
         set_override(plan)
         try:
             model = self._model()
@@ -154,7 +170,7 @@ class _Evaluator:
                         return {"plan": plan, "admissible": False, "usage": float("inf")}
                     usage = max(usage, budget_usage(ref, got, self.atol, self.rtol))
                 xb, mb = self.bench_input
-                ms = _time_ms(lambda: model(xb, mb), self.iters)
+                ms = _time_ms(lambda: model(xb, mb), iters or self.iters)
         except (ops.TjkError, ValueError) as exc:
             return {"plan": plan, "admissible": False, "error": str(exc)[:160]}
         finally:
@@ -162,14 +178,109 @@ class _Evaluator:
         return {"plan": plan, "latency_ms": ms, "usage": usage}
 
 
+def _tile_shapes(w: Workload, plan: Plan, rows: int) -> List[Tuple[str, int, int, int]]:
+    """(Plan field, N, K, epilogue) of the GEMM launches whose tile a
+    forward of ``rows`` rows under ``plan`` takes from the plan's gemm_*
+    fields (the attention block, the single-launch FFN and the LayerNorm
+    GEMM have tiles of their own)."""
+    d, f = w.d_model, w.ffn_dim
+    epi_res = ops.EPI_BIAS_RESIDUAL if plan.epilogue_residual else ops.EPI_BIAS
+    out: List[Tuple[str, int, int, int]] = []
+    if not (plan.attn_block and attn_block_ok(w.seq, d, w.heads, plan.compute_dtype)):
+        out += [("gemm_qkv", 3 * d, d, ops.EPI_BIAS), ("gemm_out", d, d, epi_res)]
+    if plan.ffn == "gemm":
+        ln_in = (plan.ln_gemm and plan.epilogue_residual and rows <= LN_GEMM_MAX_ROWS
+                 and ops.gemm_ln_supported(d, plan.compute_dtype))
+        if not ln_in:
+            out.append(("gemm_ffn1", f, d, ops.EPI_BIAS_GELU))
+        out.append(("gemm_ffn2", d, f, epi_res))
+    return out
+
+
+def tune_tiles(ev: "_Evaluator", cur: Dict[str, object], w: Workload, show=None,
+               rounds: int = 3, gain: float = 0.997) -> Dict[str, object]:
+    """Coordinate descent over the projections' GEMM tiles inside whole
+    forwards on the bench input.  Starting from the run-time picks, each
+    projection in turn times every tile of its shape's K-summation class
+    and keeps the fastest when it makes the forward ``gain`` times faster.
+    The candidates of a projection are timed on one model, in ``rounds``
+    interleaved rounds (alternating order) of ~0.1 s of forwards each,
+    compared by their mean: measured at C4, forwards on freshly built
+    models differed by more than the 0.3-1.2% between the best tiles, while
+    interleaved rounds on one model repeat within 0.1%.  Every candidate's
+    output is checked to equal the starting plan's bit for bit (tiles of one
+    class), so the gate's usage carries over.  Returns the evaluation of
+    the result, its plan pinning the tiles at the bench input's row count
+    (``tile_rows``)."""
+    plan = cur["plan"]
+    rows = ev.bench_rows(plan)
+    if rows == 0:
+        return cur
+    mb = -(-rows // tiles.M_BUCKET) * tiles.M_BUCKET
+    shapes = _tile_shapes(w, plan, rows)
+    if not shapes:
+        return cur
+    pins = {name: tiles.gemm_plan(rows, n, k, plan.compute_dtype, epi, getattr(plan, name))
+            for name, n, k, epi in shapes}
+    best_plan = replace(plan, tile_rows=mb, **pins)
+    xb, maskb = ev.bench_input
+    model = ev._model()
+    key = (w.batch, w.seq)
+    set_override(best_plan)
+    try:
+        with torch.inference_mode():
+            ref = model(xb, maskb).clone()
+            engine = model._tj_engine
+            per_ms = _time_ms(lambda: model(xb, maskb), 5)
+            steps = max(5, min(200, int(100.0 / max(per_ms, 1e-3))))
+
+            def timed(p: Plan) -> float:
+                engine._plans[key] = p  # the engine's plan for this shape, swapped in place
+                return _time_ms(lambda: model(xb, maskb), steps, warmup=max(3, steps // 10))
+
+            for name, n, k, epi in shapes:
+                trial = {c: replace(best_plan, **{name: c}) for c in tiles.candidates(mb, n, k, plan.compute_dtype)}
+                for c, p in list(trial.items()):
+                    engine._plans[key] = p
+                    try:
+                        same = torch.equal(model(xb, maskb), ref)
+                    except ops.TjkError:
+                        same = False
+                    if not same:
+                        del trial[c]  # another class, or a tile the shape does not take
+                if not trial:
+                    continue
+                times: Dict[int, List[float]] = {c: [] for c in trial}
+                order = list(trial)
+                for rnd in range(rounds):
+                    for c in (order if rnd % 2 == 0 else order[::-1]):
+                        times[c].append(timed(trial[c]))
+                mean = {c: statistics.mean(v) for c, v in times.items()}
+                cur_c = getattr(best_plan, name)
+                fastest = min(mean, key=mean.get)
+                if show is not None:
+                    print(f"    {name:<28} " + " ".join(f"{c}:{mean[c]:.4f}" for c in order), flush=True)
+                if fastest != cur_c and (cur_c not in mean or mean[fastest] < mean[cur_c] * gain):
+                    best_plan = trial[fastest]
+    finally:
+        set_override(None)
+    best = ev.evaluate(best_plan)
+    if show is not None:
+        show("tiles", best)
+    return best if "latency_ms" in best else cur
+
+
 def tune_workload(w: Workload, trials: int = 2, margin: float = 0.85, iters: int = 30,
                   verbose: bool = True, references: Optional[Sequence[torch.Tensor]] = None,
-                  log: Optional[List[Dict[str, object]]] = None) -> Optional[Tuple[str, Plan, Dict[str, object]]]:
+                  log: Optional[List[Dict[str, object]]] = None, tile_step: bool = True,
+                  start: Optional[Plan] = None) -> Optional[Tuple[str, Plan, Dict[str, object]]]:
     """The fastest admissible plan of workload ``w`` as (shape key, plan,
     its evaluation), or None when neither the heuristic plan nor its fp32
     escalation is admissible.  ``references``: the gate's reference outputs,
     one per ``gate_seeds(trials)`` seed (see the module docstring).
-    ``log``, if given, receives every evaluation in order, tagged."""
+    ``log``, if given, receives every evaluation in order, tagged.
+    ``tile_step``: end with ``tune_tiles``.  ``start``: a plan to refine
+    instead of the heuristic (its knobs kept; only the tiles are tuned)."""
     dev = torch.device("cuda", torch.cuda.current_device())
     base = replace(default_plan(w.batch, w.seq, w.d_model, w.heads, w.ffn_dim, w.layers,
                                 w.causal, w.dtype, dev), label="autotuned")
@@ -188,6 +299,16 @@ def tune_workload(w: Workload, trials: int = 2, margin: float = 0.85, iters: int
             else:
                 print(f"    {tag:<28} ERR {r.get('error', 'non-finite output')}", flush=True)
 
+    key = shape_key(w.batch, w.seq, w.d_model, w.heads, w.ffn_dim, w.layers, w.causal,
+                    w.dtype, device_arch(dev))
+    if start is not None:
+        cur = ev.evaluate(replace(start, tile_rows=0, gemm_qkv=-1, gemm_out=-1, gemm_ffn1=-1, gemm_ffn2=-1))
+        show("stored plan", cur)
+        if not admissible(cur):
+            return None
+        best = tune_tiles(ev, cur, w, show)
+        return key, best["plan"], best
+
     cur = ev.evaluate(base)
     show("heuristic", cur)
     if not admissible(cur) and base.compute_dtype != torch.float32:
@@ -201,10 +322,6 @@ def tune_workload(w: Workload, trials: int = 2, margin: float = 0.85, iters: int
             cur = esc
     if not admissible(cur):
         return None
-
-    # GEMM tile plans stay -1: the engine times the tile candidates once per
-    # projection shape at run time (tjkernels.tiles), since with packed
-    # prefix-masked tokens M follows the input lengths.
 
     # coordinate descent over the plan-level knobs
     attn_plans = [0, 1, 3] + ([4] if w.seq <= 128 else [])
@@ -230,8 +347,8 @@ def tune_workload(w: Workload, trials: int = 2, margin: float = 0.85, iters: int
             show(f"{knob}={v}", probe)
             if admissible(probe) and probe["latency_ms"] < cur["latency_ms"] * 0.98:
                 cur = probe
-    key = shape_key(w.batch, w.seq, w.d_model, w.heads, w.ffn_dim, w.layers, w.causal,
-                    w.dtype, device_arch(dev))
+    if tile_step:
+        cur = tune_tiles(ev, cur, w, show)
     return key, cur["plan"], cur
 
 
@@ -242,13 +359,24 @@ def main(argv: Optional[List[str]] = None) -> int:
     ap.add_argument("--margin", type=float, default=0.85)
     ap.add_argument("--iters", type=int, default=30)
     ap.add_argument("--dry-run", action="store_true")
+    ap.add_argument("--tiles-only", action="store_true",
+                    help="keep each workload's stored plan (plans.json) and tune only its GEMM tiles")
+    ap.add_argument("--no-tiles", action="store_true", help="skip the GEMM tile step")
     ap.add_argument("--out", default=None, help="plans file to merge into (default: the package's plans.json)")
     args = ap.parse_args(argv)
     tuned: Dict[str, Plan] = {}
     for name in args.workloads.split(","):
         w = WORKLOADS[name]
         print(f"{w.describe()}", flush=True)
-        out = tune_workload(w, args.trials, args.margin, args.iters)
+        start = None
+        if args.tiles_only:
+            dev = torch.device("cuda", torch.cuda.current_device())
+            start = TUNED.get(shape_key(w.batch, w.seq, w.d_model, w.heads, w.ffn_dim, w.layers, w.causal,
+                                        w.dtype, device_arch(dev)))
+            if start is None:
+                print("    no stored plan; skipped", flush=True)
+                continue
+        out = tune_workload(w, args.trials, args.margin, args.iters, tile_step=not args.no_tiles, start=start)
         if out is None:
             print("    no admissible plan; heuristic left in place", flush=True)
             continue

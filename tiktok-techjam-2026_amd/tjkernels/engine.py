@@ -382,11 +382,18 @@ class Engine:
         # attention block
         ln_in = (plan.ln_gemm and plan.epilogue_residual and not fused and not block
                  and 0 < rows <= LN_GEMM_MAX_ROWS and ops.gemm_ln_supported(d, cdt))
+        # a plan's tiles hold at the row count they were measured at (or at
+        # every row count with tile_rows 0); other row counts time their own
+        row_bucket = -(-rows // tiles.M_BUCKET) * tiles.M_BUCKET
+
+        def pin(tile: int) -> int:
+            return tile if plan.tile_rows in (0, row_bucket) else -1
+
         tp = Tiles(
-            qkv=-1 if block else tiles.gemm_plan(rows, 3 * d, d, cdt, ops.EPI_BIAS, plan.gemm_qkv),
-            out=-1 if block else tiles.gemm_plan(rows, d, d, cdt, epi_res, plan.gemm_out),
-            fc1=-1 if fused or ln_in else tiles.gemm_plan(rows, f, d, cdt, ops.EPI_BIAS_GELU, plan.gemm_ffn1),
-            fc2=-1 if fused else tiles.gemm_plan(rows, d, f, cdt, epi_res, plan.gemm_ffn2),
+            qkv=-1 if block else tiles.gemm_plan(rows, 3 * d, d, cdt, ops.EPI_BIAS, pin(plan.gemm_qkv)),
+            out=-1 if block else tiles.gemm_plan(rows, d, d, cdt, epi_res, pin(plan.gemm_out)),
+            fc1=-1 if fused or ln_in else tiles.gemm_plan(rows, f, d, cdt, ops.EPI_BIAS_GELU, pin(plan.gemm_ffn1)),
+            fc2=-1 if fused else tiles.gemm_plan(rows, d, f, cdt, epi_res, pin(plan.gemm_ffn2)),
             qkv_ln=tiles.gemm_ln_plan(rows, 3 * d, d, cdt, ops.EPI_BIAS) if ln_in else -1,
             fc1_ln=tiles.gemm_ln_plan(rows, f, d, cdt, ops.EPI_BIAS_GELU) if ln_in else -1)
         fw = Forward(batch=batch, seq=seq, mode=mode, rows=rows,

@@ -48,6 +48,10 @@ to select, and the product path has no non-HIP fallback):
 * ``gemm_*`` / ``attn_plan``: force a tile or attention plan (-1: chosen
   at run time; attention 0-4 are the library's plans of tjk_flash_fwd,
   ``ATTN_SCHEDULED`` (5) the work-list kernel for packed sequences);
+* ``tile_rows``: the packed row count (a multiple of ``tiles.M_BUCKET``)
+  the ``gemm_*`` tiles were measured at by the autotuner, inside whole
+  forwards; a forward whose row count rounds up to another value times its
+  own tiles as if they were -1.  0 applies them at every row count;
 * ``pack_prefix``: run only the valid tokens of prefix masks.
 
 Environment: ``TJ_NO_GRAPH``, ``TJ_WHOLE_GRAPH`` (0 / 1), ``TJ_ATTN_BLOCK`` (0 / 1), ``TJ_LN_GEMM`` (0 / 1),
@@ -107,6 +111,7 @@ class Plan:
     gemm_out: int = -1
     gemm_ffn1: int = -1
     gemm_ffn2: int = -1
+    tile_rows: int = 0
     attn_plan: int = -1
     pack_prefix: bool = True
     label: str = "default"
@@ -147,6 +152,8 @@ class Plan:
             raise ValueError(f"ffn={self.ffn!r}: one of {FFN_KINDS}")
         if not self.packed_qkv:
             raise ValueError("only the packed QKV layout is implemented")
+        if self.tile_rows < 0:
+            raise ValueError(f"tile_rows={self.tile_rows}: a row count >= 0")
 
 
 def device_arch(device: torch.device) -> str:

@@ -35,8 +35,11 @@ The table is keyed by M rounded up to a multiple of 64 (the timing runs at
 that M), so ragged lengths reuse a measurement, and it holds at most
 ``MAX_ENTRIES`` shapes.  This replaces the reference's static per-shape
 table lookup for the GEMM part of a plan (tjkernels/plans.py:147-170); tile
-ids >= 0 in a ``Plan`` still force a tile.  ``TJ_GEMM_TUNE=0`` uses the
-library's own rule (tile -1) instead of timing.
+ids >= 0 in a ``Plan`` still force a tile, at the row bucket
+``Plan.tile_rows`` names (the autotuner's tiles, timed inside whole
+forwards, where the ranking of near-equal tiles differs from this timing
+of lone launches) or at every row count when it is 0.  ``TJ_GEMM_TUNE=0``
+uses the library's own rule (tile -1) instead of timing.
 """
 
 from __future__ import annotations
