@@ -94,8 +94,14 @@ __device__ __forceinline__ int64_t map_row(const RowMap& rm, int64_t row, bool c
 }
 
 // FULL: n == 256 * MAXCH, every lane's chunks in range (no per-chunk guards).
+// ln_threads(WT) / 64 rows per workgroup: in launches that write through
+// (WT, at least kWtMinBytes of output) 8 rows measured 0.3% faster than 4
+// (and 2, 16) over whole C4 and C5 forwards, builds alternating on one box;
+// in C2's 128-row launches 8 rows made the forward 1.4% slower, so smaller
+// launches keep 4.
+constexpr int ln_threads(bool wt) { return wt ? 512 : 256; }
 template <typename TRes, typename TDelta, typename TOut, int MAXCH, bool FULL, bool WT>
-__global__ __launch_bounds__(256) void add_layernorm_kernel(
+__global__ __launch_bounds__(ln_threads(WT)) void add_layernorm_kernel(
     const TRes* res, int64_t ld_res,  // may alias res_out (in-place update)
     const TDelta* __restrict__ delta, int64_t ld_delta,
     void* res_out, int ro_dtype, int64_t ld_res_out,
@@ -104,24 +110,25 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(
     int64_t rows, int n, float eps, RowMap rmap, const uint8_t* __restrict__ row_mask) {
   const int lane = threadIdx.x & 63;
   const int nch = n >> 2;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  constexpr int NT = ln_threads(WT);
+  const int64_t row = (int64_t)blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
   const bool live = row < rows;
   const int64_t src = !live ? -1 : map_row(rmap, row, lane == 0);
 
-  // gamma / beta staged once per workgroup (4 rows), by every thread before
+  // gamma / beta staged once per workgroup (NT / 64 rows), by every thread before
   // any wave leaves: read from L2 by each wave they were 8 KB per 1024-wide
   // row, more than the row itself.  In launches large enough to write
   // through (WT) and up to 2048-wide rows, their loads go out first, in
   // flight together with the row's (measured: 6.4 -> 4.9 us per C4
   // LayerNorm together with the write-through stores; in launches of a few
   // hundred rows, 0.1 us slower).
-  constexpr int GPT = (64 * MAXCH + 255) / 256;  // gamma / beta chunks per thread
+  constexpr int GPT = (64 * MAXCH + NT - 1) / NT;  // gamma / beta chunks per thread
   constexpr bool EARLY = WT && GPT <= 2;
   float4 gl[EARLY ? GPT : 1], bl[EARLY ? GPT : 1];
   if constexpr (EARLY) {
 #pragma unroll
     for (int u = 0; u < GPT; ++u) {
-      const int c = min((int)threadIdx.x + 256 * u, nch - 1);
+      const int c = min((int)threadIdx.x + NT * u, nch - 1);
       gl[u] = reinterpret_cast<const float4*>(gamma)[c];
       bl[u] = reinterpret_cast<const float4*>(beta)[c];
     }
@@ -161,14 +168,14 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(
   if constexpr (EARLY) {
 #pragma unroll
     for (int u = 0; u < GPT; ++u) {
-      const int c = (int)threadIdx.x + 256 * u;
+      const int c = (int)threadIdx.x + NT * u;
       if (c < nch) {
         s_gamma[c] = gl[u];
         s_beta[c] = bl[u];
       }
     }
   } else {
-    for (int c = threadIdx.x; c < nch; c += 256) {
+    for (int c = threadIdx.x; c < nch; c += NT) {
       s_gamma[c] = reinterpret_cast<const float4*>(gamma)[c];
       s_beta[c] = reinterpret_cast<const float4*>(beta)[c];
     }
@@ -410,8 +417,9 @@ static int launch_ln(const void* res, int64_t ld_res, const void* delta, int64_t
                                          stream);
   }
   const int nch = n / 4;
-  dim3 grid((unsigned)((rows + 3) / 4)), block(256);
   const bool wt = rows * n * (int64_t)sizeof(TOut) >= kWtMinBytes;
+  const int rpw = ln_threads(wt) / 64;  // rows per workgroup
+  const dim3 grid((unsigned)((rows + rpw - 1) / rpw)), block(ln_threads(wt));
 #define TJK_LN_LAUNCH1(MC, FULL, WT)                                                                   \
   hipLaunchKernelGGL((add_layernorm_kernel<TRes, TDelta, TOut, MC, FULL, WT>), grid, block, 0, stream,     \
                      (const TRes*)res, ld_res, (const TDelta*)delta, ld_delta, res_out, ro_dtype, ld_res_out, \
