@@ -1262,18 +1262,27 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
     // tiles past the item write zeros too) and every wave is past its last
     // tile.
     __syncthreads();
-    constexpr int OP = HDP * 2 + 16;             // staged row pitch (bytes)
-    constexpr int PPR = HDP * 2 / 16;            // 16-byte pieces per row
+    // The GEMM epilogue's staging layout: whole 16-byte pieces per lane (the
+    // halves of pieces g = 2k, 2k + 1 trade lanes l32 and l32 + 32), piece p
+    // of row r at slot r PPR + (p ^ (r & 7)): no LDS bank conflicts for the
+    // 8-lanes-per-cycle writes or the 32-lanes-per-cycle reads.
+    constexpr int PPR = HDP * 2 / 16;            // 16-byte pieces per row (8 or 16)
     constexpr int NPASS = 32 * PPR / 64;         // store instructions per wave
-    char* stg = smem + wave * 32 * OP;
+    static_assert(!DMA || PPR % 8 == 0, "rows of whole 8-piece XOR groups");
+    auto slot = [](int r, int p) __attribute__((always_inline)) { return (r * PPR + (p ^ (r & 7))) * 16; };
+    char* stg = smem + wave * 32 * PPR * 16;
+    auto scaled = [&](int hb, int g) __attribute__((always_inline)) {
+      return Quad<T>::from(make_float4(o[hb][4 * g] * inv, o[hb][4 * g + 1] * inv, o[hb][4 * g + 2] * inv,
+                                       o[hb][4 * g + 3] * inv));
+    };
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const float4 v = make_float4(o[hb][4 * g] * inv, o[hb][4 * g + 1] * inv, o[hb][4 * g + 2] * inv,
-                                     o[hb][4 * g + 3] * inv);
-        *reinterpret_cast<typename Quad<T>::raw*>(stg + l32 * OP + (hb * 32 + 8 * g + 4 * hi) * 2) =
-            Quad<T>::from(v);
+      for (int k = 0; k < 2; ++k) {
+        const typename Quad<T>::raw x = scaled(hb, 2 * k), y = scaled(hb, 2 * k + 1);
+        const auto s0 = __builtin_amdgcn_permlane32_swap(x.x, y.x, false, false);
+        const auto s1 = __builtin_amdgcn_permlane32_swap(x.y, y.y, false, false);
+        *reinterpret_cast<uint4*>(stg + slot(l32, 4 * hb + 2 * k + hi)) = make_uint4(s0[0], s1[0], s0[1], s1[1]);
       }
     const int nrow = min(Sb - wq0, 32);
     const RowOut rows(out + (row0 + wq0) * ld_out + (int64_t)h * hd,
@@ -1284,7 +1293,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(HDP <= 
 #pragma unroll
       for (int ps = 0; ps < NPASS; ++ps) {
         const int idx = lane + 64 * ps, r = idx / PPR, pc = idx % PPR;
-        const uint4 piece = *reinterpret_cast<const uint4*>(stg + r * OP + pc * 16);
+        const uint4 piece = *reinterpret_cast<const uint4*>(stg + slot(r, pc));
         if (r < nrow) w.put((int)(((int64_t)r * ld_out + pc * 8) * (int64_t)sizeof(T)), piece);
       }
     });
