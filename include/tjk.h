@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define TJK_ABI_VERSION 9
+#define TJK_ABI_VERSION 10
 
 /* dtypes */
 #define TJK_F32 0
@@ -126,6 +126,28 @@ int tjk_gemm_bias(const void* a, int64_t lda, const void* w, int64_t ldw,
                   const void* bias, void* c, int64_t ldc,
                   int64_t m, int64_t n, int64_t k,
                   int dtype, int epilogue, int plan_id, void* stream);
+
+/*
+ * C[m, n] = sum_k A[m, k] * W[n, k] + bias[n] + x[r(m), n], C fp32 and
+ * written (not read): tjk_gemm_bias's TJK_EPI_BIAS_RESIDUAL with the
+ * residual read from x (`dtype`, leading dimension ld_x) instead of from C.
+ * r(m) = rows[m] (an int32 row map, e.g. the packing of prefix-masked
+ * tokens), or m when rows is NULL; a row r(m) outside [0, x_rows) adds
+ * zeros and is counted once in *index_errors (optional).  The sum is
+ * formed exactly as tjk_gemm_bias forms it from a residual holding x's rows
+ * in fp32 (the same bits).  Requires what tjk_gemm_bias requires, ld_x %
+ * 4 == 0 and x aligned to 4 elements.
+ * Replaces, for the first layer, the fp32 copy of x the reference makes
+ * (tjkernels/engine.py:230) and writes back from the first
+ * fused_add_layernorm (:239-242), and the add of the out-projection into
+ * it (:247-252): the first LayerNorm then writes only h.
+ */
+int tjk_gemm_bias_residual_from(const void* a, int64_t lda, const void* w, int64_t ldw,
+                                const void* bias, float* c, int64_t ldc,
+                                int64_t m, int64_t n, int64_t k,
+                                const void* x, int64_t ld_x, int64_t x_rows,
+                                const int32_t* rows, int* index_errors,
+                                int dtype, int plan_id, void* stream);
 
 /* Number of GEMM tile plans for `dtype`, and the tile of plan `id`:
  * block_m x block_n outputs, `waves` waves, the K range split over

@@ -210,6 +210,66 @@ def test_gemm_write_through_launch_equals_plain(device, epi, plan):
     _close(outs[0], ref, rtol, 1e-4)
 
 
+@pytest.mark.parametrize("dt,plan", [(torch.bfloat16, p) for p in list(STAGED16) + list(DTL16)]
+                         + [(torch.float16, p) for p in (0, 8, 14, 23, 30, 31)]
+                         + [(torch.float32, p) for p in list(STAGED32) + list(DTL32)])
+def test_gemm_residual_from_equals_residual_over_gathered_rows(device, dt, plan):
+    """tjk_gemm_bias_residual_from (residual read from x through a row map,
+    the out-projection of the first layer) equals, bit for bit, the residual
+    epilogue over an fp32 copy of the gathered rows -- the residual the first
+    LayerNorm would write -- with and without a row map, with and without
+    the residual prefetch (small and large tiles), on ragged shapes; and the
+    sum against fp64."""
+    for m, n, k, x_rows in ((513, 1028, 1088, 700), (1000, 516, 1024, 1000), (200, 256, 64, 333)):
+        g = _gen(31 + plan + m)
+        a = torch.randn(m, k, generator=g).to(dt)
+        w = (torch.randn(n, k, generator=g) / math.sqrt(k)).to(dt)
+        b = torch.randn(n, generator=g).to(dt)
+        x = torch.randn(x_rows, n, generator=g).to(dt)
+        maps = [torch.randperm(x_rows, generator=g)[:m].int() if x_rows >= m
+                else torch.randint(0, x_rows, (m,), generator=g).int()]
+        if x_rows >= m:
+            maps.append(None)
+        for rows in maps:
+            gathered = (x if rows is None else x[rows.long()])[:m].float()
+            want = gathered.to(device)
+            got = torch.full((m, n), float("nan"), device=device)
+            ad, wd, bd = a.to(device), w.to(device), b.to(device)
+            ops.gemm(ad, wd, bd, want, ops.EPI_BIAS_RESIDUAL, plan)
+            ops.gemm_residual_from(ad, wd, bd, got, x.to(device), None if rows is None else rows.to(device),
+                                   plan=plan)
+            torch.cuda.synchronize()
+            assert torch.equal(got, want), f"plan {plan} {m}x{n}x{k} map={rows is not None}"
+            ref = a.double() @ w.double().t() + b.double() + gathered.double()
+            _close(got, ref, 2e-5, 1e-4 if dt != torch.float32 else 1e-5)
+
+
+def test_gemm_residual_from_rows_outside_x_add_zeros_and_are_counted(device):
+    """Row-map entries outside [0, x_rows) (negative, or at / past x_rows)
+    add zeros, read nothing outside x and are counted once each in
+    index_errors; the other rows are unaffected."""
+    m, n, k, x_rows = 300, 512, 256, 260
+    g = _gen(5)
+    a = torch.randn(m, k, generator=g).bfloat16().to(device)
+    w = (torch.randn(n, k, generator=g) / math.sqrt(k)).bfloat16().to(device)
+    b = torch.randn(n, generator=g).bfloat16().to(device)
+    x = torch.randn(x_rows, n, generator=g).bfloat16()
+    rows = torch.randint(0, x_rows, (m,), generator=g).int()
+    bad = torch.tensor([0, 7, 64, 65, 299])
+    rows[bad] = torch.tensor([-1, x_rows, x_rows + 5, -7, 1 << 30], dtype=torch.int32)
+    for plan in (0, 9, 30):
+        errors = torch.zeros(1, dtype=torch.int32, device=device)
+        got = torch.full((m, n), float("nan"), device=device)
+        ops.gemm_residual_from(a, w, b, got, x.to(device), rows.to(device), index_errors=errors, plan=plan)
+        want = x[rows.long().clamp(0, x_rows - 1)].float()
+        want[bad] = 0
+        want = want.to(device)
+        ops.gemm(a, w, b, want, ops.EPI_BIAS_RESIDUAL, plan)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"plan {plan}"
+        assert int(errors.item()) == len(bad), f"plan {plan}: {int(errors.item())} errors counted"
+
+
 @pytest.mark.parametrize("plan", list(STAGED32) + list(DTL32))
 def test_gemm_fp32_plans(device, plan):
     _gemm_case(device, 257, 516, 256, torch.float32, ops.EPI_BIAS, plan)

@@ -16,6 +16,7 @@ import torch
 from oracle import model as oracle
 from tjkernels import Plan, TransformerConfig, UserOptimizedTransformer
 from tjkernels import plans as plans_mod
+from tjkernels.engine import MASK_NONE
 from tjkernels.workloads import WORKLOADS, Workload, make_inputs, make_state_dict
 
 pytestmark = pytest.mark.gpu
@@ -214,6 +215,11 @@ def test_graph_equals_eager(device, dtype, ffn, whole):
     try:
         with torch.inference_mode():
             expected = [eager(x.to(device), m.to(device)).cpu() for x, m in cases]
+            # eager forwards add x into the residual in layer 0's out-proj
+            # (the first LayerNorm writes no residual); graphed ones keep the
+            # residual the first LayerNorm writes: the bits must agree
+            fw = eager._tj_engine._prepare(cfg.batch_size, cfg.seq_len, MASK_NONE, None, None)
+            assert fw.res_from_x
     finally:
         plans_mod.set_override(None)
     plans_mod.set_override(Plan(compute_dtype=dtype, cuda_graph=True, whole_graph=whole, ffn=ffn, label="graphed"))

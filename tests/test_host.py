@@ -72,6 +72,22 @@ def test_abi_rejects_bad_arguments_without_launching():
     for n_lists in (0, 3, -1):
         assert lib.tjk_flash_fwd_sched(fake, 192, 64, 64, fake, 64, 1, 128, 1, 64, 0.125, 1, fake, fake, 2,
                                        n_lists, None, 0, 0, _lib.BF16, None) == _lib.EINVAL
+    # the residual GEMM reading x: x is required, bounded and aligned like the residual
+    from_x = lib.tjk_gemm_bias_residual_from
+    assert from_x(fake, 8, fake, 8, None, fake, 8, 4, 8, 8, None, 8, 4, None, None, _lib.BF16, -1, None) \
+        == _lib.EINVAL
+    assert b"null" in lib.tjk_last_error_string()
+    assert from_x(fake, 8, fake, 8, None, fake, 8, 4, 8, 8, fake, 4, 4, None, None, _lib.BF16, -1, None) \
+        == _lib.EINVAL  # ld_x < n
+    assert from_x(fake, 8, fake, 8, None, fake, 8, 4, 8, 8, fake, 8, -1, None, None, _lib.BF16, -1, None) \
+        == _lib.EINVAL  # negative x_rows
+    assert from_x(fake, 8, fake, 8, None, fake, 8, 4, 8, 8, fake + 2, 8, 4, None, None, _lib.BF16, -1, None) \
+        == _lib.EUNSUPPORTED  # x not aligned to 4 elements
+    assert from_x(fake, 8, fake, 8, None, fake, 8, 4, 8, 8, fake, 8, 4, fake + 2, None, _lib.BF16, -1, None) \
+        == _lib.EUNSUPPORTED  # misaligned row map
+    assert from_x(fake, 8, fake, 8, None, fake, 8, 4, 8, 8, fake, 10, 4, None, None, _lib.BF16, -1, None) \
+        == _lib.EUNSUPPORTED  # ld_x % 4
+    assert from_x(None, 8, None, 8, None, None, 8, 0, 8, 8, None, 8, 0, None, None, _lib.BF16, -1, None) == 0
     # empty work is a successful no-op
     assert lib.tjk_gemm_bias(None, 8, None, 8, None, None, 8, 0, 4, 8, _lib.BF16, 0, -1, None) == 0
     assert lib.tjk_gemm_plan_count(_lib.BF16) >= 4

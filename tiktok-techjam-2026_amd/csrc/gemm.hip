@@ -34,7 +34,7 @@ namespace tjk {
 template <typename T, int BM, int BN, int WM, int WN, int EPI>
 __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
     const T* __restrict__ A, int64_t lda, const T* __restrict__ W, int64_t ldw,
-    const T* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K) {
+    const T* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K, ResSrc src) {
   constexpr int NT = WM * WN * 64;
   constexpr int VEC = 16 / sizeof(T);            // elements per 16-byte chunk
   constexpr int BK = 128 / sizeof(T);            // 128 bytes of K per row
@@ -129,13 +129,14 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_kernel(
   // The loop ends on a barrier, so the operand tiles are dead: reuse LDS.
   static_assert(NT / 64 * EpiStage<T, EPI, FN>::BYTES <= (int)sizeof(smem), "epilogue staging exceeds LDS");
   epilogue<T, EPI, FM, FN>(acc, bias, Cv, ldc, M, N, m0 + wm * WTM, n0 + wn * WTN, lane,
-                           reinterpret_cast<char*>(&smem[0][0]) + wave * EpiStage<T, EPI, FN>::BYTES);
+                           reinterpret_cast<char*>(&smem[0][0]) + wave * EpiStage<T, EPI, FN>::BYTES, NoPrefetch(),
+                           nullptr, src);
 }
 
 template <typename T, int BM, int BN, int WM, int WN, int BKB, int STAGES, int EPI, int KSPLIT>
 __global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
     const T* __restrict__ A, int64_t lda, const T* __restrict__ W, int64_t ldw,
-    const T* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K) {
+    const T* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K, ResSrc src) {
   typedef DtlGeom<T, BM, BN, WM, WN, BKB, STAGES, KSPLIT> G;
   constexpr int NW = G::NW, FM = G::FM, FN = G::FN;
   __shared__ __attribute__((aligned(1024))) char smem[G::LDS];
@@ -161,17 +162,18 @@ __global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
   constexpr int WAVES_PER_SIMD = (WG_PER_CU * NW * KSPLIT + 3) / 4 > 1 ? (WG_PER_CU * NW * KSPLIT + 3) / 4 : 1;
   constexpr int BUDGET = 512 / WAVES_PER_SIMD - FM * FN * 16 - 144;
   constexpr int BIAS_REGS = FN * 4 * (int)sizeof(typename Quad<T>::raw) / 4;
-  constexpr int PRE_REGS = FM * ResPrefetch<FM, FN>::NIT * 4;
+  typedef ResPrefetch<FM, FN, T, EPI == kEpiResidualFrom> ResPre;
+  constexpr int PRE_REGS = ResPre::REGS;
   constexpr bool SMALL = sizeof(T) == 2 && FM * FN <= 4;
   constexpr bool BIAS_PRE = SMALL && BIAS_REGS <= BUDGET;
-  constexpr bool PREFETCH = EPI == TJK_EPI_BIAS_RESIDUAL && (KSPLIT == 1 || SMALL) &&
+  constexpr bool PREFETCH = epi_residual(EPI) && (KSPLIT == 1 || SMALL) &&
                             PRE_REGS + (BIAS_PRE ? BIAS_REGS : 0) <= BUDGET;
-  typedef typename std::conditional<PREFETCH, ResPrefetch<FM, FN>, NoPrefetch>::type Pre;
+  typedef typename std::conditional<PREFETCH, ResPre, NoPrefetch>::type Pre;
   BiasRaw<T, FN> bpre;
   if constexpr (BIAS_PRE) bpre.load(bias, N, n0 + wn * G::WTN, lane);
   Pre pre;
   if constexpr (PREFETCH)
-    pre.load(static_cast<const float*>(Cv), ldc, M, N, m0 + wm * G::WTM, n0 + wn * G::WTN, lane);
+    pre.load(static_cast<const float*>(Cv), ldc, M, N, m0 + wm * G::WTM, n0 + wn * G::WTN, lane, src);
 
   f32x16 acc[FN][FM];
   zero_acc<T, FM, FN>(acc);
@@ -206,9 +208,12 @@ __global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
           for (int r = 0; r < 16; ++r) acc[i][j][r] += ot[((i * FM + j) * 16 + r) * 64 + lane];
     }
   }
-  epilogue<T, EPI, FM, FN, Pre>(acc, bias, Cv, ldc, M, N, m0 + wm * G::WTM, n0 + wn * G::WTN, lane,
-                                smem + XCH + wave * EpiStage<T, EPI, FN>::BYTES, pre,
-                                BIAS_PRE ? &bpre : nullptr);
+  // batched residual reads except in the register-tight tiles (K-split
+  // groups, more than 8 accumulator blocks), where they spilled
+  constexpr int RB = KSPLIT == 1 && FM * FN <= 8 ? kResBatch : 0;
+  epilogue<T, EPI, FM, FN, Pre, RB>(acc, bias, Cv, ldc, M, N, m0 + wm * G::WTM, n0 + wn * G::WTN, lane,
+                                    smem + XCH + wave * EpiStage<T, EPI, FN>::BYTES, pre,
+                                    BIAS_PRE ? &bpre : nullptr, src);
 }
 
 
@@ -234,7 +239,7 @@ __global__ __launch_bounds__(WM * WN * KSPLIT * 64) void gemm_dtl_kernel(
 template <typename T, int BM, int BN, int WM, int WN, int STAGES, int L, int EPI>
 __global__ __launch_bounds__((WM * WN + L) * 64) void gemm_ws_kernel(
     const T* __restrict__ A, int64_t lda, const T* __restrict__ W, int64_t ldw,
-    const T* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K) {
+    const T* __restrict__ bias, void* __restrict__ Cv, int64_t ldc, int M, int N, int K, ResSrc src) {
   constexpr int BKB = 128;
   typedef DtlGeom<T, BM, BN, WM, WN, BKB, STAGES, 1> G;
   constexpr int NW = G::NW, KS = G::KS, CPS = G::CPS, WTM = G::WTM, WTN = G::WTN, FM = G::FM, FN = G::FN;
@@ -321,15 +326,16 @@ __global__ __launch_bounds__((WM * WN + L) * 64) void gemm_ws_kernel(
   // a power of two, keeps every plan here free of spills)
   constexpr int USED = FM * FN * 16 + 2 * (FM + FN) * 4 + ((STAGES & (STAGES - 1)) ? 44 : 36);
   constexpr int BIAS_REGS = FN * 4 * (int)sizeof(typename Quad<T>::raw) / 4;
-  constexpr int PRE_REGS = FM * ResPrefetch<FM, FN>::NIT * 4;
-  constexpr bool PREFETCH = EPI == TJK_EPI_BIAS_RESIDUAL && USED + PRE_REGS <= AVAIL;
+  typedef ResPrefetch<FM, FN, T, EPI == kEpiResidualFrom> ResPre;
+  constexpr int PRE_REGS = ResPre::REGS;
+  constexpr bool PREFETCH = epi_residual(EPI) && USED + PRE_REGS <= AVAIL;
   constexpr bool BIAS_PRE = USED + BIAS_REGS + (PREFETCH ? PRE_REGS : 0) <= AVAIL;
-  typedef typename std::conditional<PREFETCH, ResPrefetch<FM, FN>, NoPrefetch>::type Pre;
+  typedef typename std::conditional<PREFETCH, ResPre, NoPrefetch>::type Pre;
   BiasRaw<T, FN> bpre;
   if constexpr (BIAS_PRE) bpre.load(bias, N, n0 + wn * WTN, lane);
   Pre pre;
   if constexpr (PREFETCH)
-    pre.load(static_cast<const float*>(Cv), ldc, M, N, m0 + wm * WTM, n0 + wn * WTN, lane);
+    pre.load(static_cast<const float*>(Cv), ldc, M, N, m0 + wm * WTM, n0 + wn * WTN, lane, src);
   const int sw = swz<BKB>(l32);
   typedef typename Mfma<T>::frag Frag;
   auto frag_at = [&](const char* rowbase, int ks) -> Frag {
@@ -386,8 +392,11 @@ __global__ __launch_bounds__((WM * WN + L) * 64) void gemm_ws_kernel(
   }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();  // B_final: every ring read done, every DMA landed
-  epilogue<T, EPI, FM, FN, Pre>(acc, bias, Cv, ldc, M, N, m0 + wm * WTM, n0 + wn * WTN, lane,
-                                smem + wave * EpiStage<T, EPI, FN>::BYTES, pre, BIAS_PRE ? &bpre : nullptr);
+  // (the tiles that cannot take the prefetch are register-tight: their
+  // residual pieces are read one by one, which spills nothing)
+  epilogue<T, EPI, FM, FN, Pre, 0>(acc, bias, Cv, ldc, M, N, m0 + wm * WTM, n0 + wn * WTN, lane,
+                                   smem + wave * EpiStage<T, EPI, FN>::BYTES, pre, BIAS_PRE ? &bpre : nullptr,
+                                   src);
 }
 
 // ------------------------------------------------------------------ plans
@@ -527,6 +536,7 @@ static int auto_plan(int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldw) 
 struct GemmArgs {
   const void* a; int64_t lda; const void* w; int64_t ldw; const void* bias; void* c; int64_t ldc;
   int M, N, K; hipStream_t s;
+  ResSrc src;  // kEpiResidualFrom's residual source (unused by the other epilogues)
 };
 template <int KIND> struct Launcher;
 template <> struct Launcher<kStaged> {
@@ -534,7 +544,7 @@ template <> struct Launcher<kStaged> {
   static int go(const GemmArgs& g) {
     const dim3 grid(((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN));
     hipLaunchKernelGGL((gemm_kernel<T, BM, BN, WM, WN, EPI>), grid, dim3(WM * WN * 64), 0, g.s, (const T*)g.a,
-                       g.lda, (const T*)g.w, g.ldw, (const T*)g.bias, g.c, g.ldc, g.M, g.N, g.K);
+                       g.lda, (const T*)g.w, g.ldw, (const T*)g.bias, g.c, g.ldc, g.M, g.N, g.K, g.src);
     return TJK_OK;
   }
 };
@@ -544,7 +554,7 @@ template <int BKB, int STAGES, int KSPLIT = 1> struct DtlLauncher {
     const dim3 grid(((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN));
     hipLaunchKernelGGL((gemm_dtl_kernel<T, BM, BN, WM, WN, BKB, STAGES, EPI, KSPLIT>), grid,
                        dim3(WM * WN * KSPLIT * 64), 0, g.s, (const T*)g.a, g.lda, (const T*)g.w, g.ldw,
-                       (const T*)g.bias, g.c, g.ldc, g.M, g.N, g.K);
+                       (const T*)g.bias, g.c, g.ldc, g.M, g.N, g.K, g.src);
     return TJK_OK;
   }
 };
@@ -554,6 +564,7 @@ static int launch_epi(int epi, const GemmArgs& g) {
   switch (epi) {
     case TJK_EPI_BIAS: return L::template go<T, BM, BN, WM, WN, TJK_EPI_BIAS>(g);
     case TJK_EPI_BIAS_GELU: return L::template go<T, BM, BN, WM, WN, TJK_EPI_BIAS_GELU>(g);
+    case kEpiResidualFrom: return L::template go<T, BM, BN, WM, WN, kEpiResidualFrom>(g);
     default: return L::template go<T, BM, BN, WM, WN, TJK_EPI_BIAS_RESIDUAL>(g);
   }
 }
@@ -564,7 +575,7 @@ template <int STAGES, int L> struct WsLauncher {
     const dim3 grid(((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN));
     hipLaunchKernelGGL((gemm_ws_kernel<T, BM, BN, WM, WN, STAGES, L, EPI>), grid, dim3((WM * WN + L) * 64), 0,
                        g.s, (const T*)g.a, g.lda, (const T*)g.w, g.ldw, (const T*)g.bias, g.c, g.ldc, g.M, g.N,
-                       g.K);
+                       g.K, g.src);
     return TJK_OK;
   }
 };
@@ -641,7 +652,8 @@ static int run_gemm(int plan, int epi, const GemmArgs& g) {
 
 template <typename T>
 static int gemm_checked(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias, void* c,
-                        int64_t ldc, int64_t m, int64_t n, int64_t k, int epi, int plan, hipStream_t s) {
+                        int64_t ldc, int64_t m, int64_t n, int64_t k, int epi, int plan, hipStream_t s,
+                        const ResSrc& src = ResSrc{nullptr, 0, nullptr, 0, nullptr}) {
   int count;
   const GemmPlan* p = plans<T>(&count);
   if (plan < -1 || plan >= count) return fail(TJK_EINVAL, "tjk_gemm_bias: plan %d out of range [-1,%d)", plan, count);
@@ -651,7 +663,7 @@ static int gemm_checked(const void* a, int64_t lda, const void* w, int64_t ldw, 
   if (p[plan].kind != kStaged && ((int64_t)p[plan].bm * lda * (int64_t)sizeof(T) > INT32_MAX ||
                                   (int64_t)p[plan].bn * ldw * (int64_t)sizeof(T) > INT32_MAX))
     return fail(TJK_EUNSUPPORTED, "tjk_gemm_bias: leading dimension too large for plan %d", plan);
-  const GemmArgs g{a, lda, w, ldw, bias, c, ldc, (int)m, (int)n, (int)k, s};
+  const GemmArgs g{a, lda, w, ldw, bias, c, ldc, (int)m, (int)n, (int)k, s, src};
   return run_gemm<T>(plan, epi, g);
 }
 
@@ -709,5 +721,40 @@ extern "C" int tjk_gemm_bias(const void* a, int64_t lda, const void* w, int64_t 
       return gemm_checked<f16>(a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, plan_id, s);
     default:
       return gemm_checked<bf16>(a, lda, w, ldw, bias, c, ldc, m, n, k, epilogue, plan_id, s);
+  }
+}
+
+extern "C" int tjk_gemm_bias_residual_from(const void* a, int64_t lda, const void* w, int64_t ldw,
+                                           const void* bias, float* c, int64_t ldc,
+                                           int64_t m, int64_t n, int64_t k,
+                                           const void* x, int64_t ld_x, int64_t x_rows,
+                                           const int32_t* rows, int* index_errors,
+                                           int dtype, int plan_id, void* stream) {
+  if (m < 0 || n < 0 || k < 0 || x_rows < 0) return fail(TJK_EINVAL, "tjk_gemm_bias_residual_from: negative shape");
+  if (m == 0 || n == 0) return TJK_OK;
+  if (!a || !w || !c || !x) return fail(TJK_EINVAL, "tjk_gemm_bias_residual_from: null pointer");
+  if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX)
+    return fail(TJK_EUNSUPPORTED, "tjk_gemm_bias_residual_from: shape exceeds int32");
+  if (dtype != TJK_F32 && dtype != TJK_F16 && dtype != TJK_BF16)
+    return fail(TJK_EINVAL, "tjk_gemm_bias_residual_from: bad dtype %d", dtype);
+  const int es = dtype_size(dtype), vec = 16 / es;
+  if (k % vec) return fail(TJK_EUNSUPPORTED, "tjk_gemm_bias_residual_from: k=%lld must be a multiple of %d", (long long)k, vec);
+  if (n % 4) return fail(TJK_EUNSUPPORTED, "tjk_gemm_bias_residual_from: n=%lld must be a multiple of 4", (long long)n);
+  if (lda < k || ldw < k || ldc < n || ld_x < n)
+    return fail(TJK_EINVAL, "tjk_gemm_bias_residual_from: leading dimension too small");
+  if (lda % vec || ldw % vec) return fail(TJK_EUNSUPPORTED, "tjk_gemm_bias_residual_from: lda/ldw must be multiples of %d", vec);
+  if (ldc % 4 || ld_x % 4) return fail(TJK_EUNSUPPORTED, "tjk_gemm_bias_residual_from: ldc/ld_x must be multiples of 4");
+  if (((uintptr_t)a & 15) || ((uintptr_t)w & 15) || ((uintptr_t)c & 15) || ((uintptr_t)bias & (4 * es - 1)) ||
+      ((uintptr_t)x & (4 * es - 1)) || ((uintptr_t)rows & 3) || ((uintptr_t)index_errors & 3))
+    return fail(TJK_EUNSUPPORTED, "tjk_gemm_bias_residual_from: misaligned pointer");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const ResSrc src{x, ld_x, rows, x_rows, index_errors};
+  switch (dtype) {
+    case TJK_F32:
+      return gemm_checked<float>(a, lda, w, ldw, bias, c, ldc, m, n, k, kEpiResidualFrom, plan_id, s, src);
+    case TJK_F16:
+      return gemm_checked<f16>(a, lda, w, ldw, bias, c, ldc, m, n, k, kEpiResidualFrom, plan_id, s, src);
+    default:
+      return gemm_checked<bf16>(a, lda, w, ldw, bias, c, ldc, m, n, k, kEpiResidualFrom, plan_id, s, src);
   }
 }

@@ -57,6 +57,15 @@ __device__ __forceinline__ int xcd_remap(int bid, int nb) {
 // Internal epilogue mode beside the ABI's TJK_EPI_*: store the fp32 sum
 // (acc + bias) as is, no read-modify-write (the fused FFN's split partials).
 constexpr int kEpiStoreF32 = 3;
+// Internal epilogue mode: TJK_EPI_BIAS_RESIDUAL with the residual read from
+// a ResSrc (below) instead of from C.
+constexpr int kEpiResidualFrom = 4;
+// Residual pieces a residual epilogue without a prefetch reads per batch
+// (four VGPRs each).
+constexpr int kResBatch = 4;
+__host__ __device__ constexpr bool epi_residual(int epi) {
+  return epi == TJK_EPI_BIAS_RESIDUAL || epi == kEpiResidualFrom;
+}
 
 // Epilogue shared by the GEMM and fused-FFN kernels.  The accumulators hold
 // C^T blocks: for block (i, j), lane (l32, hi) owns output row
@@ -87,7 +96,7 @@ constexpr int kEpiStoreF32 = 3;
 // piece counted ~7 conflict cycles per write and ~4 per read in the probe.)
 template <typename T, int EPI, int FN>
 struct EpiStage {
-  static constexpr bool F32OUT = EPI == TJK_EPI_BIAS_RESIDUAL || EPI == kEpiStoreF32;
+  static constexpr bool F32OUT = epi_residual(EPI) || EPI == kEpiStoreF32;
   typedef typename std::conditional<F32OUT, float, T>::type S;  // staged type
   static constexpr int WTN = FN * 32;
   static constexpr int SV = 16 / (int)sizeof(S);  // elements per 16-byte piece
@@ -100,35 +109,91 @@ struct EpiStage {
   static __device__ __forceinline__ int at(int r, int p) { return (r * LPR + (p ^ x(r))) * 16; }
 };
 
-// The residual pieces (TJK_EPI_BIAS_RESIDUAL) a wave's epilogue will
-// update, read into registers before the main loop.  A launch whose tiles
-// all run in one round otherwise starts every residual read at the same
-// moment, after the last MFMA; read early, they overlap the main loop and
-// the epilogue only writes.  Piece (j, it) is the one the epilogue's store
-// loop handles for 32-row block j, iteration it.
+// Where kEpiResidualFrom reads the residual it adds: a matrix x in the
+// compute dtype, leading dimension ld, with an optional row map -- output
+// row m reads x row rows[m] (row m without a map).  A row outside
+// [0, nrows) reads as zeros and is counted once in *errors (when given).
+// C is written, not read: the first layer's out-projection adds the packed
+// input rows straight from x, so the first LayerNorm need not materialize
+// the fp32 residual.  (TJK_EPI_BIAS_RESIDUAL reads C and ignores it.)
+// Where there is no map entry or x row to read, the reads go to C's first
+// 16 bytes instead and their value is not used: a read from a selected
+// address needs no branch, and a branch whose paths join after reads waits
+// for them there, and for every store in flight with them.
+struct ResSrc {
+  const void* x;
+  int64_t ld;
+  const int32_t* rows;
+  int64_t nrows;
+  int* errors;
+};
+
+// The residual pieces (TJK_EPI_BIAS_RESIDUAL, kEpiResidualFrom) a wave's
+// epilogue will update, read into registers before the main loop.  A launch
+// whose tiles all run in one round otherwise starts every residual read at
+// the same moment, after the last MFMA; read early, they overlap the main
+// loop and the epilogue only writes.  Piece (j, it) is the one the
+// epilogue's store loop handles for 32-row block j, iteration it.  Pieces
+// from a ResSrc stay raw (half the registers of fp32 for a 2-byte x) until
+// the epilogue converts them.
 struct NoPrefetch {
   static constexpr bool on = false;
   __device__ float4 get(int, int) const { return make_float4(0.f, 0.f, 0.f, 0.f); }
 };
-template <int FM, int FN>
+template <int FM, int FN, typename T = float, bool FROM = false>
 struct ResPrefetch {
   static constexpr bool on = true;
   static constexpr int WTN = FN * 32, LPR = WTN / 4, NPC = 32 * LPR, NIT = (NPC + 63) / 64;
-  float4 r[FM][NIT];
+  typedef typename std::conditional<FROM, typename Quad<T>::raw, float4>::type Piece;
+  // VGPRs per lane counted against a kernel's budget: four per piece in
+  // either form (a raw piece and its x row take three)
+  static constexpr int REGS = FM * NIT * 4;
+  Piece r[FM][NIT];
+  int xrow[FROM ? FM : 1][FROM ? NIT : 1];
+  int64_t nrows = 0;
+  // From a ResSrc every read is from a clamped (always valid) address,
+  // none under a per-lane condition, so all of them go out before any
+  // returns (the row map first, then x); a clamped piece is never used.
   __device__ __forceinline__ void load(const float* __restrict__ C, int64_t ldc, int M, int N, int mw, int nw,
-                                       int lane) {
+                                       int lane, const ResSrc& s) {
 #pragma unroll
     for (int j = 0; j < FM; ++j)
 #pragma unroll
       for (int it = 0; it < NIT; ++it) {
-        const int pc = lane + 64 * it;
-        const int m = mw + 32 * j + pc / LPR, n = nw + (pc % LPR) * 4;
-        r[j][it] = ((NPC % 64 == 0 || pc < NPC) && m < M && n < N)
-                       ? *reinterpret_cast<const float4*>(C + (int64_t)m * ldc + n)
-                       : make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (FROM) {
+          const int pc = min(lane + 64 * it, NPC - 1);
+          const int m = min(mw + 32 * j + pc / LPR, M - 1);
+          const int v = *(s.rows != nullptr ? s.rows + m : reinterpret_cast<const int32_t*>(C));
+          xrow[j][it] = s.rows != nullptr ? v : m;
+        } else {
+          const int pc = lane + 64 * it;
+          const int m = mw + 32 * j + pc / LPR, n = nw + (pc % LPR) * 4;
+          const bool in = (NPC % 64 == 0 || pc < NPC) && m < M && n < N;
+          r[j][it] = in ? *reinterpret_cast<const float4*>(C + (int64_t)m * ldc + n) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
       }
+    if constexpr (FROM) {
+      nrows = s.nrows;
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+          const int pc = min(lane + 64 * it, NPC - 1);
+          const int n = min(nw + (pc % LPR) * 4, N - 4);
+          r[j][it] = *(valid(j, it) ? reinterpret_cast<const Piece*>(static_cast<const T*>(s.x) +
+                                                                     (int64_t)xrow[j][it] * s.ld + n)
+                                    : reinterpret_cast<const Piece*>(C));
+        }
+    }
   }
-  __device__ __forceinline__ float4 get(int j, int it) const { return r[j][it]; }
+  // whether piece (j, it)'s x row lies inside x (ResSrc only)
+  __device__ __forceinline__ bool valid(int j, int it) const {
+    return xrow[FROM ? j : 0][FROM ? it : 0] >= 0 && xrow[FROM ? j : 0][FROM ? it : 0] < nrows;
+  }
+  __device__ __forceinline__ float4 get(int j, int it) const {
+    if constexpr (FROM) return valid(j, it) ? Quad<T>::to(r[j][it]) : make_float4(0.f, 0.f, 0.f, 0.f);
+    else return r[j][it];
+  }
 };
 
 // The bias pieces of a wave's columns nw.. (the epilogue's layout: lane
@@ -162,11 +227,13 @@ struct BiasRaw {
 // C (rows >= M and columns >= N dropped).  `stage` is the wave's private
 // EpiStage<T, EPI, FN>::BYTES of LDS.  `bpre`, when given, holds the bias
 // pieces already loaded (BiasRaw::load with the same bias, N, nw, lane).
-template <typename T, int EPI, int FM, int FN, typename Pre = NoPrefetch>
+// RB_: residual pieces per batched read (0: read one by one).
+template <typename T, int EPI, int FM, int FN, typename Pre = NoPrefetch, int RB_ = kResBatch>
 __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* __restrict__ bias,
                                          void* __restrict__ Cv, int64_t ldc, int M, int N, int mw, int nw,
                                          int lane, char* __restrict__ stage, const Pre& pre = Pre(),
-                                         const BiasRaw<T, FN>* bpre = nullptr) {
+                                         const BiasRaw<T, FN>* bpre = nullptr,
+                                         const ResSrc& src = ResSrc{nullptr, 0, nullptr, 0, nullptr}) {
   typedef EpiStage<T, EPI, FN> E;
   constexpr int LPR = E::LPR;          // 16-byte pieces per staged row
   constexpr int NPC = 32 * LPR;        // pieces per 32-row block
@@ -217,8 +284,64 @@ __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* _
     roff[it] = E::at(pc / LPR, pc % LPR);
   }
 
+  // kEpiResidualFrom with batched reads: lane (l32, *) holds the x row of
+  // output row mw + 32 j + l32, read from the row map one block ahead (a
+  // wait for a read issued after the previous block's stores would also
+  // wait for those stores); without a map (identity) the read goes to a
+  // word of C and is not used (see ResSrc).
+  constexpr bool XMAP = EPI == kEpiResidualFrom && !Pre::on && RB_ > 0;
+  const bool has_map = src.rows != nullptr;
+  auto map_read = [&](int j) __attribute__((always_inline)) {
+    const int m = min(mw + 32 * j + l32, M - 1);
+    return *(has_map ? src.rows + m : static_cast<const int32_t*>(Cv));
+  };
+  int map_next = XMAP ? map_read(0) : 0;
+
 #pragma unroll
   for (int j = 0; j < FM; ++j) {
+    // Without a prefetch, the block's residual pieces are read ahead of
+    // their use, RB_ at a time from clamped (always valid) addresses: the
+    // first batch before the block's staging, each further one when the
+    // store loop starts the batch before it.  Read inside the store loop
+    // (RB_ == 0: the register-tight tiles, which the batches spilled), under
+    // each lane's bounds check, every piece waits for its own round trip.
+    // A clamped piece is never used.
+    constexpr bool RES_LOAD = epi_residual(EPI) && !Pre::on && RB_ > 0;
+    constexpr int NRL = RES_LOAD ? NIT : 1;
+    constexpr int RB = RB_ < 1 ? 1 : RB_ < NIT ? RB_ : NIT;
+    typedef typename std::conditional<EPI == kEpiResidualFrom, typename Quad<T>::raw, float4>::type ResPiece;
+    ResPiece rl[NRL];
+    int xrow[EPI == kEpiResidualFrom ? NRL : 1];
+    if constexpr (XMAP) {
+      const int map = map_next;
+      if (j + 1 < FM) map_next = map_read(j + 1);
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        const int pc = min(lane + 64 * it, NPC - 1);
+        const int mrow = __shfl(map, pc / LPR);  // lanes r and r + 32 hold row r's entry
+        xrow[it] = has_map ? mrow : min(mw + 32 * j + pc / LPR, M - 1);
+      }
+    }
+    auto res_read = [&](int b) __attribute__((always_inline)) {
+      if constexpr (RES_LOAD) {
+#pragma unroll
+        for (int q = 0; q < RB; ++q) {
+          const int it = RB * b + q;
+          if (it >= NIT) break;
+          const int pc = min(lane + 64 * it, NPC - 1);
+          const int m = min(mw + 32 * j + pc / LPR, M - 1), n = min(nw + (pc % LPR) * 4, N - 4);
+          if constexpr (EPI == kEpiResidualFrom) {
+            const int xr = xrow[it];
+            const bool ok = xr >= 0 && xr < src.nrows;
+            rl[it] = *(ok ? reinterpret_cast<const ResPiece*>(static_cast<const T*>(src.x) + (int64_t)xr * src.ld + n)
+                          : static_cast<const ResPiece*>(Cv));
+          } else {
+            rl[it] = *reinterpret_cast<const float4*>(static_cast<const float*>(Cv) + (int64_t)m * ldc + n);
+          }
+        }
+      }
+    };
+    res_read(0);
 #pragma unroll
     for (int i = 0; i < FN; ++i) {
       if constexpr (E::SV == 4) {  // fp32 staged: a lane's four columns are one piece
@@ -246,6 +369,7 @@ __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* _
       const auto wr = rows.writer<decltype(wt_tag)::value>();
 #pragma unroll
       for (int it = 0; it < NIT; ++it) {
+        if (RES_LOAD && it % RB == 0 && it + RB < NIT) res_read(it / RB + 1);
         const int pc = lane + 64 * it;  // piece index: row pc / LPR, piece pc % LPR
         if (NPC % 64 != 0 && pc >= NPC) break;
         const int rr = pc / LPR, cc = (pc % LPR) * E::SV;
@@ -253,10 +377,36 @@ __device__ __forceinline__ void epilogue(const f32x16 (&acc)[FN][FM], const T* _
         const uint4 piece = *reinterpret_cast<const uint4*>(stage + roff[it]);
         const int off = (int)(((int64_t)rr * ldc + cc) * OB);
         if (m < M && n < N) {
-          if constexpr (EPI == TJK_EPI_BIAS_RESIDUAL) {
+          if constexpr (epi_residual(EPI)) {
             // fp32 pieces never straddle N (N % 4 == 0)
             const float4 a = __builtin_bit_cast(float4, piece);
-            float4 o = Pre::on ? pre.get(j, it) : *reinterpret_cast<const float4*>(rows.p + off);
+            float4 o;
+            int xr = 0;  // x row (ResSrc)
+            if constexpr (Pre::on) {
+              o = pre.get(j, it);
+            } else if constexpr (RES_LOAD) {
+              if constexpr (EPI == kEpiResidualFrom) {
+                xr = xrow[it];
+                o = xr >= 0 && xr < src.nrows ? Quad<T>::to(rl[it]) : make_float4(0.f, 0.f, 0.f, 0.f);
+              } else {
+                o = rl[it];
+              }
+            } else if constexpr (EPI == kEpiResidualFrom) {
+              xr = src.rows != nullptr ? src.rows[m] : m;
+              o = xr >= 0 && xr < src.nrows
+                      ? Quad<T>::to(*reinterpret_cast<const typename Quad<T>::raw*>(
+                            static_cast<const T*>(src.x) + (int64_t)xr * src.ld + n))
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
+            } else {
+              o = *reinterpret_cast<const float4*>(rows.p + off);
+            }
+            if constexpr (EPI == kEpiResidualFrom) {
+              bool bad;
+              if constexpr (Pre::on) bad = !pre.valid(j, it);
+              else bad = !(xr >= 0 && xr < src.nrows);
+              if (bad && n == 0 && src.errors != nullptr)
+                atomicAdd(src.errors, 1);  // once per row: column 0 is one lane of one tile
+            }
             o.x += a.x; o.y += a.y; o.z += a.z; o.w += a.w;
             wr.put(off, o);
           } else if constexpr (EPI == kEpiStoreF32) {

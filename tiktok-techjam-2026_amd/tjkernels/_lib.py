@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede the library load; see module docstring)
 
 LIB_PATH = Path(__file__).with_name("libtjk.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 F32, F16, BF16 = 0, 1, 2
 OK, EINVAL, EUNSUPPORTED = 0, -1, -2
@@ -34,6 +34,8 @@ _SIGNATURES = {
                                  _vp, _vp, _i64, _i64, _f32, _vp, _i64, _vp, _vp, _vp]),
     "tjk_gemm_bias": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64,
                              _i32, _i32, _i32, _vp]),
+    "tjk_gemm_bias_residual_from": (_i32, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64,
+                                           _vp, _i64, _i64, _vp, _vp, _i32, _i32, _vp]),
     "tjk_gemm_plan_count": (_i32, [_i32]),
     "tjk_gemm_plan_info": (_i32, [_i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i32),
                                   ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),

@@ -265,6 +265,9 @@ class Forward:
     use_sched: bool = False
     use_block: bool = False
     ln_in_gemm: bool = False  # LayerNorms 1 (after layer 0) and 2 inside the QKV / FFN1 GEMMs
+    # layer 0's out-proj adds x's rows itself, so the first LayerNorm writes
+    # no residual (eager forwards: a graph would keep the first call's x)
+    res_from_x: bool = False
     splits: int = 1
     pending: Optional[torch.Tensor] = None  # what the next LayerNorm adds to res
 
@@ -400,7 +403,9 @@ class Engine:
                      ws=self._workspace(batch, seq, plan, splits, block), tiles=tp,
                      packing=packing if mode == MASK_PREFIX else None,
                      key_mask=mask if mode == MASK_GENERAL else None, use_block=block, splits=splits,
-                     ln_in_gemm=ln_in)
+                     ln_in_gemm=ln_in,
+                     res_from_x=(plan.epilogue_residual and not plan.cuda_graph and not block
+                                 and cdt == self.dtype))
         if fused:
             fw.pending = fw.view("parts")
         elif not plan.epilogue_residual:
@@ -422,11 +427,11 @@ class Engine:
 
     def _first(self, fw: Forward, x: torch.Tensor) -> None:
         """Layer-0 LN1: reads x (gathering the valid rows of a prefix mask),
-        writes the residual and h."""
+        writes h, and the residual unless layer 0's out-proj reads x."""
         n1 = self.weights.blocks[0].norm1
         gather = fw.packing.gather if fw.packing is not None else None
         ops.add_layernorm(x.reshape(fw.batch * fw.seq, self.shape.d_model), None, n1.weight, n1.bias, n1.eps,
-                          fw.view("h"), res_out=fw.view("res"), row_index=gather)
+                          fw.view("h"), res_out=None if fw.res_from_x else fw.view("res"), row_index=gather)
 
     def _attention(self, fw: Forward) -> None:
         shp = self.shape
@@ -488,10 +493,15 @@ class Engine:
             ops.gemm(h, blk.fc1.weight, blk.fc1.bias, mid, ops.EPI_BIAS_GELU, fw.tiles.fc1)
             ops.gemm(mid, blk.fc2.weight, blk.fc2.bias, delta, ops.EPI_BIAS, fw.tiles.fc2)
 
-    def _body(self, fw: Forward) -> None:
+    def _body(self, fw: Forward, x: Optional[torch.Tensor] = None) -> None:
         """Every layer between the first LayerNorm and the final one: the
-        part the hipGraph captures (fixed buffers only)."""
+        part the hipGraph captures (fixed buffers only).  With
+        ``fw.res_from_x`` layer 0's out-proj forms the residual from the
+        forward's input ``x`` (residual = x[gather] + attn_out, the sum the
+        first LayerNorm's residual write and the residual epilogue form)."""
         res, h, ctx = fw.view("res"), fw.view("h"), fw.view("ctx")
+        if fw.res_from_x and x is None:
+            raise RuntimeError("this forward's first layer reads x: pass it to _body")
         for i, blk in enumerate(self.weights.blocks):
             # LayerNorm 1 of the layers after the first: inside the QKV GEMM,
             # or a launch of its own
@@ -510,7 +520,12 @@ class Engine:
                 else:
                     ops.gemm(h, blk.qkv.weight, blk.qkv.bias, fw.view("qkv"), ops.EPI_BIAS, fw.tiles.qkv)
                 self._attention(fw)
-                if self.plan.epilogue_residual:
+                if i == 0 and fw.res_from_x:
+                    ops.gemm_residual_from(ctx, blk.out.weight, blk.out.bias, res,
+                                           x.reshape(fw.batch * fw.seq, self.shape.d_model),
+                                           rows=fw.packing.gather if fw.packing is not None else None,
+                                           plan=fw.tiles.out)
+                elif self.plan.epilogue_residual:
                     ops.gemm(ctx, blk.out.weight, blk.out.bias, res, ops.EPI_BIAS_RESIDUAL, fw.tiles.out)
                 else:
                     ops.gemm(ctx, blk.out.weight, blk.out.bias, fw.view("delta"), ops.EPI_BIAS, fw.tiles.out)
@@ -530,7 +545,7 @@ class Engine:
         fw = self._prepare(batch, seq, mode, packing, mask)
         out = torch.empty((batch, seq, d), dtype=self.dtype, device=x.device)
         self._first(fw, x)
-        self._body(fw)
+        self._body(fw, x)
         self._final(fw, out, mask.reshape(-1) if mode == MASK_GENERAL else None)
         self._check(fw)
         return out

@@ -135,6 +135,42 @@ def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], out: to
     return out
 
 
+def gemm_residual_from(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], out: torch.Tensor,
+                       x: torch.Tensor, rows: Optional[torch.Tensor] = None,
+                       index_errors: Optional[torch.Tensor] = None, plan: int = -1) -> torch.Tensor:
+    """out = a @ w.T + bias + x[rows] in fp32 (``out`` written, not read):
+    the EPI_BIAS_RESIDUAL ``gemm`` with its residual read from the
+    compute-dtype ``x`` through the int32 row map ``rows`` (identity when
+    None) instead of from ``out``.  A row outside ``x`` adds zeros and is
+    counted in ``index_errors``.  Bit-identical to copying x[rows] into an
+    fp32 ``out`` and running the residual ``gemm``; the first layer's
+    out-projection of tjkernels/engine.py:230-252."""
+    _require_gpu(a, w, bias, out, x, rows, index_errors)
+    m, k = a.shape
+    n, k2 = w.shape
+    if k != k2 or out.shape[0] != m or out.shape[1] != n:
+        raise TjkError(f"gemm shape mismatch a{tuple(a.shape)} w{tuple(w.shape)} out{tuple(out.shape)}")
+    if w.dtype != a.dtype or (bias is not None and bias.dtype != a.dtype) or x.dtype != a.dtype:
+        raise TjkError("gemm_residual_from: a, w, bias and x share the compute dtype")
+    if out.dtype != torch.float32:
+        raise TjkError("residual epilogue needs a float32 out")
+    if x.dim() != 2 or x.shape[1] != n:
+        raise TjkError(f"x must be [rows, {n}], got {tuple(x.shape)}")
+    if rows is not None:
+        if rows.dtype != torch.int32 or rows.dim() != 1 or not rows.is_contiguous() or rows.numel() < m:
+            raise TjkError("rows must be a contiguous int32 vector with an entry per output row")
+    elif x.shape[0] < m:
+        raise TjkError("x has fewer rows than out and no row map is given")
+    if index_errors is not None and (index_errors.dtype != torch.int32 or index_errors.numel() < 1):
+        raise TjkError("index_errors must be an int32 device tensor of at least one element")
+    status = _lib.load().tjk_gemm_bias_residual_from(
+        a.data_ptr(), _rowmajor(a, "a"), w.data_ptr(), _rowmajor(w, "w"), _ptr(bias), out.data_ptr(),
+        _rowmajor(out, "out"), m, n, k, x.data_ptr(), _rowmajor(x, "x"), x.shape[0], _ptr(rows),
+        _ptr(index_errors), _code(a), plan, _stream(a))
+    check(status, "tjk_gemm_bias_residual_from")
+    return out
+
+
 def gemm_ln_supported(k: int, dtype: torch.dtype) -> bool:
     """Whether tjk_gemm_ln takes a K (= d_model) and compute dtype."""
     code = _lib.DTYPE_CODES.get(dtype)
