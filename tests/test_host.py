@@ -616,6 +616,9 @@ def test_rocprof_summary_labels_deferred_projections():
     ws2 = "_ZN3tjk14gemm_ws_kernelIDF16bLi192ELi128ELi2ELi4ELi4ELi4ELi2EEEvPKT_lS3_lS3_Pvliii"
     assert rs._gemm_epilogue(ws2) == 2 and rs._kind_ok("gemm_out_residual", ws2)
     assert rs._relabel("gemm_out_residual", ws2) == "gemm_out_residual" and rs._tjk(ws2)
+    # the first layer's out-proj adding the input rows (EPI 4) is a residual GEMM as well
+    ws4 = "_ZN3tjk14gemm_ws_kernelIDF16bLi192ELi128ELi2ELi4ELi4ELi4ELi4EEEvPKT_lS3_lS3_PvliiiNS_6ResSrcE"
+    assert rs._gemm_epilogue(ws4) == 4 and rs._relabel("gemm_out_residual", ws4) == "gemm_out_residual"
 
 
 def test_plan_tile_rows_round_trip_and_validation():

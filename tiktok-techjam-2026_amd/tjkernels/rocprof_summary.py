@@ -72,7 +72,8 @@ def _labels(layers: int, fused: bool = False) -> List[str]:
 def _gemm_epilogue(name: str) -> Optional[int]:
     """EPI template argument of a gemm_dtl_kernel<T, BM, BN, WM, WN, BKB,
     STAGES, EPI, KSPLIT> or gemm_ws_kernel<T, BM, BN, WM, WN, STAGES, L, EPI>
-    name, the seventh integer in both (2: residual read-modify-write)."""
+    name, the seventh integer in both (2: residual read-modify-write, 4:
+    residual read from the input x, the first layer's out-proj)."""
     kern = GEMM if GEMM in name else GEMM_WS if GEMM_WS in name else None
     ints = re.findall(r"Li(\d+)E", name.split(kern, 1)[1]) if kern else []
     return int(ints[6]) if len(ints) >= 7 else None
@@ -81,7 +82,7 @@ def _gemm_epilogue(name: str) -> Optional[int]:
 def _relabel(label: str, name: str) -> str:
     # the out-proj / FFN2 of a deferred-residual plan write their output for
     # the next LayerNorm instead of adding into the residual
-    if label.endswith("_residual") and _gemm_epilogue(name) not in (None, 2):
+    if label.endswith("_residual") and _gemm_epilogue(name) not in (None, 2, 4):
         return label[:-len("_residual")]
     return label
 
