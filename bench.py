@@ -101,8 +101,8 @@ def _breakdown(engine, x, mask):
     import torch
     from tjkernels import ops
     classes, calls = {}, {}
-    orig = {name: getattr(ops, name) for name in ("gemm", "flash_attention", "flash_attention_sched",
-                                                  "add_layernorm", "ffn")}
+    orig = {name: getattr(ops, name) for name in ("gemm", "gemm_residual_from", "flash_attention",
+                                                  "flash_attention_sched", "add_layernorm", "ffn")}
     events = []
 
     def wrap(name, fn):
@@ -119,6 +119,9 @@ def _breakdown(engine, x, mask):
                 else:
                     label = ("gemm_out" if w.shape[1] == d else "gemm_ffn2") + ("_residual" if epi == 2 else "")
                 flops = 2.0 * a0.shape[0] * w.shape[0] * w.shape[1]
+            elif name == "gemm_residual_from":  # the first layer's out-proj, adding the input rows
+                label = "gemm_out_residual"
+                flops = 2.0 * a[0].shape[0] * a[1].shape[0] * a[1].shape[1]
             elif name == "flash_attention":
                 flops = _attn_flops(a[0], k.get("causal", True), k.get("cu_seqlens"))
             elif name == "flash_attention_sched":
