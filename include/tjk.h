@@ -133,7 +133,8 @@ int tjk_gemm_bias(const void* a, int64_t lda, const void* w, int64_t ldw,
  * residual read from x (`dtype`, leading dimension ld_x) instead of from C.
  * r(m) = rows[m] (an int32 row map, e.g. the packing of prefix-masked
  * tokens), or m when rows is NULL; a row r(m) outside [0, x_rows) adds
- * zeros and is counted once in *index_errors (optional).  The sum is
+ * zeros and is counted once in *index_errors (optional; x may be NULL when
+ * x_rows is 0).  The sum is
  * formed exactly as tjk_gemm_bias forms it from a residual holding x's rows
  * in fp32 (the same bits).  Requires what tjk_gemm_bias requires, ld_x %
  * 4 == 0 and x aligned to 4 elements.

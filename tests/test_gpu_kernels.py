@@ -268,6 +268,16 @@ def test_gemm_residual_from_rows_outside_x_add_zeros_and_are_counted(device):
         torch.cuda.synchronize()
         assert torch.equal(got, want), f"plan {plan}"
         assert int(errors.item()) == len(bad), f"plan {plan}: {int(errors.item())} errors counted"
+        # an x with no rows: every row adds zeros and is counted
+        errors.zero_()
+        xd = x.to(device)
+        got = torch.full((m, n), float("nan"), device=device)
+        ops.gemm_residual_from(a, w, b, got, xd[:0], rows.to(device), index_errors=errors, plan=plan)
+        want = torch.zeros(m, n, device=device)
+        ops.gemm(a, w, b, want, ops.EPI_BIAS_RESIDUAL, plan)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"plan {plan}, empty x"
+        assert int(errors.item()) == m, f"plan {plan}, empty x: {int(errors.item())} errors counted"
 
 
 @pytest.mark.parametrize("plan", list(STAGED32) + list(DTL32))

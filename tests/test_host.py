@@ -88,6 +88,9 @@ def test_abi_rejects_bad_arguments_without_launching():
     assert from_x(fake, 8, fake, 8, None, fake, 8, 4, 8, 8, fake, 10, 4, None, None, _lib.BF16, -1, None) \
         == _lib.EUNSUPPORTED  # ld_x % 4
     assert from_x(None, 8, None, 8, None, None, 8, 0, 8, 8, None, 8, 0, None, None, _lib.BF16, -1, None) == 0
+    # x may be NULL only when it has no rows (then nothing of it is read)
+    assert from_x(fake, 8, fake, 8, None, fake, 8, 4, 8, 8, None, 8, 1, None, None, _lib.BF16, -1, None) \
+        == _lib.EINVAL
     # empty work is a successful no-op
     assert lib.tjk_gemm_bias(None, 8, None, 8, None, None, 8, 0, 4, 8, _lib.BF16, 0, -1, None) == 0
     assert lib.tjk_gemm_plan_count(_lib.BF16) >= 4

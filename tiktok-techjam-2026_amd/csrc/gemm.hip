@@ -732,7 +732,8 @@ extern "C" int tjk_gemm_bias_residual_from(const void* a, int64_t lda, const voi
                                            int dtype, int plan_id, void* stream) {
   if (m < 0 || n < 0 || k < 0 || x_rows < 0) return fail(TJK_EINVAL, "tjk_gemm_bias_residual_from: negative shape");
   if (m == 0 || n == 0) return TJK_OK;
-  if (!a || !w || !c || !x) return fail(TJK_EINVAL, "tjk_gemm_bias_residual_from: null pointer");
+  // x is read only at rows below x_rows: it may be NULL when there are none
+  if (!a || !w || !c || (!x && x_rows > 0)) return fail(TJK_EINVAL, "tjk_gemm_bias_residual_from: null pointer");
   if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX)
     return fail(TJK_EUNSUPPORTED, "tjk_gemm_bias_residual_from: shape exceeds int32");
   if (dtype != TJK_F32 && dtype != TJK_F16 && dtype != TJK_BF16)
